@@ -1,0 +1,116 @@
+/*
+ * ternix_hip.h -- C-ABI of the MI355X (gfx950) ternary matmul library
+ * (libternix_hip.so).
+ *
+ *   C[M,N] int32 = A[M,K] int8 x W[K,N],  W in {-1,0,+1}
+ *
+ * W is passed packed: a row-major K x (N/4) byte array, four weights per byte
+ * along N, weight (k, n) in bits 2*(n%4)..2*(n%4)+1 of byte k*(N/4) + n/4, with
+ * 00 = 0, 01 = +1, 11 = -1 (reference: src/bitpack.cpp:5-15, README.md:46-53).
+ * The undefined code 10 is decoded as -2 by every kernel here, which is what
+ * the reference's scalar CPU kernel and CUDA kernels do
+ * (src/mul_mat_ternary.cpp:53, src/cuda_kernels.cu:40).
+ *
+ * Every function returns an int that is a hipError_t value: 0 (hipSuccess),
+ * 1 (hipErrorInvalidValue) when an argument is rejected -- always before any
+ * pointer is touched or any work is queued -- or the runtime error of the
+ * failing HIP call.  This mirrors the cudaError_t contract of the reference
+ * (include/ternix/cuda_kernels.cuh:8-21, src/cuda_kernels.cu:126-156).
+ *
+ * Device-pointer entry points are asynchronous on `stream` (a hipStream_t, or
+ * NULL for the default stream).  The caller owns all buffers; C is fully
+ * overwritten (never accumulated into).  Shapes are int64; N must be a
+ * multiple of 4; M, K or N may be 0.  No device-pointer entry point allocates
+ * memory.
+ * Calls are thread-safe; calls that share an output buffer race as any two
+ * kernels writing one buffer do.
+ *
+ * Kernels are written for gfx950 only; on any other device the entry points
+ * return hipErrorInvalidDeviceFunction (98) from the launch.
+ */
+#ifndef TERNIX_HIP_H
+#define TERNIX_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Automatic dispatch: the skinny split-K MFMA kernel for small M, the
+ * LDS-tiled MFMA GEMM for large M.  Any M, K >= 0; N % 4 == 0.
+ * Replaces: ternix::mul_mat_ternary_cuda_tiled / _naive
+ * (reference include/ternix/cuda_kernels.cuh:11-17) for callers that do not
+ * want to pick a kernel. */
+int ternix_hip_mul_mat_ternary(const int8_t* dA, const uint8_t* dB, int32_t* dC,
+                               int64_t M, int64_t K, int64_t N, void* stream);
+
+/* Forced skinny (decode) path: M <= 32 (returns hipErrorInvalidValue above).
+ * Weights decoded in registers, int8 MFMA, split-K over the grid.  When K is
+ * split across workgroups the kernel zeroes C and accumulates with int32
+ * atomics, which are exact and order-independent.
+ * New in this library; its reference counterpart is the M=1 use of
+ * mul_mat_ternary_cuda_naive (reference src/cuda_kernels.cu:126-132). */
+int ternix_hip_mul_mat_ternary_gemv(const int8_t* dA, const uint8_t* dB, int32_t* dC,
+                                    int64_t M, int64_t K, int64_t N, void* stream);
+
+/* Forced LDS-tiled int8-MFMA GEMM path: any M, K; N % 4 == 0.
+ * Replaces the computation of mul_mat_ternary_cuda_tiled (reference
+ * src/cuda_kernels.cu:71-122, 134-140) without its M,N,K % 64 restriction. */
+int ternix_hip_mul_mat_ternary_gemm(const int8_t* dA, const uint8_t* dB, int32_t* dC,
+                                    int64_t M, int64_t K, int64_t N, void* stream);
+
+/* Drop-in for mul_mat_ternary_cuda_tiled (reference
+ * include/ternix/cuda_kernels.cuh:14-17, src/cuda_kernels.cu:134-140): the same
+ * shape contract -- M, N and K multiples of 64, else hipErrorInvalidValue
+ * before any pointer is used -- computed by the MFMA GEMM. */
+int ternix_hip_mul_mat_ternary_tiled(const int8_t* dA, const uint8_t* dB, int32_t* dC,
+                                     int64_t M, int64_t K, int64_t N, void* stream);
+
+/* Drop-in for mul_mat_ternary_cuda_naive (reference
+ * include/ternix/cuda_kernels.cuh:10-12, src/cuda_kernels.cu:42-54, 126-132):
+ * one work-item per output element, any M, K; N % 4 == 0. */
+int ternix_hip_mul_mat_ternary_naive(const int8_t* dA, const uint8_t* dB, int32_t* dC,
+                                     int64_t M, int64_t K, int64_t N, void* stream);
+
+/* Kernel choice for ternix_hip_mul_mat_ternary_host. */
+enum ternix_hip_variant {
+    TERNIX_HIP_AUTO = 0,
+    TERNIX_HIP_NAIVE = 1,
+    TERNIX_HIP_GEMV = 2,
+    TERNIX_HIP_GEMM = 3,
+    TERNIX_HIP_TILED = 4
+};
+
+/* Synchronous host-pointer convenience wrapper: allocates device buffers,
+ * copies A and B in, runs `variant` on the default stream, synchronises,
+ * copies C out and frees every buffer on every path.
+ * Replaces mul_mat_ternary_cuda_host (reference
+ * include/ternix/cuda_kernels.cuh:19-21, src/cuda_kernels.cu:142-156), whose
+ * bool `tiled` maps to TERNIX_HIP_TILED / TERNIX_HIP_NAIVE. */
+int ternix_hip_mul_mat_ternary_host(const int8_t* A, const uint8_t* B_packed, int32_t* C,
+                                    int64_t M, int64_t K, int64_t N, int variant);
+
+/* hipGetErrorString of a status returned above (never NULL). */
+const char* ternix_hip_error_string(int status);
+
+/* Library version as an integer, major*10000 + minor*100 + patch. */
+int ternix_hip_version(void);
+
+/* ---- weight format (host), C-ABI of reference include/ternix/bitpack.hpp:6-8 ---- */
+
+/* pack_ternary_weights (reference src/bitpack.cpp:5-15): `size` elements of
+ * {-1,0,+1} -> size/4 bytes; values outside {-1,+1} encode as 00. */
+void ternix_pack_ternary_weights(uint8_t* packed, const int8_t* unpacked, size_t size);
+/* unpack_ternary_weights (reference src/bitpack.cpp:17-27): 01 -> +1,
+ * 11 -> -1, 00 and 10 -> 0. */
+void ternix_unpack_ternary_weights(int8_t* unpacked, const uint8_t* packed, size_t size);
+/* interleave_weights_offline (reference src/bitpack.cpp:29-33): identity copy
+ * of size/4 bytes (the K x N/4 layout is consumed as is by every kernel). */
+void ternix_interleave_weights_offline(uint8_t* interleaved, const uint8_t* packed, size_t size);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TERNIX_HIP_H */

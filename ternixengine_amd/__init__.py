@@ -1,0 +1,105 @@
+"""ternixengine_amd -- MI355X (gfx950) ternary matmul: C[M,N] int32 = A[M,K] int8 x W[K,N] ternary.
+
+Python face of libternix_hip.so, shaped like the reference's `ternix_engine` module
+(bindings/python/pybind11_wrapper.cpp:21-90):
+
+  pack_ternary(w)                 (K, N) int8 in {-1,0,1}  -> (K, N/4) uint8     (:21-31)
+  unpack_ternary(packed)          (K, N/4) uint8           -> (K, N) int8        (:33-39)
+  ternary_matmul(a, b_packed, impl="hip") -> (M, N) int32                         (:41-71)
+  has_cuda (False), has_hip
+
+`impl` names the GPU kernel: "hip" (automatic choice), "hip_gemv" (skinny split-K, M <= 32),
+"hip_gemm" (LDS-tiled MFMA), "hip_tiled" (the reference tiled kernel's M,N,K % 64 contract) and
+"hip_naive".  Errors follow the reference: ValueError for bad shapes, weights or impl names;
+RuntimeError("HIP error: ...") for device errors.  The GIL is released during device work (ctypes).
+
+Device-pointer access (no copies) is `mul_mat_ternary(dA, dB, dC, M, K, N, stream=None, path="auto")`
+with integer device addresses, mirroring the C-ABI in include/ternix/ternix_hip.h.
+"""
+import ctypes
+
+import numpy as np
+
+from . import _lib
+from ._lib import LibraryNotBuilt, load as _load  # noqa: F401
+
+__all__ = ["pack_ternary", "unpack_ternary", "ternary_matmul", "mul_mat_ternary", "has_cuda", "has_hip",
+           "HIP_IMPLS", "ternix_error"]
+
+has_cuda = False
+HIP_IMPLS = {"hip": 0, "hip_naive": 1, "hip_gemv": 2, "hip_gemm": 3, "hip_tiled": 4}
+_PATHS = {"auto": "ternix_hip_mul_mat_ternary", "gemv": "ternix_hip_mul_mat_ternary_gemv",
+          "gemm": "ternix_hip_mul_mat_ternary_gemm", "tiled": "ternix_hip_mul_mat_ternary_tiled",
+          "naive": "ternix_hip_mul_mat_ternary_naive"}
+
+
+def _has_hip():
+    try:
+        from . import hip_runtime
+        return hip_runtime.device_count() > 0
+    except OSError:
+        return False
+
+
+has_hip = _has_hip()
+
+
+def ternix_error(status):
+    return _load().ternix_hip_error_string(int(status)).decode(errors="replace")
+
+
+def _ptr(arr):
+    return arr.ctypes.data_as(ctypes.c_void_p)
+
+
+def pack_ternary(w):
+    """Pack a (K, N) int8 array with values in {-1, 0, +1} into the (K, N/4) uint8 layout."""
+    w = np.ascontiguousarray(np.asarray(w).astype(np.int8, copy=False))
+    if w.ndim != 2:
+        raise ValueError("pack_ternary expects a 2-D (K, N) array")
+    k, n = w.shape
+    if n % 4 != 0:
+        raise ValueError("N must be a multiple of 4")
+    if w.size and (w.min() < -1 or w.max() > 1):
+        raise ValueError("weights must be in {-1, 0, +1}")
+    out = np.empty((k, n // 4), dtype=np.uint8)
+    _load().ternix_pack_ternary_weights(_ptr(out), _ptr(w), w.size)
+    return out
+
+
+def unpack_ternary(packed):
+    """Inverse of pack_ternary: (K, N/4) uint8 -> (K, N) int8."""
+    p = np.ascontiguousarray(np.asarray(packed).astype(np.uint8, copy=False))
+    if p.ndim != 2:
+        raise ValueError("unpack_ternary expects a 2-D (K, N/4) array")
+    k, n4 = p.shape
+    out = np.empty((k, n4 * 4), dtype=np.int8)
+    _load().ternix_unpack_ternary_weights(_ptr(out), _ptr(p), out.size)
+    return out
+
+
+def ternary_matmul(a, b_packed, impl="hip"):
+    """C = A (M,K int8) @ W (K,N ternary, packed (K, N/4) uint8) -> (M,N) int32, computed on the GPU."""
+    a = np.ascontiguousarray(np.asarray(a).astype(np.int8, copy=False))
+    b = np.ascontiguousarray(np.asarray(b_packed).astype(np.uint8, copy=False))
+    if a.ndim != 2 or b.ndim != 2:
+        raise ValueError("A must be (M, K) and B_packed (K, N/4)")
+    m, k = a.shape
+    n = b.shape[1] * 4
+    if b.shape[0] != k:
+        raise ValueError("inner dimensions do not match")
+    if impl not in HIP_IMPLS:
+        raise ValueError(f"unknown impl '{impl}'")
+    c = np.empty((m, n), dtype=np.int32)
+    status = _load().ternix_hip_mul_mat_ternary_host(_ptr(a), _ptr(b), _ptr(c), m, k, n, HIP_IMPLS[impl])
+    if status != 0:
+        if status == 1:
+            raise ValueError(f"impl '{impl}' rejected shape M={m} K={k} N={n}")
+        raise RuntimeError(f"HIP error: {ternix_error(status)}")
+    return c
+
+
+def mul_mat_ternary(dA, dB, dC, M, K, N, stream=None, path="auto"):
+    """Asynchronous device-pointer call of the C-ABI; returns the hipError_t status as an int."""
+    fn = getattr(_load(), _PATHS[path])
+    return fn(dA, dB, dC, int(M), int(K), int(N), stream)

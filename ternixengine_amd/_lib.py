@@ -1,0 +1,55 @@
+"""Loader of libternix_hip.so (built in-tree by ternixengine_amd/csrc/Makefile).
+
+The library is the product: if it is missing the import fails loudly; nothing here falls back to a
+CPU implementation.
+"""
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libternix_hip.so")
+
+_lib = None
+
+
+class LibraryNotBuilt(ImportError):
+    pass
+
+
+def load():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise LibraryNotBuilt(
+            f"{LIB_PATH} is missing: build it with `make -C ternixengine_amd/csrc` "
+            "(or __graft_entry__.build()); there is no fallback implementation")
+    lib = ctypes.CDLL(LIB_PATH)
+    i8p = ctypes.c_void_p
+    i64 = ctypes.c_int64
+    for name in ("ternix_hip_mul_mat_ternary", "ternix_hip_mul_mat_ternary_gemv", "ternix_hip_mul_mat_ternary_gemm",
+                 "ternix_hip_mul_mat_ternary_tiled", "ternix_hip_mul_mat_ternary_naive"):
+        f = getattr(lib, name)
+        f.argtypes = [i8p, i8p, i8p, i64, i64, i64, ctypes.c_void_p]
+        f.restype = ctypes.c_int
+    lib.ternix_hip_mul_mat_ternary_host.argtypes = [i8p, i8p, i8p, i64, i64, i64, ctypes.c_int]
+    lib.ternix_hip_mul_mat_ternary_host.restype = ctypes.c_int
+    lib.ternix_hip_error_string.argtypes = [ctypes.c_int]
+    lib.ternix_hip_error_string.restype = ctypes.c_char_p
+    lib.ternix_hip_version.restype = ctypes.c_int
+    for name in ("ternix_pack_ternary_weights", "ternix_unpack_ternary_weights", "ternix_interleave_weights_offline"):
+        f = getattr(lib, name)
+        f.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]
+        f.restype = None
+    u64 = ctypes.c_uint64
+    lib.ternix_synth_u64.argtypes = [u64, u64, u64]
+    lib.ternix_synth_u64.restype = u64
+    lib.ternix_synth_act_uniform.argtypes = [ctypes.c_void_p, ctypes.c_size_t, u64, u64]
+    lib.ternix_synth_act_gauss.argtypes = [ctypes.c_void_p, ctypes.c_size_t, u64, u64, ctypes.c_int]
+    lib.ternix_synth_ternary.argtypes = [ctypes.c_void_p, ctypes.c_size_t, u64, u64, u64, u64]
+    lib.ternix_synth_ternary_packed.argtypes = [ctypes.c_void_p, ctypes.c_size_t, u64, u64, u64, u64]
+    for name in ("ternix_synth_act_uniform", "ternix_synth_act_gauss", "ternix_synth_ternary",
+                 "ternix_synth_ternary_packed"):
+        getattr(lib, name).restype = None
+    _lib = lib
+    return lib

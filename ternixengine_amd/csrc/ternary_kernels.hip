@@ -1,0 +1,545 @@
+// ternary_kernels.hip -- gfx950 (CDNA4) kernels for C[M,N] int32 = A[M,K] int8 x W[K,N] ternary.
+//
+// Weight layout (the contract, reference src/bitpack.cpp:5-15): row-major K x NB bytes, NB = N/4,
+// weight (k, n) in bits 2*(n%4) of byte k*NB + n/4; 00 = 0, 01 = +1, 11 = -1 (10 decodes as -2,
+// like the reference's scalar and CUDA decode, src/mul_mat_ternary.cpp:53, src/cuda_kernels.cu:40).
+//
+// Both fast kernels feed v_mfma_i32_16x16x64_i8.  The int8 MFMA reduces along K inside a lane
+// (lane l holds 16 K-consecutive bytes of one row of A and of one column of B, K-block l/16),
+// while the packed layout runs along N.  The kernels therefore
+//   1. gather, per lane, one packed byte-column (= 4 output columns) over 16 consecutive k-rows:
+//      four dwords, each holding 4 k-rows x 4 fields (a 4x4 byte transpose with v_perm_b32);
+//   2. split every dword into four MFMA B-operand dwords, one per 2-bit field j, without any
+//      per-weight work (a handful of bitwise ops per 16 weights, see "Field decode" below);
+//   3. run one MFMA per field: MFMA column i of field j is output column 4*(byte-col_i) + j.
+// Which k-rows a lane's 16 bytes hold only has to agree between A and B, so the natural row order
+// is used for both and A fragments are plain 16-byte loads.
+//
+// Field decode.  Let x be 4 bytes (4 k-rows), each holding fields f0..f3 (bits 0-1 .. 6-7).
+//   * "shift" form: (x << (6-2j)) & 0xC0C0C0C0 puts field j in the top two bits of each byte, so
+//     the signed byte is 64*w (01 -> 0x40 = +64, 11 -> 0xC0 = -64, 10 -> 0x80 = -128 = -2*64).
+//     MFMA then yields 64*(A.W); the result is an exact arithmetic shift right by 6.
+//   * "complement" form (fields 0..2): z = x ^ 0x55555555 flips each field's low bit, so
+//     z & (3 << 2j) per byte equals 4^j * (1 - w) (00 -> 1, 01 -> 0, 11 -> 2, 10 -> 3).  MFMA gives
+//     4^j * (R - A.W) with R the row sum of A over the same k range, so A.W = R - (S >> 2j).
+//     One shared XOR plus one AND per field; field 3 uses the shift form with shift 0 (one AND).
+//     R itself comes from one extra MFMA against an all-ones B per k-step, shared by all tiles.
+// The complement form costs 5 VALU ops per 16 weights and needs R (one MFMA per k-step shared by
+// all columns of the wave); the shift form costs 7 ops and needs nothing else.  The skinny kernel,
+// which has few A rows to amortise the decode over, uses the complement form; the GEMM, where the
+// extra R MFMA per m-tile would cost 25% of MFMA issue, uses the shift form.
+// Accumulator bound: |64 * A.W| <= 64*128*K, so each partial sum is exact for K <= 2^18; the
+// launch layer splits K so that no kernel accumulates more than 2^18 k-rows in one accumulator.
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "ternary_kernels.h"
+
+namespace ternix_hip {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ v4i mfma_i8(v4i a, v4i b, v4i c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+// 4x4 byte transpose.  r0..r3 are four rows (byte b of r_i = byte-column b of row i); on return
+// c_b holds byte-column b of the four rows, row i in byte i.  v_perm_b32 picks bytes of {S0,S1}:
+// selector 0-3 = bytes of the second operand, 4-7 = bytes of the first.
+__device__ __forceinline__ void transpose4x4(uint32_t r0, uint32_t r1, uint32_t r2, uint32_t r3,
+                                             uint32_t& c0, uint32_t& c1, uint32_t& c2, uint32_t& c3) {
+    const uint32_t t01l = __builtin_amdgcn_perm(r1, r0, 0x05010400u);  // r0.b0 r1.b0 r0.b1 r1.b1
+    const uint32_t t01h = __builtin_amdgcn_perm(r1, r0, 0x07030602u);  // r0.b2 r1.b2 r0.b3 r1.b3
+    const uint32_t t23l = __builtin_amdgcn_perm(r3, r2, 0x05010400u);
+    const uint32_t t23h = __builtin_amdgcn_perm(r3, r2, 0x07030602u);
+    c0 = __builtin_amdgcn_perm(t23l, t01l, 0x05040100u);
+    c1 = __builtin_amdgcn_perm(t23l, t01l, 0x07060302u);
+    c2 = __builtin_amdgcn_perm(t23h, t01h, 0x05040100u);
+    c3 = __builtin_amdgcn_perm(t23h, t01h, 0x07060302u);
+}
+
+// ------------------------------------------------------------------------------------------------
+// Loads with optional bounds / alignment handling.
+// ------------------------------------------------------------------------------------------------
+
+// Four packed bytes of row `row` starting at byte-column `bc` (bc % 4 == 0).  ALIGNED: NB % 4 == 0
+// and B is 4-byte aligned, so the dword is entirely inside or entirely outside the row.
+template <bool ALIGNED>
+__device__ __forceinline__ uint32_t load_w4(const uint8_t* __restrict__ B, int row, int bc, int K, int NB) {
+    if (row >= K) return 0u;
+    const uint8_t* p = B + (size_t)row * (size_t)NB + bc;
+    if (ALIGNED) {
+        return bc < NB ? *reinterpret_cast<const uint32_t*>(p) : 0u;
+    } else {
+        uint32_t v = 0;
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+            if (bc + b < NB) v |= (uint32_t)p[b] << (8 * b);
+        return v;
+    }
+}
+
+// 16 activation bytes of row m starting at k (k % 16 == 0).  ALIGNED: K % 16 == 0 and A is 16-byte
+// aligned, so the chunk is entirely inside or outside the row.
+template <bool ALIGNED>
+__device__ __forceinline__ v4i load_a16(const int8_t* __restrict__ A, int m, int k, int M, int K) {
+    v4i r = {0, 0, 0, 0};
+    if (m >= M) return r;
+    const int8_t* p = A + (size_t)m * (size_t)K + k;
+    if (ALIGNED) {
+        if (k < K) r = *reinterpret_cast<const v4i*>(p);
+    } else {
+        uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int b = 0; b < 16; ++b)
+            if (k + b < K) w[b >> 2] |= (uint32_t)(uint8_t)p[b] << (8 * (b & 3));
+        r = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+    }
+    return r;
+}
+
+// As load_a16 but rows end at k_end <= K (k_end % 64 == 0 or k_end == K, so an aligned chunk is
+// still entirely inside or outside).
+template <bool ALIGNED>
+__device__ __forceinline__ v4i load_a16_range(const int8_t* __restrict__ A, int m, int k, int M, int K, int k_end) {
+    if (k >= k_end) return v4i{0, 0, 0, 0};
+    if (ALIGNED || k + 16 <= k_end) return load_a16<ALIGNED>(A, m, k, M, K);
+    v4i r = {0, 0, 0, 0};
+    if (m >= M) return r;
+    const int8_t* p = A + (size_t)m * (size_t)K + k;
+    uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int b = 0; b < 16; ++b)
+        if (k + b < k_end) w[b >> 2] |= (uint32_t)(uint8_t)p[b] << (8 * (b & 3));
+    return v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+}
+
+// ------------------------------------------------------------------------------------------------
+// Skinny split-K kernel (decode shapes, M <= 16*MT).
+//
+// Workgroup = 4 waves on one 64-byte column tile (256 output columns).  Lane (q = l%16, kb = l/16)
+// owns packed dword q of the tile (byte-columns 4q..4q+3 = output columns 16q..16q+15) and k-rows
+// kb*16..kb*16+15 of every 64-row k-step.  Per k-step a lane issues 16 dword loads (one per k-row;
+// lanes 0-15 read 64 contiguous bytes of one row), transposes them into 4 byte-columns x 16 rows,
+// and drives 16 MFMAs per m-tile (4 byte-columns x 4 fields) plus one row-sum MFMA.
+// The workgroup's k-steps are dealt round-robin to its 4 waves; the waves' results are summed in
+// LDS and written (or atomically added when blockIdx.y splits K across workgroups).
+// ------------------------------------------------------------------------------------------------
+
+constexpr int SK_WAVES = 4;
+
+template <int MT, bool ALIGNED_W, bool ALIGNED_A, bool ATOMIC>
+__global__ __launch_bounds__(256) void skinny_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ B,
+                                                     int32_t* __restrict__ C, int M, int K, int N,
+                                                     int steps_per_split, int vec_store) {
+    constexpr int NV = MT * 64;  // result values per lane: MT m-tiles x 4 byte-cols x 4 fields x 4 rows
+    __shared__ int32_t red[(SK_WAVES - 1) * NV * 64];
+
+    const int NB = N >> 2;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int q = lane & 15;
+    const int kb = lane >> 4;
+    const int bc = blockIdx.x * 64 + 4 * q;        // first byte-column of this lane's dword
+    const int m0 = blockIdx.z * (16 * MT);
+    const int nsteps = (K + 63) >> 6;
+    const int s_begin = blockIdx.y * steps_per_split;
+    const int s_end = min(nsteps, s_begin + steps_per_split);
+
+    v4i acc[MT][4][4];
+    v4i accR[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+        accR[t] = v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[t][g][j] = v4i{0, 0, 0, 0};
+    }
+    const v4i ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
+
+    for (int s = s_begin + wave; s < s_end; s += SK_WAVES) {
+        const int k0 = s * 64 + kb * 16;
+        uint32_t raw[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) raw[r] = load_w4<ALIGNED_W>(B, k0 + r, bc, K, NB);
+        v4i a[MT];
+#pragma unroll
+        for (int t = 0; t < MT; ++t) a[t] = load_a16<ALIGNED_A>(A, m0 + 16 * t + q, k0, M, K);
+
+        uint32_t T[4][4];  // T[g][rq]: byte-column g, rows 4rq..4rq+3
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq)
+            transpose4x4(raw[4 * rq], raw[4 * rq + 1], raw[4 * rq + 2], raw[4 * rq + 3],
+                         T[0][rq], T[1][rq], T[2][rq], T[3][rq]);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) accR[t] = mfma_i8(a[t], ones, accR[t]);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            v4i b0, b1, b2, b3;
+#pragma unroll
+            for (int rq = 0; rq < 4; ++rq) {
+                const uint32_t x = T[g][rq];
+                const uint32_t z = x ^ 0x55555555u;
+                b0[rq] = (int)(z & 0x03030303u);
+                b1[rq] = (int)(z & 0x0C0C0C0Cu);
+                b2[rq] = (int)(z & 0x30303030u);
+                b3[rq] = (int)(x & 0xC0C0C0C0u);
+            }
+#pragma unroll
+            for (int t = 0; t < MT; ++t) {
+                acc[t][g][0] = mfma_i8(a[t], b0, acc[t][g][0]);
+                acc[t][g][1] = mfma_i8(a[t], b1, acc[t][g][1]);
+                acc[t][g][2] = mfma_i8(a[t], b2, acc[t][g][2]);
+                acc[t][g][3] = mfma_i8(a[t], b3, acc[t][g][3]);
+            }
+        }
+    }
+
+    // Per-wave results: w = R - S_j / 4^j (j < 3), S_3 / 64.  Output layout of a 16x16 MFMA tile:
+    // lane l holds column l%16 and rows 4*(l/16) + i in element i.
+    int val[MT][4][4][4];  // [t][g][j][i]
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int R = accR[t][i];
+                val[t][g][0][i] = R - acc[t][g][0][i];
+                val[t][g][1][i] = R - (acc[t][g][1][i] >> 2);
+                val[t][g][2][i] = R - (acc[t][g][2][i] >> 4);
+                val[t][g][3][i] = acc[t][g][3][i] >> 6;
+            }
+
+    // Rows this lane's values belong to: m0 + 16t + 4kb + i.  Only rows < M take part.
+    if (wave > 0) {
+        int32_t* dst = red + (wave - 1) * NV * 64 + lane;
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if (m0 + 16 * t + 4 * kb + i >= M) continue;
+#pragma unroll
+                for (int g = 0; g < 4; ++g)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) dst[(((t * 4 + i) * 4 + g) * 4 + j) * 64] = val[t][g][j][i];
+            }
+    }
+    __syncthreads();
+    if (wave != 0) return;
+
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = m0 + 16 * t + 4 * kb + i;
+            if (row >= M) continue;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                int v[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    int sum = val[t][g][j][i];
+#pragma unroll
+                    for (int w = 0; w < SK_WAVES - 1; ++w)
+                        sum += red[w * NV * 64 + (((t * 4 + i) * 4 + g) * 4 + j) * 64 + lane];
+                    v[j] = sum;
+                }
+                const int bcg = bc + g;
+                if (bcg >= NB) continue;
+                int32_t* out = C + (size_t)row * (size_t)N + 4 * bcg;
+                if (ATOMIC) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        if (v[j] != 0) atomicAdd(out + j, v[j]);
+                } else if (vec_store) {
+                    *reinterpret_cast<v4i*>(out) = v4i{v[0], v[1], v[2], v[3]};
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) out[j] = v[j];
+                }
+            }
+        }
+}
+
+// ------------------------------------------------------------------------------------------------
+// LDS-tiled GEMM (prefill shapes).
+//
+// Workgroup tile BM x (4*BNB) outputs, BNB packed byte-columns, k-step 64.  4 waves in a 2 x 2 grid,
+// wave tile (BM/2) rows x (BNB/2) byte-columns; per k-step a wave issues (BM/32) x (BNB/32) x 4
+// MFMAs.  A tile in LDS: BM rows x 64 bytes, 16-byte chunks XOR-swizzled by (row/4)%4 so the 16 rows
+// read by one ds_read_b128 land on distinct banks.  W tile in LDS is stored transposed (byte-column
+// major, the 64 k-rows of a byte-column contiguous, pitch 80 bytes) so a lane's B fragment is one
+// ds_read_b128; the transpose is done in registers (v_perm) between the global load and the LDS
+// store.  Two LDS stages: global loads of step s+1 are issued before the MFMAs of step s.
+// ------------------------------------------------------------------------------------------------
+
+constexpr int GM_THREADS = 256;
+constexpr int WT_PITCH = 80;  // bytes per transposed byte-column (64 k-rows + 16 pad)
+
+template <int BM, int BNB, bool ALIGNED_W, bool ALIGNED_A>
+__global__ __launch_bounds__(GM_THREADS) void gemm_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ B,
+                                                          int32_t* __restrict__ C, int M, int K, int N,
+                                                          int tiles_n, int k_begin, int k_end, int accumulate,
+                                                          int vec_store) {
+    constexpr int WM = BM / 2;            // rows per wave
+    constexpr int WB = BNB / 2;           // byte-columns per wave
+    constexpr int MT = WM / 16;           // m-tiles per wave
+    constexpr int GT = WB / 16;           // 16-byte-column groups per wave
+    constexpr int A_CHUNKS = BM * 4;      // 16-byte chunks per A stage
+    constexpr int A_PER_T = A_CHUNKS / GM_THREADS;
+    constexpr int W_JOBS = (BNB / 4) * 16;  // (dword column, row quad) jobs per W stage
+    constexpr int W_PER_T = (W_JOBS + GM_THREADS - 1) / GM_THREADS;
+    static_assert(A_CHUNKS % GM_THREADS == 0, "A tile must split evenly");
+
+    __shared__ __attribute__((aligned(16))) int8_t sA[2][BM * 64];
+    __shared__ __attribute__((aligned(16))) uint8_t sW[2][BNB * WT_PITCH];
+
+    const int NB = N >> 2;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int q = lane & 15, kb = lane >> 4;
+
+    // Block -> tile: consecutive block ids are dealt round-robin over the 8 XCDs; regroup so that
+    // each XCD works on a contiguous run of tiles (neighbouring tiles share A rows / W columns in
+    // that XCD's L2).
+    const int nblocks = gridDim.x;
+    const int bid = blockIdx.x;
+    const int per_xcd = (nblocks + 7) >> 3;
+    const int xcd = bid & 7, slot = bid >> 3;
+    int tile = xcd * per_xcd + slot;
+    if ((nblocks & 7) != 0) tile = bid;  // uneven split: keep the plain order
+    const int tm = tile / tiles_n, tn = tile % tiles_n;
+    const int row0 = tm * BM;
+    const int bc0 = tn * BNB;
+    // k-steps cover [k_begin, k_end); k_begin % 64 == 0.  Loads treat k >= k_end as zero.
+    const int nsteps = (k_end - k_begin + 63) >> 6;
+
+    v4i areg[A_PER_T];
+    uint32_t wreg[W_PER_T][4];
+
+    auto gload = [&](int s) {
+        const int k0 = k_begin + s * 64;
+#pragma unroll
+        for (int p = 0; p < A_PER_T; ++p) {
+            const int c = tid + p * GM_THREADS;
+            const int r = c >> 2, ch = c & 3;
+            areg[p] = load_a16_range<ALIGNED_A>(A, row0 + r, k0 + ch * 16, M, K, k_end);
+        }
+#pragma unroll
+        for (int p = 0; p < W_PER_T; ++p) {
+            const int job = tid + p * GM_THREADS;
+            if (job < W_JOBS) {
+                const int dc = job % (BNB / 4), rq = job / (BNB / 4);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) wreg[p][r] = load_w4<ALIGNED_W>(B, k0 + 4 * rq + r, bc0 + 4 * dc, k_end, NB);
+            }
+        }
+    };
+    auto sstore = [&](int buf) {
+#pragma unroll
+        for (int p = 0; p < A_PER_T; ++p) {
+            const int c = tid + p * GM_THREADS;
+            const int r = c >> 2, ch = c & 3;
+            const int sw = ch ^ ((r >> 2) & 3);
+            *reinterpret_cast<v4i*>(&sA[buf][r * 64 + sw * 16]) = areg[p];
+        }
+#pragma unroll
+        for (int p = 0; p < W_PER_T; ++p) {
+            const int job = tid + p * GM_THREADS;
+            if (job < W_JOBS) {
+                const int dc = job % (BNB / 4), rq = job / (BNB / 4);
+                uint32_t c0, c1, c2, c3;
+                transpose4x4(wreg[p][0], wreg[p][1], wreg[p][2], wreg[p][3], c0, c1, c2, c3);
+                uint8_t* base = &sW[buf][(4 * dc) * WT_PITCH + 4 * rq];
+                *reinterpret_cast<uint32_t*>(base) = c0;
+                *reinterpret_cast<uint32_t*>(base + WT_PITCH) = c1;
+                *reinterpret_cast<uint32_t*>(base + 2 * WT_PITCH) = c2;
+                *reinterpret_cast<uint32_t*>(base + 3 * WT_PITCH) = c3;
+            }
+        }
+    };
+
+    v4i acc[MT][GT][4];
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int g = 0; g < GT; ++g)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[t][g][j] = v4i{0, 0, 0, 0};
+
+    if (nsteps > 0) {
+        gload(0);
+        sstore(0);
+    }
+    __syncthreads();
+
+    for (int s = 0; s < nsteps; ++s) {
+        const int buf = s & 1;
+        if (s + 1 < nsteps) gload(s + 1);
+
+        // B fragments for this wave: GT groups of 16 byte-columns, 16 k-rows each.
+        v4i bfr[GT][4];
+#pragma unroll
+        for (int g = 0; g < GT; ++g) {
+            const int col = wn * WB + g * 16 + q;
+            const v4i x4 = *reinterpret_cast<const v4i*>(&sW[buf][col * WT_PITCH + kb * 16]);
+#pragma unroll
+            for (int rq = 0; rq < 4; ++rq) {
+                const uint32_t x = (uint32_t)x4[rq];
+                bfr[g][0][rq] = (int)((x << 6) & 0xC0C0C0C0u);
+                bfr[g][1][rq] = (int)((x << 4) & 0xC0C0C0C0u);
+                bfr[g][2][rq] = (int)((x << 2) & 0xC0C0C0C0u);
+                bfr[g][3][rq] = (int)(x & 0xC0C0C0C0u);
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            const int r = wm * WM + t * 16 + q;
+            const int sw = kb ^ ((r >> 2) & 3);
+            const v4i a = *reinterpret_cast<const v4i*>(&sA[buf][r * 64 + sw * 16]);
+#pragma unroll
+            for (int g = 0; g < GT; ++g)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[t][g][j] = mfma_i8(a, bfr[g][j], acc[t][g][j]);
+        }
+
+        if (s + 1 < nsteps) sstore(buf ^ 1);
+        __syncthreads();
+    }
+
+    // Epilogue: element i of tile (t, g, j) is row 4*kb + i of m-tile t, column 4*(byte-col) + j.
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = row0 + wm * WM + t * 16 + 4 * kb + i;
+            if (row >= M) continue;
+#pragma unroll
+            for (int g = 0; g < GT; ++g) {
+                const int bcol = bc0 + wn * WB + g * 16 + q;
+                if (bcol >= NB) continue;
+                v4i v = {acc[t][g][0][i] >> 6, acc[t][g][1][i] >> 6, acc[t][g][2][i] >> 6, acc[t][g][3][i] >> 6};
+                int32_t* out = C + (size_t)row * (size_t)N + 4 * bcol;
+                if (vec_store) {
+                    if (accumulate) v += *reinterpret_cast<const v4i*>(out);
+                    *reinterpret_cast<v4i*>(out) = v;
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) out[j] = accumulate ? out[j] + v[j] : v[j];
+                }
+            }
+        }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Naive kernel: one work-item per output, weights decoded per k from global memory with
+// w = (b & 1) - (b & 2) (the reference decode2, src/cuda_kernels.cu:40-54).
+// ------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void naive_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ B,
+                                                    int32_t* __restrict__ C, int M, int K, int N) {
+    const int col = blockIdx.x * 64 + (threadIdx.x & 63);
+    const int row = blockIdx.y * 4 + (threadIdx.x >> 6);
+    if (row >= M || col >= N) return;
+    const int NB = N >> 2;
+    const int shift = (col & 3) * 2;
+    int acc = 0;
+    for (int k = 0; k < K; ++k) {
+        const unsigned bits = (B[(size_t)k * NB + (col >> 2)] >> shift) & 3u;
+        acc += (int)A[(size_t)row * K + k] * ((int)(bits & 1u) - (int)(bits & 2u));
+    }
+    C[(size_t)row * N + col] = acc;
+}
+
+__global__ __launch_bounds__(256) void zero_kernel(int32_t* __restrict__ C, size_t n) {
+    size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const size_t stride = (size_t)gridDim.x * 256;
+    for (; i < n; i += stride) C[i] = 0;
+}
+
+template <int MT, bool AW, bool AA, bool AT>
+hipError_t launch_skinny_t(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int splits,
+                           int steps_per_split, hipStream_t st) {
+    const int NB = N >> 2;
+    dim3 grid((NB + 63) / 64, splits, (M + 16 * MT - 1) / (16 * MT));
+    const int vec_store = ((uintptr_t)C % 16) == 0;
+    hipLaunchKernelGGL((skinny_kernel<MT, AW, AA, AT>), grid, dim3(256), 0, st, A, B, C, M, K, N, steps_per_split,
+                       vec_store);
+    return hipGetLastError();
+}
+
+template <int MT>
+hipError_t launch_skinny_m(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, bool aw, bool aa,
+                           int splits, int sps, hipStream_t st) {
+    const bool at = splits > 1;
+    if (aw && aa) return at ? launch_skinny_t<MT, true, true, true>(A, B, C, M, K, N, splits, sps, st)
+                            : launch_skinny_t<MT, true, true, false>(A, B, C, M, K, N, splits, sps, st);
+    if (aw) return at ? launch_skinny_t<MT, true, false, true>(A, B, C, M, K, N, splits, sps, st)
+                      : launch_skinny_t<MT, true, false, false>(A, B, C, M, K, N, splits, sps, st);
+    if (aa) return at ? launch_skinny_t<MT, false, true, true>(A, B, C, M, K, N, splits, sps, st)
+                      : launch_skinny_t<MT, false, true, false>(A, B, C, M, K, N, splits, sps, st);
+    return at ? launch_skinny_t<MT, false, false, true>(A, B, C, M, K, N, splits, sps, st)
+              : launch_skinny_t<MT, false, false, false>(A, B, C, M, K, N, splits, sps, st);
+}
+
+template <int BM, int BNB>
+hipError_t launch_gemm_t(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, bool aw, bool aa,
+                         int kb, int ke, int acc, hipStream_t st) {
+    const int NB = N >> 2;
+    const int tiles_m = (M + BM - 1) / BM, tiles_n = (NB + BNB - 1) / BNB;
+    const dim3 grid(tiles_m * tiles_n), block(GM_THREADS);
+    const int vs = ((uintptr_t)C % 16) == 0;
+    if (aw && aa)
+        hipLaunchKernelGGL((gemm_kernel<BM, BNB, true, true>), grid, block, 0, st, A, B, C, M, K, N, tiles_n, kb, ke, acc, vs);
+    else if (aw)
+        hipLaunchKernelGGL((gemm_kernel<BM, BNB, true, false>), grid, block, 0, st, A, B, C, M, K, N, tiles_n, kb, ke, acc, vs);
+    else if (aa)
+        hipLaunchKernelGGL((gemm_kernel<BM, BNB, false, true>), grid, block, 0, st, A, B, C, M, K, N, tiles_n, kb, ke, acc, vs);
+    else
+        hipLaunchKernelGGL((gemm_kernel<BM, BNB, false, false>), grid, block, 0, st, A, B, C, M, K, N, tiles_n, kb, ke, acc, vs);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_zero(int32_t* C, size_t n, hipStream_t st) {
+    if (n == 0) return hipSuccess;
+    size_t blocks = (n + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(zero_kernel, dim3((unsigned)blocks), dim3(256), 0, st, C, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int splits,
+                         int steps_per_split, hipStream_t st) {
+    const int NB = N >> 2;
+    const bool aw = (NB % 4 == 0) && ((uintptr_t)B % 4 == 0);
+    const bool aa = (K % 16 == 0) && ((uintptr_t)A % 16 == 0);
+    if (splits > 1) {
+        const hipError_t e = launch_zero(C, (size_t)M * (size_t)N, st);
+        if (e != hipSuccess) return e;
+    }
+    if (M <= 16) return launch_skinny_m<1>(A, B, C, M, K, N, aw, aa, splits, steps_per_split, st);
+    return launch_skinny_m<2>(A, B, C, M, K, N, aw, aa, splits, steps_per_split, st);
+}
+
+hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int k_begin, int k_end,
+                       int accumulate, hipStream_t st) {
+    const int NB = N >> 2;
+    const bool aw = (NB % 4 == 0) && ((uintptr_t)B % 4 == 0);
+    const bool aa = (K % 16 == 0) && ((uintptr_t)A % 16 == 0);
+    return launch_gemm_t<128, 64>(A, B, C, M, K, N, aw, aa, k_begin, k_end, accumulate, st);
+}
+
+hipError_t launch_naive(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, hipStream_t st) {
+    const dim3 grid((N + 63) / 64, (M + 3) / 4);
+    hipLaunchKernelGGL(naive_kernel, grid, dim3(256), 0, st, A, B, C, M, K, N);
+    return hipGetLastError();
+}
+
+}  // namespace ternix_hip

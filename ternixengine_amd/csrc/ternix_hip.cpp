@@ -1,0 +1,183 @@
+// ternix_hip.cpp -- C-ABI launch layer of libternix_hip.so (declared in include/ternix/ternix_hip.h).
+//
+// Validates shapes before touching any pointer (reference contract: src/cuda_kernels.cu:127,135 and
+// tests/test_cuda_matmul.cu:41-43), picks a kernel and its split, launches asynchronously on the
+// caller's stream and returns the hipError_t of the launch.
+#include "ternix/ternix_hip.h"
+
+#include <hip/hip_runtime_api.h>
+
+#include <atomic>
+#include <climits>
+#include <cstring>
+
+#include "ternary_kernels.h"
+
+namespace {
+
+constexpr int kSkinnyMaxM = 32;
+constexpr int kSkinnyWaves = 4;       // waves per skinny workgroup (skinny_kernel's SK_WAVES)
+constexpr int kMaxDevices = 64;
+
+// Compute-unit count per device, read once (hipDeviceGetAttribute is not free on a hot path).
+std::atomic<int> g_cu_count[kMaxDevices];
+
+int cu_count() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+    int n = g_cu_count[dev].load(std::memory_order_relaxed);
+    if (n > 0) return n;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    g_cu_count[dev].store(n, std::memory_order_relaxed);
+    return n;
+}
+
+// Shape / pointer validation shared by every device entry point.  Returns hipSuccess when the call
+// is well formed; *trivial is set when there is nothing to launch (M == 0 or N == 0).
+hipError_t validate(const void* dA, const void* dB, const void* dC, int64_t M, int64_t K, int64_t N, bool* trivial) {
+    *trivial = false;
+    if (M < 0 || K < 0 || N < 0) return hipErrorInvalidValue;
+    if (N % 4 != 0) return hipErrorInvalidValue;
+    if (M > INT_MAX || K > INT_MAX || N > INT_MAX) return hipErrorInvalidValue;
+    if (M == 0 || N == 0) {
+        *trivial = true;
+        return hipSuccess;
+    }
+    if (dC == nullptr || reinterpret_cast<uintptr_t>(dC) % alignof(int32_t) != 0) return hipErrorInvalidValue;
+    if (K > 0 && (dA == nullptr || dB == nullptr)) return hipErrorInvalidValue;
+    return hipSuccess;
+}
+
+hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int K, int N, hipStream_t st) {
+    const int NB = N / 4;
+    const int col_tiles = (NB + 63) / 64;
+    const int mgroups = M <= 16 ? 1 : (M + 31) / 32;
+    const int nsteps = (K + 63) / 64;
+    // Aim for ~4 workgroups (16 waves) per CU, but give each workgroup at least one k-step per wave.
+    const long target = (4L * cu_count()) / ((long)col_tiles * mgroups);
+    long splits = target < 1 ? 1 : target;
+    const long max_splits = (nsteps + kSkinnyWaves - 1) / kSkinnyWaves;
+    if (splits > max_splits) splits = max_splits < 1 ? 1 : max_splits;
+    const long min_splits = (nsteps + (ternix_hip::kMaxKPerAccumulator / 64) - 1) / (ternix_hip::kMaxKPerAccumulator / 64);
+    if (splits < min_splits) splits = min_splits;
+    if (splits > 65535) splits = 65535;
+    int sps = (int)((nsteps + splits - 1) / splits);
+    if (sps < 1) sps = 1;
+    splits = (nsteps + sps - 1) / sps;
+    if (splits < 1) splits = 1;
+    return ternix_hip::launch_skinny(dA, dB, dC, M, K, N, (int)splits, sps, st);
+}
+
+hipError_t run_gemm(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int K, int N, hipStream_t st) {
+    if (K == 0) return ternix_hip::launch_gemm(dA, dB, dC, M, K, N, 0, 0, 0, st);
+    int acc = 0;
+    for (long k0 = 0; k0 < K; k0 += ternix_hip::kMaxKPerAccumulator) {
+        const long k1 = k0 + ternix_hip::kMaxKPerAccumulator < K ? k0 + ternix_hip::kMaxKPerAccumulator : K;
+        const hipError_t e = ternix_hip::launch_gemm(dA, dB, dC, M, K, N, (int)k0, (int)k1, acc, st);
+        if (e != hipSuccess) return e;
+        acc = 1;
+    }
+    return hipSuccess;
+}
+
+enum class Path { Auto, Skinny, Gemm, Naive };
+
+int dispatch(Path path, const int8_t* dA, const uint8_t* dB, int32_t* dC, int64_t M64, int64_t K64, int64_t N64,
+             void* stream) {
+    bool trivial = false;
+    hipError_t e = validate(dA, dB, dC, M64, K64, N64, &trivial);
+    if (e != hipSuccess) return (int)e;
+    if (path == Path::Skinny && M64 > kSkinnyMaxM) return (int)hipErrorInvalidValue;
+    if (trivial) return (int)hipSuccess;
+    const int M = (int)M64, K = (int)K64, N = (int)N64;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (path == Path::Auto) path = M <= kSkinnyMaxM ? Path::Skinny : Path::Gemm;
+    switch (path) {
+        case Path::Skinny: e = run_skinny(dA, dB, dC, M, K, N, st); break;
+        case Path::Gemm: e = run_gemm(dA, dB, dC, M, K, N, st); break;
+        default: e = ternix_hip::launch_naive(dA, dB, dC, M, K, N, st); break;
+    }
+    return (int)e;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ternix_hip_mul_mat_ternary(const int8_t* dA, const uint8_t* dB, int32_t* dC, int64_t M, int64_t K, int64_t N,
+                               void* stream) {
+    return dispatch(Path::Auto, dA, dB, dC, M, K, N, stream);
+}
+
+int ternix_hip_mul_mat_ternary_gemv(const int8_t* dA, const uint8_t* dB, int32_t* dC, int64_t M, int64_t K,
+                                    int64_t N, void* stream) {
+    return dispatch(Path::Skinny, dA, dB, dC, M, K, N, stream);
+}
+
+int ternix_hip_mul_mat_ternary_gemm(const int8_t* dA, const uint8_t* dB, int32_t* dC, int64_t M, int64_t K,
+                                    int64_t N, void* stream) {
+    return dispatch(Path::Gemm, dA, dB, dC, M, K, N, stream);
+}
+
+int ternix_hip_mul_mat_ternary_tiled(const int8_t* dA, const uint8_t* dB, int32_t* dC, int64_t M, int64_t K,
+                                     int64_t N, void* stream) {
+    // Same precondition as the reference tiled kernel (src/cuda_kernels.cu:135), checked first.
+    if (M % 64 != 0 || N % 64 != 0 || K % 64 != 0) return (int)hipErrorInvalidValue;
+    return dispatch(Path::Gemm, dA, dB, dC, M, K, N, stream);
+}
+
+int ternix_hip_mul_mat_ternary_naive(const int8_t* dA, const uint8_t* dB, int32_t* dC, int64_t M, int64_t K,
+                                     int64_t N, void* stream) {
+    return dispatch(Path::Naive, dA, dB, dC, M, K, N, stream);
+}
+
+int ternix_hip_mul_mat_ternary_host(const int8_t* A, const uint8_t* B_packed, int32_t* C, int64_t M, int64_t K,
+                                    int64_t N, int variant) {
+    bool trivial = false;
+    hipError_t e = validate(A, B_packed, C, M, K, N, &trivial);
+    if (e != hipSuccess) return (int)e;
+    if (variant < TERNIX_HIP_AUTO || variant > TERNIX_HIP_TILED) return (int)hipErrorInvalidValue;
+    if (variant == TERNIX_HIP_GEMV && M > kSkinnyMaxM) return (int)hipErrorInvalidValue;
+    if (variant == TERNIX_HIP_TILED && (M % 64 != 0 || N % 64 != 0 || K % 64 != 0)) return (int)hipErrorInvalidValue;
+    if (trivial) return (int)hipSuccess;
+    const size_t a_bytes = (size_t)M * (size_t)K, b_bytes = (size_t)K * (size_t)(N / 4),
+                 c_bytes = (size_t)M * (size_t)N * sizeof(int32_t);
+    int8_t* dA = nullptr;
+    uint8_t* dB = nullptr;
+    int32_t* dC = nullptr;
+    // hipMalloc of 0 bytes returns a null pointer; keep the pointers non-null for validation.
+    if ((e = hipMalloc(reinterpret_cast<void**>(&dA), a_bytes ? a_bytes : 16)) != hipSuccess) goto done;
+    if ((e = hipMalloc(reinterpret_cast<void**>(&dB), b_bytes ? b_bytes : 16)) != hipSuccess) goto done;
+    if ((e = hipMalloc(reinterpret_cast<void**>(&dC), c_bytes)) != hipSuccess) goto done;
+    if (a_bytes && (e = hipMemcpy(dA, A, a_bytes, hipMemcpyHostToDevice)) != hipSuccess) goto done;
+    if (b_bytes && (e = hipMemcpy(dB, B_packed, b_bytes, hipMemcpyHostToDevice)) != hipSuccess) goto done;
+    {
+        int s;
+        switch (variant) {
+            case TERNIX_HIP_NAIVE: s = ternix_hip_mul_mat_ternary_naive(dA, dB, dC, M, K, N, nullptr); break;
+            case TERNIX_HIP_GEMV: s = ternix_hip_mul_mat_ternary_gemv(dA, dB, dC, M, K, N, nullptr); break;
+            case TERNIX_HIP_GEMM: s = ternix_hip_mul_mat_ternary_gemm(dA, dB, dC, M, K, N, nullptr); break;
+            case TERNIX_HIP_TILED: s = ternix_hip_mul_mat_ternary_tiled(dA, dB, dC, M, K, N, nullptr); break;
+            default: s = ternix_hip_mul_mat_ternary(dA, dB, dC, M, K, N, nullptr); break;
+        }
+        e = static_cast<hipError_t>(s);
+    }
+    if (e != hipSuccess) goto done;
+    if ((e = hipDeviceSynchronize()) != hipSuccess) goto done;
+    e = hipMemcpy(C, dC, c_bytes, hipMemcpyDeviceToHost);
+done:
+    // Free on every path; a free failure never masks the first error.
+    if (dA) (void)hipFree(dA);
+    if (dB) (void)hipFree(dB);
+    if (dC) (void)hipFree(dC);
+    return (int)e;
+}
+
+const char* ternix_hip_error_string(int status) {
+    const char* s = hipGetErrorString(static_cast<hipError_t>(status));
+    return s ? s : "unknown error";
+}
+
+int ternix_hip_version(void) { return 100; }
+
+}  // extern "C"

@@ -1,0 +1,226 @@
+"""HIP-vs-CPU bit-exact suite (replaces the reference's tests/test_cuda_matmul.cu).
+
+Every kernel path is called through the C-ABI (include/ternix/ternix_hip.h) on device buffers and
+compared for exact int32 equality with
+  * the golden vectors written by the reference's compiled CPU code (tests/golden/),
+  * the CPU oracle (oracle/) on the same seeded inputs, at sizes it finishes in seconds,
+  * the SHA-256 digests of the reference's outputs for every benchmark configuration at full size,
+  * closed forms (worst-case magnitude, W == 0, W == +1, identity).
+C is prefilled with garbage before each call, so cells a kernel fails to write are caught
+(reference tests/test_cuda_matmul.cu:20,23)."""
+import ctypes
+import hashlib
+import sys
+
+import numpy as np
+import pytest
+
+from conftest import small_case_list
+
+pytestmark = pytest.mark.gpu
+
+import ternixengine_amd as tx  # noqa: E402
+from ternixengine_amd import configs  # noqa: E402
+from ternixengine_amd import hip_runtime as hr  # noqa: E402
+
+PATHS = ["auto", "gemv", "gemm", "naive", "tiled"]
+GARBAGE = np.int32(-0x2A2A2A2B)
+
+
+def log(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if hr.device_count() < 1:
+        pytest.skip("no HIP device")
+    tx._load()
+    yield
+    hr.synchronize()
+
+
+def supports(path, m, k, n):
+    if path == "gemv":
+        return m <= 32
+    if path == "tiled":
+        return m % 64 == 0 and n % 64 == 0 and k % 64 == 0
+    if path == "naive":
+        return m * n * k <= 1 << 28
+    return True
+
+
+def run(path, a, wp, n, a_off=0, b_off=0, c_off=0, stream=None):
+    """C = A x W on the GPU through the C-ABI; optional byte offsets misalign the pointers."""
+    a = np.ascontiguousarray(a, np.int8)
+    wp = np.ascontiguousarray(wp, np.uint8)
+    m, k = a.shape
+    da = hr.DeviceBuffer(a.nbytes + 64)
+    db = hr.DeviceBuffer(wp.nbytes + 64)
+    dc = hr.DeviceBuffer(4 * m * n + 64)
+    pa, pb, pc = da.value + a_off, db.value + b_off, dc.value + c_off
+    if a.nbytes:
+        hr.check(hr._load().hipMemcpy(ctypes.c_void_p(pa), a.ctypes.data_as(ctypes.c_void_p), a.nbytes, hr.H2D), "A")
+    if wp.nbytes:
+        hr.check(hr._load().hipMemcpy(ctypes.c_void_p(pb), wp.ctypes.data_as(ctypes.c_void_p), wp.nbytes, hr.H2D), "B")
+    garbage = np.full(m * n + 16, GARBAGE, np.int32)
+    dc.upload(garbage)
+    st = tx.mul_mat_ternary(pa, pb, pc, m, k, n, stream=stream.handle if stream else None, path=path)
+    assert st == 0, f"{path} returned {st} ({tx.ternix_error(st)})"
+    hr.synchronize()
+    out = np.empty((m, n), np.int32)
+    if out.nbytes:
+        hr.check(hr._load().hipMemcpy(out.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(pc), out.nbytes, hr.D2H),
+                 "C")
+    return out
+
+
+@pytest.mark.parametrize("path", PATHS)
+def test_reference_suite_shapes(golden, path):
+    for m, k, n, i in small_case_list(golden):
+        if not supports(path, m, k, n):
+            continue
+        log(f"[{path}] golden case {i} M={m} K={k} N={n}")
+        got = run(path, golden[f"s{i}_A"], golden[f"s{i}_Wp"], n)
+        assert (got == golden[f"s{i}_C"]).all(), (path, m, k, n)
+
+
+@pytest.mark.parametrize("path", ["auto", "gemv", "gemm", "naive"])
+def test_out_of_domain_code_matches_reference_scalar(golden, path):
+    # code 10 decodes as -2, like reference mul_mat_ternary_scalar and the CUDA decode2.
+    log(f"[{path}] out-of-domain code")
+    got = run(path, golden["invalid_A"], golden["invalid_Wp"], golden["invalid_C_scalar"].shape[1])
+    assert (got == golden["invalid_C_scalar"]).all()
+
+
+@pytest.mark.parametrize("path", ["auto", "gemv", "gemm"])
+def test_extreme_activations(golden, path):
+    log(f"[{path}] extreme activations")
+    got = run(path, golden["extreme_A"], golden["extreme_Wp"], 16)
+    assert (got == golden["extreme_C"]).all()
+
+
+@pytest.mark.parametrize("path", ["gemv", "gemm"])
+def test_closed_forms(oracle, path):
+    rng = np.random.default_rng(2)
+    for m, k, n in ((1, 320, 64), (7, 1000, 1028), (20, 130, 260)):
+        log(f"[{path}] closed forms M={m} K={k} N={n}")
+        a = rng.integers(-128, 128, size=(m, k), dtype=np.int8)
+        assert (run(path, a, oracle.pack(np.zeros((k, n), np.int8)), n) == 0).all()
+        rs = a.astype(np.int64).sum(axis=1)
+        assert (run(path, a, oracle.pack(np.ones((k, n), np.int8)), n) == rs[:, None]).all()
+        worst = np.full((m, k), -128, np.int8)
+        assert (run(path, worst, oracle.pack(-np.ones((k, n), np.int8)), n) == 128 * k).all()
+    eye = np.eye(256, dtype=np.int8)
+    a = rng.integers(-128, 128, size=(9, 256), dtype=np.int8)
+    assert (run(path, a, oracle.pack(eye), 256) == a.astype(np.int32)).all()
+
+
+@pytest.mark.parametrize("path", ["auto", "gemv", "gemm", "naive"])
+def test_random_ragged_shapes(oracle, path):
+    rng = np.random.default_rng(17)
+    for trial in range(24):
+        m = int(rng.integers(1, 33 if path == "gemv" else 150))
+        k = int(rng.integers(0, 700))
+        n = 4 * int(rng.integers(1, 300))
+        log(f"[{path}] ragged trial {trial} M={m} K={k} N={n}")
+        a = rng.integers(-128, 128, size=(m, k), dtype=np.int8)
+        wp = rng.integers(0, 256, size=(k, n // 4), dtype=np.uint8)
+        expect = oracle.mm("scalar", a, wp, n)
+        assert (run(path, a, wp, n) == expect).all(), (m, k, n)
+
+
+@pytest.mark.parametrize("path", ["gemv", "gemm"])
+def test_misaligned_pointers(oracle, path):
+    rng = np.random.default_rng(23)
+    for (m, k, n), (ao, bo, co) in (((3, 256, 512), (1, 3, 4)), ((40 if path == "gemm" else 30, 512, 1024), (5, 2, 8)),
+                                    ((2, 64, 64), (16, 4, 16))):
+        log(f"[{path}] misaligned M={m} K={k} N={n} offsets A+{ao} B+{bo} C+{co}")
+        a = rng.integers(-128, 128, size=(m, k), dtype=np.int8)
+        wp = rng.integers(0, 256, size=(k, n // 4), dtype=np.uint8)
+        assert (run(path, a, wp, n, ao, bo, co) == oracle.mm("scalar", a, wp, n)).all()
+
+
+def test_k_beyond_accumulator_bound(oracle):
+    # K > 2^18 forces the launch layer to split K (scaled partial sums stay exact).
+    m, k, n = 2, (1 << 18) + 200, 16
+    a = np.full((m, k), -128, np.int8)
+    a[1, ::3] = 127
+    w = -np.ones((k, n), np.int8)
+    w[:, 5] = 1
+    wp = oracle.pack(w)
+    expect = (a.astype(np.int64) @ w.astype(np.int64))
+    assert np.abs(expect).max() < 2 ** 31
+    for path in ("gemv", "gemm"):
+        log(f"[{path}] K={k}")
+        assert (run(path, a, wp, n) == expect).all(), path
+
+
+def test_k_zero_writes_zeros():
+    for path in ("auto", "gemv", "gemm", "naive"):
+        got = run(path, np.zeros((3, 0), np.int8), np.zeros((0, 8), np.uint8), 32)
+        assert (got == 0).all(), path
+
+
+def test_on_user_stream(oracle):
+    s = hr.Stream()
+    rng = np.random.default_rng(4)
+    a = rng.integers(-128, 128, size=(4, 640), dtype=np.int8)
+    wp = rng.integers(0, 256, size=(640, 96), dtype=np.uint8)
+    assert (run("auto", a, wp, 384, stream=s) == oracle.mm("scalar", a, wp, 384)).all()
+
+
+def test_host_wrapper_and_python_api(oracle, golden):
+    for m, k, n, i in small_case_list(golden):
+        for impl in ("hip", "hip_gemm", "hip_naive") + (("hip_gemv",) if m <= 32 else ()):
+            got = tx.ternary_matmul(golden[f"s{i}_A"], golden[f"s{i}_Wp"], impl)
+            assert (got == golden[f"s{i}_C"]).all(), (impl, m, k, n)
+    # reference tests/test_python_binding.py:35-39 shape through the tiled contract
+    rng = np.random.default_rng(3)
+    a = rng.integers(-128, 128, size=(128, 256), dtype=np.int8)
+    w = rng.integers(-1, 2, size=(256, 192), dtype=np.int8)
+    assert (tx.ternary_matmul(a, tx.pack_ternary(w), "hip_tiled") == a.astype(np.int32) @ w.astype(np.int32)).all()
+    with pytest.raises(ValueError):
+        tx.ternary_matmul(a[:65], tx.pack_ternary(w), "hip_tiled")
+
+
+ORACLE_CASES = ["cfg1", "cfg2_up", "cfg2_down", "cfg3_m4_up", "cfg3_m4_down", "cfg3_m16_up", "cfg3_m16_down",
+                "cfg3_m64_up", "cfg3_m64_down", "cfg5_ragged_1x1000x3076", "cfg5_ragged_17x4093x1028",
+                "cfg5_ragged_129x8191x2052", "cfg5_big_m1"]
+
+
+@pytest.mark.parametrize("name", ORACLE_CASES)
+def test_config_against_oracle(oracle, digests, name):
+    case = configs.CASES[name]
+    a, wp = configs.gen_a(case), configs.gen_w_packed(case)
+    expect = oracle.mm("scalar_mt", a, wp, case.N)
+    for path in ("auto", "gemv", "gemm"):
+        if not supports(path, case.M, case.K, case.N):
+            continue
+        log(f"[{path}] {name} M={case.M} K={case.K} N={case.N}")
+        got = run(path, a, wp, case.N)
+        assert (got == expect).all(), (path, name)
+        assert hashlib.sha256(got.tobytes()).hexdigest() == digests[name]["sha256_C"]
+
+
+FULL_CASES = ["cfg4_4096x4096", "cfg4_4096x14336", "cfg4_14336x4096", "cfg5_big_m4096", "cfg5_worst"]
+
+
+@pytest.mark.parametrize("name", FULL_CASES)
+def test_config_full_size_digest(digests, name):
+    """Full-size MFMA configurations: bit-exact via the SHA-256 of the reference avx2_blocked output."""
+    case = configs.CASES[name]
+    a, wp = configs.gen_a(case), configs.gen_w_packed(case)
+    d = digests[name]
+    assert hashlib.sha256(a.tobytes()).hexdigest() == d["sha256_A"]
+    assert hashlib.sha256(wp.tobytes()).hexdigest() == d["sha256_Wp"]
+    for path in ("auto", "gemm"):
+        log(f"[{path}] {name} M={case.M} K={case.K} N={case.N}")
+        got = run(path, a, wp, case.N)
+        assert [int(x) for x in got.ravel()[:8]] == d["C_first8"], (path, name)
+        assert int(got.astype(np.int64).sum()) == d["C_checksum_int64"], (path, name)
+        assert hashlib.sha256(got.tobytes()).hexdigest() == d["sha256_C"], (path, name)
+        if name == "cfg5_worst":
+            assert (got == 2097152).all()
+        del got
