@@ -1,0 +1,246 @@
+"""Benchmark of the ternary matmul hot path on one MI355X.
+
+Headline (`value`): GEMV effective bandwidth at M=1 on the decode-shape FFN pair of configuration 2
+(up 2560x6912, down 6912x2560).  One step = the up and the down GEMV.  Weights rotate over a pool of
+distinct copies larger than twice the 256 MB last-level cache, so every step reads its weights from
+HBM, as decode over a model's layers does.  Effective bytes per GEMV = M*K + K*N/4 + 4*M*N
+(each operand once).  Inputs are resident in HBM before timing; timing uses HIP events on the stream
+the kernels run on, bracketing exactly `--steps` steps after `--warmup` untimed ones.
+
+Also reported on the same line: the prefill GEMM of configuration 4 (M=2048; ops = 2*M*N*K, against
+the int8 dense MFMA peak), the large-M=1 GEMV of configuration 5 (K=8192, N=28672), and the
+reference's own CPU kernel (mul_mat_ternary_avx2_blocked, compiled from the reference sources into
+oracle/_ref, or the plain-C restatement in oracle/ when that is absent) timed on this host on a
+bounded sample of the same workload.
+"""
+import argparse
+import ctypes
+import json
+import os
+import statistics
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "GEMV eff. GB/s (% HBM peak) at M=1; GEMM TOPS (% int8 MFMA peak) M=2048"
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+POOL_MIN_BYTES = 512 << 20
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--gemm-steps", type=int, default=20)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", choices=["all", "gemv", "gemm", "bigm1"], default="all")
+    return ap.parse_args()
+
+
+class Problem:
+    """Device-resident inputs of one case, with `copies` distinct weight buffers."""
+
+    def __init__(self, case, copies=1):
+        from ternixengine_amd import configs
+        from ternixengine_amd import hip_runtime as hr
+        self.case = case
+        self.a = configs.gen_a(case)
+        self.wp = configs.gen_w_packed(case)
+        self.dA = hr.DeviceBuffer.from_array(self.a)
+        self.dW = [hr.DeviceBuffer.from_array(self.wp) for _ in range(copies)]
+        self.dC = hr.DeviceBuffer(4 * case.M * case.N)
+
+
+def time_launches(launches, steps, warmup, stream):
+    """Run `launches(i)` for warmup + steps iterations; return (total_ms of the timed steps)."""
+    from ternixengine_amd import hip_runtime as hr
+    for i in range(warmup):
+        launches(i)
+    stream.synchronize()
+    hr.synchronize()
+    e0, e1 = hr.Event(), hr.Event()
+    e0.record(stream)
+    for i in range(steps):
+        launches(warmup + i)
+    e1.record(stream)
+    e1.synchronize()
+    hr.synchronize()
+    return e0.elapsed_ms(e1)
+
+
+def launch(fn, prob, widx, stream):
+    c = prob.case
+    st = fn(prob.dA.value, prob.dW[widx].value, prob.dC.value, c.M, c.K, c.N, stream.handle)
+    if st != 0:
+        raise RuntimeError(f"launch failed: {st}")
+
+
+def verify(prob):
+    """Output of the last launch vs the reference digest (bit-exact)."""
+    import hashlib
+    with open(os.path.join(ROOT, "tests", "golden", "config_digests.json")) as f:
+        d = json.load(f)["cases"][prob.case.name]
+    got = prob.dC.download(np.int32, (prob.case.M, prob.case.N))
+    return hashlib.sha256(got.tobytes()).hexdigest() == d["sha256_C"]
+
+
+def bench_gemv_pair(args, stream, lib):
+    from ternixengine_amd import configs
+    up, down = configs.CASES["cfg2_up"], configs.CASES["cfg2_down"]
+    pair_w = up.K * up.N // 4 + down.K * down.N // 4
+    copies = max(2, -(-POOL_MIN_BYTES // pair_w))
+    pu, pd = Problem(up, copies), Problem(down, copies)
+    fn = lib.ternix_hip_mul_mat_ternary
+
+    def step(i):
+        launch(fn, pu, i % copies, stream)
+        launch(fn, pd, i % copies, stream)
+
+    ms = time_launches(step, args.steps, args.warmup, stream)
+    ok = verify(pu) and verify(pd)
+    bytes_step = up.bytes_algorithmic + down.bytes_algorithmic
+    # hot-cache variant (same weights every step) for reference only
+    ms_hot = time_launches(lambda i: (launch(fn, pu, 0, stream), launch(fn, pd, 0, stream)), args.steps,
+                           args.warmup, stream)
+    return {
+        "ms_per_step": ms / args.steps,
+        "bytes_per_step": bytes_step,
+        "gbs": bytes_step / (ms / args.steps * 1e-3) / 1e9,
+        "gbs_hot_cache": bytes_step / (ms_hot / args.steps * 1e-3) / 1e9,
+        "launch_us": ms / args.steps / 2 * 1e3,
+        "pool_copies": copies,
+        "pool_bytes": copies * pair_w,
+        "verified": ok,
+    }
+
+
+def bench_big_m1(args, stream, lib):
+    from ternixengine_amd import configs
+    case = configs.CASES["cfg5_big_m1"]
+    w = case.K * case.N // 4
+    copies = max(2, -(-POOL_MIN_BYTES // w))
+    p = Problem(case, copies)
+    fn = lib.ternix_hip_mul_mat_ternary
+    steps = max(10, args.steps // 4)
+    ms = time_launches(lambda i: launch(fn, p, i % copies, stream), steps, max(2, args.warmup // 4), stream)
+    return {"shape": [case.M, case.K, case.N], "launch_us": ms / steps * 1e3,
+            "gbs": case.bytes_algorithmic / (ms / steps * 1e-3) / 1e9, "verified": verify(p), "pool_copies": copies}
+
+
+def bench_gemm(args, stream, lib):
+    from ternixengine_amd import configs
+    fn = lib.ternix_hip_mul_mat_ternary
+    out, tot_ops, tot_ms = [], 0, 0.0
+    for name in ("cfg4_4096x4096", "cfg4_4096x14336", "cfg4_14336x4096"):
+        case = configs.CASES[name]
+        p = Problem(case, 1)
+        ms = time_launches(lambda i: launch(fn, p, 0, stream), args.gemm_steps, max(2, args.gemm_steps // 4), stream)
+        per = ms / args.gemm_steps
+        tops = case.ops / (per * 1e-3) / 1e12
+        out.append({"shape": [case.M, case.K, case.N], "us": per * 1e3, "tops": tops,
+                    "frac": tops / INT8_PEAK_TOPS, "verified": verify(p)})
+        tot_ops += case.ops
+        tot_ms += per
+        del p
+    return {"shapes": out, "tops": tot_ops / (tot_ms * 1e-3) / 1e12,
+            "frac": tot_ops / (tot_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS}
+
+
+def cpu_baseline(seconds):
+    """Reference avx2_blocked (oracle/_ref) or the oracle's restatement, one thread, on the cfg2 pair."""
+    from ternixengine_amd import configs
+    ref_so = os.path.join(ROOT, "oracle", "_ref", "libternix_ref.so")
+    vp, sz = ctypes.c_void_p, ctypes.c_size_t
+    if os.path.exists(ref_so):
+        lib = ctypes.CDLL(ref_so)
+        fn = lib.ref_mm_avx2_blocked
+        kind = "reference"
+    else:
+        lib = ctypes.CDLL(os.path.join(ROOT, "oracle", "liboracle.so"))
+        fn = lib.oracle_mm_avx2_blocked
+        kind = "port"
+    fn.argtypes = [vp, vp, vp, sz, sz, sz]
+    cases = [configs.CASES["cfg2_up"], configs.CASES["cfg2_down"]]
+    data = [(configs.gen_a(c), configs.gen_w_packed(c), np.empty((c.M, c.N), np.int32)) for c in cases]
+    times = []
+    t_end = time.time() + seconds
+    while time.time() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        for c, (a, wp, out) in zip(cases, data):
+            fn(a.ctypes.data_as(vp), wp.ctypes.data_as(vp), out.ctypes.data_as(vp), c.M, c.K, c.N)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    bytes_step = sum(c.bytes_algorithmic for c in cases)
+    return {"value": bytes_step / med / 1e9, "unit": "GB/s", "cores": 1, "kind": kind,
+            "sample": f"{len(times)} cfg2 FFN pairs (M=1, 2560x6912 + 6912x2560), median "
+                      f"{med * 1e3:.2f} ms/pair, mul_mat_ternary_avx2_blocked, 1 thread, ~{seconds:.0f} s"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this build runs the ternary "
+              "matmul on a single MI355X and has no multi-GPU path.", file=sys.stderr)
+        sys.exit(2)
+    import ternixengine_amd as tx
+    from ternixengine_amd import hip_runtime as hr
+    lib = tx._load()
+    stream = hr.Stream()
+    res = {}
+    if args.only in ("all", "gemv"):
+        res["gemv"] = bench_gemv_pair(args, stream, lib)
+    if args.only in ("all", "bigm1"):
+        res["bigm1"] = bench_big_m1(args, stream, lib)
+    if args.only in ("all", "gemm"):
+        res["gemm"] = bench_gemm(args, stream, lib)
+    g = res.get("gemv")
+    line = {
+        "metric": METRIC,
+        "value": round(g["gbs"], 2) if g else None,
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(g["ms_per_step"], 5) if g else None,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": "cfg2 decode FFN GEMV pair, M=1: up K=2560 N=6912 + down K=6912 N=2560, "
+                               "int8 uniform activations, ternary P(+-1)=0.3, weights rotating over a "
+                               f"{(g or {}).get('pool_bytes', 0) / 2**20:.0f} MiB pool of distinct copies "
+                               "(cold HBM reads)", "M": 1, "pair": [[2560, 6912], [6912, 2560]],
+                   "parallelism": "single GPU"},
+    }
+    if g:
+        line["roofline"] = {"bound": "hbm", "achieved": round(g["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                            "frac": round(g["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                            "kernel": "skinny_kernel (ternix_hip_mul_mat_ternary, M=1)",
+                            "avg_launch_us": round(g["launch_us"], 3)}
+        line["gemv_detail"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in g.items()}
+    if "bigm1" in res:
+        b = res["bigm1"]
+        line["gemv_big_m1"] = {"shape": b["shape"], "gbs": round(b["gbs"], 1), "frac": round(b["gbs"] / HBM_PEAK_GBS, 4),
+                               "launch_us": round(b["launch_us"], 3), "verified": b["verified"]}
+    if "gemm" in res:
+        gm = res["gemm"]
+        line["gemm_m2048"] = {"tops": round(gm["tops"], 1), "peak": INT8_PEAK_TOPS, "unit": "TOPS",
+                              "frac": round(gm["frac"], 4),
+                              "shapes": [{k: (round(v, 3) if isinstance(v, float) else v) for k, v in s.items()}
+                                         for s in gm["shapes"]]}
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        line["cpu_baseline"]["value"] = round(line["cpu_baseline"]["value"], 3)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

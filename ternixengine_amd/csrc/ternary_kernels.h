@@ -6,9 +6,11 @@
 
 namespace ternix_hip {
 
-// Largest number of k-rows one accumulator may sum without risking int32 overflow of the
-// scaled (x64) MFMA partial sums: 64 * 128 * 2^18 = 2^31.
-constexpr int kMaxKPerAccumulator = 1 << 18;
+// Largest number of k-rows one accumulator may sum (a multiple of 64) without int32 overflow of the
+// scaled MFMA partial sums.  The worst per-row term is the out-of-domain code 10 in a field decoded
+// as a signed byte of -128 times an activation of -128 (+16384), so K rows stay exact while
+// 16384 * K < 2^31, i.e. K < 2^17.  (In-domain codes reach at most 8192 per row.)
+constexpr int kMaxKPerAccumulator = (1 << 17) - 64;
 
 hipError_t launch_zero(int32_t* C, size_t n, hipStream_t st);
 // Skinny split-K kernel; M <= 32.  splits > 1 zeroes C first and accumulates atomically.

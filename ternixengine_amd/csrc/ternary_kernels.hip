@@ -28,8 +28,9 @@
 // all columns of the wave); the shift form costs 7 ops and needs nothing else.  The skinny kernel,
 // which has few A rows to amortise the decode over, uses the complement form; the GEMM, where the
 // extra R MFMA per m-tile would cost 25% of MFMA issue, uses the shift form.
-// Accumulator bound: |64 * A.W| <= 64*128*K, so each partial sum is exact for K <= 2^18; the
-// launch layer splits K so that no kernel accumulates more than 2^18 k-rows in one accumulator.
+// Accumulator bound: each k-row adds at most 64*128 = 8192 in magnitude to a scaled accumulator
+// (16384 for the out-of-domain code 10, byte -128 times activation -128); the launch layer splits K
+// so that no accumulator sums more than kMaxKPerAccumulator = 2^17 - 64 k-rows.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>

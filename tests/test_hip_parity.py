@@ -143,7 +143,8 @@ def test_misaligned_pointers(oracle, path):
 
 
 def test_k_beyond_accumulator_bound(oracle):
-    # K > 2^18 forces the launch layer to split K (scaled partial sums stay exact).
+    # K > 2^17 forces the launch layer to split K (scaled partial sums stay exact); the largest
+    # in-domain term is -128 * -1 per row, so a single unsplit accumulator would overflow here.
     m, k, n = 2, (1 << 18) + 200, 16
     a = np.full((m, k), -128, np.int8)
     a[1, ::3] = 127
@@ -155,6 +156,13 @@ def test_k_beyond_accumulator_bound(oracle):
     for path in ("gemv", "gemm"):
         log(f"[{path}] K={k}")
         assert (run(path, a, wp, n) == expect).all(), path
+    # out-of-domain code 10 everywhere (reference scalar decode: -2 per weight) just above 2^17 rows
+    k = (1 << 17) + 100
+    a = np.full((m, k), -128, np.int8)
+    wp = np.full((k, n // 4), 0xAA, np.uint8)
+    for path in ("gemv", "gemm"):
+        log(f"[{path}] K={k} code 10")
+        assert (run(path, a, wp, n) == 256 * k).all(), path
 
 
 def test_k_zero_writes_zeros():
