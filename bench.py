@@ -58,18 +58,28 @@ class Problem:
         self.dC = hr.DeviceBuffer(4 * case.M * case.N)
 
 
-def time_launches(launches, steps, warmup, stream):
-    """Run `launches(i)` for warmup + steps iterations; return (total_ms of the timed steps)."""
+def time_launches(launches, steps, warmup, stream, graph=True):
+    """Run `launches(i)` for `warmup` untimed steps, then time exactly `steps` steps with HIP events on
+    `stream`.  graph=True captures the timed steps into one hipGraph (replayed once untimed first, so
+    host launch overhead is out of the timed region); graph=False issues them eagerly."""
     from ternixengine_amd import hip_runtime as hr
     for i in range(warmup):
         launches(i)
     stream.synchronize()
     hr.synchronize()
     e0, e1 = hr.Event(), hr.Event()
-    e0.record(stream)
-    for i in range(steps):
-        launches(warmup + i)
-    e1.record(stream)
+    if graph:
+        g = hr.Graph(stream, lambda: [launches(warmup + i) for i in range(steps)])
+        g.launch()
+        stream.synchronize()
+        e0.record(stream)
+        g.launch()
+        e1.record(stream)
+    else:
+        e0.record(stream)
+        for i in range(steps):
+            launches(warmup + i)
+        e1.record(stream)
     e1.synchronize()
     hr.synchronize()
     return e0.elapsed_ms(e1)
@@ -106,6 +116,8 @@ def bench_gemv_pair(args, stream, lib):
     ms = time_launches(step, args.steps, args.warmup, stream)
     ok = verify(pu) and verify(pd)
     bytes_step = up.bytes_algorithmic + down.bytes_algorithmic
+    ms_eager = time_launches(step, args.steps, args.warmup, stream, graph=False)
+    ok = ok and verify(pu) and verify(pd)
     # hot-cache variant (same weights every step) for reference only
     ms_hot = time_launches(lambda i: (launch(fn, pu, 0, stream), launch(fn, pd, 0, stream)), args.steps,
                            args.warmup, stream)
@@ -113,6 +125,7 @@ def bench_gemv_pair(args, stream, lib):
         "ms_per_step": ms / args.steps,
         "bytes_per_step": bytes_step,
         "gbs": bytes_step / (ms / args.steps * 1e-3) / 1e9,
+        "gbs_eager_launches": bytes_step / (ms_eager / args.steps * 1e-3) / 1e9,
         "gbs_hot_cache": bytes_step / (ms_hot / args.steps * 1e-3) / 1e9,
         "launch_us": ms / args.steps / 2 * 1e3,
         "pool_copies": copies,

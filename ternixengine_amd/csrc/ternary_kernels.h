@@ -13,9 +13,22 @@ namespace ternix_hip {
 constexpr int kMaxKPerAccumulator = (1 << 17) - 64;
 
 hipError_t launch_zero(int32_t* C, size_t n, hipStream_t st);
-// Skinny split-K kernel; M <= 32.  splits > 1 zeroes C first and accumulates atomically.
-hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int splits,
-                         int steps_per_split, hipStream_t st);
+// LDS bytes the skinny fast kernel uses for one workgroup's activation slice (the rows of one
+// m-group x steps_per_split * 64 bytes, each row padded by 16 bytes); the fast kernel runs only up
+// to kSkinnyALdsMax, so planners keep steps_per_split small enough for it.
+constexpr size_t kSkinnyALdsMax = 32 * 1024;
+inline size_t skinny_a_lds_bytes(int M, int steps_per_split) {
+    const int rows = M <= 16 ? M : 32;
+    return (size_t)rows * ((size_t)steps_per_split * 64 + 16);
+}
+// True when launch_skinny takes the fast kernel for this call.
+bool skinny_fast_ok(const int8_t* A, const uint8_t* B, int M, int K, int N, int steps_per_split);
+// Skinny split-K GEMV/GEMM for M <= 32.  tb: 64-byte (1) or 128-byte (2) column slab per wave (fast
+// kernel, M <= 16); kw: waves per slab inside a workgroup (1, 2 or 4; fast kernel).  With
+// splits > 1 each split's partial C goes to `partials` ([splits][M][N] int32, 16-byte aligned) and a
+// reduce kernel sums them into C; without a workspace C is zeroed and accumulated with atomics.
+hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int tb, int kw,
+                         int splits, int steps_per_split, int32_t* partials, hipStream_t st);
 // LDS-tiled MFMA GEMM over k-rows [k_begin, k_end); accumulate != 0 adds into C instead of storing.
 hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int k_begin,
                        int k_end, int accumulate, hipStream_t st);

@@ -118,94 +118,102 @@ __device__ __forceinline__ v4i load_a16_range(const int8_t* __restrict__ A, int 
 }
 
 // ------------------------------------------------------------------------------------------------
-// Skinny split-K kernel (decode shapes, M <= 16*MT).
+// Skinny split-K kernels (decode shapes, M <= 32).
 //
-// Workgroup = 4 waves on one 64-byte column tile (256 output columns).  Lane (q = l%16, kb = l/16)
-// owns packed dword q of the tile (byte-columns 4q..4q+3 = output columns 16q..16q+15) and k-rows
-// kb*16..kb*16+15 of every 64-row k-step.  Per k-step a lane issues 16 dword loads (one per k-row;
-// lanes 0-15 read 64 contiguous bytes of one row), transposes them into 4 byte-columns x 16 rows,
-// and drives 16 MFMAs per m-tile (4 byte-columns x 4 fields) plus one row-sum MFMA.
-// The workgroup's k-steps are dealt round-robin to its 4 waves; the waves' results are summed in
-// LDS and written (or atomically added when blockIdx.y splits K across workgroups).
+// MFMA mapping.  A wave owns a column slab of 64*TB packed bytes (256*TB output columns).  Lane
+// (q = l%16, kb = l/16) owns dwords q + 16h (h < TB) of the slab -- byte-columns g = 4h..4h+3 of the
+// lane -- and k-rows 16kb..16kb+15 of every 64-row k-step.  Per k-step it transposes its 16 rows x
+// 4*TB byte-columns (v_perm) and drives 16*TB MFMAs per m-tile (4*TB byte-columns x 4 fields) plus
+// one row-sum MFMA for the complement decode.
+//
+// Fast kernel (K % 64 == 0, NB % 64 == 0, 16-byte aligned A and W): weights are read with coalesced
+// 16-byte loads -- one wave instruction covers 16/TB rows x 64*TB bytes, whole 128-byte lines when
+// TB == 2 -- into registers, two k-steps in flight per wave, and go through a per-wave LDS block to
+// come back in the transposed lane layout.  The workgroup's activation slice (its rows x its
+// k-range) is copied to LDS once, so activation fragments never wait behind weight loads.
+// Generic kernel (any shape / alignment): branch-free clamped dword loads, no LDS staging.
+//
+// Split-K.  A workgroup has 4 waves: 4/KW column slabs x KW waves per slab; the KW waves of a slab
+// take alternate k-steps and are summed in LDS.  blockIdx.y splits K further over `splits`
+// workgroups: each stores its partial tile with plain stores in the workspace P[split][M][N] and
+// splitk_reduce_kernel (the next launch on the stream) adds the partials.  Cross-workgroup exchange
+// inside one launch would need device-scope release/acquire fences, which on this multi-XCD part
+// write back and invalidate a whole L2 per workgroup, and same-address device-scope atomics from
+// several XCDs serialise at the memory side; the kernel boundary gives the ordering for free.
+// (SK_ATOMIC, used only when no workspace is available, accumulates into a pre-zeroed C instead.)
+// LOW_M: at most 4 rows in this m-group, all held by lanes 0-15 (rows 4*kb + i of an MFMA tile), so
+// only those lanes take part in the LDS exchange and the epilogue.
 // ------------------------------------------------------------------------------------------------
 
 constexpr int SK_WAVES = 4;
 
-template <int MT, bool ALIGNED_W, bool ALIGNED_A, bool ATOMIC>
-__global__ __launch_bounds__(256) void skinny_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ B,
-                                                     int32_t* __restrict__ C, int M, int K, int N,
-                                                     int steps_per_split, int vec_store) {
-    constexpr int NV = MT * 64;  // result values per lane: MT m-tiles x 4 byte-cols x 4 fields x 4 rows
-    __shared__ int32_t red[(SK_WAVES - 1) * NV * 64];
+enum SkinnyMode { SK_STORE = 0, SK_ATOMIC = 1, SK_PARTIAL = 2 };
 
-    const int NB = N >> 2;
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int q = lane & 15;
-    const int kb = lane >> 4;
-    const int bc = blockIdx.x * 64 + 4 * q;        // first byte-column of this lane's dword
-    const int m0 = blockIdx.z * (16 * MT);
-    const int nsteps = (K + 63) >> 6;
-    const int s_begin = blockIdx.y * steps_per_split;
-    const int s_end = min(nsteps, s_begin + steps_per_split);
+struct SkinnyArgs {
+    const int8_t* A;
+    const uint8_t* B;
+    int32_t* C;
+    int32_t* P;           // workspace partials [splits][M][N] (SK_PARTIAL)
+    int M, K, N;
+    int steps_per_split;
+    int splits;
+    int mode;             // SkinnyMode
+    int vec_store;        // C is 16-byte aligned
+    int aligned_w;        // generic kernel: NB % 4 == 0 and W 4-byte aligned
+    int aligned_a;        // generic kernel: K % 16 == 0 and A 16-byte aligned
+};
 
-    v4i acc[MT][4][4];
-    v4i accR[MT];
+// One k-step of MFMA work for one 16-row x 4-byte-column block: raw[r] is the dword of row r.
+// Byte-column g of the block feeds tiles acc[t][gbase + g][0..3] (one per 2-bit field).
+template <int MT, int G>
+__device__ __forceinline__ void skinny_mfma_block(const uint32_t (&raw)[16], const v4i (&a)[MT], int gbase,
+                                                  v4i (&acc)[MT][G][4]) {
+    uint32_t T[4][4];  // T[g][rq]: byte-column g, rows 4rq..4rq+3
 #pragma unroll
-    for (int t = 0; t < MT; ++t) {
-        accR[t] = v4i{0, 0, 0, 0};
+    for (int rq = 0; rq < 4; ++rq)
+        transpose4x4(raw[4 * rq], raw[4 * rq + 1], raw[4 * rq + 2], raw[4 * rq + 3], T[0][rq], T[1][rq], T[2][rq],
+                     T[3][rq]);
 #pragma unroll
-        for (int g = 0; g < 4; ++g)
+    for (int g = 0; g < 4; ++g) {
+        v4i b0, b1, b2, b3;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[t][g][j] = v4i{0, 0, 0, 0};
-    }
-    const v4i ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
-
-    for (int s = s_begin + wave; s < s_end; s += SK_WAVES) {
-        const int k0 = s * 64 + kb * 16;
-        uint32_t raw[16];
+        for (int rq = 0; rq < 4; ++rq) {
+            const uint32_t x = T[g][rq];
+            const uint32_t z = x ^ 0x55555555u;
+            b0[rq] = (int)(z & 0x03030303u);
+            b1[rq] = (int)(z & 0x0C0C0C0Cu);
+            b2[rq] = (int)(z & 0x30303030u);
+            b3[rq] = (int)(x & 0xC0C0C0C0u);
+        }
 #pragma unroll
-        for (int r = 0; r < 16; ++r) raw[r] = load_w4<ALIGNED_W>(B, k0 + r, bc, K, NB);
-        v4i a[MT];
-#pragma unroll
-        for (int t = 0; t < MT; ++t) a[t] = load_a16<ALIGNED_A>(A, m0 + 16 * t + q, k0, M, K);
-
-        uint32_t T[4][4];  // T[g][rq]: byte-column g, rows 4rq..4rq+3
-#pragma unroll
-        for (int rq = 0; rq < 4; ++rq)
-            transpose4x4(raw[4 * rq], raw[4 * rq + 1], raw[4 * rq + 2], raw[4 * rq + 3],
-                         T[0][rq], T[1][rq], T[2][rq], T[3][rq]);
-#pragma unroll
-        for (int t = 0; t < MT; ++t) accR[t] = mfma_i8(a[t], ones, accR[t]);
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            v4i b0, b1, b2, b3;
-#pragma unroll
-            for (int rq = 0; rq < 4; ++rq) {
-                const uint32_t x = T[g][rq];
-                const uint32_t z = x ^ 0x55555555u;
-                b0[rq] = (int)(z & 0x03030303u);
-                b1[rq] = (int)(z & 0x0C0C0C0Cu);
-                b2[rq] = (int)(z & 0x30303030u);
-                b3[rq] = (int)(x & 0xC0C0C0C0u);
-            }
-#pragma unroll
-            for (int t = 0; t < MT; ++t) {
-                acc[t][g][0] = mfma_i8(a[t], b0, acc[t][g][0]);
-                acc[t][g][1] = mfma_i8(a[t], b1, acc[t][g][1]);
-                acc[t][g][2] = mfma_i8(a[t], b2, acc[t][g][2]);
-                acc[t][g][3] = mfma_i8(a[t], b3, acc[t][g][3]);
-            }
+        for (int t = 0; t < MT; ++t) {
+            acc[t][gbase + g][0] = mfma_i8(a[t], b0, acc[t][gbase + g][0]);
+            acc[t][gbase + g][1] = mfma_i8(a[t], b1, acc[t][gbase + g][1]);
+            acc[t][gbase + g][2] = mfma_i8(a[t], b2, acc[t][gbase + g][2]);
+            acc[t][gbase + g][3] = mfma_i8(a[t], b3, acc[t][gbase + g][3]);
         }
     }
+}
 
-    // Per-wave results: w = R - S_j / 4^j (j < 3), S_3 / 64.  Output layout of a 16x16 MFMA tile:
-    // lane l holds column l%16 and rows 4*(l/16) + i in element i.
-    int val[MT][4][4][4];  // [t][g][j][i]
+// Finishes a wave's accumulators: complement decode, LDS sum over the KW waves of the slab, and the
+// store / partial store / atomic add of the slab's outputs.  Must be reached by every wave.
+// bcol(g) = byte-column of lane value g = tile_bc + 64*(g/4) + 4q + g%4.
+template <int MT, int G, int KW, int TILES, bool LOW_M>
+__device__ __forceinline__ void skinny_epilogue(const SkinnyArgs& args, int32_t* red, v4i (&acc)[MT][G][4],
+                                                const v4i (&accR)[MT], int tw, int kw, int tile_bc, int m0) {
+    constexpr int NV = MT * 16 * G;
+    constexpr int XL = LOW_M ? 16 : 64;
+    const int lane = threadIdx.x & 63;
+    const int q = lane & 15, kb = lane >> 4;
+    const int M = args.M, N = args.N, NB = N >> 2;
+
+    // w = R - S_j / 4^j (j < 3), S_3 / 64.  MFMA tile layout: lane l holds column l%16 and rows
+    // 4*(l/16) + i in element i.
+    int val[MT][G][4][4];  // [t][g][j][i]
 #pragma unroll
     for (int t = 0; t < MT; ++t)
 #pragma unroll
-        for (int g = 0; g < 4; ++g)
+        for (int g = 0; g < G; ++g)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int R = accR[t][i];
@@ -215,23 +223,47 @@ __global__ __launch_bounds__(256) void skinny_kernel(const int8_t* __restrict__ 
                 val[t][g][3][i] = acc[t][g][3][i] >> 6;
             }
 
-    // Rows this lane's values belong to: m0 + 16t + 4kb + i.  Only rows < M take part.
-    if (wave > 0) {
-        int32_t* dst = red + (wave - 1) * NV * 64 + lane;
+    const bool xlane = !LOW_M || kb == 0;
+    const int xl = LOW_M ? q : lane;
+    if (KW > 1) {
+        // Halving tree over the KW waves of the slab: the upper half writes, the lower half adds.
+        __syncthreads();  // the buffer may alias the staging blocks still in use by other waves
 #pragma unroll
-        for (int t = 0; t < MT; ++t)
+        for (int h = KW / 2; h >= 1; h >>= 1) {
+            if (kw >= h && kw < 2 * h && xlane) {
+                int32_t* dst = red + ((kw - h) * TILES + tw) * NV * XL + xl;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                if (m0 + 16 * t + 4 * kb + i >= M) continue;
+                for (int t = 0; t < MT; ++t)
 #pragma unroll
-                for (int g = 0; g < 4; ++g)
+                    for (int i = 0; i < 4; ++i) {
+                        if (m0 + 16 * t + 4 * kb + i >= M) continue;
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) dst[(((t * 4 + i) * 4 + g) * 4 + j) * 64] = val[t][g][j][i];
+                        for (int g = 0; g < G; ++g)
+#pragma unroll
+                            for (int j = 0; j < 4; ++j) dst[(((t * 4 + i) * G + g) * 4 + j) * XL] = val[t][g][j][i];
+                    }
             }
+            __syncthreads();
+            if (kw < h && xlane) {
+                const int32_t* src = red + (kw * TILES + tw) * NV * XL + xl;
+#pragma unroll
+                for (int t = 0; t < MT; ++t)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        if (m0 + 16 * t + 4 * kb + i >= M) continue;
+#pragma unroll
+                        for (int g = 0; g < G; ++g)
+#pragma unroll
+                            for (int j = 0; j < 4; ++j) val[t][g][j][i] += src[(((t * 4 + i) * G + g) * 4 + j) * XL];
+                    }
+            }
+            if (h > 1) __syncthreads();
+        }
     }
-    __syncthreads();
-    if (wave != 0) return;
+    if (kw != 0 || !xlane) return;
 
+    int32_t* out_base = args.mode == SK_PARTIAL ? args.P + (size_t)blockIdx.y * (size_t)M * (size_t)N : args.C;
+    const bool vec = args.mode == SK_PARTIAL || args.vec_store;
 #pragma unroll
     for (int t = 0; t < MT; ++t)
 #pragma unroll
@@ -239,31 +271,242 @@ __global__ __launch_bounds__(256) void skinny_kernel(const int8_t* __restrict__ 
             const int row = m0 + 16 * t + 4 * kb + i;
             if (row >= M) continue;
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                int v[4];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    int sum = val[t][g][j][i];
-#pragma unroll
-                    for (int w = 0; w < SK_WAVES - 1; ++w)
-                        sum += red[w * NV * 64 + (((t * 4 + i) * 4 + g) * 4 + j) * 64 + lane];
-                    v[j] = sum;
-                }
-                const int bcg = bc + g;
-                if (bcg >= NB) continue;
-                int32_t* out = C + (size_t)row * (size_t)N + 4 * bcg;
-                if (ATOMIC) {
+            for (int g = 0; g < G; ++g) {
+                const int bcol = tile_bc + 64 * (g >> 2) + 4 * q + (g & 3);
+                if (bcol >= NB) continue;
+                int32_t* out = out_base + (size_t)row * (size_t)N + 4 * bcol;
+                if (args.mode == SK_ATOMIC) {
 #pragma unroll
                     for (int j = 0; j < 4; ++j)
-                        if (v[j] != 0) atomicAdd(out + j, v[j]);
-                } else if (vec_store) {
-                    *reinterpret_cast<v4i*>(out) = v4i{v[0], v[1], v[2], v[3]};
+                        if (val[t][g][j][i] != 0) atomicAdd(out + j, val[t][g][j][i]);
+                } else if (vec) {
+                    *reinterpret_cast<v4i*>(out) = v4i{val[t][g][0][i], val[t][g][1][i], val[t][g][2][i], val[t][g][3][i]};
                 } else {
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) out[j] = v[j];
+                    for (int j = 0; j < 4; ++j) out[j] = val[t][g][j][i];
                 }
             }
         }
+}
+
+template <int MT, int TB, int KW, bool LOW_M>
+struct SkinnyFastGeometry {
+    static constexpr int G = 4 * TB;                  // byte-columns per lane
+    static constexpr int TILES = SK_WAVES / KW;       // column slabs per workgroup
+    static constexpr int ROW_DW = 16 * TB;            // dwords per staged row
+    static constexpr int STAGE_DW = 64 * ROW_DW + 4 * 16;  // + 64-byte pad per 16 rows
+    static constexpr int RED_DW = TILES * (KW / 2) * MT * 16 * G * (LOW_M ? 16 : 64);
+    static constexpr int SMEM_DW = (SK_WAVES * STAGE_DW > RED_DW) ? SK_WAVES * STAGE_DW : RED_DW;
+};
+
+template <int MT, int TB, int KW, bool LOW_M>
+__global__ __launch_bounds__(64 * SK_WAVES) void skinny_fast_kernel(SkinnyArgs args) {
+    using Geo = SkinnyFastGeometry<MT, TB, KW, LOW_M>;
+    constexpr int G = Geo::G, TILES = Geo::TILES, ROW_DW = Geo::ROW_DW, STAGE_DW = Geo::STAGE_DW;
+    constexpr int RPI = 16 / TB;        // rows per load instruction
+    constexpr int NLD = 4 * TB;         // load instructions per k-step
+    constexpr int PD = 2;               // k-steps in flight per wave
+    constexpr int BS = 64 * SK_WAVES;
+    __shared__ __attribute__((aligned(16))) int32_t smem[Geo::SMEM_DW];
+    // this workgroup's activation slice, row pitch a_pitch bytes (k-range + 16, so the 16 rows read by
+    // one ds_read_b128 fall on distinct banks)
+    extern __shared__ __attribute__((aligned(16))) int8_t a_lds[];
+
+    const int8_t* __restrict__ A = args.A;
+    const uint8_t* __restrict__ B = args.B;
+    const int M = args.M, K = args.K, NB = args.N >> 2;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (scalar)
+    const int tw = wave % TILES, kw = wave / TILES;
+    const int q = lane & 15, kb = lane >> 4;
+    const int tile_bc = (blockIdx.x * TILES + tw) * 64 * TB;
+    const int m0 = blockIdx.z * (16 * MT);
+    const int nsteps = K >> 6;
+    const int s_begin = blockIdx.y * args.steps_per_split;
+    const int s_stop = min(nsteps, s_begin + args.steps_per_split);
+    const int s_end = tile_bc < NB ? s_stop : s_begin;  // a slab past the last column loads nothing
+    const int s0 = s_begin + kw;
+
+    v4i acc[MT][G][4];
+    v4i accR[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+        accR[t] = v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[t][g][j] = v4i{0, 0, 0, 0};
+    }
+    const v4i ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
+
+    // Weight loads: lane (rr, cc) reads 16-byte chunk cc of row h*RPI + rr of the slab.
+    const int rr = lane / (4 * TB), cc = lane % (4 * TB);
+    const uint32_t goff = (uint32_t)rr * (uint32_t)NB + (uint32_t)(tile_bc + cc * 16);
+    auto gload = [&](int s, v4i (&g4)[NLD]) {
+        const uint8_t* rowbase = B + (size_t)s * 64 * (size_t)NB;  // wave-uniform
+#pragma unroll
+        for (int h = 0; h < NLD; ++h)
+            g4[h] = *reinterpret_cast<const v4i*>(rowbase + goff + (uint32_t)(RPI * h) * (uint32_t)NB);
+    };
+
+    // Activation slice: first batch of loads, then the weight prologue, then the LDS stores.
+    const int a_rows = min(16 * MT, M - m0);
+    const int n16 = (s_stop - s_begin) * 4;  // 16-byte chunks per activation row
+    const int a_total = a_rows * n16;
+    const int a_pitch = args.steps_per_split * 64 + 16;
+    auto a_src = [&](int c) {
+        return reinterpret_cast<const v4i*>(A + (size_t)(m0 + c / n16) * (size_t)K + (size_t)s_begin * 64 +
+                                            (c % n16) * 16);
+    };
+    auto a_dst = [&](int c) { return reinterpret_cast<v4i*>(a_lds + (c / n16) * a_pitch + (c % n16) * 16); };
+    v4i areg[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) areg[u] = *a_src(min((int)threadIdx.x + u * BS, a_total - 1));
+
+    // Ring of PD steps in flight: slot p holds step s0 + (it + p) * KW.  The prologue loads are
+    // unconditional (clamped to the wave's last step) so that the same number of loads is in flight
+    // on every path into the steady-state loop and the compiler waits for exactly the slot it uses.
+    const bool has_steps = s0 < s_end;  // wave-uniform
+    v4i gbuf[PD][NLD];
+    if (has_steps) {
+#pragma unroll
+        for (int p = 0; p < PD; ++p) gload(min(s0 + p * KW, s_end - 1), gbuf[p]);
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+        if ((int)threadIdx.x + u * BS < a_total) *a_dst(threadIdx.x + u * BS) = areg[u];
+    for (int c = threadIdx.x + 2 * BS; c < a_total; c += BS) *a_dst(c) = *a_src(c);
+    __syncthreads();
+
+    int a_off[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) a_off[t] = min(16 * t + q, a_rows - 1) * a_pitch + kb * 16;
+    int32_t* stage = smem + wave * STAGE_DW;
+
+    // One k-step: weights through the wave's LDS block into the transposed layout, activations from
+    // the slice, then the MFMAs.
+    auto consume = [&](int cur, v4i (&g4)[NLD], uint32_t (&raw)[TB][16], v4i (&a)[MT]) {
+#pragma unroll
+        for (int h = 0; h < NLD; ++h) {
+            const int R = RPI * h + rr;
+            *reinterpret_cast<v4i*>(stage + R * ROW_DW + (R >> 4) * 16 + cc * 4) = g4[h];
+        }
+        __asm__ volatile("" ::: "memory");  // LDS is in order within a wave; keep the compiler so
+#pragma unroll
+        for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                raw[tb][r] = (uint32_t)stage[(16 * kb + r) * ROW_DW + 16 * kb + q + 16 * tb];
+#pragma unroll
+        for (int t = 0; t < MT; ++t) a[t] = *reinterpret_cast<const v4i*>(a_lds + a_off[t] + (cur - s_begin) * 64);
+        __asm__ volatile("" ::: "memory");
+    };
+    auto compute = [&](const uint32_t (&raw)[TB][16], const v4i (&a)[MT]) {
+#pragma unroll
+        for (int t = 0; t < MT; ++t) accR[t] = mfma_i8(a[t], ones, accR[t]);
+#pragma unroll
+        for (int tb = 0; tb < TB; ++tb) skinny_mfma_block<MT, G>(raw[tb], a, 4 * tb, acc);
+    };
+
+    if (has_steps) {
+        int it = 0;
+        // steady state: every slot consumed and refilled, no conditions
+        for (; s0 + (it + 2 * PD - 1) * KW < s_end; it += PD) {
+#pragma unroll
+            for (int p = 0; p < PD; ++p) {
+                const int cur = s0 + (it + p) * KW;
+                uint32_t raw[TB][16];
+                v4i a[MT];
+                consume(cur, gbuf[p], raw, a);
+                gload(cur + PD * KW, gbuf[p]);
+                compute(raw, a);
+                // keep the next slot's LDS stores (and their wait for its loads) after this math
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        // tail: fewer than 2*PD steps left
+        for (; s0 + it * KW < s_end; it += PD) {
+#pragma unroll
+            for (int p = 0; p < PD; ++p) {
+                const int cur = s0 + (it + p) * KW;
+                if (cur < s_end) {
+                    uint32_t raw[TB][16];
+                    v4i a[MT];
+                    consume(cur, gbuf[p], raw, a);
+                    if (cur + PD * KW < s_end) gload(cur + PD * KW, gbuf[p]);
+                    compute(raw, a);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+        }
+    }
+    skinny_epilogue<MT, G, KW, TILES, LOW_M>(args, smem, acc, accR, tw, kw, tile_bc, m0);
+}
+
+// Four packed bytes at (row, bc), 0 outside the K x NB matrix; clamped indices, masked value.
+__device__ __forceinline__ uint32_t ld_w4(const uint8_t* __restrict__ B, int row, int bc, int K, int NB, bool aligned) {
+    const int rc = min(row, K - 1);
+    if (aligned) {
+        const int bcc = min(bc, NB - 4);
+        const uint32_t v = *reinterpret_cast<const uint32_t*>(B + (size_t)rc * (size_t)NB + bcc);
+        return (bc < NB && row < K) ? v : 0u;
+    }
+    uint32_t v = 0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        const int c = min(bc + b, NB - 1);
+        const uint32_t byte = B[(size_t)rc * (size_t)NB + c];
+        v |= ((bc + b < NB) ? byte : 0u) << (8 * b);
+    }
+    return row < K ? v : 0u;
+}
+
+// Generic skinny kernel: any K, N % 4 == 0, any alignment.  TB = 1, 2 slabs x 2 waves.
+template <int MT, bool LOW_M>
+__global__ __launch_bounds__(64 * SK_WAVES) void skinny_generic_kernel(SkinnyArgs args) {
+    constexpr int KW = 2, TILES = 2, G = 4;
+    __shared__ __attribute__((aligned(16))) int32_t smem[TILES * (KW / 2) * MT * 16 * G * (LOW_M ? 16 : 64)];
+    const int8_t* __restrict__ A = args.A;
+    const uint8_t* __restrict__ B = args.B;
+    const int M = args.M, K = args.K, NB = args.N >> 2;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int tw = wave % TILES, kw = wave / TILES;
+    const int q = lane & 15, kb = lane >> 4;
+    const int tile_bc = (blockIdx.x * TILES + tw) * 64;
+    const int bc = tile_bc + 4 * q;
+    const int m0 = blockIdx.z * (16 * MT);
+    const int nsteps = (K + 63) >> 6;
+    const int s_begin = blockIdx.y * args.steps_per_split;
+    const int s_end = tile_bc < NB ? min(nsteps, s_begin + args.steps_per_split) : s_begin;
+    const bool aw = args.aligned_w, aa = args.aligned_a;
+
+    v4i acc[MT][G][4];
+    v4i accR[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+        accR[t] = v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[t][g][j] = v4i{0, 0, 0, 0};
+    }
+    const v4i ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
+    for (int s = s_begin + kw; s < s_end; s += KW) {
+        const int k0 = s * 64 + kb * 16;
+        uint32_t raw[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) raw[r] = ld_w4(B, k0 + r, bc, K, NB, aw);
+        v4i a[MT];
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+            a[t] = aa ? load_a16<true>(A, min(m0 + 16 * t + q, M - 1), k0, M, K)
+                      : load_a16<false>(A, min(m0 + 16 * t + q, M - 1), k0, M, K);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) accR[t] = mfma_i8(a[t], ones, accR[t]);
+        skinny_mfma_block<MT, G>(raw, a, 0, acc);
+    }
+    skinny_epilogue<MT, G, KW, TILES, LOW_M>(args, smem, acc, accR, tw, kw, tile_bc, m0);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -463,29 +706,52 @@ __global__ __launch_bounds__(256) void zero_kernel(int32_t* __restrict__ C, size
     for (; i < n; i += stride) C[i] = 0;
 }
 
-template <int MT, bool AW, bool AA, bool AT>
-hipError_t launch_skinny_t(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int splits,
-                           int steps_per_split, hipStream_t st) {
-    const int NB = N >> 2;
-    dim3 grid((NB + 63) / 64, splits, (M + 16 * MT - 1) / (16 * MT));
-    const int vec_store = ((uintptr_t)C % 16) == 0;
-    hipLaunchKernelGGL((skinny_kernel<MT, AW, AA, AT>), grid, dim3(256), 0, st, A, B, C, M, K, N, steps_per_split,
-                       vec_store);
+// C[m][n] = sum over splits of P[s][m][n].  A workgroup owns 64 consecutive groups of 4 outputs
+// (lane = group); its 4 waves take splits s = w, w+4, ... with all their loads issued at once (one
+// memory round trip for up to 64 splits), then add in LDS.  Integer addition is exact, so the order
+// does not change the result.
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const int32_t* __restrict__ P, int32_t* __restrict__ C,
+                                                            size_t n4, int splits, int vec_store) {
+    __shared__ v4i part[3][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const size_t i = (size_t)blockIdx.x * 64 + lane;
+    const size_t ic = i < n4 ? i : n4 - 1;
+    const v4i* src = reinterpret_cast<const v4i*>(P) + ic;
+    v4i sum = {0, 0, 0, 0};
+    for (int s0 = wave; s0 < splits; s0 += 64) {
+        v4i v[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const int s = s0 + 4 * u;
+            v[u] = s < splits ? src[(size_t)s * n4] : v4i{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int u = 0; u < 16; ++u) sum += v[u];
+    }
+    if (wave > 0) part[wave - 1][lane] = sum;
+    __syncthreads();
+    if (wave != 0 || i >= n4) return;
+    sum += part[0][lane] + part[1][lane] + part[2][lane];
+    if (vec_store) {
+        reinterpret_cast<v4i*>(C)[i] = sum;
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) C[4 * i + j] = sum[j];
+    }
+}
+
+template <int MT, int TB, int KW, bool LOW_M>
+hipError_t launch_fast_t(const SkinnyArgs& a, dim3 grid, hipStream_t st) {
+    hipLaunchKernelGGL((skinny_fast_kernel<MT, TB, KW, LOW_M>), grid, dim3(64 * SK_WAVES),
+                       skinny_a_lds_bytes(a.M, a.steps_per_split), st, a);
     return hipGetLastError();
 }
 
-template <int MT>
-hipError_t launch_skinny_m(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, bool aw, bool aa,
-                           int splits, int sps, hipStream_t st) {
-    const bool at = splits > 1;
-    if (aw && aa) return at ? launch_skinny_t<MT, true, true, true>(A, B, C, M, K, N, splits, sps, st)
-                            : launch_skinny_t<MT, true, true, false>(A, B, C, M, K, N, splits, sps, st);
-    if (aw) return at ? launch_skinny_t<MT, true, false, true>(A, B, C, M, K, N, splits, sps, st)
-                      : launch_skinny_t<MT, true, false, false>(A, B, C, M, K, N, splits, sps, st);
-    if (aa) return at ? launch_skinny_t<MT, false, true, true>(A, B, C, M, K, N, splits, sps, st)
-                      : launch_skinny_t<MT, false, true, false>(A, B, C, M, K, N, splits, sps, st);
-    return at ? launch_skinny_t<MT, false, false, true>(A, B, C, M, K, N, splits, sps, st)
-              : launch_skinny_t<MT, false, false, false>(A, B, C, M, K, N, splits, sps, st);
+template <int MT, int TB, bool LOW_M>
+hipError_t launch_fast_kw(const SkinnyArgs& a, int kw, dim3 grid, hipStream_t st) {
+    if (kw >= 4) return launch_fast_t<MT, TB, 4, LOW_M>(a, grid, st);
+    if (kw == 2) return launch_fast_t<MT, TB, 2, LOW_M>(a, grid, st);
+    return launch_fast_t<MT, TB, 1, LOW_M>(a, grid, st);
 }
 
 template <int BM, int BNB>
@@ -516,17 +782,46 @@ hipError_t launch_zero(int32_t* C, size_t n, hipStream_t st) {
     return hipGetLastError();
 }
 
-hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int splits,
-                         int steps_per_split, hipStream_t st) {
+bool skinny_fast_ok(const int8_t* A, const uint8_t* B, int M, int K, int N, int steps_per_split) {
     const int NB = N >> 2;
-    const bool aw = (NB % 4 == 0) && ((uintptr_t)B % 4 == 0);
-    const bool aa = (K % 16 == 0) && ((uintptr_t)A % 16 == 0);
-    if (splits > 1) {
+    return (K % 64 == 0) && (NB % 64 == 0) && ((uintptr_t)B % 16 == 0) && ((uintptr_t)A % 16 == 0) &&
+           (NB < (1 << 26)) && skinny_a_lds_bytes(M, steps_per_split) <= kSkinnyALdsMax;
+}
+
+hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int tb, int kw,
+                         int splits, int steps_per_split, int32_t* partials, hipStream_t st) {
+    const int NB = N >> 2;
+    const int mode = splits <= 1 ? SK_STORE : (partials ? SK_PARTIAL : SK_ATOMIC);
+    if (mode == SK_ATOMIC) {
         const hipError_t e = launch_zero(C, (size_t)M * (size_t)N, st);
         if (e != hipSuccess) return e;
     }
-    if (M <= 16) return launch_skinny_m<1>(A, B, C, M, K, N, aw, aa, splits, steps_per_split, st);
-    return launch_skinny_m<2>(A, B, C, M, K, N, aw, aa, splits, steps_per_split, st);
+    const int vec_store = ((uintptr_t)C % 16) == 0;
+    const int aw = (NB % 4 == 0) && ((uintptr_t)B % 4 == 0);
+    const int aa = (K % 16 == 0) && ((uintptr_t)A % 16 == 0);
+    SkinnyArgs a{A, B, C, partials, M, K, N, steps_per_split, splits, mode, vec_store, aw, aa};
+    const int mt = M <= 16 ? 1 : 2;
+    const int mgroups = (M + 16 * mt - 1) / (16 * mt);
+    hipError_t e;
+    if (skinny_fast_ok(A, B, M, K, N, steps_per_split)) {
+        if (mt == 2) tb = 1;
+        const int slab = 64 * tb * (SK_WAVES / (kw >= 4 ? 4 : (kw == 2 ? 2 : 1)));  // bytes per workgroup
+        const dim3 grid((NB + slab - 1) / slab, splits, mgroups);
+        if (M <= 4) e = tb == 2 ? launch_fast_kw<1, 2, true>(a, kw, grid, st) : launch_fast_kw<1, 1, true>(a, kw, grid, st);
+        else if (M <= 16) e = tb == 2 ? launch_fast_kw<1, 2, false>(a, kw, grid, st) : launch_fast_kw<1, 1, false>(a, kw, grid, st);
+        else e = launch_fast_kw<2, 1, false>(a, kw, grid, st);
+    } else {
+        const dim3 grid((NB + 127) / 128, splits, mgroups);
+        if (M <= 4) hipLaunchKernelGGL((skinny_generic_kernel<1, true>), grid, dim3(64 * SK_WAVES), 0, st, a);
+        else if (M <= 16) hipLaunchKernelGGL((skinny_generic_kernel<1, false>), grid, dim3(64 * SK_WAVES), 0, st, a);
+        else hipLaunchKernelGGL((skinny_generic_kernel<2, false>), grid, dim3(64 * SK_WAVES), 0, st, a);
+        e = hipGetLastError();
+    }
+    if (e != hipSuccess || mode != SK_PARTIAL) return e;
+    const size_t n4 = (size_t)M * (size_t)N / 4;
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n4 + 63) / 64)), dim3(256), 0, st, partials, C, n4,
+                       splits, vec_store);
+    return hipGetLastError();
 }
 
 hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int k_begin, int k_end,

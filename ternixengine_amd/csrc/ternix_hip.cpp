@@ -7,16 +7,21 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
 #include <atomic>
 #include <climits>
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
+#include <map>
+#include <mutex>
+#include <utility>
 
 #include "ternary_kernels.h"
 
 namespace {
 
 constexpr int kSkinnyMaxM = 32;
-constexpr int kSkinnyWaves = 4;       // waves per skinny workgroup (skinny_kernel's SK_WAVES)
 constexpr int kMaxDevices = 64;
 
 // Compute-unit count per device, read once (hipDeviceGetAttribute is not free on a hot path).
@@ -30,6 +35,44 @@ int cu_count() {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
     g_cu_count[dev].store(n, std::memory_order_relaxed);
     return n;
+}
+
+// ---- split-K workspace -------------------------------------------------------------------------
+// The skinny kernel's split-K writes one partial C per split into a device workspace that the
+// following reduce kernel sums.  One workspace per (device, stream), so concurrent streams never
+// share one.  It is allocated the first time a shape needs more than the current size -- never
+// while the stream is being captured into a graph (the call then takes the atomic path, which needs
+// no workspace) -- and kept until the process ends.
+constexpr size_t kWorkspaceMax = size_t(256) << 20;
+
+struct Workspace {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+};
+std::mutex g_ws_mutex;
+std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
+
+void* workspace(hipStream_t st, size_t bytes) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    Workspace& w = g_ws[{dev, st}];
+    if (w.bytes >= bytes) return w.ptr;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
+    size_t nb = std::max(bytes, size_t(8) << 20);
+    nb = (nb + (size_t(1) << 20) - 1) & ~((size_t(1) << 20) - 1);
+    if (w.ptr) {
+        if (hipStreamSynchronize(st) != hipSuccess) return nullptr;
+        (void)hipFree(w.ptr);
+        w.ptr = nullptr;
+        w.bytes = 0;
+    }
+    void* p = nullptr;
+    if (hipMalloc(&p, nb) != hipSuccess) return nullptr;
+    w.ptr = p;
+    w.bytes = nb;
+    return p;
 }
 
 // Shape / pointer validation shared by every device entry point.  Returns hipSuccess when the call
@@ -48,24 +91,61 @@ hipError_t validate(const void* dA, const void* dB, const void* dC, int64_t M, i
     return hipSuccess;
 }
 
-hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int K, int N, hipStream_t st) {
+// Split-K plan of the skinny kernels: tb (64- or 128-byte column slab per wave), kw (waves per slab
+// inside a workgroup of 4 waves), `splits` workgroups along K (splits > 1 adds the partial-sum
+// reduce launch) with sps k-steps each.
+struct SkinnyPlan {
+    int tb, kw, splits, sps;
+};
+
+SkinnyPlan plan_skinny(int M, int K, int N) {
     const int NB = N / 4;
-    const int col_tiles = (NB + 63) / 64;
-    const int mgroups = M <= 16 ? 1 : (M + 31) / 32;
     const int nsteps = (K + 63) / 64;
-    // Aim for ~4 workgroups (16 waves) per CU, but give each workgroup at least one k-step per wave.
-    const long target = (4L * cu_count()) / ((long)col_tiles * mgroups);
-    long splits = target < 1 ? 1 : target;
-    const long max_splits = (nsteps + kSkinnyWaves - 1) / kSkinnyWaves;
-    if (splits > max_splits) splits = max_splits < 1 ? 1 : max_splits;
-    const long min_splits = (nsteps + (ternix_hip::kMaxKPerAccumulator / 64) - 1) / (ternix_hip::kMaxKPerAccumulator / 64);
-    if (splits < min_splits) splits = min_splits;
-    if (splits > 65535) splits = 65535;
-    int sps = (int)((nsteps + splits - 1) / splits);
-    if (sps < 1) sps = 1;
-    splits = (nsteps + sps - 1) / sps;
-    if (splits < 1) splits = 1;
-    return ternix_hip::launch_skinny(dA, dB, dC, M, K, N, (int)splits, sps, st);
+    const int mgroups = M <= 16 ? 1 : (M + 31) / 32;
+    SkinnyPlan p{M <= 16 ? 2 : 1, 2, 1, nsteps};
+    // Narrow outputs get 64-byte slabs so that more workgroups share the columns.
+    if (p.tb == 2 && NB < 64 * 2 * 2 * 16) p.tb = 1;
+    const long col_wgs = (NB + 64L * p.tb * (4 / p.kw) - 1) / (64L * p.tb * (4 / p.kw));
+    // About two workgroups per CU; split K only as far as every wave keeps >= 2 k-steps.
+    const long target = 2L * cu_count();
+    const long wgs = col_wgs * mgroups;
+    if (wgs < target) {
+        long splits = (target + wgs - 1) / wgs;
+        const long max_splits = nsteps / (2 * p.kw);
+        if (splits > max_splits) splits = max_splits;
+        if (splits > 1) p.splits = (int)splits;
+    }
+    // Tuning override for experiments: TERNIX_SKINNY_PLAN="tb,kw,splits".
+    if (const char* env = std::getenv("TERNIX_SKINNY_PLAN")) {
+        int etb = 0, ekw = 0, esp = 0;
+        if (std::sscanf(env, "%d,%d,%d", &etb, &ekw, &esp) == 3 && (etb == 1 || etb == 2) &&
+            (ekw == 1 || ekw == 2 || ekw == 4) && esp >= 1) {
+            p.tb = etb;
+            p.kw = ekw;
+            p.splits = esp;
+        }
+    }
+    // Each split's k-range must stay within the accumulator bound and, for the fast kernel, its
+    // activation slice within the LDS budget.
+    int max_sps = ternix_hip::kMaxKPerAccumulator / 64;
+    while (max_sps > 1 && ternix_hip::skinny_a_lds_bytes(M, max_sps) > ternix_hip::kSkinnyALdsMax) max_sps >>= 1;
+    if (p.splits > 65535) p.splits = 65535;
+    p.sps = (nsteps + p.splits - 1) / p.splits;
+    if (p.sps > max_sps) p.sps = max_sps;
+    if (p.sps < 1) p.sps = 1;
+    p.splits = (nsteps + p.sps - 1) / p.sps;
+    if (p.splits < 1) p.splits = 1;
+    return p;
+}
+
+hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int K, int N, hipStream_t st) {
+    const SkinnyPlan p = plan_skinny(M, K, N);
+    int32_t* partials = nullptr;
+    if (p.splits > 1) {
+        const size_t need = (size_t)p.splits * (size_t)M * (size_t)N * sizeof(int32_t);
+        if (need <= kWorkspaceMax) partials = static_cast<int32_t*>(workspace(st, need));
+    }
+    return ternix_hip::launch_skinny(dA, dB, dC, M, K, N, p.tb, p.kw, p.splits, p.sps, partials, st);
 }
 
 hipError_t run_gemm(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int K, int N, hipStream_t st) {

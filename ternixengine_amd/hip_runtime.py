@@ -53,6 +53,12 @@ def _load():
     _hip.hipGetErrorString.restype = ctypes.c_char_p
     _hip.hipDeviceGetAttribute.argtypes = [p(i), i, i]
     _hip.hipDeviceGetName.argtypes = [ctypes.c_char_p, i, i]
+    _hip.hipStreamBeginCapture.argtypes = [v, i]
+    _hip.hipStreamEndCapture.argtypes = [v, p(v)]
+    _hip.hipGraphInstantiate.argtypes = [p(v), v, v, v, sz]
+    _hip.hipGraphLaunch.argtypes = [v, v]
+    _hip.hipGraphExecDestroy.argtypes = [v]
+    _hip.hipGraphDestroy.argtypes = [v]
     return _hip
 
 
@@ -183,5 +189,34 @@ class Event:
         try:
             if self.handle.value:
                 _load().hipEventDestroy(self.handle)
+        except Exception:
+            pass
+
+
+class Graph:
+    """Captures the work a callable enqueues on `stream` into a hipGraph; replay with launch()."""
+
+    def __init__(self, stream, fn):
+        hip = _load()
+        self.graph = ctypes.c_void_p()
+        self.exec = ctypes.c_void_p()
+        check(hip.hipStreamBeginCapture(stream.handle, 0), "hipStreamBeginCapture")
+        try:
+            fn()
+        finally:
+            check(hip.hipStreamEndCapture(stream.handle, ctypes.byref(self.graph)), "hipStreamEndCapture")
+        check(hip.hipGraphInstantiate(ctypes.byref(self.exec), self.graph, None, None, 0), "hipGraphInstantiate")
+        self.stream = stream
+
+    def launch(self):
+        check(_load().hipGraphLaunch(self.exec, self.stream.handle), "hipGraphLaunch")
+
+    def __del__(self):
+        try:
+            hip = _load()
+            if self.exec.value:
+                hip.hipGraphExecDestroy(self.exec)
+            if self.graph.value:
+                hip.hipGraphDestroy(self.graph)
         except Exception:
             pass
