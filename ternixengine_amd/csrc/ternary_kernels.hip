@@ -299,13 +299,13 @@ struct SkinnyFastGeometry {
     static constexpr int SMEM_DW = (SK_WAVES * STAGE_DW > RED_DW) ? SK_WAVES * STAGE_DW : RED_DW;
 };
 
-template <int MT, int TB, int KW, bool LOW_M>
-__global__ __launch_bounds__(64 * SK_WAVES) void skinny_fast_kernel(SkinnyArgs args) {
+template <int MT, int TB, int KW, int PD, bool LOW_M>
+__global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu((TB == 1 && MT == 1) ? 2 : 1)))
+void skinny_fast_kernel(SkinnyArgs args) {
     using Geo = SkinnyFastGeometry<MT, TB, KW, LOW_M>;
     constexpr int G = Geo::G, TILES = Geo::TILES, ROW_DW = Geo::ROW_DW, STAGE_DW = Geo::STAGE_DW;
     constexpr int RPI = 16 / TB;        // rows per load instruction
     constexpr int NLD = 4 * TB;         // load instructions per k-step
-    constexpr int PD = 2;               // k-steps in flight per wave
     constexpr int BS = 64 * SK_WAVES;
     __shared__ __attribute__((aligned(16))) int32_t smem[Geo::SMEM_DW];
     // this workgroup's activation slice, row pitch a_pitch bytes (k-range + 16, so the 16 rows read by
@@ -740,18 +740,20 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const int32_t* __res
     }
 }
 
-template <int MT, int TB, int KW, bool LOW_M>
+template <int MT, int TB, int KW, int PD, bool LOW_M>
 hipError_t launch_fast_t(const SkinnyArgs& a, dim3 grid, hipStream_t st) {
-    hipLaunchKernelGGL((skinny_fast_kernel<MT, TB, KW, LOW_M>), grid, dim3(64 * SK_WAVES),
+    hipLaunchKernelGGL((skinny_fast_kernel<MT, TB, KW, PD, LOW_M>), grid, dim3(64 * SK_WAVES),
                        skinny_a_lds_bytes(a.M, a.steps_per_split), st, a);
     return hipGetLastError();
 }
 
+// PD (k-steps in flight per wave): 4 for 64-byte slabs, 2 for 128-byte slabs (register budget).
 template <int MT, int TB, bool LOW_M>
 hipError_t launch_fast_kw(const SkinnyArgs& a, int kw, dim3 grid, hipStream_t st) {
-    if (kw >= 4) return launch_fast_t<MT, TB, 4, LOW_M>(a, grid, st);
-    if (kw == 2) return launch_fast_t<MT, TB, 2, LOW_M>(a, grid, st);
-    return launch_fast_t<MT, TB, 1, LOW_M>(a, grid, st);
+    constexpr int PD = TB == 1 ? 4 : 2;
+    if (kw >= 4) return launch_fast_t<MT, TB, 4, PD, LOW_M>(a, grid, st);
+    if (kw == 2) return launch_fast_t<MT, TB, 2, PD, LOW_M>(a, grid, st);
+    return launch_fast_t<MT, TB, 1, PD, LOW_M>(a, grid, st);
 }
 
 template <int BM, int BNB>

@@ -102,17 +102,16 @@ SkinnyPlan plan_skinny(int M, int K, int N) {
     const int NB = N / 4;
     const int nsteps = (K + 63) / 64;
     const int mgroups = M <= 16 ? 1 : (M + 31) / 32;
-    SkinnyPlan p{M <= 16 ? 2 : 1, 2, 1, nsteps};
-    // Narrow outputs get 64-byte slabs so that more workgroups share the columns.
-    if (p.tb == 2 && NB < 64 * 2 * 2 * 16) p.tb = 1;
-    const long col_wgs = (NB + 64L * p.tb * (4 / p.kw) - 1) / (64L * p.tb * (4 / p.kw));
-    // About two workgroups per CU; split K only as far as every wave keeps >= 2 k-steps.
-    const long target = 2L * cu_count();
+    // Measured on MI355X (cfg2 / cfg5 M=1 shapes): 64-byte slabs, four slabs per workgroup (256
+    // contiguous bytes of every weight row per workgroup), and K split until there is about one
+    // workgroup per CU; the split's partial sums cost one small reduce launch.
+    SkinnyPlan p{1, 1, 1, nsteps};
+    const long col_wgs = (NB + 255) / 256;
     const long wgs = col_wgs * mgroups;
+    const long target = cu_count();
     if (wgs < target) {
         long splits = (target + wgs - 1) / wgs;
-        const long max_splits = nsteps / (2 * p.kw);
-        if (splits > max_splits) splits = max_splits;
+        if (splits > nsteps) splits = nsteps;
         if (splits > 1) p.splits = (int)splits;
     }
     // Tuning override for experiments: TERNIX_SKINNY_PLAN="tb,kw,splits".

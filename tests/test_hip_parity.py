@@ -232,3 +232,47 @@ def test_config_full_size_digest(digests, name):
         if name == "cfg5_worst":
             assert (got == 2097152).all()
         del got
+
+
+@pytest.mark.parametrize("capture", [False, True])
+def test_split_k_repeated_launches_exact(oracle, capture):
+    """Split-K partial sums go through the workspace and a reduce launch; every one of many
+    back-to-back launches must be bit-exact.  capture=True records the launches into a hipGraph on
+    a fresh stream (no workspace can be allocated while capturing, so the split-K falls back to
+    zero-fill + atomics) and replays it several times, checking each replay."""
+    s = hr.Stream()
+    if capture:
+        for name in ("cfg2_up", "cfg3_m4_up"):
+            case = configs.CASES[name]
+            a, wp = configs.gen_a(case), configs.gen_w_packed(case)
+            expect = oracle.mm("scalar_mt", a, wp, case.N)
+            da, db = hr.DeviceBuffer.from_array(a), hr.DeviceBuffer.from_array(wp)
+            dc = hr.DeviceBuffer(4 * case.M * case.N)
+            log(f"[graph] {name}")
+            g = hr.Graph(s, lambda: [tx.mul_mat_ternary(da.value, db.value, dc.value, case.M, case.K, case.N,
+                                                        stream=s.handle) for _ in range(3)])
+            for rep in range(5):
+                dc.upload(np.full(case.M * case.N, GARBAGE, np.int32))
+                g.launch()
+                s.synchronize()
+                assert (dc.download(np.int32, (case.M, case.N)) == expect).all(), (name, rep)
+        return
+    for name in ("cfg2_up", "cfg2_down", "cfg3_m4_up", "cfg3_m16_down"):
+        case = configs.CASES[name]
+        a, wp = configs.gen_a(case), configs.gen_w_packed(case)
+        expect = oracle.mm("scalar_mt", a, wp, case.N)
+        da, db = hr.DeviceBuffer.from_array(a), hr.DeviceBuffer.from_array(wp)
+        dc = hr.DeviceBuffer(4 * case.M * case.N)
+        log(f"[eager] {name}: 120 launches")
+        for it in range(120):
+            dc.upload(np.full(case.M * case.N, GARBAGE, np.int32))
+            st = tx.mul_mat_ternary(da.value, db.value, dc.value, case.M, case.K, case.N, stream=s.handle)
+            assert st == 0
+            s.synchronize()
+            got = dc.download(np.int32, (case.M, case.N))
+            assert (got == expect).all(), (name, it)
+        # back-to-back without host sync in between, then check the final one
+        for it in range(200):
+            assert tx.mul_mat_ternary(da.value, db.value, dc.value, case.M, case.K, case.N, stream=s.handle) == 0
+        s.synchronize()
+        assert (dc.download(np.int32, (case.M, case.N)) == expect).all(), name
