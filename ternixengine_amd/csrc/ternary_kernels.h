@@ -10,7 +10,7 @@ namespace ternix_hip {
 // scaled MFMA partial sums.  The worst per-row term is the out-of-domain code 10 in a field decoded
 // as a signed byte of -128 times an activation of -128 (+16384), so K rows stay exact while
 // 16384 * K < 2^31, i.e. K < 2^17.  (In-domain codes reach at most 8192 per row.)
-constexpr int kMaxKPerAccumulator = (1 << 17) - 64;
+constexpr int kMaxKPerAccumulator = (1 << 17) - 128;
 
 hipError_t launch_zero(int32_t* C, size_t n, hipStream_t st);
 // LDS bytes the skinny fast kernel uses for one workgroup's activation slice (the rows of one

@@ -30,10 +30,11 @@
 // extra R MFMA per m-tile would cost 25% of MFMA issue, uses the shift form.
 // Accumulator bound: each k-row adds at most 64*128 = 8192 in magnitude to a scaled accumulator
 // (16384 for the out-of-domain code 10, byte -128 times activation -128); the launch layer splits K
-// so that no accumulator sums more than kMaxKPerAccumulator = 2^17 - 64 k-rows.
+// so that no accumulator sums more than kMaxKPerAccumulator = 2^17 - 128 k-rows.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdlib.h>
 
 #include "ternary_kernels.h"
 
@@ -682,6 +683,222 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_kernel(const int8_t* __restri
 }
 
 // ------------------------------------------------------------------------------------------------
+// Pipelined LDS-tiled GEMM (prefill shapes; K % 128 == 0, NB % 64 == 0, aligned A and W).
+//
+// Workgroup = 8 waves (8/WGN along M x WGN along N) on a BM x 64-byte-column tile (BM x 256
+// outputs); wave tile BM*WGN/8 rows x 64/WGN byte-columns, i.e. m-tiles x 16-byte-column groups x
+// 4 fields of 16x16 MFMA outputs.  Each decoded weight fragment feeds all m-tiles of the wave.
+// K advances in stages of 128 (two MFMA k-steps), NS LDS stages deep.
+//   * A and W both go global -> LDS with direct 16-byte loads (global_load_lds_dwordx4): no
+//     registers held, so NS-1 stages are in flight while one is consumed.  Each wave instruction
+//     fills 64 consecutive 16-byte LDS slots; the bank-conflict swizzles are applied by choosing
+//     which global chunk each lane loads.
+//   * A rows (128 bytes per stage): chunk c of row r at position c ^ ((r/2) % 8), so the 16 rows of
+//     one ds_read_b128 fragment read fall on distinct banks.
+//   * W rows stay row-major (64 bytes = 4 chunks per stage row): chunk c of row r at position
+//     c ^ ((r/2) % 4).  B fragments are read with ds_read_b64_tr_b8, which transposes bytes within
+//     each 16-lane group: result lane j, byte i = byte (j % 8) of the 8 bytes addressed by lane
+//     2i + j/8.  Lane x addresses k-row (x/2) at byte offset 8*(x%2) of its 16-byte-column group,
+//     so lane q receives byte-column q of 8 consecutive k-rows; two reads give the 16 k-rows of its
+//     MFMA B operand, with no VALU transpose and no transposed stores.
+// Stage s: wait until stage s has landed (vmcnt with a static count: every thread issues the same
+// loads each stage, tails are clamped), raw s_barrier, issue stage s+NS-1, then the MFMAs of stage
+// s.  A buffer is refilled only after the barrier that follows its last read.
+// ------------------------------------------------------------------------------------------------
+
+#define TX_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 0xF) | (((n) >> 4) << 14) | (7 << 4) | (0xF << 8))
+#define TX_LGKMCNT0() __builtin_amdgcn_s_waitcnt((0xF) | (3 << 14) | (7 << 4) | (0 << 8))
+
+// 16 bytes per lane from global memory straight into LDS: lane l of the wave writes lds + 16*l.
+// (A plain device function, so the kernel templates that call it instantiate cleanly for the host.)
+__device__ __forceinline__ void lds_dma16(const void* gsrc, void* lds) {
+    __builtin_amdgcn_global_load_lds(gsrc, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+
+// Transposing 8-byte LDS read (see above).  Issued as inline assembly: the compiler then neither
+// waits for the LDS DMA in flight into other stage buffers before it (it cannot tell they do not
+// alias) nor for its own result -- the caller waits with lgkmcnt before using the value.
+__device__ __forceinline__ uint64_t lds_read_tr8(const void* lds) {
+    uint64_t v;
+    const uint32_t addr = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)lds;
+    __asm__ volatile("ds_read_b64_tr_b8 %0, %1" : "=v"(v) : "v"(addr));
+    return v;
+}
+
+constexpr int GF_THREADS = 512;
+constexpr int GF_BK = 128;
+constexpr int GF_BNB = 64;
+
+__device__ __forceinline__ int gf_swz_a(int r) { return (r >> 1) & 7; }
+__device__ __forceinline__ int gf_swz_w(int r) { return (r >> 1) & 3; }
+
+template <int BM, int WGN, int NS>
+__global__ __launch_bounds__(GF_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
+void gemm_fast_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ B, int32_t* __restrict__ C, int M,
+                      int K, int N, int tiles_n, int k_begin, int k_end, int accumulate, int vec_store) {
+    constexpr int WGM = 8 / WGN;             // waves along M
+    constexpr int WM = BM / WGM;             // rows per wave
+    constexpr int MT = WM / 16;              // m-tiles per wave
+    constexpr int GT = 4 / WGN;              // 16-byte-column groups per wave
+    constexpr int A_STAGE = BM * GF_BK;      // bytes
+    constexpr int W_STAGE = GF_BK * GF_BNB;  // bytes
+    constexpr int NA = A_STAGE / 16 / GF_THREADS;  // A loads per thread per stage
+    static_assert(W_STAGE / 16 == GF_THREADS, "one W load per thread per stage");
+    // Separate arrays per stage: the compiler tracks in-flight LDS DMA per array, so reads of one
+    // stage do not wait for loads into the others.
+    __shared__ __attribute__((aligned(16))) int8_t sA0[A_STAGE];
+    __shared__ __attribute__((aligned(16))) int8_t sA1[A_STAGE];
+    __shared__ __attribute__((aligned(16))) int8_t sA2[A_STAGE];
+    __shared__ __attribute__((aligned(16))) int8_t sA3[NS > 3 ? A_STAGE : 16];
+    __shared__ __attribute__((aligned(16))) uint8_t sW0[W_STAGE];
+    __shared__ __attribute__((aligned(16))) uint8_t sW1[W_STAGE];
+    __shared__ __attribute__((aligned(16))) uint8_t sW2[W_STAGE];
+    __shared__ __attribute__((aligned(16))) uint8_t sW3[NS > 3 ? W_STAGE : 16];
+    auto stage_a = [&](int i) -> int8_t* { return i == 0 ? sA0 : (i == 1 ? sA1 : (i == 2 ? sA2 : sA3)); };
+    auto stage_w = [&](int i) -> uint8_t* { return i == 0 ? sW0 : (i == 1 ? sW1 : (i == 2 ? sW2 : sW3)); };
+
+    const int NB = N >> 2;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WGN, wn = wave % WGN;
+    const int q = lane & 15, kb = lane >> 4;
+
+    // Block -> tile, XCD-aware: consecutive block ids go round-robin over the 8 XCDs; give each XCD
+    // a contiguous run of tiles (tiles of one row band share A in that XCD's L2).
+    const int nblocks = gridDim.x, bid = blockIdx.x;
+    int tile = bid;
+    if ((nblocks & 7) == 0) tile = (bid & 7) * (nblocks >> 3) + (bid >> 3);
+    const int tm = tile / tiles_n, tn = tile % tiles_n;
+    const int row0 = tm * BM;
+    const int bc0 = tn * GF_BNB;
+    const int nst = (k_end - k_begin) / GF_BK;  // stages
+
+    // Load geometry.  Instruction p of wave w fills 16-byte slots (p*8 + w)*64 + lane.  32-bit lane
+    // offsets (M*K and K*NB < 2^32, checked by the launcher) from wave-uniform bases.
+    uint32_t a_off[NA];
+#pragma unroll
+    for (int p = 0; p < NA; ++p) {
+        const int slot = (p * 8 + wave) * 64 + lane;
+        const int r = slot >> 3, pos = slot & 7;
+        const int grow = min(row0 + r, M - 1);  // rows past M load row M-1; never stored
+        a_off[p] = (uint32_t)grow * (uint32_t)K + (uint32_t)((pos ^ gf_swz_a(r)) * 16);
+    }
+    uint32_t w_off;
+    {
+        const int slot = wave * 64 + lane;
+        const int r = slot >> 2, pos = slot & 3;
+        w_off = (uint32_t)r * (uint32_t)NB + (uint32_t)(bc0 + (pos ^ gf_swz_w(r)) * 16);
+    }
+    auto issue = [&](int st, int buf) {
+        const int sc = min(st, nst - 1);  // clamped: keeps the per-stage load count static
+        const int8_t* abase = A + k_begin + (size_t)sc * GF_BK;
+        int8_t* adst = stage_a(buf);
+#pragma unroll
+        for (int p = 0; p < NA; ++p) lds_dma16(abase + a_off[p], adst + (p * 8 + wave) * 1024);
+        const uint8_t* wbase = B + (size_t)(k_begin + sc * GF_BK) * (size_t)NB;
+        lds_dma16(wbase + w_off, stage_w(buf) + wave * 1024);
+    };
+
+    v4i acc[MT][GT][4];
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int g = 0; g < GT; ++g)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[t][g][j] = v4i{0, 0, 0, 0};
+
+    auto compute = [&](int buf) {
+        const int8_t* a_st = stage_a(buf);
+        const uint8_t* w_st = stage_w(buf);
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            v4i a[MT];
+#pragma unroll
+            for (int t = 0; t < MT; ++t) {
+                const int r = wm * WM + t * 16 + q;
+                const int c = kk * 4 + kb;
+                a[t] = *reinterpret_cast<const v4i*>(a_st + r * GF_BK + 16 * (c ^ gf_swz_a(r)));
+            }
+#pragma unroll
+            for (int g = 0; g < GT; ++g) {
+                const int cg = wn * GT + g;  // 16-byte column group within the tile
+                const int r0 = kk * 64 + kb * 16 + (q >> 1);
+                const int r1 = r0 + 8;
+                uint64_t lo = lds_read_tr8(w_st + r0 * GF_BNB + 16 * (cg ^ gf_swz_w(r0)) + 8 * (q & 1));
+                uint64_t hi = lds_read_tr8(w_st + r1 * GF_BNB + 16 * (cg ^ gf_swz_w(r1)) + 8 * (q & 1));
+                // The wait names the results, so no use of them can be scheduled before it.
+                __asm__ volatile("s_waitcnt lgkmcnt(0)" : "+v"(lo), "+v"(hi));
+                const uint32_t x4[4] = {(uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32)};
+                v4i bfr[4];
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4) {
+                    const uint32_t x = x4[r4];
+                    bfr[0][r4] = (int)((x << 6) & 0xC0C0C0C0u);
+                    bfr[1][r4] = (int)((x << 4) & 0xC0C0C0C0u);
+                    bfr[2][r4] = (int)((x << 2) & 0xC0C0C0C0u);
+                    bfr[3][r4] = (int)(x & 0xC0C0C0C0u);
+                }
+#pragma unroll
+                for (int t = 0; t < MT; ++t)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) acc[t][g][j] = mfma_i8(a[t], bfr[j], acc[t][g][j]);
+            }
+        }
+    };
+
+    // Prologue: stages 0 .. NS-2 in flight.
+#pragma unroll
+    for (int p = 0; p < NS - 1; ++p) issue(p, p);
+
+    // h is always a literal at the call sites, so after inlining every buffer index is a constant;
+    // the main loop has no conditions, so the compiler counts the loads in flight exactly as the
+    // waits assume.
+    auto stage = [&](int st, int h) {
+        TX_VMCNT((NS - 2) * (NA + 1));  // stage st has landed (the NS-2 later stages may not)
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        issue(st + NS - 1, (h + NS - 1) % NS);
+        compute(h % NS);
+        TX_LGKMCNT0();  // this stage's LDS reads are done before the next barrier
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    int s = 0;
+    for (; s + NS <= nst; s += NS) {
+        stage(s + 0, 0);
+        stage(s + 1, 1);
+        stage(s + 2, 2);
+        if (NS > 3) stage(s + 3, 3);
+    }
+    if (s + 0 < nst) stage(s + 0, 0);
+    if (s + 1 < nst) stage(s + 1, 1);
+    if (NS > 3 && s + 2 < nst) stage(s + 2, 2);
+    TX_VMCNT(0);  // no LDS DMA may land after the workgroup exits
+
+    // Epilogue: element i of tile (t, g, j) is row 4*kb + i of m-tile t, column 4*(byte-col) + j.
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = row0 + wm * WM + t * 16 + 4 * kb + i;
+            if (row >= M) continue;
+#pragma unroll
+            for (int g = 0; g < GT; ++g) {
+                const int bcol = bc0 + (wn * GT + g) * 16 + q;
+                v4i v = {acc[t][g][0][i] >> 6, acc[t][g][1][i] >> 6, acc[t][g][2][i] >> 6, acc[t][g][3][i] >> 6};
+                int32_t* out = C + (size_t)row * (size_t)N + 4 * bcol;
+                if (vec_store) {
+                    if (accumulate) v += *reinterpret_cast<const v4i*>(out);
+                    *reinterpret_cast<v4i*>(out) = v;
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) out[j] = accumulate ? out[j] + v[j] : v[j];
+                }
+            }
+        }
+}
+
+// ------------------------------------------------------------------------------------------------
 // Naive kernel: one work-item per output, weights decoded per k from global memory with
 // w = (b & 1) - (b & 2) (the reference decode2, src/cuda_kernels.cu:40-54).
 // ------------------------------------------------------------------------------------------------
@@ -829,6 +1046,34 @@ hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, i
 hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int k_begin, int k_end,
                        int accumulate, hipStream_t st) {
     const int NB = N >> 2;
+    const char* force_generic = std::getenv("TERNIX_GEMM_GENERIC");
+    const bool fast = (K % GF_BK == 0) && ((k_end - k_begin) % GF_BK == 0) && (k_begin % GF_BK == 0) &&
+                      (NB % GF_BNB == 0) && ((uintptr_t)A % 16 == 0) && ((uintptr_t)B % 16 == 0) &&
+                      k_end > k_begin && (size_t)M * (size_t)K < ((size_t)1 << 32) &&
+                      (size_t)GF_BK * (size_t)NB < ((size_t)1 << 32) && !(force_generic && force_generic[0] == '1');
+    if (fast) {
+        const int vs = ((uintptr_t)C % 16) == 0;
+        const int tiles_n = NB / GF_BNB;
+        const char* bm_env = std::getenv("TERNIX_GEMM_BM");
+        const char* wgn_env = std::getenv("TERNIX_GEMM_WGN");
+        int bm = (M >= 2048 && (long)((M + 255) / 256) * tiles_n >= 256) ? 256 : 128;
+        if (bm_env) bm = std::atoi(bm_env) == 128 ? 128 : 256;
+        const int wgn = wgn_env && std::atoi(wgn_env) == 2 ? 2 : 4;
+        const dim3 grid(((M + bm - 1) / bm) * tiles_n);
+        if (bm == 256 && wgn == 4)
+            hipLaunchKernelGGL((gemm_fast_kernel<256, 4, 3>), grid, dim3(GF_THREADS), 0, st, A, B, C, M, K, N,
+                               tiles_n, k_begin, k_end, accumulate, vs);
+        else if (bm == 256)
+            hipLaunchKernelGGL((gemm_fast_kernel<256, 2, 3>), grid, dim3(GF_THREADS), 0, st, A, B, C, M, K, N,
+                               tiles_n, k_begin, k_end, accumulate, vs);
+        else if (wgn == 4)
+            hipLaunchKernelGGL((gemm_fast_kernel<128, 4, 4>), grid, dim3(GF_THREADS), 0, st, A, B, C, M, K, N,
+                               tiles_n, k_begin, k_end, accumulate, vs);
+        else
+            hipLaunchKernelGGL((gemm_fast_kernel<128, 2, 4>), grid, dim3(GF_THREADS), 0, st, A, B, C, M, K, N,
+                               tiles_n, k_begin, k_end, accumulate, vs);
+        return hipGetLastError();
+    }
     const bool aw = (NB % 4 == 0) && ((uintptr_t)B % 4 == 0);
     const bool aa = (K % 16 == 0) && ((uintptr_t)A % 16 == 0);
     return launch_gemm_t<128, 64>(A, B, C, M, K, N, aw, aa, k_begin, k_end, accumulate, st);
