@@ -732,7 +732,7 @@ constexpr int GF_BNB = 64;
 __device__ __forceinline__ int gf_swz_a(int r) { return (r >> 1) & 7; }
 __device__ __forceinline__ int gf_swz_w(int r) { return (r >> 1) & 3; }
 
-template <int BM, int WGN, int NS>
+template <int BM, int WGN, int NS, int BK>
 __global__ __launch_bounds__(GF_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
 void gemm_fast_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ B, int32_t* __restrict__ C, int M,
                       int K, int N, int tiles_n, int k_begin, int k_end, int accumulate, int vec_store) {
@@ -740,10 +740,12 @@ void gemm_fast_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ 
     constexpr int WM = BM / WGM;             // rows per wave
     constexpr int MT = WM / 16;              // m-tiles per wave
     constexpr int GT = 4 / WGN;              // 16-byte-column groups per wave
-    constexpr int A_STAGE = BM * GF_BK;      // bytes
-    constexpr int W_STAGE = GF_BK * GF_BNB;  // bytes
+    constexpr int KS = BK / 64;              // MFMA k-steps per stage
+    constexpr int CPR = BK / 16;             // 16-byte A chunks per row per stage
+    constexpr int A_STAGE = BM * BK;         // bytes
+    constexpr int W_STAGE = BK * GF_BNB;     // bytes
     constexpr int NA = A_STAGE / 16 / GF_THREADS;  // A loads per thread per stage
-    static_assert(W_STAGE / 16 == GF_THREADS, "one W load per thread per stage");
+    constexpr int NW = W_STAGE / 16 / GF_THREADS;  // W loads per thread per stage
     // Separate arrays per stage: the compiler tracks in-flight LDS DMA per array, so reads of one
     // stage do not wait for loads into the others.
     __shared__ __attribute__((aligned(16))) int8_t sA0[A_STAGE];
@@ -772,7 +774,7 @@ void gemm_fast_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ 
     const int tm = tile / tiles_n, tn = tile % tiles_n;
     const int row0 = tm * BM;
     const int bc0 = tn * GF_BNB;
-    const int nst = (k_end - k_begin) / GF_BK;  // stages
+    const int nst = (k_end - k_begin) / BK;  // stages
 
     // Load geometry.  Instruction p of wave w fills 16-byte slots (p*8 + w)*64 + lane.  32-bit lane
     // offsets (M*K and K*NB < 2^32, checked by the launcher) from wave-uniform bases.
@@ -780,24 +782,27 @@ void gemm_fast_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ 
 #pragma unroll
     for (int p = 0; p < NA; ++p) {
         const int slot = (p * 8 + wave) * 64 + lane;
-        const int r = slot >> 3, pos = slot & 7;
+        const int r = slot / CPR, pos = slot % CPR;
         const int grow = min(row0 + r, M - 1);  // rows past M load row M-1; never stored
-        a_off[p] = (uint32_t)grow * (uint32_t)K + (uint32_t)((pos ^ gf_swz_a(r)) * 16);
+        a_off[p] = (uint32_t)grow * (uint32_t)K + (uint32_t)(((pos & ~7) | ((pos & 7) ^ gf_swz_a(r))) * 16);
     }
-    uint32_t w_off;
-    {
-        const int slot = wave * 64 + lane;
+    uint32_t w_off[NW];
+#pragma unroll
+    for (int p = 0; p < NW; ++p) {
+        const int slot = (p * 8 + wave) * 64 + lane;
         const int r = slot >> 2, pos = slot & 3;
-        w_off = (uint32_t)r * (uint32_t)NB + (uint32_t)(bc0 + (pos ^ gf_swz_w(r)) * 16);
+        w_off[p] = (uint32_t)r * (uint32_t)NB + (uint32_t)(bc0 + (pos ^ gf_swz_w(r)) * 16);
     }
     auto issue = [&](int st, int buf) {
         const int sc = min(st, nst - 1);  // clamped: keeps the per-stage load count static
-        const int8_t* abase = A + k_begin + (size_t)sc * GF_BK;
+        const int8_t* abase = A + k_begin + (size_t)sc * BK;
         int8_t* adst = stage_a(buf);
 #pragma unroll
         for (int p = 0; p < NA; ++p) lds_dma16(abase + a_off[p], adst + (p * 8 + wave) * 1024);
-        const uint8_t* wbase = B + (size_t)(k_begin + sc * GF_BK) * (size_t)NB;
-        lds_dma16(wbase + w_off, stage_w(buf) + wave * 1024);
+        const uint8_t* wbase = B + (size_t)(k_begin + sc * BK) * (size_t)NB;
+        uint8_t* wdst = stage_w(buf);
+#pragma unroll
+        for (int p = 0; p < NW; ++p) lds_dma16(wbase + w_off[p], wdst + (p * 8 + wave) * 1024);
     };
 
     v4i acc[MT][GT][4];
@@ -812,13 +817,13 @@ void gemm_fast_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ 
         const int8_t* a_st = stage_a(buf);
         const uint8_t* w_st = stage_w(buf);
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
+        for (int kk = 0; kk < KS; ++kk) {
             v4i a[MT];
 #pragma unroll
             for (int t = 0; t < MT; ++t) {
                 const int r = wm * WM + t * 16 + q;
-                const int c = kk * 4 + kb;
-                a[t] = *reinterpret_cast<const v4i*>(a_st + r * GF_BK + 16 * (c ^ gf_swz_a(r)));
+                const int c = kk * 4 + kb;  // chunk; the swizzle permutes within groups of 8
+                a[t] = *reinterpret_cast<const v4i*>(a_st + r * BK + 16 * ((c & ~7) | ((c & 7) ^ gf_swz_a(r))));
             }
 #pragma unroll
             for (int g = 0; g < GT; ++g) {
@@ -855,7 +860,7 @@ void gemm_fast_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ 
     // the main loop has no conditions, so the compiler counts the loads in flight exactly as the
     // waits assume.
     auto stage = [&](int st, int h) {
-        TX_VMCNT((NS - 2) * (NA + 1));  // stage st has landed (the NS-2 later stages may not)
+        TX_VMCNT((NS - 2) * (NA + NW));  // stage st has landed (the NS-2 later stages may not)
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
         issue(st + NS - 1, (h + NS - 1) % NS);
@@ -1056,22 +1061,30 @@ hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int
         const int tiles_n = NB / GF_BNB;
         const char* bm_env = std::getenv("TERNIX_GEMM_BM");
         const char* wgn_env = std::getenv("TERNIX_GEMM_WGN");
-        int bm = (M >= 2048 && (long)((M + 255) / 256) * tiles_n >= 256) ? 256 : 128;
+        const char* bk_env = std::getenv("TERNIX_GEMM_BK");
+        // Measured on MI355X (cfg4 shapes): 256-row tiles only when they still give >= 1.5 tiles per
+        // CU, else 128-row tiles; 8 waves as 2 (M) x 4 (N); 128-deep stages.
+        int cus = 256;
+        {
+            int dev = 0;
+            if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+        }
+        int bm = ((long)((M + 255) / 256) * tiles_n * 2 >= 3L * cus) ? 256 : 128;
         if (bm_env) bm = std::atoi(bm_env) == 128 ? 128 : 256;
         const int wgn = wgn_env && std::atoi(wgn_env) == 2 ? 2 : 4;
+        int bk = 128;
+        if (bk_env && std::atoi(bk_env) == 256 && bm == 128 && (k_end - k_begin) % 256 == 0) bk = 256;
         const dim3 grid(((M + bm - 1) / bm) * tiles_n);
-        if (bm == 256 && wgn == 4)
-            hipLaunchKernelGGL((gemm_fast_kernel<256, 4, 3>), grid, dim3(GF_THREADS), 0, st, A, B, C, M, K, N,
-                               tiles_n, k_begin, k_end, accumulate, vs);
-        else if (bm == 256)
-            hipLaunchKernelGGL((gemm_fast_kernel<256, 2, 3>), grid, dim3(GF_THREADS), 0, st, A, B, C, M, K, N,
-                               tiles_n, k_begin, k_end, accumulate, vs);
-        else if (wgn == 4)
-            hipLaunchKernelGGL((gemm_fast_kernel<128, 4, 4>), grid, dim3(GF_THREADS), 0, st, A, B, C, M, K, N,
-                               tiles_n, k_begin, k_end, accumulate, vs);
-        else
-            hipLaunchKernelGGL((gemm_fast_kernel<128, 2, 4>), grid, dim3(GF_THREADS), 0, st, A, B, C, M, K, N,
-                               tiles_n, k_begin, k_end, accumulate, vs);
+#define TX_GF_LAUNCH(BM_, WGN_, NS_, BK_)                                                                         \
+    hipLaunchKernelGGL((gemm_fast_kernel<BM_, WGN_, NS_, BK_>), grid, dim3(GF_THREADS), 0, st, A, B, C, M, K, N, \
+                       tiles_n, k_begin, k_end, accumulate, vs)
+        if (bm == 256 && wgn == 4) TX_GF_LAUNCH(256, 4, 3, 128);
+        else if (bm == 256) TX_GF_LAUNCH(256, 2, 3, 128);
+        else if (bk == 256 && wgn == 4) TX_GF_LAUNCH(128, 4, 3, 256);
+        else if (bk == 256) TX_GF_LAUNCH(128, 2, 3, 256);
+        else if (wgn == 4) TX_GF_LAUNCH(128, 4, 4, 128);
+        else TX_GF_LAUNCH(128, 2, 4, 128);
+#undef TX_GF_LAUNCH
         return hipGetLastError();
     }
     const bool aw = (NB % 4 == 0) && ((uintptr_t)B % 4 == 0);
