@@ -41,7 +41,19 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", choices=["all", "gemv", "gemm", "bigm1"], default="all")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="first run 4 device-to-device copies of 256 MiB (the runtime's copy kernel), the "
+                         "known-size reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
     return ap.parse_args()
+
+
+def calibrate_copy():
+    from ternixengine_amd import hip_runtime as hr
+    n = 256 << 20
+    src, dst = hr.DeviceBuffer(n), hr.DeviceBuffer(n)
+    for _ in range(4):
+        hr.check(hr._load().hipMemcpy(dst.ptr, src.ptr, n, hr.D2D), "hipMemcpy D2D")
+    hr.synchronize()
 
 
 class Problem:
@@ -206,6 +218,8 @@ def main():
     from ternixengine_amd import hip_runtime as hr
     lib = tx._load()
     stream = hr.Stream()
+    if args.calibrate_copy:
+        calibrate_copy()
     res = {}
     if args.only in ("all", "gemv"):
         res["gemv"] = bench_gemv_pair(args, stream, lib)

@@ -18,10 +18,17 @@
  * (include/ternix/cuda_kernels.cuh:8-21, src/cuda_kernels.cu:126-156).
  *
  * Device-pointer entry points are asynchronous on `stream` (a hipStream_t, or
- * NULL for the default stream).  The caller owns all buffers; C is fully
+ * NULL for the default stream).  The caller owns A, B and C; C is fully
  * overwritten (never accumulated into).  Shapes are int64; N must be a
- * multiple of 4; M, K or N may be 0.  No device-pointer entry point allocates
- * memory.
+ * multiple of 4; M, K or N may be 0.
+ * Workspace: the skinny path (small M) splits K over workgroups; the partial
+ * sums go through a device workspace that the library allocates per (device,
+ * stream) the first time a shape needs it (at most 256 MiB, kept until the
+ * process ends) and that a second, small kernel adds into C.  No allocation
+ * happens while the stream is being captured into a hipGraph: a call that
+ * would need one then zeroes C and accumulates the partial sums with int32
+ * atomics instead (exact, order-independent).  Warm the shapes up eagerly
+ * before capturing to keep the faster path in the graph.
  * Calls are thread-safe; calls that share an output buffer race as any two
  * kernels writing one buffer do.
  *
@@ -47,9 +54,8 @@ int ternix_hip_mul_mat_ternary(const int8_t* dA, const uint8_t* dB, int32_t* dC,
                                int64_t M, int64_t K, int64_t N, void* stream);
 
 /* Forced skinny (decode) path: M <= 32 (returns hipErrorInvalidValue above).
- * Weights decoded in registers, int8 MFMA, split-K over the grid.  When K is
- * split across workgroups the kernel zeroes C and accumulates with int32
- * atomics, which are exact and order-independent.
+ * Weights decoded in registers, int8 MFMA, split-K over the grid (see
+ * Workspace above).
  * New in this library; its reference counterpart is the M=1 use of
  * mul_mat_ternary_cuda_naive (reference src/cuda_kernels.cu:126-132). */
 int ternix_hip_mul_mat_ternary_gemv(const int8_t* dA, const uint8_t* dB, int32_t* dC,

@@ -62,6 +62,15 @@ __device__ __forceinline__ void transpose4x4(uint32_t r0, uint32_t r1, uint32_t 
     c3 = __builtin_amdgcn_perm(t23h, t01h, 0x07060302u);
 }
 
+// Block ids are dealt round-robin over the 8 XCDs (XCD = id % 8).  xcd_linear(id, total) renumbers
+// them so that each XCD's blocks get consecutive numbers: XCD x holds ids x, x+8, ... and receives
+// the numbers [prefix(x), prefix(x) + count(x)).  A bijection on [0, total) for any total; it only
+// steers which blocks share an XCD's L2 and does not affect results.
+__device__ __forceinline__ int xcd_linear(int id, int total) {
+    const int q = total >> 3, r = total & 7, x = id & 7;
+    return x * q + min(x, r) + (id >> 3);
+}
+
 // ------------------------------------------------------------------------------------------------
 // Loads with optional bounds / alignment handling.
 // ------------------------------------------------------------------------------------------------
@@ -201,7 +210,8 @@ __device__ __forceinline__ void skinny_mfma_block(const uint32_t (&raw)[16], con
 // bcol(g) = byte-column of lane value g = tile_bc + 64*(g/4) + 4q + g%4.
 template <int MT, int G, int KW, int TILES, bool LOW_M>
 __device__ __forceinline__ void skinny_epilogue(const SkinnyArgs& args, int32_t* red, v4i (&acc)[MT][G][4],
-                                                const v4i (&accR)[MT], int tw, int kw, int tile_bc, int m0) {
+                                                const v4i (&accR)[MT], int tw, int kw, int tile_bc, int m0,
+                                                int split) {
     constexpr int NV = MT * 16 * G;
     constexpr int XL = LOW_M ? 16 : 64;
     const int lane = threadIdx.x & 63;
@@ -263,7 +273,7 @@ __device__ __forceinline__ void skinny_epilogue(const SkinnyArgs& args, int32_t*
     }
     if (kw != 0 || !xlane) return;
 
-    int32_t* out_base = args.mode == SK_PARTIAL ? args.P + (size_t)blockIdx.y * (size_t)M * (size_t)N : args.C;
+    int32_t* out_base = args.mode == SK_PARTIAL ? args.P + (size_t)split * (size_t)M * (size_t)N : args.C;
     const bool vec = args.mode == SK_PARTIAL || args.vec_store;
 #pragma unroll
     for (int t = 0; t < MT; ++t)
@@ -320,10 +330,19 @@ void skinny_fast_kernel(SkinnyArgs args) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (scalar)
     const int tw = wave % TILES, kw = wave / TILES;
     const int q = lane & 15, kb = lane >> 4;
-    const int tile_bc = (blockIdx.x * TILES + tw) * 64 * TB;
+    // (column workgroup, split) from the block id, XCD-aware: block ids are dealt round-robin over
+    // the 8 XCDs, so renumber them such that the workgroups of one split that sit next to each other
+    // along N run on the same XCD and share the cache lines that straddle their column ranges.
+    int cx, sy;
+    {
+        const int lin = xcd_linear(blockIdx.x + gridDim.x * blockIdx.y, gridDim.x * gridDim.y);
+        cx = lin % gridDim.x;
+        sy = lin / gridDim.x;
+    }
+    const int tile_bc = (cx * TILES + tw) * 64 * TB;
     const int m0 = blockIdx.z * (16 * MT);
     const int nsteps = K >> 6;
-    const int s_begin = blockIdx.y * args.steps_per_split;
+    const int s_begin = sy * args.steps_per_split;
     const int s_stop = min(nsteps, s_begin + args.steps_per_split);
     const int s_end = tile_bc < NB ? s_stop : s_begin;  // a slab past the last column loads nothing
     const int s0 = s_begin + kw;
@@ -441,7 +460,7 @@ void skinny_fast_kernel(SkinnyArgs args) {
             }
         }
     }
-    skinny_epilogue<MT, G, KW, TILES, LOW_M>(args, smem, acc, accR, tw, kw, tile_bc, m0);
+    skinny_epilogue<MT, G, KW, TILES, LOW_M>(args, smem, acc, accR, tw, kw, tile_bc, m0, sy);
 }
 
 // Four packed bytes at (row, bc), 0 outside the K x NB matrix; clamped indices, masked value.
@@ -507,7 +526,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) void skinny_generic_kernel(SkinnyArg
         for (int t = 0; t < MT; ++t) accR[t] = mfma_i8(a[t], ones, accR[t]);
         skinny_mfma_block<MT, G>(raw, a, 0, acc);
     }
-    skinny_epilogue<MT, G, KW, TILES, LOW_M>(args, smem, acc, accR, tw, kw, tile_bc, m0);
+    skinny_epilogue<MT, G, KW, TILES, LOW_M>(args, smem, acc, accR, tw, kw, tile_bc, m0, blockIdx.y);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -766,12 +785,21 @@ void gemm_fast_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ 
     const int wm = wave / WGN, wn = wave % WGN;
     const int q = lane & 15, kb = lane >> 4;
 
-    // Block -> tile, XCD-aware: consecutive block ids go round-robin over the 8 XCDs; give each XCD
-    // a contiguous run of tiles (tiles of one row band share A in that XCD's L2).
-    const int nblocks = gridDim.x, bid = blockIdx.x;
-    int tile = bid;
-    if ((nblocks & 7) == 0) tile = (bid & 7) * (nblocks >> 3) + (bid >> 3);
-    const int tm = tile / tiles_n, tn = tile % tiles_n;
+    // Block -> tile, XCD-aware: each XCD gets a contiguous run of tile numbers (xcd_linear).
+    // Grouped order: consecutive tile numbers walk 4 row bands before moving to the next column
+    // band, so each XCD's contiguous run of tiles is a ~4 x 8 block (A read by ~2 XCDs and W by
+    // ~4, instead of W by all 8).
+    int tm, tn;
+    {
+        const int t = xcd_linear(blockIdx.x, gridDim.x);
+        const int tiles_m = gridDim.x / tiles_n;
+        constexpr int GM = 4;
+        const int first_m = (t / (GM * tiles_n)) * GM;
+        const int gm = min(tiles_m - first_m, GM);
+        const int local = t % (GM * tiles_n);
+        tm = first_m + local % gm;
+        tn = local / gm;
+    }
     const int row0 = tm * BM;
     const int bc0 = tn * GF_BNB;
     const int nst = (k_end - k_begin) / BK;  // stages
