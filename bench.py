@@ -47,6 +47,17 @@ def parse():
     return ap.parse_args()
 
 
+def profiled_traffic():
+    """HBM bytes per GEMV call from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary, or None."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic_fetch_write.md")
+    try:
+        text = open(path).read()
+        block = text.split("```json", 1)[1].split("```", 1)[0]
+        return int(json.loads(block)["gemv_cfg2_traffic_bytes_per_call"])
+    except (OSError, IndexError, KeyError, ValueError):
+        return None
+
+
 def calibrate_copy():
     from ternixengine_amd import hip_runtime as hr
     n = 256 << 20
@@ -249,8 +260,9 @@ def main():
     }
     if g:
         line["roofline"] = {"bound": "hbm", "achieved": round(g["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                            "frac": round(g["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
-                            "kernel": "skinny_kernel (ternix_hip_mul_mat_ternary, M=1)",
+                            "frac": round(g["gbs"] / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(),
+                            "algorithmic_bytes": g["bytes_per_step"] // 2,
+                            "kernel": "skinny_fast_kernel + splitk_reduce_kernel (one ternix_hip_mul_mat_ternary call, M=1)",
                             "avg_launch_us": round(g["launch_us"], 3)}
         line["gemv_detail"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in g.items()}
     if "bigm1" in res:
