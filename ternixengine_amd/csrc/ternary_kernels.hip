@@ -463,6 +463,78 @@ void skinny_fast_kernel(SkinnyArgs args) {
     skinny_epilogue<MT, G, KW, TILES, LOW_M>(args, smem, acc, accR, tw, kw, tile_bc, m0, sy);
 }
 
+// Short-range skinny kernel: the fast kernel's column geometry (4 waves, one 64-byte slab each) for
+// workgroups whose k-range is at most SPS k-steps, the decode case where K is split over the whole
+// chip.  Every weight and activation load of the workgroup is issued up front (no ring, no LDS copy
+// of the activations, no barrier), so the code a workgroup runs is short and its loads all overlap.
+template <int SPS, bool LOW_M>
+__global__ __launch_bounds__(64 * SK_WAVES) void skinny_short_kernel(SkinnyArgs args) {
+    using Geo = SkinnyFastGeometry<1, 1, 1, LOW_M>;
+    constexpr int ROW_DW = Geo::ROW_DW, STAGE_DW = Geo::STAGE_DW;
+    __shared__ __attribute__((aligned(16))) int32_t smem[Geo::SMEM_DW];
+    const int8_t* __restrict__ A = args.A;
+    const uint8_t* __restrict__ B = args.B;
+    const int M = args.M, K = args.K, NB = args.N >> 2;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int q = lane & 15, kb = lane >> 4;
+    int cx, sy;
+    {
+        const int lin = xcd_linear(blockIdx.x + gridDim.x * blockIdx.y, gridDim.x * gridDim.y);
+        cx = lin % gridDim.x;
+        sy = lin / gridDim.x;
+    }
+    const int tile_bc = (cx * SK_WAVES + wave) * 64;
+    const int m0 = blockIdx.z * 16;
+    const int s_begin = sy * args.steps_per_split;
+    const int cnt = tile_bc < NB ? min(min(SPS, args.steps_per_split), (K >> 6) - s_begin) : 0;  // wave-uniform
+    const int s_last = s_begin + max(cnt, 1) - 1;
+
+    // Weights: lane (rr, cc) reads 16 bytes at column 16cc of rows 16h + rr of each step; addresses
+    // clamped into the matrix, so every load is unconditional.
+    const int rr = lane >> 2, cc = lane & 3;
+    const uint8_t* wbase = B + (size_t)rr * (size_t)NB + (size_t)(min(tile_bc, NB - 64) + cc * 16);
+    v4i g4[SPS][4];
+#pragma unroll
+    for (int u = 0; u < SPS; ++u) {
+        const uint8_t* sb = wbase + (size_t)min(s_begin + u, s_last) * 64 * (size_t)NB;
+#pragma unroll
+        for (int h = 0; h < 4; ++h) g4[u][h] = *reinterpret_cast<const v4i*>(sb + (size_t)(16 * h) * (size_t)NB);
+    }
+    // Activations: row m0 + q (clamped; rows >= M are never stored), bytes 16kb.. of each step.
+    const int8_t* abase = A + (size_t)min(m0 + q, M - 1) * (size_t)K + kb * 16;
+    v4i a[SPS][1];
+#pragma unroll
+    for (int u = 0; u < SPS; ++u) a[u][0] = *reinterpret_cast<const v4i*>(abase + (size_t)min(s_begin + u, s_last) * 64);
+
+    v4i acc[1][4][4];
+    v4i accR[1] = {v4i{0, 0, 0, 0}};
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[0][g][j] = v4i{0, 0, 0, 0};
+    const v4i ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
+    int32_t* stage = smem + wave * STAGE_DW;
+#pragma unroll
+    for (int u = 0; u < SPS; ++u) {
+        if (u < cnt) {
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+                const int R = 16 * h + rr;
+                *reinterpret_cast<v4i*>(stage + R * ROW_DW + (R >> 4) * 16 + cc * 4) = g4[u][h];
+            }
+            __asm__ volatile("" ::: "memory");  // LDS is in order within a wave; keep the compiler so
+            uint32_t raw[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) raw[r] = (uint32_t)stage[(16 * kb + r) * ROW_DW + 16 * kb + q];
+            __asm__ volatile("" ::: "memory");
+            accR[0] = mfma_i8(a[u][0], ones, accR[0]);
+            skinny_mfma_block<1, 4>(raw, a[u], 0, acc);
+        }
+    }
+    skinny_epilogue<1, 4, 1, SK_WAVES, LOW_M>(args, smem, acc, accR, wave, 0, tile_bc, m0, sy);
+}
+
 // Four packed bytes at (row, bc), 0 outside the K x NB matrix; clamped indices, masked value.
 __device__ __forceinline__ uint32_t ld_w4(const uint8_t* __restrict__ B, int row, int bc, int K, int NB, bool aligned) {
     const int rc = min(row, K - 1);
@@ -1055,7 +1127,25 @@ hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, i
     const int mt = M <= 16 ? 1 : 2;
     const int mgroups = (M + 16 * mt - 1) / (16 * mt);
     hipError_t e;
-    if (skinny_fast_ok(A, B, M, K, N, steps_per_split)) {
+    static const bool no_short = [] {
+        const char* e = std::getenv("TERNIX_SKINNY_SHORT");
+        return e && e[0] == '0';
+    }();
+    if (mt == 1 && tb == 1 && kw == 1 && steps_per_split <= 4 && !no_short &&
+        skinny_fast_ok(A, B, M, K, N, steps_per_split)) {
+        const dim3 grid((NB + 255) / 256, splits, mgroups);
+        const int sps = steps_per_split;
+        if (M <= 4) {
+            if (sps == 1) hipLaunchKernelGGL((skinny_short_kernel<1, true>), grid, dim3(64 * SK_WAVES), 0, st, a);
+            else if (sps == 2) hipLaunchKernelGGL((skinny_short_kernel<2, true>), grid, dim3(64 * SK_WAVES), 0, st, a);
+            else hipLaunchKernelGGL((skinny_short_kernel<4, true>), grid, dim3(64 * SK_WAVES), 0, st, a);
+        } else {
+            if (sps == 1) hipLaunchKernelGGL((skinny_short_kernel<1, false>), grid, dim3(64 * SK_WAVES), 0, st, a);
+            else if (sps == 2) hipLaunchKernelGGL((skinny_short_kernel<2, false>), grid, dim3(64 * SK_WAVES), 0, st, a);
+            else hipLaunchKernelGGL((skinny_short_kernel<4, false>), grid, dim3(64 * SK_WAVES), 0, st, a);
+        }
+        e = hipGetLastError();
+    } else if (skinny_fast_ok(A, B, M, K, N, steps_per_split)) {
         if (mt == 2) tb = 1;
         const int slab = 64 * tb * (SK_WAVES / (kw >= 4 ? 4 : (kw == 2 ? 2 : 1)));  // bytes per workgroup
         const dim3 grid((NB + slab - 1) / slab, splits, mgroups);

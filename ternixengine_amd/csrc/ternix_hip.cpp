@@ -102,15 +102,19 @@ SkinnyPlan plan_skinny(int M, int K, int N) {
     const int NB = N / 4;
     const int nsteps = (K + 63) / 64;
     const int mgroups = M <= 16 ? 1 : (M + 31) / 32;
-    // Measured on MI355X (cfg2 / cfg5 M=1 shapes): 64-byte slabs, four slabs per workgroup (256
-    // contiguous bytes of every weight row per workgroup), and K split until there is about one
-    // workgroup per CU; the split's partial sums cost one small reduce launch.
+    // Measured on MI355X (cfg1-3, cfg5 M=1 shapes): 64-byte slabs, four slabs per workgroup (256
+    // contiguous bytes of every weight row per workgroup), and K split into as many ranges as keep
+    // the grid within one workgroup per CU (a CU holding two of them finishes last).  With several
+    // rows the partial sums ([splits][M][N] int32, written and read back once) are capped at about
+    // the weight bytes (K*N/4): splits <= K / (32 M).
     SkinnyPlan p{1, 1, 1, nsteps};
     const long col_wgs = (NB + 255) / 256;
     const long wgs = col_wgs * mgroups;
     const long target = cu_count();
     if (wgs < target) {
-        long splits = (target + wgs - 1) / wgs;
+        long splits = target / wgs;
+        const long traffic_cap = std::max(1L, (long)K / (32L * M));
+        if (splits > traffic_cap) splits = traffic_cap;
         if (splits > nsteps) splits = nsteps;
         if (splits > 1) p.splits = (int)splits;
     }
