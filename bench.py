@@ -37,7 +37,9 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--gemm-steps", type=int, default=20)
+    ap.add_argument("--gemm-steps", type=int, default=100)
+    ap.add_argument("--prewarm-s", type=float, default=0.5,
+                    help="untimed sustained load before each GPU measurement (clock ramp)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", choices=["all", "gemv", "gemm", "bigm1"], default="all")
@@ -108,6 +110,18 @@ def time_launches(launches, steps, warmup, stream, graph=True):
     return e0.elapsed_ms(e1)
 
 
+def prewarm(launches, seconds, stream):
+    """Untimed launches for about `seconds` of wall time before a measurement: MI355X raises its
+    clocks only under sustained load, and a short timed region right after idle measures the ramp."""
+    t_end = time.perf_counter() + seconds
+    i = 0
+    while time.perf_counter() < t_end:
+        for _ in range(20):
+            launches(i)
+            i += 1
+        stream.synchronize()
+
+
 def launch(fn, prob, widx, stream):
     c = prob.case
     st = fn(prob.dA.value, prob.dW[widx].value, prob.dC.value, c.M, c.K, c.N, stream.handle)
@@ -136,6 +150,7 @@ def bench_gemv_pair(args, stream, lib):
         launch(fn, pu, i % copies, stream)
         launch(fn, pd, i % copies, stream)
 
+    prewarm(step, args.prewarm_s, stream)
     ms = time_launches(step, args.steps, args.warmup, stream)
     ok = verify(pu) and verify(pd)
     bytes_step = up.bytes_algorithmic + down.bytes_algorithmic
@@ -165,6 +180,7 @@ def bench_big_m1(args, stream, lib):
     p = Problem(case, copies)
     fn = lib.ternix_hip_mul_mat_ternary
     steps = max(10, args.steps // 4)
+    prewarm(lambda i: launch(fn, p, i % copies, stream), args.prewarm_s, stream)
     ms = time_launches(lambda i: launch(fn, p, i % copies, stream), steps, max(2, args.warmup // 4), stream)
     return {"shape": [case.M, case.K, case.N], "launch_us": ms / steps * 1e3,
             "gbs": case.bytes_algorithmic / (ms / steps * 1e-3) / 1e9, "verified": verify(p), "pool_copies": copies}
@@ -177,6 +193,7 @@ def bench_gemm(args, stream, lib):
     for name in ("cfg4_4096x4096", "cfg4_4096x14336", "cfg4_14336x4096"):
         case = configs.CASES[name]
         p = Problem(case, 1)
+        prewarm(lambda i: launch(fn, p, 0, stream), args.prewarm_s, stream)
         ms = time_launches(lambda i: launch(fn, p, 0, stream), args.gemm_steps, max(2, args.gemm_steps // 4), stream)
         per = ms / args.gemm_steps
         tops = case.ops / (per * 1e-3) / 1e12

@@ -764,7 +764,7 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_kernel(const int8_t* __restri
                 int32_t* out = C + (size_t)row * (size_t)N + 4 * bcol;
                 if (vec_store) {
                     if (accumulate) v += *reinterpret_cast<const v4i*>(out);
-                    *reinterpret_cast<v4i*>(out) = v;
+                    __builtin_nontemporal_store(v, reinterpret_cast<v4i*>(out));  // streamed, not re-read
                 } else {
 #pragma unroll
                     for (int j = 0; j < 4; ++j) out[j] = accumulate ? out[j] + v[j] : v[j];
@@ -787,7 +787,10 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_kernel(const int8_t* __restri
 //   * A rows (128 bytes per stage): chunk c of row r at position c ^ ((r/2) % 8), so the 16 rows of
 //     one ds_read_b128 fragment read fall on distinct banks.
 //   * W rows stay row-major (64 bytes = 4 chunks per stage row): chunk c of row r at position
-//     c ^ ((r/2) % 4).  B fragments are read with ds_read_b64_tr_b8, which transposes bytes within
+//     c ^ ((r/2) % 4) ^ ((r/16) % 2).  The first term spreads the 8 rows one 16-lane group reads over
+//     32 banks; the second gives the group of the next 16 rows (the other half of the wave's k-block,
+//     read in the same pass) the other 32 banks (measured: no LDS bank conflicts left).
+//     B fragments are read with ds_read_b64_tr_b8, which transposes bytes within
 //     each 16-lane group: result lane j, byte i = byte (j % 8) of the 8 bytes addressed by lane
 //     2i + j/8.  Lane x addresses k-row (x/2) at byte offset 8*(x%2) of its 16-byte-column group,
 //     so lane q receives byte-column q of 8 consecutive k-rows; two reads give the 16 k-rows of its
@@ -821,7 +824,7 @@ constexpr int GF_BK = 128;
 constexpr int GF_BNB = 64;
 
 __device__ __forceinline__ int gf_swz_a(int r) { return (r >> 1) & 7; }
-__device__ __forceinline__ int gf_swz_w(int r) { return (r >> 1) & 3; }
+__device__ __forceinline__ int gf_swz_w(int r) { return ((r >> 1) & 3) ^ ((r >> 4) & 1); }
 
 template <int BM, int WGN, int NS, int BK>
 __global__ __launch_bounds__(GF_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
@@ -994,7 +997,245 @@ void gemm_fast_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ 
                 int32_t* out = C + (size_t)row * (size_t)N + 4 * bcol;
                 if (vec_store) {
                     if (accumulate) v += *reinterpret_cast<const v4i*>(out);
-                    *reinterpret_cast<v4i*>(out) = v;
+                    __builtin_nontemporal_store(v, reinterpret_cast<v4i*>(out));  // streamed, not re-read
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) out[j] = accumulate ? out[j] + v[j] : v[j];
+                }
+            }
+        }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Software-pipelined variant of the LDS-tiled GEMM.  Same tiles, LDS layouts and DMA as
+// gemm_fast_kernel; the difference is the order of work inside a wave:
+//   * every LDS fragment read is inline assembly, so the only LDS waits are the explicit ones;
+//   * the fragments of the next MFMA k-step are read while the MFMAs of the current one run
+//     (two register sets, alternating);
+//   * the stage barrier (stage s+1 landed everywhere, stage s free for reuse) and the DMA issue of
+//     stage s+NS happen before the last k-step's MFMAs of stage s, and the first fragments of
+//     stage s+1 are read right after it, so the MFMA pipe never waits for a fresh stage's reads.
+// NS stages are in flight: NS-1 DMA stages ahead of the one being read.
+// ------------------------------------------------------------------------------------------------
+__device__ __forceinline__ v4i lds_read_b128_asm(uint32_t addr) {
+    v4i v;
+    __asm__ volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+    return v;
+}
+__device__ __forceinline__ uint64_t lds_read_tr8_asm(uint32_t addr) {
+    uint64_t v;
+    __asm__ volatile("ds_read_b64_tr_b8 %0, %1" : "=v"(v) : "v"(addr));
+    return v;
+}
+__device__ __forceinline__ uint32_t lds_u32(const void* p) {
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
+}
+
+template <int MT, int GT>
+struct PipeFrag {
+    v4i a[MT];
+    uint64_t lo[GT], hi[GT];
+};
+
+template <int BM, int WGN, int NS, int BK>
+__global__ __launch_bounds__(GF_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
+void gemm_pipe_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ B, int32_t* __restrict__ C, int M,
+                      int K, int N, int tiles_n, int k_begin, int k_end, int accumulate, int vec_store) {
+    constexpr int WGM = 8 / WGN;
+    constexpr int WM = BM / WGM;
+    constexpr int MT = WM / 16;
+    constexpr int GT = 4 / WGN;
+    constexpr int KS = BK / 64;
+    constexpr int CPR = BK / 16;
+    constexpr int A_STAGE = BM * BK;
+    constexpr int W_STAGE = BK * GF_BNB;
+    constexpr int NA = A_STAGE / 16 / GF_THREADS;
+    constexpr int NW = W_STAGE / 16 / GF_THREADS;
+    static_assert(KS % 2 == 0, "fragment sets alternate per k-step");
+    __shared__ __attribute__((aligned(16))) int8_t sA0[A_STAGE];
+    __shared__ __attribute__((aligned(16))) int8_t sA1[A_STAGE];
+    __shared__ __attribute__((aligned(16))) int8_t sA2[A_STAGE];
+    __shared__ __attribute__((aligned(16))) int8_t sA3[NS > 3 ? A_STAGE : 16];
+    __shared__ __attribute__((aligned(16))) uint8_t sW0[W_STAGE];
+    __shared__ __attribute__((aligned(16))) uint8_t sW1[W_STAGE];
+    __shared__ __attribute__((aligned(16))) uint8_t sW2[W_STAGE];
+    __shared__ __attribute__((aligned(16))) uint8_t sW3[NS > 3 ? W_STAGE : 16];
+    auto stage_a = [&](int i) -> int8_t* { return i == 0 ? sA0 : (i == 1 ? sA1 : (i == 2 ? sA2 : sA3)); };
+    auto stage_w = [&](int i) -> uint8_t* { return i == 0 ? sW0 : (i == 1 ? sW1 : (i == 2 ? sW2 : sW3)); };
+
+    const int NB = N >> 2;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WGN, wn = wave % WGN;
+    const int q = lane & 15, kb = lane >> 4;
+
+    const int tiles_m = (M + BM - 1) / BM;
+    int tm, tn;
+    {
+        const int t = xcd_linear(blockIdx.x, gridDim.x);
+        constexpr int GM = 4;
+        const int first_m = (t / (GM * tiles_n)) * GM;
+        const int gm = min(tiles_m - first_m, GM);
+        const int local = t % (GM * tiles_n);
+        tm = first_m + local % gm;
+        tn = local / gm;
+    }
+    const int row0 = tm * BM;
+    const int bc0 = tn * GF_BNB;
+    const int nst = (k_end - k_begin) / BK;
+
+    uint32_t a_off[NA];
+#pragma unroll
+    for (int p = 0; p < NA; ++p) {
+        const int slot = (p * 8 + wave) * 64 + lane;
+        const int r = slot / CPR, pos = slot % CPR;
+        const int grow = min(row0 + r, M - 1);
+        a_off[p] = (uint32_t)grow * (uint32_t)K + (uint32_t)(((pos & ~7) | ((pos & 7) ^ gf_swz_a(r))) * 16);
+    }
+    uint32_t w_off[NW];
+#pragma unroll
+    for (int p = 0; p < NW; ++p) {
+        const int slot = (p * 8 + wave) * 64 + lane;
+        const int r = slot >> 2, pos = slot & 3;
+        w_off[p] = (uint32_t)r * (uint32_t)NB + (uint32_t)(bc0 + (pos ^ gf_swz_w(r)) * 16);
+    }
+    auto issue = [&](int st, int buf) {
+        const int sc = min(st, nst - 1);
+        const int8_t* abase = A + k_begin + (size_t)sc * BK;
+        int8_t* adst = stage_a(buf);
+#pragma unroll
+        for (int p = 0; p < NA; ++p) lds_dma16(abase + a_off[p], adst + (p * 8 + wave) * 1024);
+        const uint8_t* wbase = B + (size_t)(k_begin + sc * BK) * (size_t)NB;
+        uint8_t* wdst = stage_w(buf);
+#pragma unroll
+        for (int p = 0; p < NW; ++p) lds_dma16(wbase + w_off[p], wdst + (p * 8 + wave) * 1024);
+    };
+
+    // Per-lane fragment offsets inside a stage.  A: row wm*WM + 16t + q, chunk kk*4 + kb (the swizzle
+    // depends on the row only through (row/2) % 8, the same for all t).  W: k-row 64kk + 16kb + q/2
+    // (+8 for the second read), 16-byte group wn*GT + g (swizzle through (row/2) % 4, the same for all
+    // kk and for the +8 row).
+    uint32_t a_lane[KS];
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) {
+        const int r = wm * WM + q;
+        const int c = kk * 4 + kb;
+        a_lane[kk] = (uint32_t)(r * BK + 16 * ((c & ~7) | ((c & 7) ^ gf_swz_a(r))));
+    }
+    uint32_t w_lane[GT];
+#pragma unroll
+    for (int g = 0; g < GT; ++g) {
+        const int cg = wn * GT + g;
+        const int r0 = kb * 16 + (q >> 1);
+        w_lane[g] = (uint32_t)(r0 * GF_BNB + 16 * (cg ^ gf_swz_w(r0)) + 8 * (q & 1));
+    }
+    auto read = [&](PipeFrag<MT, GT>& f, int buf, int kk) {
+        const uint32_t ab = lds_u32(stage_a(buf)) + a_lane[kk];
+#pragma unroll
+        for (int t = 0; t < MT; ++t) f.a[t] = lds_read_b128_asm(ab + (uint32_t)(t * 16 * BK));
+        const uint32_t wb = lds_u32(stage_w(buf)) + (uint32_t)(kk * 64 * GF_BNB);
+#pragma unroll
+        for (int g = 0; g < GT; ++g) {
+            f.lo[g] = lds_read_tr8_asm(wb + w_lane[g]);
+            f.hi[g] = lds_read_tr8_asm(wb + w_lane[g] + 8 * GF_BNB);
+        }
+    };
+    // All LDS reads issued so far have returned; the empty asm statements tie each fragment register
+    // to that point, so no use of them is scheduled before it.
+    auto wait_frag = [&](PipeFrag<MT, GT>& f) {
+        TX_LGKMCNT0();
+#pragma unroll
+        for (int t = 0; t < MT; ++t) __asm__ volatile("" : "+v"(f.a[t]));
+#pragma unroll
+        for (int g = 0; g < GT; ++g) __asm__ volatile("" : "+v"(f.lo[g]), "+v"(f.hi[g]));
+    };
+
+    v4i acc[MT][GT][4];
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int g = 0; g < GT; ++g)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[t][g][j] = v4i{0, 0, 0, 0};
+
+    auto mfmas = [&](const PipeFrag<MT, GT>& f) {
+#pragma unroll
+        for (int g = 0; g < GT; ++g) {
+            const uint32_t x4[4] = {(uint32_t)f.lo[g], (uint32_t)(f.lo[g] >> 32), (uint32_t)f.hi[g],
+                                    (uint32_t)(f.hi[g] >> 32)};
+            v4i bfr[4];
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) {
+                const uint32_t x = x4[r4];
+                bfr[0][r4] = (int)((x << 6) & 0xC0C0C0C0u);
+                bfr[1][r4] = (int)((x << 4) & 0xC0C0C0C0u);
+                bfr[2][r4] = (int)((x << 2) & 0xC0C0C0C0u);
+                bfr[3][r4] = (int)(x & 0xC0C0C0C0u);
+            }
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[t][g][j] = mfma_i8(f.a[t], bfr[j], acc[t][g][j]);
+        }
+    };
+
+    PipeFrag<MT, GT> f0, f1;
+    // Prologue: all NS stages in flight, wait for stage 0, first fragments.
+#pragma unroll
+    for (int p = 0; p < NS; ++p) issue(p, p);
+    TX_VMCNT((NS - 1) * (NA + NW));
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    read(f0, 0, 0);
+
+    // One stage in buffer h (a literal at every call site).  Fragment set f0 serves even k-steps.
+    auto stage = [&](int st, int h) {
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk) {
+            PipeFrag<MT, GT>& cur = (kk & 1) ? f1 : f0;
+            PipeFrag<MT, GT>& nxt = (kk & 1) ? f0 : f1;
+            wait_frag(cur);
+            __builtin_amdgcn_sched_barrier(0);
+            if (kk + 1 < KS) {
+                read(nxt, h, kk + 1);
+            } else if (st + 1 < nst) {
+                TX_VMCNT((NS - 2) * (NA + NW));  // stage st+1 has landed (NS-2 later stages may not)
+                __builtin_amdgcn_s_barrier();     // ... everywhere, and every wave is done reading stage st
+                __builtin_amdgcn_sched_barrier(0);
+                issue(st + NS, h);
+                read(nxt, (h + 1) % NS, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas(cur);
+        }
+    };
+    int s = 0;
+    for (; s + NS <= nst; s += NS) {
+        stage(s + 0, 0);
+        stage(s + 1, 1);
+        stage(s + 2, 2);
+        if (NS > 3) stage(s + 3, 3);
+    }
+    if (s + 0 < nst) stage(s + 0, 0);
+    if (s + 1 < nst) stage(s + 1, 1);
+    if (NS > 3 && s + 2 < nst) stage(s + 2, 2);
+    TX_VMCNT(0);  // no LDS DMA may land after the workgroup exits
+
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = row0 + wm * WM + t * 16 + 4 * kb + i;
+            if (row >= M) continue;
+#pragma unroll
+            for (int g = 0; g < GT; ++g) {
+                const int bcol = bc0 + (wn * GT + g) * 16 + q;
+                v4i v = {acc[t][g][0][i] >> 6, acc[t][g][1][i] >> 6, acc[t][g][2][i] >> 6, acc[t][g][3][i] >> 6};
+                int32_t* out = C + (size_t)row * (size_t)N + 4 * bcol;
+                if (vec_store) {
+                    if (accumulate) v += *reinterpret_cast<const v4i*>(out);
+                    __builtin_nontemporal_store(v, reinterpret_cast<v4i*>(out));  // streamed, not re-read
                 } else {
 #pragma unroll
                     for (int j = 0; j < 4; ++j) out[j] = accumulate ? out[j] + v[j] : v[j];
@@ -1193,6 +1434,32 @@ hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int
         int bk = 128;
         if (bk_env && std::atoi(bk_env) == 256 && bm == 128 && (k_end - k_begin) % 256 == 0) bk = 256;
         const dim3 grid(((M + bm - 1) / bm) * tiles_n);
+        // 128-row tiles run the software-pipelined kernel (measured faster on MI355X); 256-row tiles
+        // keep gemm_fast_kernel, whose wave tile leaves no registers for a second fragment set.
+        static const int pipe_env = [] {
+            const char* e = std::getenv("TERNIX_GEMM_PIPE");
+            return e ? std::atoi(e) : -1;
+        }();
+        const int pipe = pipe_env >= 0 ? pipe_env : (bm == 128 ? 1 : 0);
+        static const int pipe_ns = [] {
+            const char* e = std::getenv("TERNIX_GEMM_NS");
+            return e && std::atoi(e) == 4 ? 4 : 3;
+        }();
+        if (pipe) {
+#define TX_GP_LAUNCH(BM_, WGN_, NS_, BK_)                                                                         \
+    hipLaunchKernelGGL((gemm_pipe_kernel<BM_, WGN_, NS_, BK_>), grid, dim3(GF_THREADS), 0, st, A, B, C, M, K, N, \
+                       tiles_n, k_begin, k_end, accumulate, vs)
+            if (bm == 256 && wgn == 4) TX_GP_LAUNCH(256, 4, 3, 128);
+            else if (bm == 256) TX_GP_LAUNCH(256, 2, 3, 128);
+            else if (bk == 256 && wgn == 4) TX_GP_LAUNCH(128, 4, 3, 256);
+            else if (bk == 256) TX_GP_LAUNCH(128, 2, 3, 256);
+            else if (wgn == 4 && pipe_ns == 4) TX_GP_LAUNCH(128, 4, 4, 128);
+            else if (wgn == 4) TX_GP_LAUNCH(128, 4, 3, 128);
+            else if (pipe_ns == 4) TX_GP_LAUNCH(128, 2, 4, 128);
+            else TX_GP_LAUNCH(128, 2, 3, 128);
+#undef TX_GP_LAUNCH
+            return hipGetLastError();
+        }
 #define TX_GF_LAUNCH(BM_, WGN_, NS_, BK_)                                                                         \
     hipLaunchKernelGGL((gemm_fast_kernel<BM_, WGN_, NS_, BK_>), grid, dim3(GF_THREADS), 0, st, A, B, C, M, K, N, \
                        tiles_n, k_begin, k_end, accumulate, vs)
