@@ -1208,6 +1208,9 @@ void gemm_pipe_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ 
             }
             __builtin_amdgcn_sched_barrier(0);
             mfmas(cur);
+            // keep the next k-step's wait below these MFMAs (it would otherwise be hoisted among them
+            // and wait for the reads just issued)
+            __builtin_amdgcn_sched_barrier(0);
         }
     };
     int s = 0;
