@@ -42,7 +42,7 @@ def parse():
                     help="untimed sustained load before each GPU measurement (clock ramp)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["all", "gemv", "gemm", "bigm1"], default="all")
+    ap.add_argument("--only", choices=["all", "gemv", "gemm", "bigm1", "pack"], default="all")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run 4 device-to-device copies of 256 MiB (the runtime's copy kernel), the "
                          "known-size reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -206,6 +206,32 @@ def bench_gemm(args, stream, lib):
             "frac": tot_ops / (tot_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS}
 
 
+def bench_pack(args, stream, lib):
+    """Device pack_ternary_weights of the cfg5 big weights (8192 x 28672 int8 -> 58.7 MB packed)."""
+    import hashlib
+    from ternixengine_amd import configs
+    from ternixengine_amd import hip_runtime as hr
+    case = configs.CASES["cfg5_big_m1"]
+    w = configs.gen_w(case).reshape(-1)
+    dw, dp = hr.DeviceBuffer.from_array(w), hr.DeviceBuffer(w.size // 4)
+    fn = lib.ternix_hip_pack_ternary_weights
+
+    def one(i):
+        st = fn(dp.value, dw.value, w.size, stream.handle)
+        if st != 0:
+            raise RuntimeError(f"pack failed: {st}")
+
+    steps = 20
+    prewarm(one, args.prewarm_s / 2, stream)
+    ms = time_launches(one, steps, 2, stream)
+    with open(os.path.join(ROOT, "tests", "golden", "config_digests.json")) as f:
+        want = json.load(f)["cases"][case.name]["sha256_Wp"]
+    ok = hashlib.sha256(dp.download(np.uint8, (w.size // 4,)).tobytes()).hexdigest() == want
+    moved = w.size + w.size // 4
+    return {"shape": [case.K, case.N], "us": ms / steps * 1e3, "gbs": moved / (ms / steps * 1e-3) / 1e9,
+            "bytes": moved, "verified": ok}
+
+
 def cpu_baseline(seconds):
     """Reference avx2_blocked (oracle/_ref) or the oracle's restatement, one thread, on the cfg2 pair."""
     from ternixengine_amd import configs
@@ -255,6 +281,8 @@ def main():
         res["bigm1"] = bench_big_m1(args, stream, lib)
     if args.only in ("all", "gemm"):
         res["gemm"] = bench_gemm(args, stream, lib)
+    if args.only in ("all", "pack"):
+        res["pack"] = bench_pack(args, stream, lib)
     g = res.get("gemv")
     line = {
         "metric": METRIC,
@@ -292,6 +320,10 @@ def main():
                               "frac": round(gm["frac"], 4),
                               "shapes": [{k: (round(v, 3) if isinstance(v, float) else v) for k, v in s.items()}
                                          for s in gm["shapes"]]}
+    if "pack" in res:
+        pk = res["pack"]
+        line["pack_device"] = {"shape": pk["shape"], "us": round(pk["us"], 2), "gbs": round(pk["gbs"], 1),
+                               "frac": round(pk["gbs"] / HBM_PEAK_GBS, 4), "verified": pk["verified"]}
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
         line["cpu_baseline"]["value"] = round(line["cpu_baseline"]["value"], 3)

@@ -116,6 +116,20 @@ void ternix_unpack_ternary_weights(int8_t* unpacked, const uint8_t* packed, size
  * of size/4 bytes (the K x N/4 layout is consumed as is by every kernel). */
 void ternix_interleave_weights_offline(uint8_t* interleaved, const uint8_t* packed, size_t size);
 
+/* ---- weight format on the device (asynchronous on `stream`) ---- */
+
+/* pack_ternary_weights on device memory (reference src/bitpack.cpp:5-15, same
+ * semantics as ternix_pack_ternary_weights): `size` int8 weights at dW ->
+ * size/4 bytes at dPacked.  hipErrorInvalidValue for a null pointer when
+ * size/4 > 0. */
+int ternix_hip_pack_ternary_weights(uint8_t* dPacked, const int8_t* dW, size_t size, void* stream);
+/* unpack_ternary_weights on device memory (reference src/bitpack.cpp:17-27):
+ * size/4 bytes at dPacked -> 4*(size/4) int8 weights at dW. */
+int ternix_hip_unpack_ternary_weights(int8_t* dW, const uint8_t* dPacked, size_t size, void* stream);
+/* interleave_weights_offline on device memory (reference src/bitpack.cpp:29-33):
+ * the identity, a device-to-device copy of size/4 bytes (none when dOut == dPacked). */
+int ternix_hip_interleave_weights_offline(uint8_t* dOut, const uint8_t* dPacked, size_t size, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -14,7 +14,8 @@ Python face of libternix_hip.so, shaped like the reference's `ternix_engine` mod
 RuntimeError("HIP error: ...") for device errors.  The GIL is released during device work (ctypes).
 
 Device-pointer access (no copies) is `mul_mat_ternary(dA, dB, dC, M, K, N, stream=None, path="auto")`
-with integer device addresses, mirroring the C-ABI in include/ternix/ternix_hip.h.
+with integer device addresses, mirroring the C-ABI in include/ternix/ternix_hip.h; the weight format
+on device memory is `pack_ternary_device` / `unpack_ternary_device`.
 """
 import ctypes
 
@@ -23,8 +24,8 @@ import numpy as np
 from . import _lib
 from ._lib import LibraryNotBuilt, load as _load  # noqa: F401
 
-__all__ = ["pack_ternary", "unpack_ternary", "ternary_matmul", "mul_mat_ternary", "has_cuda", "has_hip",
-           "HIP_IMPLS", "ternix_error"]
+__all__ = ["pack_ternary", "unpack_ternary", "ternary_matmul", "mul_mat_ternary", "pack_ternary_device",
+           "unpack_ternary_device", "has_cuda", "has_hip", "HIP_IMPLS", "ternix_error"]
 
 has_cuda = False
 HIP_IMPLS = {"hip": 0, "hip_naive": 1, "hip_gemv": 2, "hip_gemm": 3, "hip_tiled": 4}
@@ -97,6 +98,17 @@ def ternary_matmul(a, b_packed, impl="hip"):
             raise ValueError(f"impl '{impl}' rejected shape M={m} K={k} N={n}")
         raise RuntimeError(f"HIP error: {ternix_error(status)}")
     return c
+
+
+def pack_ternary_device(d_packed, d_w, size, stream=None):
+    """Device-memory pack_ternary_weights: `size` int8 weights at address d_w -> size//4 bytes at
+    d_packed, asynchronously on `stream`.  Returns the hipError_t status as an int."""
+    return _load().ternix_hip_pack_ternary_weights(d_packed, d_w, int(size), stream)
+
+
+def unpack_ternary_device(d_w, d_packed, size, stream=None):
+    """Device-memory unpack_ternary_weights: size//4 bytes at d_packed -> 4*(size//4) int8 at d_w."""
+    return _load().ternix_hip_unpack_ternary_weights(d_w, d_packed, int(size), stream)
 
 
 def mul_mat_ternary(dA, dB, dC, M, K, N, stream=None, path="auto"):

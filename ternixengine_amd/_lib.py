@@ -41,6 +41,11 @@ def load():
         f = getattr(lib, name)
         f.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]
         f.restype = None
+    for name in ("ternix_hip_pack_ternary_weights", "ternix_hip_unpack_ternary_weights",
+                 "ternix_hip_interleave_weights_offline"):
+        f = getattr(lib, name)
+        f.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+        f.restype = ctypes.c_int
     u64 = ctypes.c_uint64
     lib.ternix_synth_u64.argtypes = [u64, u64, u64]
     lib.ternix_synth_u64.restype = u64

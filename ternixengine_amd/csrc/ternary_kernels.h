@@ -33,5 +33,8 @@ hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, i
 hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int k_begin,
                        int k_end, int accumulate, hipStream_t st);
 hipError_t launch_naive(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, hipStream_t st);
+// 2-bit weight format on the device (bitpack_kernels.hip): `size` weights <-> size/4 packed bytes.
+hipError_t launch_pack(uint8_t* packed, const int8_t* w, size_t size, hipStream_t st);
+hipError_t launch_unpack(int8_t* w, const uint8_t* packed, size_t size, hipStream_t st);
 
 }  // namespace ternix_hip

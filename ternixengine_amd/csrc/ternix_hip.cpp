@@ -256,6 +256,26 @@ done:
     return (int)e;
 }
 
+int ternix_hip_pack_ternary_weights(uint8_t* dPacked, const int8_t* dW, size_t size, void* stream) {
+    if (size / 4 == 0) return (int)hipSuccess;
+    if (dPacked == nullptr || dW == nullptr) return (int)hipErrorInvalidValue;
+    return (int)ternix_hip::launch_pack(dPacked, dW, size, static_cast<hipStream_t>(stream));
+}
+
+int ternix_hip_unpack_ternary_weights(int8_t* dW, const uint8_t* dPacked, size_t size, void* stream) {
+    if (size / 4 == 0) return (int)hipSuccess;
+    if (dPacked == nullptr || dW == nullptr) return (int)hipErrorInvalidValue;
+    return (int)ternix_hip::launch_unpack(dW, dPacked, size, static_cast<hipStream_t>(stream));
+}
+
+int ternix_hip_interleave_weights_offline(uint8_t* dOut, const uint8_t* dPacked, size_t size, void* stream) {
+    const size_t nbytes = size / 4;
+    if (nbytes == 0) return (int)hipSuccess;
+    if (dOut == nullptr || dPacked == nullptr) return (int)hipErrorInvalidValue;
+    if (dOut == dPacked) return (int)hipSuccess;
+    return (int)hipMemcpyAsync(dOut, dPacked, nbytes, hipMemcpyDeviceToDevice, static_cast<hipStream_t>(stream));
+}
+
 const char* ternix_hip_error_string(int status) {
     const char* s = hipGetErrorString(static_cast<hipError_t>(status));
     return s ? s : "unknown error";

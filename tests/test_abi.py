@@ -143,3 +143,13 @@ def test_gauss_distribution():
     a = configs.gen_a(configs.CASES["cfg3_m64_up"])
     assert abs(float(a.mean())) < 0.5 and 30.5 < float(a.std()) < 32.5
     assert a.min() >= -128 and a.max() <= 127
+
+
+def test_device_bitpack_validation_without_launch():
+    """Null device pointers are rejected before any HIP call; nothing to do for fewer than 4 weights."""
+    lib = tx._load()
+    for name in ("ternix_hip_pack_ternary_weights", "ternix_hip_unpack_ternary_weights",
+                 "ternix_hip_interleave_weights_offline"):
+        fn = getattr(lib, name)
+        assert fn(None, None, 64, None) == 1, name
+        assert fn(None, None, 3, None) == 0, name
