@@ -42,7 +42,7 @@ def parse():
                     help="untimed sustained load before each GPU measurement (clock ramp)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["all", "gemv", "gemm", "bigm1", "pack"], default="all")
+    ap.add_argument("--only", choices=["all", "gemv", "gemm", "bigm1", "pack", "layer"], default="all")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run 4 device-to-device copies of 256 MiB (the runtime's copy kernel), the "
                          "known-size reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -232,6 +232,63 @@ def bench_pack(args, stream, lib):
             "bytes": moved, "verified": ok}
 
 
+def bench_layer(args, stream, lib):
+    """The quantised layer boundary on the GPU: per-row absmax quantisation of fp32 activations
+    (decode M=1 x 2560 and prefill M=2048 x 4096) and the matmul with the fp32 dequantisation fused
+    into its output (cfg2 pair at M=1, cold weights; cfg4 4096x4096 at M=2048)."""
+    from ternixengine_amd import configs
+    from ternixengine_amd import hip_runtime as hr
+    out = {}
+    rng = np.random.default_rng(0)
+    for (m, k) in ((1, 2560), (2048, 4096)):
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        dx, dq, ds = hr.DeviceBuffer.from_array(x), hr.DeviceBuffer(m * k), hr.DeviceBuffer(4 * m)
+
+        def q(i, dx=dx, dq=dq, ds=ds, m=m, k=k):
+            st = lib.ternix_hip_quantize_activations(dx.value, dq.value, ds.value, m, k, stream.handle)
+            if st != 0:
+                raise RuntimeError(f"quantize failed: {st}")
+
+        steps = 100
+        prewarm(q, args.prewarm_s / 4, stream)
+        ms = time_launches(q, steps, 5, stream)
+        moved = 5 * m * k + 4 * m
+        out[f"quantize_{m}x{k}"] = {"us": ms / steps * 1e3, "gbs": moved / (ms / steps * 1e-3) / 1e9}
+
+    fn = lib.ternix_hip_mul_mat_ternary_dequant
+    up, down = configs.CASES["cfg2_up"], configs.CASES["cfg2_down"]
+    pair_w = up.K * up.N // 4 + down.K * down.N // 4
+    copies = max(2, -(-POOL_MIN_BYTES // pair_w))
+    pu, pd = Problem(up, copies), Problem(down, copies)
+    drs = hr.DeviceBuffer.from_array(np.full(1, 0.01, np.float32))
+
+    def dl(p, widx):
+        c = p.case
+        st = fn(p.dA.value, p.dW[widx].value, p.dC.value, c.M, c.K, c.N, drs.value, 0.5, stream.handle)
+        if st != 0:
+            raise RuntimeError(f"dequant matmul failed: {st}")
+
+    def pair(i):
+        dl(pu, i % copies)
+        dl(pd, i % copies)
+
+    prewarm(pair, args.prewarm_s / 2, stream)
+    ms = time_launches(pair, args.steps, args.warmup, stream)
+    bytes_step = up.bytes_algorithmic + down.bytes_algorithmic + 8
+    out["gemv_pair_dequant"] = {"us_per_gemv": ms / args.steps / 2 * 1e3,
+                                "gbs": bytes_step / (ms / args.steps * 1e-3) / 1e9}
+    del pu, pd
+    case = configs.CASES["cfg4_4096x4096"]
+    p = Problem(case, 1)
+    drs = hr.DeviceBuffer.from_array(np.full(case.M, 0.01, np.float32))
+    prewarm(lambda i: dl(p, 0), args.prewarm_s, stream)
+    steps = args.gemm_steps
+    ms = time_launches(lambda i: dl(p, 0), steps, 3, stream)
+    out["gemm_dequant_2048x4096x4096"] = {"us": ms / steps * 1e3,
+                                          "tops": case.ops / (ms / steps * 1e-3) / 1e12}
+    return out
+
+
 def cpu_baseline(seconds):
     """Reference avx2_blocked (oracle/_ref) or the oracle's restatement, one thread, on the cfg2 pair."""
     from ternixengine_amd import configs
@@ -283,6 +340,8 @@ def main():
         res["gemm"] = bench_gemm(args, stream, lib)
     if args.only in ("all", "pack"):
         res["pack"] = bench_pack(args, stream, lib)
+    if args.only in ("all", "layer"):
+        res["layer"] = bench_layer(args, stream, lib)
     g = res.get("gemv")
     line = {
         "metric": METRIC,
@@ -324,6 +383,8 @@ def main():
         pk = res["pack"]
         line["pack_device"] = {"shape": pk["shape"], "us": round(pk["us"], 2), "gbs": round(pk["gbs"], 1),
                                "frac": round(pk["gbs"] / HBM_PEAK_GBS, 4), "verified": pk["verified"]}
+    if "layer" in res:
+        line["layer_boundary"] = {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in res["layer"].items()}
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
         line["cpu_baseline"]["value"] = round(line["cpu_baseline"]["value"], 3)

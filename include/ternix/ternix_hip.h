@@ -116,6 +116,32 @@ void ternix_unpack_ternary_weights(int8_t* unpacked, const uint8_t* packed, size
  * of size/4 bytes (the K x N/4 layout is consumed as is by every kernel). */
 void ternix_interleave_weights_offline(uint8_t* interleaved, const uint8_t* packed, size_t size);
 
+/* ---- quantised layer boundary (BitNet b1.58 scheme; no reference counterpart: the
+ *      reference leaves weight and activation quantisation as a stub, scripts/quantize.py:5,
+ *      README.md:203) ---- */
+
+/* Per-row absmax int8 quantisation of fp32 activations X[M][K] (row-major), asynchronous:
+ *   a_m = max(max_k |X[m][k]|, 1e-5),  Q[m][k] = clamp(rint(X[m][k] * (127 / a_m)), -128, 127),
+ *   dRowScale[m] = a_m / 127  (IEEE fp32 division and multiplication, round half to even).
+ * NaN and infinite inputs are outside the domain. */
+int ternix_hip_quantize_activations(const float* dX, int8_t* dQ, float* dRowScale, int64_t M, int64_t K,
+                                    void* stream);
+
+/* ternix_hip_mul_mat_ternary with the dequantisation fused into the output:
+ *   Y[m][n] = (float)C[m][n] * (dRowScale[m] * w_scale)    (fp32, row-major M x N)
+ * (the scale product rounded once, then one rounding per output), where C is the exact int32
+ * product.  Same shapes, dispatch and status contract as ternix_hip_mul_mat_ternary; dRowScale must
+ * not be NULL when M > 0. */
+int ternix_hip_mul_mat_ternary_dequant(const int8_t* dA, const uint8_t* dB, float* dY, int64_t M, int64_t K,
+                                       int64_t N, const float* dRowScale, float w_scale, void* stream);
+
+/* Host, offline: absmean ternary quantisation of fp32 weights W (size elements, K x N row-major,
+ * size % 4 == 0) straight into the packed format:
+ *   gamma = max(mean |W|, 1e-5) (summed in double in index order),
+ *   w = clamp(rint(W / gamma), -1, 1), packed as ternix_pack_ternary_weights; *w_scale = gamma.
+ * Returns 0, or 1 for a size that is not a multiple of 4 or a NULL pointer. */
+int ternix_quantize_weights_absmean(uint8_t* packed, float* w_scale, const float* W, size_t size);
+
 /* ---- weight format on the device (asynchronous on `stream`) ---- */
 
 /* pack_ternary_weights on device memory (reference src/bitpack.cpp:5-15, same

@@ -6,6 +6,8 @@
  */
 #include "ternix_oracle.h"
 
+#include <math.h>
+
 #include <pthread.h>
 #include <string.h>
 
@@ -205,4 +207,48 @@ void oracle_mm_scalar_mt(const int8_t* A, const uint8_t* Bp, int32_t* C, size_t 
         pthread_create(&tid[t], NULL, mt_run, j);
     }
     for (int t = 0; t < nthreads; ++t) pthread_join(tid[t], NULL);
+}
+
+/* ---- quantised layer boundary (see the header: no reference counterpart) ---- */
+
+/* a = max(absmax, 1e-5); s = 127 / a; q = clamp(rint(x * s), -128, 127); row_scale = a / 127. */
+void oracle_quantize_rows_absmax(const float* X, int8_t* Q, float* row_scale, size_t M, size_t K) {
+    for (size_t m = 0; m < M; ++m) {
+        const float* x = X + m * K;
+        float amax = 0.0f;
+        for (size_t k = 0; k < K; ++k) {
+            const float v = fabsf(x[k]);
+            if (v > amax) amax = v;
+        }
+        const float a = amax > 1e-5f ? amax : 1e-5f;
+        const float s = 127.0f / a;
+        row_scale[m] = a / 127.0f;
+        for (size_t k = 0; k < K; ++k) {
+            float r = rintf(x[k] * s);
+            if (r > 127.0f) r = 127.0f;
+            if (r < -128.0f) r = -128.0f;
+            Q[m * K + k] = (int8_t)r;
+        }
+    }
+}
+
+/* f = row_scale[m] * w_scale (one rounding), y = (float)c * f (one rounding). */
+void oracle_dequant(const int32_t* C, float* Y, const float* row_scale, float w_scale, size_t M, size_t N) {
+    for (size_t m = 0; m < M; ++m) {
+        const float f = row_scale[m] * w_scale;
+        for (size_t n = 0; n < N; ++n) Y[m * N + n] = (float)C[m * N + n] * f;
+    }
+}
+
+/* gamma = max(mean|W|, 1e-5) (sum in double, index order); w = clamp(rint(W / gamma), -1, 1). */
+float oracle_quantize_weights_absmean(int8_t* Wq, const float* W, size_t size) {
+    double sum = 0.0;
+    for (size_t i = 0; i < size; ++i) sum += fabs((double)W[i]);
+    float gamma = size ? (float)(sum / (double)size) : 0.0f;
+    if (!(gamma >= 1e-5f)) gamma = 1e-5f;
+    for (size_t i = 0; i < size; ++i) {
+        const float r = rintf(W[i] / gamma);
+        Wq[i] = (int8_t)(r > 1.0f ? 1 : (r < -1.0f ? -1 : (int)r));
+    }
+    return gamma;
 }

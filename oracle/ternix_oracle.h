@@ -29,6 +29,20 @@
  *     compiled reference sources (oracle/_ref).
  *   - invalid code 0b10 (outside the domain): naive -> 0, scalar -> -2a,
  *     avx2 -> -a, each checked against the compiled reference's output.
+ *
+ * Quantised layer boundary (no reference implementation: the reference leaves
+ * weight and activation quantisation as a stub, scripts/quantize.py:5,
+ * README.md:203; these restate the BitNet b1.58 formulas the library documents
+ * in include/ternix/ternix_hip.h, step for step in IEEE fp32):
+ *   oracle_quantize_rows_absmax      per-row absmax int8 activation quantisation
+ *   oracle_dequant                   y = (float)c * (row_scale[m] * w_scale)
+ *   oracle_quantize_weights_absmean  absmean ternary weight quantisation
+ * Pinned in tests/test_quant.py by closed forms that a wrong sign, index, scale
+ * or rounding mode breaks: zero rows (q = 0, scale = 1e-5/127), a row whose
+ * absmax element maps to exactly +-127, constant rows, ties rounding to even,
+ * row independence (permuting rows permutes outputs), int32 values that are
+ * exact in fp32 times power-of-two scales (exact products), and a float64 numpy
+ * evaluation of the same formulas within one fp32 rounding.
  */
 #ifndef TERNIX_ORACLE_H
 #define TERNIX_ORACLE_H
@@ -51,6 +65,10 @@ int oracle_mm_avx2(const int8_t* A, const uint8_t* Bp, int32_t* C, size_t M, siz
 int oracle_mm_avx2_blocked(const int8_t* A, const uint8_t* Bp, int32_t* C, size_t M, size_t K, size_t N);
 
 void oracle_gemm_unpacked(const int8_t* A, const int8_t* W, int32_t* C, size_t M, size_t K, size_t N);
+
+void oracle_quantize_rows_absmax(const float* X, int8_t* Q, float* row_scale, size_t M, size_t K);
+void oracle_dequant(const int32_t* C, float* Y, const float* row_scale, float w_scale, size_t M, size_t N);
+float oracle_quantize_weights_absmean(int8_t* Wq, const float* W, size_t size);
 
 /* Row-parallel driver over oracle_mm_scalar (rows split over nthreads). */
 void oracle_mm_scalar_mt(const int8_t* A, const uint8_t* Bp, int32_t* C, size_t M, size_t K, size_t N,

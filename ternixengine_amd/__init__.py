@@ -25,7 +25,8 @@ from . import _lib
 from ._lib import LibraryNotBuilt, load as _load  # noqa: F401
 
 __all__ = ["pack_ternary", "unpack_ternary", "ternary_matmul", "mul_mat_ternary", "pack_ternary_device",
-           "unpack_ternary_device", "has_cuda", "has_hip", "HIP_IMPLS", "ternix_error"]
+           "unpack_ternary_device", "quantize_weights_absmean", "quantize_activations", "ternary_matmul_dequant",
+           "has_cuda", "has_hip", "HIP_IMPLS", "ternix_error"]
 
 has_cuda = False
 HIP_IMPLS = {"hip": 0, "hip_naive": 1, "hip_gemv": 2, "hip_gemm": 3, "hip_tiled": 4}
@@ -109,6 +110,61 @@ def pack_ternary_device(d_packed, d_w, size, stream=None):
 def unpack_ternary_device(d_w, d_packed, size, stream=None):
     """Device-memory unpack_ternary_weights: size//4 bytes at d_packed -> 4*(size//4) int8 at d_w."""
     return _load().ternix_hip_unpack_ternary_weights(d_w, d_packed, int(size), stream)
+
+
+def quantize_weights_absmean(w):
+    """Offline absmean ternary quantisation of fp32 weights (K, N) -> ((K, N/4) uint8 packed, w_scale):
+    gamma = max(mean|W|, 1e-5), w = clamp(rint(W / gamma), -1, 1) (host C code in the library)."""
+    w = np.ascontiguousarray(np.asarray(w, dtype=np.float32))
+    if w.ndim != 2 or w.shape[1] % 4 != 0:
+        raise ValueError("quantize_weights_absmean expects a 2-D (K, N) array with N % 4 == 0")
+    out = np.empty((w.shape[0], w.shape[1] // 4), dtype=np.uint8)
+    scale = np.zeros(1, dtype=np.float32)
+    if _load().ternix_quantize_weights_absmean(_ptr(out), _ptr(scale), _ptr(w), w.size) != 0:
+        raise ValueError("quantize_weights_absmean rejected its arguments")
+    return out, float(scale[0])
+
+
+def quantize_activations(x):
+    """Per-row absmax int8 quantisation of fp32 activations (M, K) on the GPU -> (q int8 (M, K),
+    row_scale float32 (M,)) with q = clamp(rint(x * 127 / a), -128, 127), row_scale = a / 127,
+    a = max(max|x_row|, 1e-5)."""
+    from . import hip_runtime as hr
+    x = np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+    if x.ndim != 2:
+        raise ValueError("quantize_activations expects a 2-D (M, K) array")
+    m, k = x.shape
+    dx, dq, ds = hr.DeviceBuffer.from_array(x), hr.DeviceBuffer(max(m * k, 1)), hr.DeviceBuffer(max(4 * m, 4))
+    status = _load().ternix_hip_quantize_activations(dx.value, dq.value, ds.value, m, k, None)
+    if status != 0:
+        raise RuntimeError(f"HIP error: {ternix_error(status)}")
+    hr.synchronize()
+    return dq.download(np.int8, (m, k)), ds.download(np.float32, (m,))
+
+
+def ternary_matmul_dequant(a, b_packed, row_scale, w_scale):
+    """Y = (A @ W) * row_scale[:, None] * w_scale as fp32 on the GPU, the scaling fused into the
+    matmul's output (see ternix_hip_mul_mat_ternary_dequant)."""
+    from . import hip_runtime as hr
+    a = np.ascontiguousarray(np.asarray(a).astype(np.int8, copy=False))
+    b = np.ascontiguousarray(np.asarray(b_packed).astype(np.uint8, copy=False))
+    rs = np.ascontiguousarray(np.asarray(row_scale, dtype=np.float32).reshape(-1))
+    if a.ndim != 2 or b.ndim != 2:
+        raise ValueError("A must be (M, K) and B_packed (K, N/4)")
+    m, k = a.shape
+    n = b.shape[1] * 4
+    if b.shape[0] != k:
+        raise ValueError("inner dimensions do not match")
+    if rs.shape[0] != m:
+        raise ValueError("row_scale must have M entries")
+    da, db, drs = hr.DeviceBuffer.from_array(a), hr.DeviceBuffer.from_array(b), hr.DeviceBuffer.from_array(rs)
+    dy = hr.DeviceBuffer(max(4 * m * n, 4))
+    status = _load().ternix_hip_mul_mat_ternary_dequant(da.value, db.value, dy.value, m, k, n, drs.value,
+                                                        float(w_scale), None)
+    if status != 0:
+        raise RuntimeError(f"HIP error: {ternix_error(status)}")
+    hr.synchronize()
+    return dy.download(np.float32, (m, n))
 
 
 def mul_mat_ternary(dA, dB, dC, M, K, N, stream=None, path="auto"):

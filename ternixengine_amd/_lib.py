@@ -46,6 +46,13 @@ def load():
         f = getattr(lib, name)
         f.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
         f.restype = ctypes.c_int
+    vp = ctypes.c_void_p
+    lib.ternix_hip_quantize_activations.argtypes = [vp, vp, vp, i64, i64, vp]
+    lib.ternix_hip_quantize_activations.restype = ctypes.c_int
+    lib.ternix_hip_mul_mat_ternary_dequant.argtypes = [vp, vp, vp, i64, i64, i64, vp, ctypes.c_float, vp]
+    lib.ternix_hip_mul_mat_ternary_dequant.restype = ctypes.c_int
+    lib.ternix_quantize_weights_absmean.argtypes = [vp, vp, vp, ctypes.c_size_t]
+    lib.ternix_quantize_weights_absmean.restype = ctypes.c_int
     u64 = ctypes.c_uint64
     lib.ternix_synth_u64.argtypes = [u64, u64, u64]
     lib.ternix_synth_u64.restype = u64

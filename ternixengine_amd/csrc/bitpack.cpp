@@ -7,7 +7,9 @@
 //
 // Implementation: a 256-entry table per direction is built once at load time; packing combines four
 // 2-bit codes per output byte, unpacking copies one 4-byte table entry per input byte.
+#include <cmath>
 #include <cstring>
+#include <vector>
 
 #include "ternix/bitpack.hpp"
 #include "ternix/ternix_hip.h"
@@ -64,7 +66,35 @@ void interleave_weights_offline(uint8_t* interleaved, const uint8_t* packed, siz
 
 }  // namespace ternix
 
+namespace {
+
+// BitNet b1.58 absmean weight quantisation (the offline step the reference leaves as a stub,
+// scripts/quantize.py:5): gamma = max(mean|W|, 1e-5) with the mean summed in double in index
+// order, then w = clamp(rint(W / gamma), -1, 1) with an IEEE fp32 division (round half to even).
+float absmean_quantize(int8_t* q, const float* w, size_t size) {
+    double sum = 0.0;
+    for (size_t i = 0; i < size; ++i) sum += std::fabs(static_cast<double>(w[i]));
+    float gamma = size ? static_cast<float>(sum / static_cast<double>(size)) : 0.0f;
+    if (!(gamma >= 1e-5f)) gamma = 1e-5f;
+    for (size_t i = 0; i < size; ++i) {
+        const float r = std::nearbyint(w[i] / gamma);
+        q[i] = static_cast<int8_t>(r > 1.0f ? 1 : (r < -1.0f ? -1 : static_cast<int>(r)));
+    }
+    return gamma;
+}
+
+}  // namespace
+
 extern "C" {
+
+int ternix_quantize_weights_absmean(uint8_t* packed, float* w_scale, const float* W, size_t size) {
+    if (size % 4 != 0 || w_scale == nullptr || (size && (packed == nullptr || W == nullptr))) return 1;
+    std::vector<int8_t> q(size);
+    *w_scale = absmean_quantize(q.data(), W, size);
+    ternix::pack_ternary_weights(packed, q.data(), size);
+    return 0;
+}
+
 
 void ternix_pack_ternary_weights(uint8_t* packed, const int8_t* unpacked, size_t size) {
     ternix::pack_ternary_weights(packed, unpacked, size);

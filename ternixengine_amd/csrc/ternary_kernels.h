@@ -12,6 +12,14 @@ namespace ternix_hip {
 // 16384 * K < 2^31, i.e. K < 2^17.  (In-domain codes reach at most 8192 per row.)
 constexpr int kMaxKPerAccumulator = (1 << 17) - 128;
 
+// Optional dequantised output of a matmul launch: when Y is set the kernels write
+// Y[m][n] = (float)C[m][n] * (rs[m] * ws) (fp32, row-major M x N) instead of the int32 C.
+struct OutScale {
+    float* Y = nullptr;
+    const float* rs = nullptr;  // per-row activation scale [M]
+    float ws = 0.0f;            // weight scale
+};
+
 hipError_t launch_zero(int32_t* C, size_t n, hipStream_t st);
 // LDS bytes the skinny fast kernel uses for one workgroup's activation slice (the rows of one
 // m-group x steps_per_split * 64 bytes, each row padded by 16 bytes); the fast kernel runs only up
@@ -27,11 +35,20 @@ bool skinny_fast_ok(const int8_t* A, const uint8_t* B, int M, int K, int N, int 
 // kernel, M <= 16); kw: waves per slab inside a workgroup (1, 2 or 4; fast kernel).  With
 // splits > 1 each split's partial C goes to `partials` ([splits][M][N] int32, 16-byte aligned) and a
 // reduce kernel sums them into C; without a workspace C is zeroed and accumulated with atomics.
+// With os.Y set, the store and partial-sum modes write the dequantised floats (fused into the store or
+// the reduce); the atomic mode accumulates int32 in C, which the caller converts afterwards.
 hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int tb, int kw,
-                         int splits, int steps_per_split, int32_t* partials, hipStream_t st);
+                         int splits, int steps_per_split, int32_t* partials, hipStream_t st,
+                         const OutScale& os = OutScale{});
 // LDS-tiled MFMA GEMM over k-rows [k_begin, k_end); accumulate != 0 adds into C instead of storing.
+// With os.Y set the tile epilogue writes the dequantised floats instead (accumulate must be 0).
 hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int k_begin,
-                       int k_end, int accumulate, hipStream_t st);
+                       int k_end, int accumulate, hipStream_t st, const OutScale& os = OutScale{});
+// In-place-capable conversion of an int32 C to the dequantised float Y (Y may alias C).
+hipError_t launch_dequant(const int32_t* C, const OutScale& os, int M, int N, hipStream_t st);
+// Per-row absmax int8 quantisation of fp32 activations: row_scale[m] = max(absmax_m, 1e-5) / 127,
+// Q = clamp(rint(X * (127 / max(absmax_m, 1e-5))), -128, 127).
+hipError_t launch_quantize_rows(const float* X, int8_t* Q, float* row_scale, int M, int K, hipStream_t st);
 hipError_t launch_naive(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, hipStream_t st);
 // 2-bit weight format on the device (bitpack_kernels.hip): `size` weights <-> size/4 packed bytes.
 hipError_t launch_pack(uint8_t* packed, const int8_t* w, size_t size, hipStream_t st);

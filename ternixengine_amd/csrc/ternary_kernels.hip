@@ -42,6 +42,7 @@ namespace ternix_hip {
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ v4i mfma_i8(v4i a, v4i b, v4i c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
@@ -69,6 +70,20 @@ __device__ __forceinline__ void transpose4x4(uint32_t r0, uint32_t r1, uint32_t 
 __device__ __forceinline__ int xcd_linear(int id, int total) {
     const int q = total >> 3, r = total & 7, x = id & 7;
     return x * q + min(x, r) + (id >> 3);
+}
+
+// Dequantising store of four consecutive outputs of one row: y = (float)c * (rs[row] * ws), the scale
+// product rounded once, then one rounding per output (the CPU oracle uses the same two steps).
+__device__ __forceinline__ void store_scaled(const OutScale& os, int row, int N, int col, v4i c, int vec) {
+    const float f = os.rs[row] * os.ws;
+    const v4f y = {(float)c[0] * f, (float)c[1] * f, (float)c[2] * f, (float)c[3] * f};
+    float* out = os.Y + (size_t)row * (size_t)N + col;
+    if (vec) {
+        __builtin_nontemporal_store(y, reinterpret_cast<v4f*>(out));
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) out[j] = y[j];
+    }
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -171,6 +186,7 @@ struct SkinnyArgs {
     int vec_store;        // C is 16-byte aligned
     int aligned_w;        // generic kernel: NB % 4 == 0 and W 4-byte aligned
     int aligned_a;        // generic kernel: K % 16 == 0 and A 16-byte aligned
+    OutScale os;          // SK_STORE: dequantised float output instead of C when os.Y is set
 };
 
 // One k-step of MFMA work for one 16-row x 4-byte-column block: raw[r] is the dword of row r.
@@ -285,6 +301,12 @@ __device__ __forceinline__ void skinny_epilogue(const SkinnyArgs& args, int32_t*
             for (int g = 0; g < G; ++g) {
                 const int bcol = tile_bc + 64 * (g >> 2) + 4 * q + (g & 3);
                 if (bcol >= NB) continue;
+                if (args.mode == SK_STORE && args.os.Y) {
+                    store_scaled(args.os, row, N, 4 * bcol,
+                                 v4i{val[t][g][0][i], val[t][g][1][i], val[t][g][2][i], val[t][g][3][i]},
+                                 args.vec_store);
+                    continue;
+                }
                 int32_t* out = out_base + (size_t)row * (size_t)N + 4 * bcol;
                 if (args.mode == SK_ATOMIC) {
 #pragma unroll
@@ -620,7 +642,7 @@ template <int BM, int BNB, bool ALIGNED_W, bool ALIGNED_A>
 __global__ __launch_bounds__(GM_THREADS) void gemm_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ B,
                                                           int32_t* __restrict__ C, int M, int K, int N,
                                                           int tiles_n, int k_begin, int k_end, int accumulate,
-                                                          int vec_store) {
+                                                          int vec_store, OutScale os) {
     constexpr int WM = BM / 2;            // rows per wave
     constexpr int WB = BNB / 2;           // byte-columns per wave
     constexpr int MT = WM / 16;           // m-tiles per wave
@@ -761,6 +783,10 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_kernel(const int8_t* __restri
                 const int bcol = bc0 + wn * WB + g * 16 + q;
                 if (bcol >= NB) continue;
                 v4i v = {acc[t][g][0][i] >> 6, acc[t][g][1][i] >> 6, acc[t][g][2][i] >> 6, acc[t][g][3][i] >> 6};
+                if (os.Y) {  // dequantised float output: y = c * (row_scale[row] * w_scale)
+                    store_scaled(os, row, N, 4 * bcol, v, vec_store);
+                    continue;
+                }
                 int32_t* out = C + (size_t)row * (size_t)N + 4 * bcol;
                 if (vec_store) {
                     if (accumulate) v += *reinterpret_cast<const v4i*>(out);
@@ -829,7 +855,8 @@ __device__ __forceinline__ int gf_swz_w(int r) { return ((r >> 1) & 3) ^ ((r >> 
 template <int BM, int WGN, int NS, int BK>
 __global__ __launch_bounds__(GF_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
 void gemm_fast_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ B, int32_t* __restrict__ C, int M,
-                      int K, int N, int tiles_n, int k_begin, int k_end, int accumulate, int vec_store) {
+                      int K, int N, int tiles_n, int k_begin, int k_end, int accumulate, int vec_store,
+                      OutScale os) {
     constexpr int WGM = 8 / WGN;             // waves along M
     constexpr int WM = BM / WGM;             // rows per wave
     constexpr int MT = WM / 16;              // m-tiles per wave
@@ -994,6 +1021,10 @@ void gemm_fast_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ 
             for (int g = 0; g < GT; ++g) {
                 const int bcol = bc0 + (wn * GT + g) * 16 + q;
                 v4i v = {acc[t][g][0][i] >> 6, acc[t][g][1][i] >> 6, acc[t][g][2][i] >> 6, acc[t][g][3][i] >> 6};
+                if (os.Y) {  // dequantised float output: y = c * (row_scale[row] * w_scale)
+                    store_scaled(os, row, N, 4 * bcol, v, vec_store);
+                    continue;
+                }
                 int32_t* out = C + (size_t)row * (size_t)N + 4 * bcol;
                 if (vec_store) {
                     if (accumulate) v += *reinterpret_cast<const v4i*>(out);
@@ -1040,7 +1071,8 @@ struct PipeFrag {
 template <int BM, int WGN, int NS, int BK>
 __global__ __launch_bounds__(GF_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
 void gemm_pipe_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ B, int32_t* __restrict__ C, int M,
-                      int K, int N, int tiles_n, int k_begin, int k_end, int accumulate, int vec_store) {
+                      int K, int N, int tiles_n, int k_begin, int k_end, int accumulate, int vec_store,
+                      OutScale os) {
     constexpr int WGM = 8 / WGN;
     constexpr int WM = BM / WGM;
     constexpr int MT = WM / 16;
@@ -1235,6 +1267,10 @@ void gemm_pipe_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ 
             for (int g = 0; g < GT; ++g) {
                 const int bcol = bc0 + (wn * GT + g) * 16 + q;
                 v4i v = {acc[t][g][0][i] >> 6, acc[t][g][1][i] >> 6, acc[t][g][2][i] >> 6, acc[t][g][3][i] >> 6};
+                if (os.Y) {  // dequantised float output: y = c * (row_scale[row] * w_scale)
+                    store_scaled(os, row, N, 4 * bcol, v, vec_store);
+                    continue;
+                }
                 int32_t* out = C + (size_t)row * (size_t)N + 4 * bcol;
                 if (vec_store) {
                     if (accumulate) v += *reinterpret_cast<const v4i*>(out);
@@ -1277,7 +1313,8 @@ __global__ __launch_bounds__(256) void zero_kernel(int32_t* __restrict__ C, size
 // memory round trip for up to 64 splits), then add in LDS.  Integer addition is exact, so the order
 // does not change the result.
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const int32_t* __restrict__ P, int32_t* __restrict__ C,
-                                                            size_t n4, int splits, int vec_store) {
+                                                            size_t n4, int splits, int vec_store, OutScale os,
+                                                            int N) {
     __shared__ v4i part[3][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const size_t i = (size_t)blockIdx.x * 64 + lane;
@@ -1298,6 +1335,11 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const int32_t* __res
     __syncthreads();
     if (wave != 0 || i >= n4) return;
     sum += part[0][lane] + part[1][lane] + part[2][lane];
+    if (os.Y) {
+        const size_t e = 4 * i;  // N % 4 == 0: the four outputs share a row
+        store_scaled(os, (int)(e / (size_t)N), N, (int)(e % (size_t)N), sum, vec_store);
+        return;
+    }
     if (vec_store) {
         reinterpret_cast<v4i*>(C)[i] = sum;
     } else {
@@ -1324,20 +1366,91 @@ hipError_t launch_fast_kw(const SkinnyArgs& a, int kw, dim3 grid, hipStream_t st
 
 template <int BM, int BNB>
 hipError_t launch_gemm_t(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, bool aw, bool aa,
-                         int kb, int ke, int acc, hipStream_t st) {
+                         int kb, int ke, int acc, hipStream_t st, const OutScale& os) {
     const int NB = N >> 2;
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (NB + BNB - 1) / BNB;
     const dim3 grid(tiles_m * tiles_n), block(GM_THREADS);
-    const int vs = ((uintptr_t)C % 16) == 0;
+    const int vs = ((uintptr_t)(os.Y ? (const void*)os.Y : (const void*)C) % 16) == 0;
     if (aw && aa)
-        hipLaunchKernelGGL((gemm_kernel<BM, BNB, true, true>), grid, block, 0, st, A, B, C, M, K, N, tiles_n, kb, ke, acc, vs);
+        hipLaunchKernelGGL((gemm_kernel<BM, BNB, true, true>), grid, block, 0, st, A, B, C, M, K, N, tiles_n, kb, ke, acc, vs, os);
     else if (aw)
-        hipLaunchKernelGGL((gemm_kernel<BM, BNB, true, false>), grid, block, 0, st, A, B, C, M, K, N, tiles_n, kb, ke, acc, vs);
+        hipLaunchKernelGGL((gemm_kernel<BM, BNB, true, false>), grid, block, 0, st, A, B, C, M, K, N, tiles_n, kb, ke, acc, vs, os);
     else if (aa)
-        hipLaunchKernelGGL((gemm_kernel<BM, BNB, false, true>), grid, block, 0, st, A, B, C, M, K, N, tiles_n, kb, ke, acc, vs);
+        hipLaunchKernelGGL((gemm_kernel<BM, BNB, false, true>), grid, block, 0, st, A, B, C, M, K, N, tiles_n, kb, ke, acc, vs, os);
     else
-        hipLaunchKernelGGL((gemm_kernel<BM, BNB, false, false>), grid, block, 0, st, A, B, C, M, K, N, tiles_n, kb, ke, acc, vs);
+        hipLaunchKernelGGL((gemm_kernel<BM, BNB, false, false>), grid, block, 0, st, A, B, C, M, K, N, tiles_n, kb, ke, acc, vs, os);
     return hipGetLastError();
+}
+
+// ------------------------------------------------------------------------------------------------
+// Activation quantisation and dequantisation (the steps either side of the matmul in a BitNet b1.58
+// layer; the reference leaves them as a stub, scripts/quantize.py:5, README.md:203).
+//   quantize_rows_kernel: one workgroup per row; absmax by a max-reduction (exact, order-free),
+//     s = 127 / max(absmax, 1e-5), q = clamp(rint(x * s), -128, 127) (round half to even),
+//     row_scale = max(absmax, 1e-5) / 127 -- IEEE division and multiplication, no contraction, so the
+//     CPU restatement reproduces every bit.
+//   dequant_kernel: y = (float)c * (row_scale[m] * w_scale) for an int32 C (Y may alias C: each
+//     element is read before the same element is written by the same thread).
+// Both are HBM streams (quantise: 4 bytes read + 1 written per element, twice over the row if it
+// does not stay in cache; dequantise: 4 + 4 bytes per output).
+// ------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void dequant_kernel(const int32_t* C, OutScale os, int N, size_t items, int vec) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= items) return;
+    const size_t e = 4 * i;
+    const int row = (int)(e / (size_t)N), col = (int)(e % (size_t)N);
+    v4i c;
+    if (vec) {
+        c = reinterpret_cast<const v4i*>(C)[i];
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) c[j] = C[e + j];
+    }
+    store_scaled(os, row, N, col, c, vec);
+}
+
+__global__ __launch_bounds__(256) void quantize_rows_kernel(const float* __restrict__ X, int8_t* __restrict__ Q,
+                                                            float* __restrict__ row_scale, int K, int vec) {
+    __shared__ float red[4];
+    const int m = blockIdx.x;
+    const float* x = X + (size_t)m * (size_t)K;
+    int8_t* q = Q + (size_t)m * (size_t)K;
+    float amax = 0.0f;
+    if (vec) {
+        for (int c = threadIdx.x; c < K / 4; c += 256) {
+            const v4f v = reinterpret_cast<const v4f*>(x)[c];
+            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+        }
+    } else {
+        for (int c = threadIdx.x; c < K; c += 256) amax = fmaxf(amax, fabsf(x[c]));
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float a = fmaxf(amax, 1e-5f);
+    const float s = 127.0f / a;
+    if (threadIdx.x == 0) row_scale[m] = a / 127.0f;
+    auto qz = [&](float v) -> int {
+        const float r = rintf(v * s);
+        return (int)fminf(fmaxf(r, -128.0f), 127.0f);
+    };
+    if (vec) {
+        for (int c = threadIdx.x; c < K / 16; c += 256) {
+            const v4f* src = reinterpret_cast<const v4f*>(x) + 4 * c;
+            v4i out;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const v4f v = src[u];
+                out[u] = (int)((uint32_t)(qz(v[0]) & 0xFF) | ((uint32_t)(qz(v[1]) & 0xFF) << 8) |
+                               ((uint32_t)(qz(v[2]) & 0xFF) << 16) | ((uint32_t)(qz(v[3]) & 0xFF) << 24));
+            }
+            reinterpret_cast<v4i*>(q)[c] = out;
+        }
+    } else {
+        for (int c = threadIdx.x; c < K; c += 256) q[c] = (int8_t)qz(x[c]);
+    }
 }
 
 }  // namespace
@@ -1357,17 +1470,19 @@ bool skinny_fast_ok(const int8_t* A, const uint8_t* B, int M, int K, int N, int 
 }
 
 hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int tb, int kw,
-                         int splits, int steps_per_split, int32_t* partials, hipStream_t st) {
+                         int splits, int steps_per_split, int32_t* partials, hipStream_t st, const OutScale& os) {
     const int NB = N >> 2;
     const int mode = splits <= 1 ? SK_STORE : (partials ? SK_PARTIAL : SK_ATOMIC);
     if (mode == SK_ATOMIC) {
         const hipError_t e = launch_zero(C, (size_t)M * (size_t)N, st);
         if (e != hipSuccess) return e;
     }
-    const int vec_store = ((uintptr_t)C % 16) == 0;
+    const bool scaled = os.Y != nullptr;
+    const int vec_store = ((uintptr_t)(scaled ? (const void*)os.Y : (const void*)C) % 16) == 0;
     const int aw = (NB % 4 == 0) && ((uintptr_t)B % 4 == 0);
     const int aa = (K % 16 == 0) && ((uintptr_t)A % 16 == 0);
-    SkinnyArgs a{A, B, C, partials, M, K, N, steps_per_split, splits, mode, vec_store, aw, aa};
+    SkinnyArgs a{A, B, C, partials, M, K, N, steps_per_split, splits, mode, vec_store, aw, aa,
+                 mode == SK_STORE ? os : OutScale{}};
     const int mt = M <= 16 ? 1 : 2;
     const int mgroups = (M + 16 * mt - 1) / (16 * mt);
     hipError_t e;
@@ -1403,15 +1518,17 @@ hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, i
         else hipLaunchKernelGGL((skinny_generic_kernel<2, false>), grid, dim3(64 * SK_WAVES), 0, st, a);
         e = hipGetLastError();
     }
-    if (e != hipSuccess || mode != SK_PARTIAL) return e;
+    if (e != hipSuccess) return e;
+    if (mode == SK_ATOMIC && scaled) return launch_dequant(C, os, M, N, st);  // C aliases os.Y
+    if (mode != SK_PARTIAL) return e;
     const size_t n4 = (size_t)M * (size_t)N / 4;
     hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n4 + 63) / 64)), dim3(256), 0, st, partials, C, n4,
-                       splits, vec_store);
+                       splits, vec_store, os, N);
     return hipGetLastError();
 }
 
 hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int k_begin, int k_end,
-                       int accumulate, hipStream_t st) {
+                       int accumulate, hipStream_t st, const OutScale& os) {
     const int NB = N >> 2;
     const char* force_generic = std::getenv("TERNIX_GEMM_GENERIC");
     const bool fast = (K % GF_BK == 0) && ((k_end - k_begin) % GF_BK == 0) && (k_begin % GF_BK == 0) &&
@@ -1419,7 +1536,7 @@ hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int
                       k_end > k_begin && (size_t)M * (size_t)K < ((size_t)1 << 32) &&
                       (size_t)GF_BK * (size_t)NB < ((size_t)1 << 32) && !(force_generic && force_generic[0] == '1');
     if (fast) {
-        const int vs = ((uintptr_t)C % 16) == 0;
+        const int vs = ((uintptr_t)(os.Y ? (const void*)os.Y : (const void*)C) % 16) == 0;
         const int tiles_n = NB / GF_BNB;
         const char* bm_env = std::getenv("TERNIX_GEMM_BM");
         const char* wgn_env = std::getenv("TERNIX_GEMM_WGN");
@@ -1451,7 +1568,7 @@ hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int
         if (pipe) {
 #define TX_GP_LAUNCH(BM_, WGN_, NS_, BK_)                                                                         \
     hipLaunchKernelGGL((gemm_pipe_kernel<BM_, WGN_, NS_, BK_>), grid, dim3(GF_THREADS), 0, st, A, B, C, M, K, N, \
-                       tiles_n, k_begin, k_end, accumulate, vs)
+                       tiles_n, k_begin, k_end, accumulate, vs, os)
             if (bm == 256 && wgn == 4) TX_GP_LAUNCH(256, 4, 3, 128);
             else if (bm == 256) TX_GP_LAUNCH(256, 2, 3, 128);
             else if (bk == 256 && wgn == 4) TX_GP_LAUNCH(128, 4, 3, 256);
@@ -1465,7 +1582,7 @@ hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int
         }
 #define TX_GF_LAUNCH(BM_, WGN_, NS_, BK_)                                                                         \
     hipLaunchKernelGGL((gemm_fast_kernel<BM_, WGN_, NS_, BK_>), grid, dim3(GF_THREADS), 0, st, A, B, C, M, K, N, \
-                       tiles_n, k_begin, k_end, accumulate, vs)
+                       tiles_n, k_begin, k_end, accumulate, vs, os)
         if (bm == 256 && wgn == 4) TX_GF_LAUNCH(256, 4, 3, 128);
         else if (bm == 256) TX_GF_LAUNCH(256, 2, 3, 128);
         else if (bk == 256 && wgn == 4) TX_GF_LAUNCH(128, 4, 3, 256);
@@ -1477,7 +1594,23 @@ hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int
     }
     const bool aw = (NB % 4 == 0) && ((uintptr_t)B % 4 == 0);
     const bool aa = (K % 16 == 0) && ((uintptr_t)A % 16 == 0);
-    return launch_gemm_t<128, 64>(A, B, C, M, K, N, aw, aa, k_begin, k_end, accumulate, st);
+    return launch_gemm_t<128, 64>(A, B, C, M, K, N, aw, aa, k_begin, k_end, accumulate, st, os);
+}
+
+hipError_t launch_dequant(const int32_t* C, const OutScale& os, int M, int N, hipStream_t st) {
+    const size_t n = (size_t)M * (size_t)N;
+    if (n == 0) return hipSuccess;
+    const int vec = ((uintptr_t)C % 16 == 0) && ((uintptr_t)os.Y % 16 == 0);
+    const size_t items = n / 4;
+    hipLaunchKernelGGL(dequant_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, st, C, os, N, items, vec);
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize_rows(const float* X, int8_t* Q, float* row_scale, int M, int K, hipStream_t st) {
+    if (M == 0) return hipSuccess;
+    const int vec = (K % 16 == 0) && ((uintptr_t)X % 16 == 0) && ((uintptr_t)Q % 16 == 0);
+    hipLaunchKernelGGL(quantize_rows_kernel, dim3((unsigned)M), dim3(256), 0, st, X, Q, row_scale, K, vec);
+    return hipGetLastError();
 }
 
 hipError_t launch_naive(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, hipStream_t st) {

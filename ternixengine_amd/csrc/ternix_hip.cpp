@@ -141,18 +141,20 @@ SkinnyPlan plan_skinny(int M, int K, int N) {
     return p;
 }
 
-hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int K, int N, hipStream_t st) {
+hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int K, int N, hipStream_t st,
+                      const ternix_hip::OutScale& os = ternix_hip::OutScale{}) {
     const SkinnyPlan p = plan_skinny(M, K, N);
     int32_t* partials = nullptr;
     if (p.splits > 1) {
         const size_t need = (size_t)p.splits * (size_t)M * (size_t)N * sizeof(int32_t);
         if (need <= kWorkspaceMax) partials = static_cast<int32_t*>(workspace(st, need));
     }
-    return ternix_hip::launch_skinny(dA, dB, dC, M, K, N, p.tb, p.kw, p.splits, p.sps, partials, st);
+    return ternix_hip::launch_skinny(dA, dB, dC, M, K, N, p.tb, p.kw, p.splits, p.sps, partials, st, os);
 }
 
-hipError_t run_gemm(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int K, int N, hipStream_t st) {
-    if (K == 0) return ternix_hip::launch_gemm(dA, dB, dC, M, K, N, 0, 0, 0, st);
+hipError_t run_gemm(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int K, int N, hipStream_t st,
+                    const ternix_hip::OutScale& os = ternix_hip::OutScale{}) {
+    if (K <= ternix_hip::kMaxKPerAccumulator) return ternix_hip::launch_gemm(dA, dB, dC, M, K, N, 0, K, 0, st, os);
     int acc = 0;
     for (long k0 = 0; k0 < K; k0 += ternix_hip::kMaxKPerAccumulator) {
         const long k1 = k0 + ternix_hip::kMaxKPerAccumulator < K ? k0 + ternix_hip::kMaxKPerAccumulator : K;
@@ -160,7 +162,8 @@ hipError_t run_gemm(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int
         if (e != hipSuccess) return e;
         acc = 1;
     }
-    return hipSuccess;
+    // Several K chunks accumulate int32 in dC (which aliases os.Y when dequantising); convert last.
+    return os.Y ? ternix_hip::launch_dequant(dC, os, M, N, st) : hipSuccess;
 }
 
 enum class Path { Auto, Skinny, Gemm, Naive };
@@ -254,6 +257,34 @@ done:
     if (dB) (void)hipFree(dB);
     if (dC) (void)hipFree(dC);
     return (int)e;
+}
+
+int ternix_hip_mul_mat_ternary_dequant(const int8_t* dA, const uint8_t* dB, float* dY, int64_t M, int64_t K,
+                                       int64_t N, const float* dRowScale, float w_scale, void* stream) {
+    bool trivial = false;
+    hipError_t e = validate(dA, dB, dY, M, K, N, &trivial);
+    if (e != hipSuccess) return (int)e;
+    if (trivial) return (int)hipSuccess;
+    if (dRowScale == nullptr) return (int)hipErrorInvalidValue;
+    const int m = (int)M, k = (int)K, n = (int)N;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    ternix_hip::OutScale os;
+    os.Y = dY;
+    os.rs = dRowScale;
+    os.ws = w_scale;
+    // The int32 C never exists in memory on the fused paths; where one is needed (atomic split-K, K
+    // chunks) it is kept in dY itself (same size) and converted in place.
+    int32_t* c_alias = reinterpret_cast<int32_t*>(dY);
+    e = m <= kSkinnyMaxM ? run_skinny(dA, dB, c_alias, m, k, n, st, os) : run_gemm(dA, dB, c_alias, m, k, n, st, os);
+    return (int)e;
+}
+
+int ternix_hip_quantize_activations(const float* dX, int8_t* dQ, float* dRowScale, int64_t M, int64_t K,
+                                    void* stream) {
+    if (M < 0 || K < 0 || M > INT_MAX || K > INT_MAX) return (int)hipErrorInvalidValue;
+    if (M == 0) return (int)hipSuccess;
+    if (dRowScale == nullptr || (K > 0 && (dX == nullptr || dQ == nullptr))) return (int)hipErrorInvalidValue;
+    return (int)ternix_hip::launch_quantize_rows(dX, dQ, dRowScale, (int)M, (int)K, static_cast<hipStream_t>(stream));
 }
 
 int ternix_hip_pack_ternary_weights(uint8_t* dPacked, const int8_t* dW, size_t size, void* stream) {
