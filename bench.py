@@ -42,7 +42,7 @@ def parse():
                     help="untimed sustained load before each GPU measurement (clock ramp)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["all", "gemv", "gemm", "bigm1", "pack", "layer"], default="all")
+    ap.add_argument("--only", choices=["all", "gemv", "gemm", "bigm1", "pack", "layer", "ffn"], default="all")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run 4 device-to-device copies of 256 MiB (the runtime's copy kernel), the "
                          "known-size reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -289,6 +289,39 @@ def bench_layer(args, stream, lib):
     return out
 
 
+def bench_ffn(args, stream, lib):
+    """Decode feed-forward block of the cfg2 model shape (hidden 2560, intermediate 6912, M=1):
+    RMSNorm+quantise, gate/up GEMV (2560 x 13824) with SwiGLU fused, requantise, down GEMV
+    (6912 x 2560) dequantised -- four launches per block, weights rotating over >= 512 MiB."""
+    from ternixengine_amd import hip_runtime as hr
+    m, h, f = 1, 2560, 6912
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((m, h)).astype(np.float32)
+    g = np.ones(h, np.float32)
+    wgu = rng.integers(0, 256, size=(h, 2 * f // 4), dtype=np.uint16).astype(np.uint8) & 0x77  # codes 00/01/11
+    wd = rng.integers(0, 256, size=(f, h // 4), dtype=np.uint16).astype(np.uint8) & 0x77
+    per = wgu.nbytes + wd.nbytes
+    copies = max(2, -(-POOL_MIN_BYTES // per))
+    dgu = [hr.DeviceBuffer.from_array(wgu) for _ in range(copies)]
+    dd = [hr.DeviceBuffer.from_array(wd) for _ in range(copies)]
+    dx, dg, dy = hr.DeviceBuffer.from_array(x), hr.DeviceBuffer.from_array(g), hr.DeviceBuffer(4 * m * h)
+    nws = lib.ternix_hip_ffn_workspace_size(m, h, f)
+    dws = hr.DeviceBuffer(nws)
+
+    def one(i):
+        st = lib.ternix_hip_ffn_forward(dy.value, dx.value, dg.value, 1e-5, dgu[i % copies].value, 0.02,
+                                        dd[i % copies].value, 0.02, m, h, f, dws.value, nws, stream.handle)
+        if st != 0:
+            raise RuntimeError(f"ffn failed: {st}")
+
+    prewarm(one, args.prewarm_s / 2, stream)
+    ms = time_launches(one, args.steps, args.warmup, stream)
+    y = dy.download(np.float32, (m, h))
+    moved = per + 4 * m * h * 2 + 4 * h
+    return {"us_per_block": ms / args.steps * 1e3, "weight_bytes": per,
+            "gbs": moved / (ms / args.steps * 1e-3) / 1e9, "finite": bool(np.isfinite(y).all())}
+
+
 def cpu_baseline(seconds):
     """Reference avx2_blocked (oracle/_ref) or the oracle's restatement, one thread, on the cfg2 pair."""
     from ternixengine_amd import configs
@@ -342,6 +375,8 @@ def main():
         res["pack"] = bench_pack(args, stream, lib)
     if args.only in ("all", "layer"):
         res["layer"] = bench_layer(args, stream, lib)
+    if args.only in ("all", "ffn"):
+        res["ffn"] = bench_ffn(args, stream, lib)
     g = res.get("gemv")
     line = {
         "metric": METRIC,
@@ -385,6 +420,8 @@ def main():
                                "frac": round(pk["gbs"] / HBM_PEAK_GBS, 4), "verified": pk["verified"]}
     if "layer" in res:
         line["layer_boundary"] = {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in res["layer"].items()}
+    if "ffn" in res:
+        line["ffn_decode"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in res["ffn"].items()}
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
         line["cpu_baseline"]["value"] = round(line["cpu_baseline"]["value"], 3)

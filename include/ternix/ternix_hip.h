@@ -142,6 +142,47 @@ int ternix_hip_mul_mat_ternary_dequant(const int8_t* dA, const uint8_t* dB, floa
  * Returns 0, or 1 for a size that is not a multiple of 4 or a NULL pointer. */
 int ternix_quantize_weights_absmean(uint8_t* packed, float* w_scale, const float* W, size_t size);
 
+/* ---- feed-forward block on the device (asynchronous on `stream`) ---- */
+
+/* rms_norm_avx2 / rms_norm_scalar of reference include/ternix/simd_math.hpp:8-10
+ * (src/simd_math.cpp:7-38) applied to each of `rows` rows of `size` floats:
+ * out = in * inv * weight, inv = 1 / sqrt(sum(in^2) / size + eps).  The sum of squares is
+ * a parallel reduction: results match the reference to float rounding (its own
+ * scalar-vs-AVX2 tolerance is 1e-4 relative). */
+int ternix_hip_rms_norm(float* dOut, const float* dIn, const float* dWeight, int64_t rows, int64_t size, float eps,
+                        void* stream);
+/* swiglu of reference include/ternix/simd_math.hpp:11-12 (src/simd_math.cpp:40-46):
+ * out[i] = silu(in[2i]) * in[2i+1], silu(g) = g / (1 + exp(-g)), for i < size / 2. */
+int ternix_hip_swiglu(float* dOut, const float* dIn, int64_t size, void* stream);
+/* RMSNorm fused with ternix_hip_quantize_activations: each normalised row is quantised
+ * straight to int8 (no float output). */
+int ternix_hip_rms_norm_quantize(int8_t* dQ, float* dRowScale, const float* dIn, const float* dWeight, int64_t rows,
+                                 int64_t size, float eps, void* stream);
+/* Up-projection with dequantisation and SwiGLU fused into its output: the N output columns
+ * are interleaved (gate, up) pairs, dH is M x N/2 fp32 with
+ *   dH[m][i] = silu(y[m][2i]) * y[m][2i+1],  y = (float)C * (dRowScale[m] * w_scale).
+ * dScratch (M x N int32, may be NULL) is used only when the split-K or K-chunk path cannot
+ * fuse the epilogue (first use of a shape inside graph capture, K > 131008); such a call
+ * with dScratch == NULL returns hipErrorInvalidValue. */
+int ternix_hip_mul_mat_ternary_swiglu(const int8_t* dA, const uint8_t* dB, float* dH, int64_t M, int64_t K,
+                                      int64_t N, const float* dRowScale, float w_scale, int32_t* dScratch,
+                                      void* stream);
+/* Bytes of device workspace ternix_hip_ffn_forward needs for M rows, hidden size H and
+ * intermediate size F. */
+size_t ternix_hip_ffn_workspace_size(int64_t M, int64_t H, int64_t F);
+/* One BitNet-style feed-forward block, four launches on `stream`:
+ *   q1, rs1 = rms_norm_quantize(dX, dNormWeight, eps)                  [M x H]
+ *   h       = swiglu matmul(q1, dWgu: H x 2F packed, interleaved gate/up columns, ws_gu)
+ *   q2, rs2 = quantize_activations(h)                                  [M x F]
+ *   dY      = dequant matmul(q2, dWd: F x H packed, ws_d)              [M x H] fp32
+ * H % 4 == 0, F % 2 == 0; dWorkspace is 256-byte aligned with at least
+ * ternix_hip_ffn_workspace_size(M, H, F) bytes.  No reference counterpart (the reference's
+ * TransformerLayer::forward is a stub, README.md:204); its pieces mirror simd_math.hpp and the
+ * matmul entry points above. */
+int ternix_hip_ffn_forward(float* dY, const float* dX, const float* dNormWeight, float eps, const uint8_t* dWgu,
+                           float ws_gu, const uint8_t* dWd, float ws_d, int64_t M, int64_t H, int64_t F,
+                           void* dWorkspace, size_t workspace_bytes, void* stream);
+
 /* ---- weight format on the device (asynchronous on `stream`) ---- */
 
 /* pack_ternary_weights on device memory (reference src/bitpack.cpp:5-15, same

@@ -1,5 +1,5 @@
 // ref_shim.cpp -- C-ABI wrappers around the reference's own CPU sources
-// (/root/reference/src/mul_mat_ternary.cpp and src/bitpack.cpp), compiled
+// (/root/reference/src/mul_mat_ternary.cpp, src/bitpack.cpp, src/simd_math.cpp), compiled
 // unchanged by oracle/Makefile into oracle/_ref/libternix_ref.so.
 // TEST INFRASTRUCTURE ONLY: used to write golden vectors (tests/golden) and as
 // bench.py's "reference" CPU baseline; the product never loads it.
@@ -10,6 +10,7 @@
 
 #include "ternix/bitpack.hpp"
 #include "ternix/mul_mat_ternary.h"
+#include "ternix/simd_math.hpp"
 
 extern "C" {
 
@@ -24,6 +25,13 @@ void ref_mm_scalar(const int8_t* A, const uint8_t* B, int32_t* C, size_t M, size
 void ref_mm_avx2(const int8_t* A, const uint8_t* B, int32_t* C, size_t M, size_t K, size_t N) {
     ternix::mul_mat_ternary_avx2(A, B, C, M, K, N);
 }
+void ref_rms_norm_scalar(float* out, const float* in, const float* w, size_t n, float eps) {
+    ternix::rms_norm_scalar(out, in, w, n, eps);
+}
+void ref_rms_norm_avx2(float* out, const float* in, const float* w, size_t n, float eps) {
+    ternix::rms_norm_avx2(out, in, w, n, eps);
+}
+void ref_swiglu(float* out, const float* in, size_t n) { ternix::swiglu(out, in, n); }
 void ref_mm_avx2_blocked(const int8_t* A, const uint8_t* B, int32_t* C, size_t M, size_t K, size_t N) {
     ternix::mul_mat_ternary_avx2_blocked(A, B, C, M, K, N);
 }

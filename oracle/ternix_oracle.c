@@ -252,3 +252,19 @@ float oracle_quantize_weights_absmean(int8_t* Wq, const float* W, size_t size) {
     }
     return gamma;
 }
+
+/* src/simd_math.cpp:7-12 -- sequential float sum of squares, inv = 1 / sqrt(mean + eps). */
+void oracle_rms_norm(float* out, const float* in, const float* weight, size_t size, float eps) {
+    float sum_sq = 0.0f;
+    for (size_t i = 0; i < size; ++i) sum_sq += in[i] * in[i];
+    const float inv = 1.0f / sqrtf(sum_sq / (float)size + eps);
+    for (size_t i = 0; i < size; ++i) out[i] = in[i] * inv * weight[i];
+}
+
+/* src/simd_math.cpp:40-46 -- interleaved (gate, up) pairs. */
+void oracle_swiglu(float* out, const float* in, size_t size) {
+    for (size_t i = 0; i + 1 < size; i += 2) {
+        const float x = in[i], y = in[i + 1];
+        out[i / 2] = (x / (1.0f + expf(-x))) * y;
+    }
+}

@@ -18,6 +18,8 @@
  *   oracle_mm_avx2_blocked     src/mul_mat_ternary.cpp:107-152
  *   oracle_gemm_unpacked       tests/test_ternary_matmul.cpp:31-39 (the
  *                              closed-form int32 GEMM on unpacked weights)
+ *   oracle_rms_norm            src/simd_math.cpp:7-12 (rms_norm_scalar)
+ *   oracle_swiglu              src/simd_math.cpp:40-46
  *
  * Parity pinning (how each function is checked, tests/test_oracle.py):
  *   - pack/unpack: known answer {1,0,-1,1,-1,0,1,0} -> {0x71,0x13}
@@ -29,6 +31,9 @@
  *     compiled reference sources (oracle/_ref).
  *   - invalid code 0b10 (outside the domain): naive -> 0, scalar -> -2a,
  *     avx2 -> -a, each checked against the compiled reference's output.
+ *   - rms_norm / swiglu: the reference's known values (tests/test_simd_math.cpp:7-15,
+ *     :29-35) and bit equality with the compiled reference's rms_norm_scalar and
+ *     swiglu (oracle/_ref) on random inputs.
  *
  * Quantised layer boundary (no reference implementation: the reference leaves
  * weight and activation quantisation as a stub, scripts/quantize.py:5,
@@ -65,6 +70,9 @@ int oracle_mm_avx2(const int8_t* A, const uint8_t* Bp, int32_t* C, size_t M, siz
 int oracle_mm_avx2_blocked(const int8_t* A, const uint8_t* Bp, int32_t* C, size_t M, size_t K, size_t N);
 
 void oracle_gemm_unpacked(const int8_t* A, const int8_t* W, int32_t* C, size_t M, size_t K, size_t N);
+
+void oracle_rms_norm(float* out, const float* in, const float* weight, size_t size, float eps);
+void oracle_swiglu(float* out, const float* in, size_t size);
 
 void oracle_quantize_rows_absmax(const float* X, int8_t* Q, float* row_scale, size_t M, size_t K);
 void oracle_dequant(const int32_t* C, float* Y, const float* row_scale, float w_scale, size_t M, size_t N);

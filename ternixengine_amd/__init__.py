@@ -25,7 +25,8 @@ from . import _lib
 from ._lib import LibraryNotBuilt, load as _load  # noqa: F401
 
 __all__ = ["pack_ternary", "unpack_ternary", "ternary_matmul", "mul_mat_ternary", "pack_ternary_device",
-           "unpack_ternary_device", "quantize_weights_absmean", "quantize_activations", "ternary_matmul_dequant",
+           "unpack_ternary_device", "quantize_weights_absmean", "quantize_activations", "ternary_matmul_dequant", "rms_norm", "swiglu",
+           "ffn_forward",
            "has_cuda", "has_hip", "HIP_IMPLS", "ternix_error"]
 
 has_cuda = False
@@ -165,6 +166,60 @@ def ternary_matmul_dequant(a, b_packed, row_scale, w_scale):
         raise RuntimeError(f"HIP error: {ternix_error(status)}")
     hr.synchronize()
     return dy.download(np.float32, (m, n))
+
+
+def _check(status):
+    if status != 0:
+        if status == 1:
+            raise ValueError("arguments rejected (hipErrorInvalidValue)")
+        raise RuntimeError(f"HIP error: {ternix_error(status)}")
+
+
+def rms_norm(x, weight, eps=1e-5):
+    """Row-wise RMSNorm of fp32 (rows, size) on the GPU (reference rms_norm_avx2 per row)."""
+    from . import hip_runtime as hr
+    x = np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+    x2 = x.reshape(1, -1) if x.ndim == 1 else x
+    w = np.ascontiguousarray(np.asarray(weight, dtype=np.float32).reshape(-1))
+    rows, size = x2.shape
+    if w.shape[0] != size:
+        raise ValueError("weight must have one entry per column")
+    dx, dw, do = hr.DeviceBuffer.from_array(x2), hr.DeviceBuffer.from_array(w), hr.DeviceBuffer(max(x2.nbytes, 4))
+    _check(_load().ternix_hip_rms_norm(do.value, dx.value, dw.value, rows, size, float(eps), None))
+    hr.synchronize()
+    return do.download(np.float32, x2.shape).reshape(x.shape)
+
+
+def swiglu(x):
+    """Reference swiglu on the GPU: interleaved (gate, up) pairs of a flat fp32 array -> size//2 outputs."""
+    from . import hip_runtime as hr
+    x = np.ascontiguousarray(np.asarray(x, dtype=np.float32).reshape(-1))
+    dx, do = hr.DeviceBuffer.from_array(x), hr.DeviceBuffer(max(4 * (x.size // 2), 4))
+    _check(_load().ternix_hip_swiglu(do.value, dx.value, x.size, None))
+    hr.synchronize()
+    return do.download(np.float32, (x.size // 2,))
+
+
+def ffn_forward(x, norm_weight, eps, w_gateup_packed, ws_gateup, w_down_packed, ws_down):
+    """One feed-forward block on the GPU (see ternix_hip_ffn_forward): x (M, H) fp32 -> (M, H) fp32,
+    w_gateup_packed (H, 2F/4) with interleaved gate/up columns, w_down_packed (F, H/4)."""
+    from . import hip_runtime as hr
+    x = np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+    g = np.ascontiguousarray(np.asarray(norm_weight, dtype=np.float32).reshape(-1))
+    wgu = np.ascontiguousarray(np.asarray(w_gateup_packed, dtype=np.uint8))
+    wd = np.ascontiguousarray(np.asarray(w_down_packed, dtype=np.uint8))
+    m, h = x.shape
+    f = wgu.shape[1] * 2
+    if wgu.shape[0] != h or wd.shape != (f, h // 4) or g.shape[0] != h:
+        raise ValueError("inconsistent FFN shapes")
+    lib = _load()
+    nws = lib.ternix_hip_ffn_workspace_size(m, h, f)
+    dx, dg, dgu, dd = (hr.DeviceBuffer.from_array(a) for a in (x, g, wgu, wd))
+    dy, dws = hr.DeviceBuffer(max(x.nbytes, 4)), hr.DeviceBuffer(max(nws, 256))
+    _check(lib.ternix_hip_ffn_forward(dy.value, dx.value, dg.value, float(eps), dgu.value, float(ws_gateup),
+                                      dd.value, float(ws_down), m, h, f, dws.value, nws, None))
+    hr.synchronize()
+    return dy.download(np.float32, (m, h))
 
 
 def mul_mat_ternary(dA, dB, dC, M, K, N, stream=None, path="auto"):

@@ -53,6 +53,17 @@ def load():
     lib.ternix_hip_mul_mat_ternary_dequant.restype = ctypes.c_int
     lib.ternix_quantize_weights_absmean.argtypes = [vp, vp, vp, ctypes.c_size_t]
     lib.ternix_quantize_weights_absmean.restype = ctypes.c_int
+    f32 = ctypes.c_float
+    lib.ternix_hip_rms_norm.argtypes = [vp, vp, vp, i64, i64, f32, vp]
+    lib.ternix_hip_rms_norm_quantize.argtypes = [vp, vp, vp, vp, i64, i64, f32, vp]
+    lib.ternix_hip_swiglu.argtypes = [vp, vp, i64, vp]
+    lib.ternix_hip_mul_mat_ternary_swiglu.argtypes = [vp, vp, vp, i64, i64, i64, vp, f32, vp, vp]
+    lib.ternix_hip_ffn_workspace_size.argtypes = [i64, i64, i64]
+    lib.ternix_hip_ffn_workspace_size.restype = ctypes.c_size_t
+    lib.ternix_hip_ffn_forward.argtypes = [vp, vp, vp, f32, vp, f32, vp, f32, i64, i64, i64, vp, ctypes.c_size_t, vp]
+    for name in ("ternix_hip_rms_norm", "ternix_hip_rms_norm_quantize", "ternix_hip_swiglu",
+                 "ternix_hip_mul_mat_ternary_swiglu", "ternix_hip_ffn_forward"):
+        getattr(lib, name).restype = ctypes.c_int
     u64 = ctypes.c_uint64
     lib.ternix_synth_u64.argtypes = [u64, u64, u64]
     lib.ternix_synth_u64.restype = u64

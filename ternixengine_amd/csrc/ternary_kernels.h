@@ -14,10 +14,13 @@ constexpr int kMaxKPerAccumulator = (1 << 17) - 128;
 
 // Optional dequantised output of a matmul launch: when Y is set the kernels write
 // Y[m][n] = (float)C[m][n] * (rs[m] * ws) (fp32, row-major M x N) instead of the int32 C.
+// With swiglu set, Y is M x N/2: each interleaved (gate, up) column pair of the dequantised product
+// becomes silu(gate) * up (reference swiglu, src/simd_math.cpp:40-46); Y must not alias C then.
 struct OutScale {
     float* Y = nullptr;
     const float* rs = nullptr;  // per-row activation scale [M]
     float ws = 0.0f;            // weight scale
+    int swiglu = 0;
 };
 
 hipError_t launch_zero(int32_t* C, size_t n, hipStream_t st);
@@ -46,6 +49,14 @@ hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int
                        int k_end, int accumulate, hipStream_t st, const OutScale& os = OutScale{});
 // In-place-capable conversion of an int32 C to the dequantised float Y (Y may alias C).
 hipError_t launch_dequant(const int32_t* C, const OutScale& os, int M, int N, hipStream_t st);
+// Per-row RMSNorm (reference rms_norm_scalar, src/simd_math.cpp:7-12): out = x * inv * w with
+// inv = 1 / sqrt(sum(x^2) / K + eps); with Q set, the normalised row is quantised like
+// launch_quantize_rows instead of stored (out may then be NULL).
+hipError_t launch_rmsnorm(const float* X, const float* W, float eps, float* out, int8_t* Q, float* row_scale, int M,
+                          int K, hipStream_t st);
+// Reference swiglu (src/simd_math.cpp:40-46) over each row of interleaved (gate, up) pairs:
+// out[m][i] = silu(in[m][2i]) * in[m][2i+1], `pairs` outputs per row.
+hipError_t launch_swiglu(const float* in, float* out, size_t pairs, hipStream_t st);
 // Per-row absmax int8 quantisation of fp32 activations: row_scale[m] = max(absmax_m, 1e-5) / 127,
 // Q = clamp(rint(X * (127 / max(absmax_m, 1e-5))), -128, 127).
 hipError_t launch_quantize_rows(const float* X, int8_t* Q, float* row_scale, int M, int K, hipStream_t st);

@@ -74,9 +74,23 @@ __device__ __forceinline__ int xcd_linear(int id, int total) {
 
 // Dequantising store of four consecutive outputs of one row: y = (float)c * (rs[row] * ws), the scale
 // product rounded once, then one rounding per output (the CPU oracle uses the same two steps).
+// With os.swiglu the four values are two interleaved (gate, up) pairs and the stored row is N/2 wide:
+// h[col/2 + p] = silu(y[2p]) * y[2p+1], silu(g) = g / (1 + exp(-g)) (reference src/simd_math.cpp:40-46).
+typedef float v2f __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ void store_scaled(const OutScale& os, int row, int N, int col, v4i c, int vec) {
     const float f = os.rs[row] * os.ws;
     const v4f y = {(float)c[0] * f, (float)c[1] * f, (float)c[2] * f, (float)c[3] * f};
+    if (os.swiglu) {
+        const v2f h = {(y[0] / (1.0f + expf(-y[0]))) * y[1], (y[2] / (1.0f + expf(-y[2]))) * y[3]};
+        float* out = os.Y + (size_t)row * (size_t)(N / 2) + col / 2;
+        if (vec) {
+            __builtin_nontemporal_store(h, reinterpret_cast<v2f*>(out));
+        } else {
+            out[0] = h[0];
+            out[1] = h[1];
+        }
+        return;
+    }
     float* out = os.Y + (size_t)row * (size_t)N + col;
     if (vec) {
         __builtin_nontemporal_store(y, reinterpret_cast<v4f*>(out));
@@ -1473,6 +1487,7 @@ hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, i
                          int splits, int steps_per_split, int32_t* partials, hipStream_t st, const OutScale& os) {
     const int NB = N >> 2;
     const int mode = splits <= 1 ? SK_STORE : (partials ? SK_PARTIAL : SK_ATOMIC);
+    if (mode == SK_ATOMIC && C == nullptr) return hipErrorInvalidValue;  // scaled call without int scratch
     if (mode == SK_ATOMIC) {
         const hipError_t e = launch_zero(C, (size_t)M * (size_t)N, st);
         if (e != hipSuccess) return e;
@@ -1519,7 +1534,7 @@ hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, i
         e = hipGetLastError();
     }
     if (e != hipSuccess) return e;
-    if (mode == SK_ATOMIC && scaled) return launch_dequant(C, os, M, N, st);  // C aliases os.Y
+    if (mode == SK_ATOMIC && scaled) return launch_dequant(C, os, M, N, st);  // C: alias of os.Y or scratch
     if (mode != SK_PARTIAL) return e;
     const size_t n4 = (size_t)M * (size_t)N / 4;
     hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n4 + 63) / 64)), dim3(256), 0, st, partials, C, n4,

@@ -155,6 +155,7 @@ hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
 hipError_t run_gemm(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int K, int N, hipStream_t st,
                     const ternix_hip::OutScale& os = ternix_hip::OutScale{}) {
     if (K <= ternix_hip::kMaxKPerAccumulator) return ternix_hip::launch_gemm(dA, dB, dC, M, K, N, 0, K, 0, st, os);
+    if (dC == nullptr) return hipErrorInvalidValue;  // scaled call without int scratch
     int acc = 0;
     for (long k0 = 0; k0 < K; k0 += ternix_hip::kMaxKPerAccumulator) {
         const long k1 = k0 + ternix_hip::kMaxKPerAccumulator < K ? k0 + ternix_hip::kMaxKPerAccumulator : K;
@@ -277,6 +278,109 @@ int ternix_hip_mul_mat_ternary_dequant(const int8_t* dA, const uint8_t* dB, floa
     int32_t* c_alias = reinterpret_cast<int32_t*>(dY);
     e = m <= kSkinnyMaxM ? run_skinny(dA, dB, c_alias, m, k, n, st, os) : run_gemm(dA, dB, c_alias, m, k, n, st, os);
     return (int)e;
+}
+
+int ternix_hip_mul_mat_ternary_swiglu(const int8_t* dA, const uint8_t* dB, float* dH, int64_t M, int64_t K,
+                                      int64_t N, const float* dRowScale, float w_scale, int32_t* dScratch,
+                                      void* stream) {
+    bool trivial = false;
+    hipError_t e = validate(dA, dB, dH, M, K, N, &trivial);
+    if (e != hipSuccess) return (int)e;
+    if (trivial) return (int)hipSuccess;
+    if (dRowScale == nullptr) return (int)hipErrorInvalidValue;
+    if (dScratch != nullptr && reinterpret_cast<uintptr_t>(dScratch) % alignof(int32_t) != 0)
+        return (int)hipErrorInvalidValue;
+    const int m = (int)M, k = (int)K, n = (int)N;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    ternix_hip::OutScale os;
+    os.Y = dH;
+    os.rs = dRowScale;
+    os.ws = w_scale;
+    os.swiglu = 1;
+    e = m <= kSkinnyMaxM ? run_skinny(dA, dB, dScratch, m, k, n, st, os) : run_gemm(dA, dB, dScratch, m, k, n, st, os);
+    return (int)e;
+}
+
+int ternix_hip_rms_norm(float* dOut, const float* dIn, const float* dWeight, int64_t rows, int64_t size, float eps,
+                        void* stream) {
+    if (rows < 0 || size < 0 || rows > INT_MAX || size > INT_MAX) return (int)hipErrorInvalidValue;
+    if (rows == 0 || size == 0) return (int)hipSuccess;
+    if (dOut == nullptr || dIn == nullptr || dWeight == nullptr) return (int)hipErrorInvalidValue;
+    return (int)ternix_hip::launch_rmsnorm(dIn, dWeight, eps, dOut, nullptr, nullptr, (int)rows, (int)size,
+                                           static_cast<hipStream_t>(stream));
+}
+
+int ternix_hip_rms_norm_quantize(int8_t* dQ, float* dRowScale, const float* dIn, const float* dWeight, int64_t rows,
+                                 int64_t size, float eps, void* stream) {
+    if (rows < 0 || size < 0 || rows > INT_MAX || size > INT_MAX) return (int)hipErrorInvalidValue;
+    if (rows == 0) return (int)hipSuccess;
+    if (dRowScale == nullptr || (size > 0 && (dQ == nullptr || dIn == nullptr || dWeight == nullptr)))
+        return (int)hipErrorInvalidValue;
+    return (int)ternix_hip::launch_rmsnorm(dIn, dWeight, eps, nullptr, dQ, dRowScale, (int)rows, (int)size,
+                                           static_cast<hipStream_t>(stream));
+}
+
+int ternix_hip_swiglu(float* dOut, const float* dIn, int64_t size, void* stream) {
+    if (size < 0) return (int)hipErrorInvalidValue;
+    if (size < 2) return (int)hipSuccess;
+    if (dOut == nullptr || dIn == nullptr) return (int)hipErrorInvalidValue;
+    return (int)ternix_hip::launch_swiglu(dIn, dOut, (size_t)size / 2, static_cast<hipStream_t>(stream));
+}
+
+namespace {
+
+// Feed-forward workspace: q1 [M][H] int8 | rs1 [M] | h [M][F] f32 | q2 [M][F] int8 | rs2 [M] |
+// scratch [M][2F] int32 (used only when a matmul cannot fuse its epilogue); 256-byte aligned regions.
+struct FfnLayout {
+    size_t q1, rs1, h, q2, rs2, scratch, total;
+};
+FfnLayout ffn_layout(int64_t M, int64_t H, int64_t F) {
+    auto up = [](size_t x) { return (x + 255) & ~size_t(255); };
+    FfnLayout l{};
+    size_t o = 0;
+    l.q1 = o; o = up(o + (size_t)M * (size_t)H);
+    l.rs1 = o; o = up(o + 4 * (size_t)M);
+    l.h = o; o = up(o + 4 * (size_t)M * (size_t)F);
+    l.q2 = o; o = up(o + (size_t)M * (size_t)F);
+    l.rs2 = o; o = up(o + 4 * (size_t)M);
+    l.scratch = o; o = up(o + 8 * (size_t)M * (size_t)F);
+    l.total = o;
+    return l;
+}
+
+}  // namespace
+
+size_t ternix_hip_ffn_workspace_size(int64_t M, int64_t H, int64_t F) {
+    if (M < 0 || H < 0 || F < 0) return 0;
+    return ffn_layout(M, H, F).total;
+}
+
+int ternix_hip_ffn_forward(float* dY, const float* dX, const float* dNormWeight, float eps, const uint8_t* dWgu,
+                           float ws_gu, const uint8_t* dWd, float ws_d, int64_t M, int64_t H, int64_t F,
+                           void* dWorkspace, size_t workspace_bytes, void* stream) {
+    if (M < 0 || H < 0 || F < 0 || M > INT_MAX || H > INT_MAX || 2 * F > INT_MAX) return (int)hipErrorInvalidValue;
+    if (H % 4 != 0 || F % 2 != 0) return (int)hipErrorInvalidValue;
+    if (M == 0 || H == 0) return (int)hipSuccess;
+    const FfnLayout l = ffn_layout(M, H, F);
+    if (dWorkspace == nullptr || workspace_bytes < l.total || reinterpret_cast<uintptr_t>(dWorkspace) % 256 != 0)
+        return (int)hipErrorInvalidValue;
+    if (dY == nullptr || dX == nullptr || dNormWeight == nullptr || (F > 0 && (dWgu == nullptr || dWd == nullptr)))
+        return (int)hipErrorInvalidValue;
+    char* ws = static_cast<char*>(dWorkspace);
+    int8_t* q1 = reinterpret_cast<int8_t*>(ws + l.q1);
+    float* rs1 = reinterpret_cast<float*>(ws + l.rs1);
+    float* h = reinterpret_cast<float*>(ws + l.h);
+    int8_t* q2 = reinterpret_cast<int8_t*>(ws + l.q2);
+    float* rs2 = reinterpret_cast<float*>(ws + l.rs2);
+    int32_t* scratch = reinterpret_cast<int32_t*>(ws + l.scratch);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    int s = ternix_hip_rms_norm_quantize(q1, rs1, dX, dNormWeight, M, H, eps, stream);
+    if (s != 0) return s;
+    s = ternix_hip_mul_mat_ternary_swiglu(q1, dWgu, h, M, H, 2 * F, rs1, ws_gu, scratch, stream);
+    if (s != 0) return s;
+    s = (int)ternix_hip::launch_quantize_rows(h, q2, rs2, (int)M, (int)F, st);
+    if (s != 0) return s;
+    return ternix_hip_mul_mat_ternary_dequant(q2, dWd, dY, M, F, H, rs2, ws_d, stream);
 }
 
 int ternix_hip_quantize_activations(const float* dX, int8_t* dQ, float* dRowScale, int64_t M, int64_t K,
