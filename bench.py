@@ -8,10 +8,12 @@ HBM, as decode over a model's layers does.  Effective bytes per GEMV = M*K + K*N
 the kernels run on, bracketing exactly `--steps` steps after `--warmup` untimed ones.
 
 Also reported on the same line: the prefill GEMM of configuration 4 (M=2048; ops = 2*M*N*K, against
-the int8 dense MFMA peak), the large-M=1 GEMV of configuration 5 (K=8192, N=28672), and the
-reference's own CPU kernel (mul_mat_ternary_avx2_blocked, compiled from the reference sources into
-oracle/_ref, or the plain-C restatement in oracle/ when that is absent) timed on this host on a
-bounded sample of the same workload.
+the int8 dense MFMA peak; `roofline_gemm`), the large-M=1 GEMV of configuration 5 (K=8192, N=28672),
+the device weight packer, the quantised layer boundary (activation quantisation, dequantising
+matmuls), the decode feed-forward block, and the reference's own CPU kernel
+(mul_mat_ternary_avx2_blocked, compiled from the reference sources into oracle/_ref, or the plain-C
+restatement in oracle/ when that is absent) timed on this host on a bounded sample of the same
+workload.  Every GPU measurement is preceded by about --prewarm-s seconds of untimed load (clock ramp).
 """
 import argparse
 import ctypes
@@ -410,6 +412,9 @@ def main():
                                "launch_us": round(b["launch_us"], 3), "verified": b["verified"]}
     if "gemm" in res:
         gm = res["gemm"]
+        line["roofline_gemm"] = {"bound": "mfma", "achieved": round(gm["tops"], 1), "peak": INT8_PEAK_TOPS,
+                                 "unit": "TFLOP/s", "frac": round(gm["frac"], 4), "traffic": None,
+                                 "kernel": "gemm_pipe_kernel / gemm_fast_kernel (cfg4, M=2048, int8 ops)"}
         line["gemm_m2048"] = {"tops": round(gm["tops"], 1), "peak": INT8_PEAK_TOPS, "unit": "TOPS",
                               "frac": round(gm["frac"], 4),
                               "shapes": [{k: (round(v, 3) if isinstance(v, float) else v) for k, v in s.items()}
