@@ -865,6 +865,11 @@ constexpr int GF_BNB = 64;
 
 __device__ __forceinline__ int gf_swz_a(int r) { return (r >> 1) & 7; }
 __device__ __forceinline__ int gf_swz_w(int r) { return ((r >> 1) & 3) ^ ((r >> 4) & 1); }
+// W swizzle for a given stage-row width: 64-byte rows as gf_swz_w; 32-byte rows (two chunks) keep the
+// 8 rows of one transposing read on distinct banks by their pitch alone and flip the chunk for the
+// second 16-row half of a wave's k-block, which is read in the same pass.
+template <int BNB>
+__device__ __forceinline__ int swz_w(int r) { return BNB == 64 ? gf_swz_w(r) : ((r >> 4) & 1); }
 
 template <int BM, int WGN, int NS, int BK>
 __global__ __launch_bounds__(GF_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
@@ -1082,22 +1087,25 @@ struct PipeFrag {
     uint64_t lo[GT], hi[GT];
 };
 
-template <int BM, int WGN, int NS, int BK>
-__global__ __launch_bounds__(GF_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
+template <int BM, int WGN, int NS, int BK, int NWV, int BNB>
+__global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2)))
 void gemm_pipe_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ B, int32_t* __restrict__ C, int M,
                       int K, int N, int tiles_n, int k_begin, int k_end, int accumulate, int vec_store,
                       OutScale os) {
-    constexpr int WGM = 8 / WGN;
+    constexpr int THR = 64 * NWV;           // threads per workgroup
+    constexpr int CW = BNB / 16;            // 16-byte chunks per W stage row
+    constexpr int WGM = NWV / WGN;
     constexpr int WM = BM / WGM;
     constexpr int MT = WM / 16;
-    constexpr int GT = 4 / WGN;
+    constexpr int GT = CW / WGN;
     constexpr int KS = BK / 64;
     constexpr int CPR = BK / 16;
     constexpr int A_STAGE = BM * BK;
-    constexpr int W_STAGE = BK * GF_BNB;
-    constexpr int NA = A_STAGE / 16 / GF_THREADS;
-    constexpr int NW = W_STAGE / 16 / GF_THREADS;
+    constexpr int W_STAGE = BK * BNB;
+    constexpr int NA = A_STAGE / 16 / THR;
+    constexpr int NW = W_STAGE / 16 / THR;
     static_assert(KS % 2 == 0, "fragment sets alternate per k-step");
+    static_assert(NA >= 1 && NW >= 1 && GT >= 1, "tile too small for the workgroup");
     __shared__ __attribute__((aligned(16))) int8_t sA0[A_STAGE];
     __shared__ __attribute__((aligned(16))) int8_t sA1[A_STAGE];
     __shared__ __attribute__((aligned(16))) int8_t sA2[A_STAGE];
@@ -1128,13 +1136,13 @@ void gemm_pipe_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ 
         tn = local / gm;
     }
     const int row0 = tm * BM;
-    const int bc0 = tn * GF_BNB;
+    const int bc0 = tn * BNB;
     const int nst = (k_end - k_begin) / BK;
 
     uint32_t a_off[NA];
 #pragma unroll
     for (int p = 0; p < NA; ++p) {
-        const int slot = (p * 8 + wave) * 64 + lane;
+        const int slot = (p * NWV + wave) * 64 + lane;
         const int r = slot / CPR, pos = slot % CPR;
         const int grow = min(row0 + r, M - 1);
         a_off[p] = (uint32_t)grow * (uint32_t)K + (uint32_t)(((pos & ~7) | ((pos & 7) ^ gf_swz_a(r))) * 16);
@@ -1142,20 +1150,20 @@ void gemm_pipe_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ 
     uint32_t w_off[NW];
 #pragma unroll
     for (int p = 0; p < NW; ++p) {
-        const int slot = (p * 8 + wave) * 64 + lane;
-        const int r = slot >> 2, pos = slot & 3;
-        w_off[p] = (uint32_t)r * (uint32_t)NB + (uint32_t)(bc0 + (pos ^ gf_swz_w(r)) * 16);
+        const int slot = (p * NWV + wave) * 64 + lane;
+        const int r = slot / CW, pos = slot % CW;
+        w_off[p] = (uint32_t)r * (uint32_t)NB + (uint32_t)(bc0 + (pos ^ swz_w<BNB>(r)) * 16);
     }
     auto issue = [&](int st, int buf) {
         const int sc = min(st, nst - 1);
         const int8_t* abase = A + k_begin + (size_t)sc * BK;
         int8_t* adst = stage_a(buf);
 #pragma unroll
-        for (int p = 0; p < NA; ++p) lds_dma16(abase + a_off[p], adst + (p * 8 + wave) * 1024);
+        for (int p = 0; p < NA; ++p) lds_dma16(abase + a_off[p], adst + (p * NWV + wave) * 1024);
         const uint8_t* wbase = B + (size_t)(k_begin + sc * BK) * (size_t)NB;
         uint8_t* wdst = stage_w(buf);
 #pragma unroll
-        for (int p = 0; p < NW; ++p) lds_dma16(wbase + w_off[p], wdst + (p * 8 + wave) * 1024);
+        for (int p = 0; p < NW; ++p) lds_dma16(wbase + w_off[p], wdst + (p * NWV + wave) * 1024);
     };
 
     // Per-lane fragment offsets inside a stage.  A: row wm*WM + 16t + q, chunk kk*4 + kb (the swizzle
@@ -1174,17 +1182,17 @@ void gemm_pipe_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ 
     for (int g = 0; g < GT; ++g) {
         const int cg = wn * GT + g;
         const int r0 = kb * 16 + (q >> 1);
-        w_lane[g] = (uint32_t)(r0 * GF_BNB + 16 * (cg ^ gf_swz_w(r0)) + 8 * (q & 1));
+        w_lane[g] = (uint32_t)(r0 * BNB + 16 * (cg ^ swz_w<BNB>(r0)) + 8 * (q & 1));
     }
     auto read = [&](PipeFrag<MT, GT>& f, int buf, int kk) {
         const uint32_t ab = lds_u32(stage_a(buf)) + a_lane[kk];
 #pragma unroll
         for (int t = 0; t < MT; ++t) f.a[t] = lds_read_b128_asm(ab + (uint32_t)(t * 16 * BK));
-        const uint32_t wb = lds_u32(stage_w(buf)) + (uint32_t)(kk * 64 * GF_BNB);
+        const uint32_t wb = lds_u32(stage_w(buf)) + (uint32_t)(kk * 64 * BNB);
 #pragma unroll
         for (int g = 0; g < GT; ++g) {
             f.lo[g] = lds_read_tr8_asm(wb + w_lane[g]);
-            f.hi[g] = lds_read_tr8_asm(wb + w_lane[g] + 8 * GF_BNB);
+            f.hi[g] = lds_read_tr8_asm(wb + w_lane[g] + 8 * BNB);
         }
     };
     // All LDS reads issued so far have returned; the empty asm statements tie each fragment register
@@ -1369,10 +1377,11 @@ hipError_t launch_fast_t(const SkinnyArgs& a, dim3 grid, hipStream_t st) {
     return hipGetLastError();
 }
 
-// PD (k-steps in flight per wave): 4 for 64-byte slabs, 2 for 128-byte slabs (register budget).
+// PD (k-steps in flight per wave): 2 (measured on MI355X: 17.9 us vs 18.8 us with 4 on cfg5 big; the
+// smaller ring also frees registers).
 template <int MT, int TB, bool LOW_M>
 hipError_t launch_fast_kw(const SkinnyArgs& a, int kw, dim3 grid, hipStream_t st) {
-    constexpr int PD = TB == 1 ? 4 : 2;
+    constexpr int PD = 2;
     if (kw >= 4) return launch_fast_t<MT, TB, 4, PD, LOW_M>(a, grid, st);
     if (kw == 2) return launch_fast_t<MT, TB, 2, PD, LOW_M>(a, grid, st);
     return launch_fast_t<MT, TB, 1, PD, LOW_M>(a, grid, st);
@@ -1575,18 +1584,16 @@ hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int
             const char* e = std::getenv("TERNIX_GEMM_PIPE");
             return e ? std::atoi(e) : -1;
         }();
-        const int pipe = pipe_env >= 0 ? pipe_env : (bm == 128 ? 1 : 0);
+        const int pipe = pipe_env >= 0 ? (pipe_env == 1 && bm == 256 ? 0 : pipe_env) : (bm == 128 ? 1 : 0);
         static const int pipe_ns = [] {
             const char* e = std::getenv("TERNIX_GEMM_NS");
             return e && std::atoi(e) == 4 ? 4 : 3;
         }();
         if (pipe) {
-#define TX_GP_LAUNCH(BM_, WGN_, NS_, BK_)                                                                         \
-    hipLaunchKernelGGL((gemm_pipe_kernel<BM_, WGN_, NS_, BK_>), grid, dim3(GF_THREADS), 0, st, A, B, C, M, K, N, \
-                       tiles_n, k_begin, k_end, accumulate, vs, os)
-            if (bm == 256 && wgn == 4) TX_GP_LAUNCH(256, 4, 3, 128);
-            else if (bm == 256) TX_GP_LAUNCH(256, 2, 3, 128);
-            else if (bk == 256 && wgn == 4) TX_GP_LAUNCH(128, 4, 3, 256);
+#define TX_GP_LAUNCH(BM_, WGN_, NS_, BK_)                                                                      \
+    hipLaunchKernelGGL((gemm_pipe_kernel<BM_, WGN_, NS_, BK_, 8, GF_BNB>), grid, dim3(GF_THREADS), 0, st, A, B, C, M, \
+                       K, N, tiles_n, k_begin, k_end, accumulate, vs, os)
+            if (bk == 256 && wgn == 4) TX_GP_LAUNCH(128, 4, 3, 256);
             else if (bk == 256) TX_GP_LAUNCH(128, 2, 3, 256);
             else if (wgn == 4 && pipe_ns == 4) TX_GP_LAUNCH(128, 4, 4, 128);
             else if (wgn == 4) TX_GP_LAUNCH(128, 4, 3, 128);

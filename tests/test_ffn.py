@@ -222,3 +222,34 @@ def test_ffn_validation():
     assert lib.ternix_hip_ffn_forward(None, None, None, 1e-5, None, 1.0, None, 1.0, 1, 8, 4, None, 0, None) == 1
     assert lib.ternix_hip_swiglu(None, None, 1, None) == 0
     assert lib.ternix_hip_rms_norm(None, None, None, 1, 4, 1e-5, None) == 1
+
+
+@gpu
+@pytest.mark.parametrize("shape", [(1, 2560, 6912), (4, 1024, 2048)])
+def test_gpu_ffn_graph_replays_match_eager(shape):
+    """ffn_forward recorded into a hipGraph on a fresh stream (its split-K matmuls are first used
+    inside the capture, so they take the zero-fill + atomic path through the caller's scratch) and
+    replayed several times, with eager work on another stream in between: every replay equals the
+    eager result (partial-sum path) bit for bit."""
+    from ternixengine_amd import hip_runtime as hr
+    m, hd, f = shape
+    log(f"[ffn graph] M={m} H={hd} F={f}")
+    rng = np.random.default_rng(17 + m)
+    x = rng.normal(0, 1, (m, hd)).astype(F32)
+    g = rng.normal(1, 0.1, hd).astype(F32)
+    t_gu, t_d = _ffn_weights(rng, hd, f)
+    wgu, wd = tx.pack_ternary(t_gu), tx.pack_ternary(t_d)
+    eager = tx.ffn_forward(x, g, 1e-5, wgu, 0.02, wd, 0.03)
+    lib = tx._load()
+    nws = lib.ternix_hip_ffn_workspace_size(m, hd, f)
+    dx, dg, dgu, dd = _dev(x), _dev(g), _dev(wgu), _dev(wd)
+    dy, dws = hr.DeviceBuffer(4 * m * hd), hr.DeviceBuffer(nws)
+    s = hr.Stream()
+    graph = hr.Graph(s, lambda: lib.ternix_hip_ffn_forward(dy.value, dx.value, dg.value, 1e-5, dgu.value, 0.02,
+                                                           dd.value, 0.03, m, hd, f, dws.value, nws, s.handle))
+    for rep in range(4):
+        dy.upload(np.full(m * hd, np.nan, F32))
+        graph.launch()
+        s.synchronize()
+        np.testing.assert_array_equal(dy.download(F32, (m, hd)), eager, err_msg=f"replay {rep}")
+        tx.ffn_forward(x, g, 1e-5, wgu, 0.02, wd, 0.03)  # eager work between replays
