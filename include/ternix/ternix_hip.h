@@ -28,7 +28,11 @@
  * happens while the stream is being captured into a hipGraph: a call that
  * would need one then zeroes C and accumulates the partial sums with int32
  * atomics instead (exact, order-independent).  Warm the shapes up eagerly
- * before capturing to keep the faster path in the graph.
+ * before capturing to keep the faster path in the graph; such a graph uses
+ * the capturing stream's workspace, so it must not run concurrently with
+ * other small-M work issued on that stream.  Workspace buffers are never
+ * freed before the process ends (an outgrown one is kept for the graphs and
+ * queued work that still reference it).
  * Calls are thread-safe; calls that share an output buffer race as any two
  * kernels writing one buffer do.
  *

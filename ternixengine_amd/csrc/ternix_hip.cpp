@@ -16,6 +16,7 @@
 #include <map>
 #include <mutex>
 #include <utility>
+#include <vector>
 
 #include "ternary_kernels.h"
 
@@ -42,12 +43,14 @@ int cu_count() {
 // following reduce kernel sums.  One workspace per (device, stream), so concurrent streams never
 // share one.  It is allocated the first time a shape needs more than the current size -- never
 // while the stream is being captured into a graph (the call then takes the atomic path, which needs
-// no workspace) -- and kept until the process ends.
+// no workspace) -- and kept until the process ends.  A buffer outgrown by a larger shape is retired,
+// not freed: work already queued and graphs captured earlier on the stream keep using it.
 constexpr size_t kWorkspaceMax = size_t(256) << 20;
 
 struct Workspace {
     void* ptr = nullptr;
     size_t bytes = 0;
+    std::vector<void*> retired;
 };
 std::mutex g_ws_mutex;
 std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
@@ -60,16 +63,14 @@ void* workspace(hipStream_t st, size_t bytes) {
     if (w.bytes >= bytes) return w.ptr;
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
-    size_t nb = std::max(bytes, size_t(8) << 20);
+    // Grow geometrically (at least 8 MiB, at least double), capped at kWorkspaceMax unless the
+    // request itself is larger, rounded to 1 MiB.
+    const size_t grown = std::min(std::max(size_t(8) << 20, 2 * w.bytes), kWorkspaceMax);
+    size_t nb = std::max(bytes, grown);
     nb = (nb + (size_t(1) << 20) - 1) & ~((size_t(1) << 20) - 1);
-    if (w.ptr) {
-        if (hipStreamSynchronize(st) != hipSuccess) return nullptr;
-        (void)hipFree(w.ptr);
-        w.ptr = nullptr;
-        w.bytes = 0;
-    }
     void* p = nullptr;
     if (hipMalloc(&p, nb) != hipSuccess) return nullptr;
+    if (w.ptr) w.retired.push_back(w.ptr);  // sizes at least double, so retired memory < the live buffer
     w.ptr = p;
     w.bytes = nb;
     return p;

@@ -276,3 +276,34 @@ def test_split_k_repeated_launches_exact(oracle, capture):
             assert tx.mul_mat_ternary(da.value, db.value, dc.value, case.M, case.K, case.N, stream=s.handle) == 0
         s.synchronize()
         assert (dc.download(np.int32, (case.M, case.N)) == expect).all(), name
+
+
+def test_graph_survives_workspace_growth(oracle):
+    """A graph captured while the stream's split-K workspace is small keeps working after a larger
+    shape on the same stream grows the workspace (outgrown buffers are retired, never freed)."""
+    s = hr.Stream()
+    small = configs.CASES["cfg1"]
+    a, wp = configs.gen_a(small), configs.gen_w_packed(small)
+    expect = oracle.mm("scalar_mt", a, wp, small.N)
+    da, db, dc = hr.DeviceBuffer.from_array(a), hr.DeviceBuffer.from_array(wp), hr.DeviceBuffer(4 * small.N)
+    assert tx.mul_mat_ternary(da.value, db.value, dc.value, small.M, small.K, small.N, stream=s.handle) == 0
+    s.synchronize()  # workspace now allocated for this stream: the graph below records the split-K path
+    log("[graph + growth] capture cfg1")
+    g = hr.Graph(s, lambda: tx.mul_mat_ternary(da.value, db.value, dc.value, small.M, small.K, small.N,
+                                               stream=s.handle))
+    # M=16, K=1 << 16, N=16384: 16 splits x 16 x 16384 int32 partials = 16 MiB > the first 8 MiB workspace
+    m, k, n = 16, 1 << 16, 16384
+    rng = np.random.default_rng(4)
+    a2 = rng.integers(-128, 128, size=(m, k), dtype=np.int8)
+    w2 = tx.pack_ternary((rng.integers(0, 3, size=(k, n)) - 1).astype(np.int8))
+    d2a, d2b, d2c = hr.DeviceBuffer.from_array(a2), hr.DeviceBuffer.from_array(w2), hr.DeviceBuffer(4 * m * n)
+    log("[graph + growth] large eager call")
+    assert tx.mul_mat_ternary(d2a.value, d2b.value, d2c.value, m, k, n, stream=s.handle) == 0
+    s.synchronize()
+    for rep in range(3):
+        dc.upload(np.full(small.N, GARBAGE, np.int32))
+        g.launch()
+        s.synchronize()
+        assert (dc.download(np.int32, (1, small.N)) == expect).all(), rep
+    got = d2c.download(np.int32, (m, n))
+    assert (got[:2] == oracle.mm("scalar", a2[:2], w2, n)).all()
