@@ -16,29 +16,11 @@
 #include <math.h>
 #include <stdint.h>
 
+#include "row_stats.h"
 #include "ternary_kernels.h"
 
 namespace ternix_hip {
 namespace {
-
-// Sum over the 256 threads of a workgroup; every thread gets the result.
-__device__ __forceinline__ float block_sum(float v, float* red) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
-    __syncthreads();  // red may still be read from a previous call
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    return (red[0] + red[1]) + (red[2] + red[3]);
-}
-
-__device__ __forceinline__ float block_max(float v, float* red) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-}
 
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ X, const float* __restrict__ W,
                                                       float eps, float* __restrict__ out, int8_t* __restrict__ Q,
@@ -46,27 +28,18 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
     __shared__ float red[4];
     const int m = blockIdx.x;
     const float* x = X + (size_t)m * (size_t)K;
-    float ss = 0.0f;
-    for (int k = threadIdx.x; k < K; k += 256) ss += x[k] * x[k];
-    ss = block_sum(ss, red);
-    const float inv = 1.0f / sqrtf(ss / (float)K + eps);
+    const float inv = row_rms_inv(x, K, eps, red);
     if (Q == nullptr) {
         float* o = out + (size_t)m * (size_t)K;
-        for (int k = threadIdx.x; k < K; k += 256) o[k] = x[k] * inv * W[k];
+        for (int k = threadIdx.x; k < K; k += 256) o[k] = row_value(x, W, inv, k);
         return;
     }
-    // Fused quantisation of the normalised row (same rule as quantize_rows_kernel).
-    float amax = 0.0f;
-    for (int k = threadIdx.x; k < K; k += 256) amax = fmaxf(amax, fabsf(x[k] * inv * W[k]));
-    amax = block_max(amax, red);
-    const float a = fmaxf(amax, 1e-5f);
+    // Fused quantisation of the normalised row (the rule of quantize_rows_kernel).
+    const float a = fmaxf(row_absmax(x, W, inv, K, red), 1e-5f);
     const float s = 127.0f / a;
     if (threadIdx.x == 0) row_scale[m] = a / 127.0f;
     int8_t* q = Q + (size_t)m * (size_t)K;
-    for (int k = threadIdx.x; k < K; k += 256) {
-        const float r = rintf((x[k] * inv * W[k]) * s);
-        q[k] = (int8_t)(int)fminf(fmaxf(r, -128.0f), 127.0f);
-    }
+    for (int k = threadIdx.x; k < K; k += 256) q[k] = (int8_t)quantize_value(row_value(x, W, inv, k), s);
 }
 
 __global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ in, float* __restrict__ out,

@@ -40,9 +40,21 @@ bool skinny_fast_ok(const int8_t* A, const uint8_t* B, int M, int K, int N, int 
 // reduce kernel sums them into C; without a workspace C is zeroed and accumulated with atomics.
 // With os.Y set, the store and partial-sum modes write the dequantised floats (fused into the store or
 // the reduce); the atomic mode accumulates int32 in C, which the caller converts afterwards.
+// Fused activation quantisation for the skinny path (mode 1: quantise fp32 rows X; mode 2: RMSNorm
+// with weight G and eps, then quantise); the int8 A argument is then unused and the row scales go to
+// rs_out.  Only valid when skinny_short_ok() holds for the plan (launch_skinny returns
+// hipErrorInvalidValue otherwise, before launching anything).
+struct ActQuant {
+    int mode = 0;
+    const float* X = nullptr;
+    const float* G = nullptr;
+    float eps = 0.0f;
+    float* rs_out = nullptr;
+};
+bool skinny_short_ok(const uint8_t* B, int M, int K, int N, int steps_per_split, int splits);
 hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int tb, int kw,
                          int splits, int steps_per_split, int32_t* partials, hipStream_t st,
-                         const OutScale& os = OutScale{});
+                         const OutScale& os = OutScale{}, const ActQuant& aq = ActQuant{});
 // LDS-tiled MFMA GEMM over k-rows [k_begin, k_end); accumulate != 0 adds into C instead of storing.
 // With os.Y set the tile epilogue writes the dequantised floats instead (accumulate must be 0).
 hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int k_begin,

@@ -36,6 +36,7 @@
 #include <stdint.h>
 #include <stdlib.h>
 
+#include "row_stats.h"
 #include "ternary_kernels.h"
 
 namespace ternix_hip {
@@ -185,6 +186,7 @@ __device__ __forceinline__ v4i load_a16_range(const int8_t* __restrict__ A, int 
 // ------------------------------------------------------------------------------------------------
 
 constexpr int SK_WAVES = 4;
+constexpr int kRowRegs = 32;  // fused activation quantisation: row elements per thread (K <= 8192)
 
 enum SkinnyMode { SK_STORE = 0, SK_ATOMIC = 1, SK_PARTIAL = 2 };
 
@@ -201,6 +203,12 @@ struct SkinnyArgs {
     int aligned_w;        // generic kernel: NB % 4 == 0 and W 4-byte aligned
     int aligned_a;        // generic kernel: K % 16 == 0 and A 16-byte aligned
     OutScale os;          // SK_STORE: dequantised float output instead of C when os.Y is set
+    // Fused activation quantisation (skinny_short_kernel with AQ > 0): A is produced from the fp32
+    // rows X (optionally RMS-normalised with weight G), and rs_out receives the row scales.
+    const float* X;
+    const float* G;
+    float eps;
+    float* rs_out;
 };
 
 // One k-step of MFMA work for one 16-row x 4-byte-column block: raw[r] is the dword of row r.
@@ -503,7 +511,14 @@ void skinny_fast_kernel(SkinnyArgs args) {
 // workgroups whose k-range is at most SPS k-steps, the decode case where K is split over the whole
 // chip.  Every weight and activation load of the workgroup is issued up front (no ring, no LDS copy
 // of the activations, no barrier), so the code a workgroup runs is short and its loads all overlap.
-template <int SPS, bool LOW_M>
+// AQ selects the activation source: 0 the int8 A; 1 fp32 rows X quantised on the fly (absmax, the
+// rule of quantize_rows_kernel); 2 fp32 rows X RMS-normalised with weight G, then quantised (the rule
+// of rmsnorm_kernel).  With AQ > 0 every workgroup computes the statistics of its m-group's rows with
+// the shared row_stats.h loops (the rows are small and cached; the weight loads are already in flight),
+// so its int8 fragments are bit-identical to the standalone kernels' output; workgroup (0, 0) also
+// stores the row scales for the launch that applies them (split-K reduce or dequant), which is why the
+// launcher only uses AQ > 0 with splits > 1.
+template <int SPS, bool LOW_M, int AQ>
 __global__ __launch_bounds__(64 * SK_WAVES) void skinny_short_kernel(SkinnyArgs args) {
     using Geo = SkinnyFastGeometry<1, 1, 1, LOW_M>;
     constexpr int ROW_DW = Geo::ROW_DW, STAGE_DW = Geo::STAGE_DW;
@@ -538,10 +553,61 @@ __global__ __launch_bounds__(64 * SK_WAVES) void skinny_short_kernel(SkinnyArgs 
         for (int h = 0; h < 4; ++h) g4[u][h] = *reinterpret_cast<const v4i*>(sb + (size_t)(16 * h) * (size_t)NB);
     }
     // Activations: row m0 + q (clamped; rows >= M are never stored), bytes 16kb.. of each step.
-    const int8_t* abase = A + (size_t)min(m0 + q, M - 1) * (size_t)K + kb * 16;
     v4i a[SPS][1];
+    if constexpr (AQ == 0) {
+        const int8_t* abase = A + (size_t)min(m0 + q, M - 1) * (size_t)K + kb * 16;
 #pragma unroll
-    for (int u = 0; u < SPS; ++u) a[u][0] = *reinterpret_cast<const v4i*>(abase + (size_t)min(s_begin + u, s_last) * 64);
+        for (int u = 0; u < SPS; ++u)
+            a[u][0] = *reinterpret_cast<const v4i*>(abase + (size_t)min(s_begin + u, s_last) * 64);
+    } else {
+        // Each thread loads its elements k = tid + 256 j of a row once (K <= 256 * kRowRegs), the row
+        // statistics come from registers (same accumulation order as row_stats.h), and the int8 values
+        // of this workgroup's k-range go through LDS to the lanes that feed them to the MFMAs.
+        __shared__ float red[4];
+        __shared__ __attribute__((aligned(16))) int8_t qbuf[16][SPS * 64];
+        const int rows = min(16, M - m0);
+        const int kbase = s_begin * 64;
+        // the workgroup's k-range (cnt is per wave: 0 for a slab past the last column)
+        const int krange = max(min(min(SPS, args.steps_per_split), (K >> 6) - s_begin), 1) * 64;
+        for (int r = 0; r < rows; ++r) {  // uniform: every thread takes part in the reductions
+            const float* x = args.X + (size_t)(m0 + r) * (size_t)K;
+            float xv[kRowRegs], gv[AQ == 2 ? kRowRegs : 1];
+#pragma unroll
+            for (int j = 0; j < kRowRegs; ++j) {
+                const int k = (int)threadIdx.x + 256 * j;
+                xv[j] = k < K ? x[k] : 0.0f;
+                if constexpr (AQ == 2) gv[j] = k < K ? args.G[k] : 0.0f;
+            }
+            float inv = 1.0f;
+            if constexpr (AQ == 2) {
+                float ss = 0.0f;
+#pragma unroll
+                for (int j = 0; j < kRowRegs; ++j) ss = fmaf(xv[j], xv[j], ss);  // +0 past K changes nothing
+                ss = row_block_sum(ss, red);
+                inv = 1.0f / sqrtf(ss / (float)K + args.eps);
+            }
+            auto val = [&](int j) {
+                if constexpr (AQ == 2) return xv[j] * inv * gv[j];
+                else return xv[j];
+            };
+            float amax = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kRowRegs; ++j) amax = fmaxf(amax, fabsf(val(j)));
+            const float am = fmaxf(row_block_max(amax, red), 1e-5f);
+            const float sc = 127.0f / am;
+            if (threadIdx.x == 0 && cx == 0 && sy == 0) args.rs_out[m0 + r] = am / 127.0f;
+#pragma unroll
+            for (int j = 0; j < kRowRegs; ++j) {
+                const int kk = (int)threadIdx.x + 256 * j - kbase;
+                if (kk >= 0 && kk < krange) qbuf[r][kk] = (int8_t)quantize_value(val(j), sc);
+            }
+        }
+        __syncthreads();
+        const int row = min(m0 + q, M - 1) - m0;
+#pragma unroll
+        for (int u = 0; u < SPS; ++u)
+            a[u][0] = *reinterpret_cast<const v4i*>(&qbuf[row][min(u, max(cnt, 1) - 1) * 64 + kb * 16]);
+    }
 
     v4i acc[1][4][4];
     v4i accR[1] = {v4i{0, 0, 0, 0}};
@@ -1370,6 +1436,28 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const int32_t* __res
     }
 }
 
+template <int AQ>
+void launch_short_aq(const SkinnyArgs& a, dim3 grid, hipStream_t st) {
+    const int sps = a.steps_per_split;
+    const dim3 block(64 * SK_WAVES);
+    if (a.M <= 4) {
+        if (sps == 1) hipLaunchKernelGGL((skinny_short_kernel<1, true, AQ>), grid, block, 0, st, a);
+        else if (sps == 2) hipLaunchKernelGGL((skinny_short_kernel<2, true, AQ>), grid, block, 0, st, a);
+        else hipLaunchKernelGGL((skinny_short_kernel<4, true, AQ>), grid, block, 0, st, a);
+    } else {
+        if (sps == 1) hipLaunchKernelGGL((skinny_short_kernel<1, false, AQ>), grid, block, 0, st, a);
+        else if (sps == 2) hipLaunchKernelGGL((skinny_short_kernel<2, false, AQ>), grid, block, 0, st, a);
+        else hipLaunchKernelGGL((skinny_short_kernel<4, false, AQ>), grid, block, 0, st, a);
+    }
+}
+
+hipError_t launch_short(const SkinnyArgs& a, dim3 grid, int aq, hipStream_t st) {
+    if (aq == 2) launch_short_aq<2>(a, grid, st);
+    else if (aq == 1) launch_short_aq<1>(a, grid, st);
+    else launch_short_aq<0>(a, grid, st);
+    return hipGetLastError();
+}
+
 template <int MT, int TB, int KW, int PD, bool LOW_M>
 hipError_t launch_fast_t(const SkinnyArgs& a, dim3 grid, hipStream_t st) {
     hipLaunchKernelGGL((skinny_fast_kernel<MT, TB, KW, PD, LOW_M>), grid, dim3(64 * SK_WAVES),
@@ -1492,11 +1580,19 @@ bool skinny_fast_ok(const int8_t* A, const uint8_t* B, int M, int K, int N, int 
            (NB < (1 << 26)) && skinny_a_lds_bytes(M, steps_per_split) <= kSkinnyALdsMax;
 }
 
+bool skinny_short_ok(const uint8_t* B, int M, int K, int N, int steps_per_split, int splits) {
+    const int NB = N >> 2;
+    return M <= 16 && steps_per_split <= 4 && splits > 1 && (K % 64 == 0) && (NB % 64 == 0) &&
+           ((uintptr_t)B % 16 == 0) && (NB < (1 << 26)) && K <= 256 * kRowRegs;
+}
+
 hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int tb, int kw,
-                         int splits, int steps_per_split, int32_t* partials, hipStream_t st, const OutScale& os) {
+                         int splits, int steps_per_split, int32_t* partials, hipStream_t st, const OutScale& os,
+                         const ActQuant& aq) {
     const int NB = N >> 2;
     const int mode = splits <= 1 ? SK_STORE : (partials ? SK_PARTIAL : SK_ATOMIC);
     if (mode == SK_ATOMIC && C == nullptr) return hipErrorInvalidValue;  // scaled call without int scratch
+    if (aq.mode != 0 && !skinny_short_ok(B, M, K, N, steps_per_split, splits)) return hipErrorInvalidValue;
     if (mode == SK_ATOMIC) {
         const hipError_t e = launch_zero(C, (size_t)M * (size_t)N, st);
         if (e != hipSuccess) return e;
@@ -1514,20 +1610,18 @@ hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, i
         const char* e = std::getenv("TERNIX_SKINNY_SHORT");
         return e && e[0] == '0';
     }();
-    if (mt == 1 && tb == 1 && kw == 1 && steps_per_split <= 4 && !no_short &&
-        skinny_fast_ok(A, B, M, K, N, steps_per_split)) {
+    if (aq.mode != 0) {
+        // Fused activation quantisation: only on the short kernel with a split (see skinny_short_kernel).
+        a.X = aq.X;
+        a.G = aq.G;
+        a.eps = aq.eps;
+        a.rs_out = aq.rs_out;
         const dim3 grid((NB + 255) / 256, splits, mgroups);
-        const int sps = steps_per_split;
-        if (M <= 4) {
-            if (sps == 1) hipLaunchKernelGGL((skinny_short_kernel<1, true>), grid, dim3(64 * SK_WAVES), 0, st, a);
-            else if (sps == 2) hipLaunchKernelGGL((skinny_short_kernel<2, true>), grid, dim3(64 * SK_WAVES), 0, st, a);
-            else hipLaunchKernelGGL((skinny_short_kernel<4, true>), grid, dim3(64 * SK_WAVES), 0, st, a);
-        } else {
-            if (sps == 1) hipLaunchKernelGGL((skinny_short_kernel<1, false>), grid, dim3(64 * SK_WAVES), 0, st, a);
-            else if (sps == 2) hipLaunchKernelGGL((skinny_short_kernel<2, false>), grid, dim3(64 * SK_WAVES), 0, st, a);
-            else hipLaunchKernelGGL((skinny_short_kernel<4, false>), grid, dim3(64 * SK_WAVES), 0, st, a);
-        }
-        e = hipGetLastError();
+        e = launch_short(a, grid, aq.mode, st);
+    } else if (mt == 1 && tb == 1 && kw == 1 && steps_per_split <= 4 && !no_short &&
+               skinny_fast_ok(A, B, M, K, N, steps_per_split)) {
+        const dim3 grid((NB + 255) / 256, splits, mgroups);
+        e = launch_short(a, grid, 0, st);
     } else if (skinny_fast_ok(A, B, M, K, N, steps_per_split)) {
         if (mt == 2) tb = 1;
         const int slab = 64 * tb * (SK_WAVES / (kw >= 4 ? 4 : (kw == 2 ? 2 : 1)));  // bytes per workgroup

@@ -143,14 +143,18 @@ SkinnyPlan plan_skinny(int M, int K, int N) {
 }
 
 hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int K, int N, hipStream_t st,
-                      const ternix_hip::OutScale& os = ternix_hip::OutScale{}) {
+                      const ternix_hip::OutScale& os = ternix_hip::OutScale{},
+                      const ternix_hip::ActQuant& aq = ternix_hip::ActQuant{}) {
     const SkinnyPlan p = plan_skinny(M, K, N);
+    // Fused activation quantisation needs the short kernel with a split; the caller falls back to the
+    // standalone quantisation launch when this returns hipErrorInvalidValue.
+    if (aq.mode != 0 && !ternix_hip::skinny_short_ok(dB, M, K, N, p.sps, p.splits)) return hipErrorInvalidValue;
     int32_t* partials = nullptr;
     if (p.splits > 1) {
         const size_t need = (size_t)p.splits * (size_t)M * (size_t)N * sizeof(int32_t);
         if (need <= kWorkspaceMax) partials = static_cast<int32_t*>(workspace(st, need));
     }
-    return ternix_hip::launch_skinny(dA, dB, dC, M, K, N, p.tb, p.kw, p.splits, p.sps, partials, st, os);
+    return ternix_hip::launch_skinny(dA, dB, dC, M, K, N, p.tb, p.kw, p.splits, p.sps, partials, st, os, aq);
 }
 
 hipError_t run_gemm(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int K, int N, hipStream_t st,
@@ -375,6 +379,38 @@ int ternix_hip_ffn_forward(float* dY, const float* dX, const float* dNormWeight,
     float* rs2 = reinterpret_cast<float*>(ws + l.rs2);
     int32_t* scratch = reinterpret_cast<int32_t*>(ws + l.scratch);
     hipStream_t st = static_cast<hipStream_t>(stream);
+    const int m = (int)M, hd = (int)H, f = (int)F;
+    // Decode shapes: the RMSNorm + quantisation of x and the requantisation of h run inside the two
+    // skinny GEMVs (fused activation prologue, bit-identical to the standalone kernels), leaving
+    // GEMV + reduce twice.  Otherwise: the four separate launches.
+    if (m <= kSkinnyMaxM && F > 0) {
+        ternix_hip::OutScale os1;
+        os1.Y = h;
+        os1.rs = rs1;
+        os1.ws = ws_gu;
+        os1.swiglu = 1;
+        ternix_hip::ActQuant aq1;
+        aq1.mode = 2;
+        aq1.X = dX;
+        aq1.G = dNormWeight;
+        aq1.eps = eps;
+        aq1.rs_out = rs1;
+        ternix_hip::OutScale os2;
+        os2.Y = dY;
+        os2.rs = rs2;
+        os2.ws = ws_d;
+        ternix_hip::ActQuant aq2;
+        aq2.mode = 1;
+        aq2.X = h;
+        aq2.rs_out = rs2;
+        const SkinnyPlan p1 = plan_skinny(m, hd, 2 * f), p2 = plan_skinny(m, f, hd);
+        if (ternix_hip::skinny_short_ok(dWgu, m, hd, 2 * f, p1.sps, p1.splits) &&
+            ternix_hip::skinny_short_ok(dWd, m, f, hd, p2.sps, p2.splits)) {
+            hipError_t e = run_skinny(nullptr, dWgu, scratch, m, hd, 2 * f, st, os1, aq1);
+            if (e != hipSuccess) return (int)e;
+            return (int)run_skinny(nullptr, dWd, reinterpret_cast<int32_t*>(dY), m, f, hd, st, os2, aq2);
+        }
+    }
     int s = ternix_hip_rms_norm_quantize(q1, rs1, dX, dNormWeight, M, H, eps, stream);
     if (s != 0) return s;
     s = ternix_hip_mul_mat_ternary_swiglu(q1, dWgu, h, M, H, 2 * F, rs1, ws_gu, scratch, stream);
