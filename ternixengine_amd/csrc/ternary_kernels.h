@@ -57,8 +57,15 @@ hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, i
                          const OutScale& os = OutScale{}, const ActQuant& aq = ActQuant{});
 // LDS-tiled MFMA GEMM over k-rows [k_begin, k_end); accumulate != 0 adds into C instead of storing.
 // With os.Y set the tile epilogue writes the dequantised floats instead (accumulate must be 0).
+// splits > 1: split-K over gridDim.y, each workgroup row of the grid covering k_split k-rows (a
+// multiple of 64, of 128 for the fast kernels) and writing its partial tile to C + y * M * N
+// (accumulate must be 0 and os unset; launch_splitk_reduce finishes the sum).
 hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int k_begin,
-                       int k_end, int accumulate, hipStream_t st, const OutScale& os = OutScale{});
+                       int k_end, int accumulate, hipStream_t st, const OutScale& os = OutScale{}, int splits = 1,
+                       int k_split = 0);
+// C (or os.Y) = sum over `splits` slabs of P ([splits][M][N] int32).
+hipError_t launch_splitk_reduce(const int32_t* P, int32_t* C, int M, int N, int splits, const OutScale& os,
+                                hipStream_t st);
 // In-place-capable conversion of an int32 C to the dequantised float Y (Y may alias C).
 hipError_t launch_dequant(const int32_t* C, const OutScale& os, int M, int N, hipStream_t st);
 // Per-row RMSNorm (reference rms_norm_scalar, src/simd_math.cpp:7-12): out = x * inv * w with

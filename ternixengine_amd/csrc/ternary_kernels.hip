@@ -655,8 +655,11 @@ __device__ __forceinline__ uint32_t ld_w4(const uint8_t* __restrict__ B, int row
     return row < K ? v : 0u;
 }
 
-// Generic skinny kernel: any K, N % 4 == 0, any alignment.  TB = 1, 2 slabs x 2 waves.
-template <int MT, bool LOW_M>
+// Generic skinny kernel: any K, N % 4 == 0, any alignment.  TB = 1, 2 slabs x 2 waves.  AW / AA:
+// weights / activations aligned for dword / 16-byte loads (template parameters, so every load is
+// straight-line code).  The next k-step's loads are issued before the current step's MFMAs (two
+// register sets, clamped indices, so the number of loads in flight is the same on every path).
+template <int MT, bool LOW_M, bool AW, bool AA>
 __global__ __launch_bounds__(64 * SK_WAVES) void skinny_generic_kernel(SkinnyArgs args) {
     constexpr int KW = 2, TILES = 2, G = 4;
     __shared__ __attribute__((aligned(16))) int32_t smem[TILES * (KW / 2) * MT * 16 * G * (LOW_M ? 16 : 64)];
@@ -673,7 +676,6 @@ __global__ __launch_bounds__(64 * SK_WAVES) void skinny_generic_kernel(SkinnyArg
     const int nsteps = (K + 63) >> 6;
     const int s_begin = blockIdx.y * args.steps_per_split;
     const int s_end = tile_bc < NB ? min(nsteps, s_begin + args.steps_per_split) : s_begin;
-    const bool aw = args.aligned_w, aa = args.aligned_a;
 
     v4i acc[MT][G][4];
     v4i accR[MT];
@@ -686,19 +688,34 @@ __global__ __launch_bounds__(64 * SK_WAVES) void skinny_generic_kernel(SkinnyArg
             for (int j = 0; j < 4; ++j) acc[t][g][j] = v4i{0, 0, 0, 0};
     }
     const v4i ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
-    for (int s = s_begin + kw; s < s_end; s += KW) {
-        const int k0 = s * 64 + kb * 16;
-        uint32_t raw[16];
+    auto load_step = [&](int st, uint32_t (&raw)[16], v4i (&a)[MT]) {
+        const int k0 = st * 64 + kb * 16;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) raw[r] = ld_w4(B, k0 + r, bc, K, NB, aw);
-        v4i a[MT];
+        for (int r = 0; r < 16; ++r) raw[r] = ld_w4(B, k0 + r, bc, K, NB, AW);
 #pragma unroll
-        for (int t = 0; t < MT; ++t)
-            a[t] = aa ? load_a16<true>(A, min(m0 + 16 * t + q, M - 1), k0, M, K)
-                      : load_a16<false>(A, min(m0 + 16 * t + q, M - 1), k0, M, K);
+        for (int t = 0; t < MT; ++t) a[t] = load_a16<AA>(A, min(m0 + 16 * t + q, M - 1), k0, M, K);
+    };
+    auto compute = [&](const uint32_t (&raw)[16], const v4i (&a)[MT]) {
 #pragma unroll
         for (int t = 0; t < MT; ++t) accR[t] = mfma_i8(a[t], ones, accR[t]);
         skinny_mfma_block<MT, G>(raw, a, 0, acc);
+    };
+    const int s0 = s_begin + kw;
+    if (s0 < s_end) {
+        const int s_last = s0 + ((s_end - 1 - s0) / KW) * KW;  // this wave's last step
+        uint32_t raw0[16], raw1[16];
+        v4i a0[MT], a1[MT];
+        load_step(s0, raw0, a0);
+        for (int st = s0;;) {
+            load_step(min(st + KW, s_last), raw1, a1);
+            compute(raw0, a0);
+            st += KW;
+            if (st >= s_end) break;
+            load_step(min(st + KW, s_last), raw0, a0);
+            compute(raw1, a1);
+            st += KW;
+            if (st >= s_end) break;
+        }
     }
     skinny_epilogue<MT, G, KW, TILES, LOW_M>(args, smem, acc, accR, tw, kw, tile_bc, m0, blockIdx.y);
 }
@@ -722,7 +739,12 @@ template <int BM, int BNB, bool ALIGNED_W, bool ALIGNED_A>
 __global__ __launch_bounds__(GM_THREADS) void gemm_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ B,
                                                           int32_t* __restrict__ C, int M, int K, int N,
                                                           int tiles_n, int k_begin, int k_end, int accumulate,
-                                                          int vec_store, OutScale os) {
+                                                          int vec_store, int k_split, OutScale os) {
+    if (gridDim.y > 1) {  // split-K: this workgroup's k-range, partial tile in slab blockIdx.y
+        k_begin += (int)blockIdx.y * k_split;
+        k_end = min(k_end, k_begin + k_split);
+        C += (size_t)blockIdx.y * (size_t)M * (size_t)N;
+    }
     constexpr int WM = BM / 2;            // rows per wave
     constexpr int WB = BNB / 2;           // byte-columns per wave
     constexpr int MT = WM / 16;           // m-tiles per wave
@@ -941,7 +963,12 @@ template <int BM, int WGN, int NS, int BK>
 __global__ __launch_bounds__(GF_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
 void gemm_fast_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ B, int32_t* __restrict__ C, int M,
                       int K, int N, int tiles_n, int k_begin, int k_end, int accumulate, int vec_store,
-                      OutScale os) {
+                      int k_split, OutScale os) {
+    if (gridDim.y > 1) {  // split-K: this workgroup's k-range, partial tile in slab blockIdx.y
+        k_begin += (int)blockIdx.y * k_split;
+        k_end = min(k_end, k_begin + k_split);
+        C += (size_t)blockIdx.y * (size_t)M * (size_t)N;
+    }
     constexpr int WGM = 8 / WGN;             // waves along M
     constexpr int WM = BM / WGM;             // rows per wave
     constexpr int MT = WM / 16;              // m-tiles per wave
@@ -1157,7 +1184,12 @@ template <int BM, int WGN, int NS, int BK, int NWV, int BNB>
 __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2)))
 void gemm_pipe_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ B, int32_t* __restrict__ C, int M,
                       int K, int N, int tiles_n, int k_begin, int k_end, int accumulate, int vec_store,
-                      OutScale os) {
+                      int k_split, OutScale os) {
+    if (gridDim.y > 1) {  // split-K: this workgroup's k-range, partial tile in slab blockIdx.y
+        k_begin += (int)blockIdx.y * k_split;
+        k_end = min(k_end, k_begin + k_split);
+        C += (size_t)blockIdx.y * (size_t)M * (size_t)N;
+    }
     constexpr int THR = 64 * NWV;           // threads per workgroup
     constexpr int CW = BNB / 16;            // 16-byte chunks per W stage row
     constexpr int WGM = NWV / WGN;
@@ -1436,6 +1468,16 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const int32_t* __res
     }
 }
 
+template <int MT, bool LOW_M>
+hipError_t launch_generic(const SkinnyArgs& a, dim3 grid, hipStream_t st) {
+    const dim3 block(64 * SK_WAVES);
+    if (a.aligned_w && a.aligned_a) hipLaunchKernelGGL((skinny_generic_kernel<MT, LOW_M, true, true>), grid, block, 0, st, a);
+    else if (a.aligned_w) hipLaunchKernelGGL((skinny_generic_kernel<MT, LOW_M, true, false>), grid, block, 0, st, a);
+    else if (a.aligned_a) hipLaunchKernelGGL((skinny_generic_kernel<MT, LOW_M, false, true>), grid, block, 0, st, a);
+    else hipLaunchKernelGGL((skinny_generic_kernel<MT, LOW_M, false, false>), grid, block, 0, st, a);
+    return hipGetLastError();
+}
+
 template <int AQ>
 void launch_short_aq(const SkinnyArgs& a, dim3 grid, hipStream_t st) {
     const int sps = a.steps_per_split;
@@ -1477,19 +1519,19 @@ hipError_t launch_fast_kw(const SkinnyArgs& a, int kw, dim3 grid, hipStream_t st
 
 template <int BM, int BNB>
 hipError_t launch_gemm_t(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, bool aw, bool aa,
-                         int kb, int ke, int acc, hipStream_t st, const OutScale& os) {
+                         int kb, int ke, int acc, hipStream_t st, const OutScale& os, int splits, int k_split) {
     const int NB = N >> 2;
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (NB + BNB - 1) / BNB;
-    const dim3 grid(tiles_m * tiles_n), block(GM_THREADS);
+    const dim3 grid(tiles_m * tiles_n, splits), block(GM_THREADS);
     const int vs = ((uintptr_t)(os.Y ? (const void*)os.Y : (const void*)C) % 16) == 0;
     if (aw && aa)
-        hipLaunchKernelGGL((gemm_kernel<BM, BNB, true, true>), grid, block, 0, st, A, B, C, M, K, N, tiles_n, kb, ke, acc, vs, os);
+        hipLaunchKernelGGL((gemm_kernel<BM, BNB, true, true>), grid, block, 0, st, A, B, C, M, K, N, tiles_n, kb, ke, acc, vs, k_split, os);
     else if (aw)
-        hipLaunchKernelGGL((gemm_kernel<BM, BNB, true, false>), grid, block, 0, st, A, B, C, M, K, N, tiles_n, kb, ke, acc, vs, os);
+        hipLaunchKernelGGL((gemm_kernel<BM, BNB, true, false>), grid, block, 0, st, A, B, C, M, K, N, tiles_n, kb, ke, acc, vs, k_split, os);
     else if (aa)
-        hipLaunchKernelGGL((gemm_kernel<BM, BNB, false, true>), grid, block, 0, st, A, B, C, M, K, N, tiles_n, kb, ke, acc, vs, os);
+        hipLaunchKernelGGL((gemm_kernel<BM, BNB, false, true>), grid, block, 0, st, A, B, C, M, K, N, tiles_n, kb, ke, acc, vs, k_split, os);
     else
-        hipLaunchKernelGGL((gemm_kernel<BM, BNB, false, false>), grid, block, 0, st, A, B, C, M, K, N, tiles_n, kb, ke, acc, vs, os);
+        hipLaunchKernelGGL((gemm_kernel<BM, BNB, false, false>), grid, block, 0, st, A, B, C, M, K, N, tiles_n, kb, ke, acc, vs, k_split, os);
     return hipGetLastError();
 }
 
@@ -1631,10 +1673,9 @@ hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, i
         else e = launch_fast_kw<2, 1, false>(a, kw, grid, st);
     } else {
         const dim3 grid((NB + 127) / 128, splits, mgroups);
-        if (M <= 4) hipLaunchKernelGGL((skinny_generic_kernel<1, true>), grid, dim3(64 * SK_WAVES), 0, st, a);
-        else if (M <= 16) hipLaunchKernelGGL((skinny_generic_kernel<1, false>), grid, dim3(64 * SK_WAVES), 0, st, a);
-        else hipLaunchKernelGGL((skinny_generic_kernel<2, false>), grid, dim3(64 * SK_WAVES), 0, st, a);
-        e = hipGetLastError();
+        if (M <= 4) e = launch_generic<1, true>(a, grid, st);
+        else if (M <= 16) e = launch_generic<1, false>(a, grid, st);
+        else e = launch_generic<2, false>(a, grid, st);
     }
     if (e != hipSuccess) return e;
     if (mode == SK_ATOMIC && scaled) return launch_dequant(C, os, M, N, st);  // C: alias of os.Y or scratch
@@ -1646,10 +1687,12 @@ hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, i
 }
 
 hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int k_begin, int k_end,
-                       int accumulate, hipStream_t st, const OutScale& os) {
+                       int accumulate, hipStream_t st, const OutScale& os, int splits, int k_split) {
     const int NB = N >> 2;
     const char* force_generic = std::getenv("TERNIX_GEMM_GENERIC");
+    if (splits < 1) splits = 1;
     const bool fast = (K % GF_BK == 0) && ((k_end - k_begin) % GF_BK == 0) && (k_begin % GF_BK == 0) &&
+                      (splits == 1 || k_split % GF_BK == 0) &&
                       (NB % GF_BNB == 0) && ((uintptr_t)A % 16 == 0) && ((uintptr_t)B % 16 == 0) &&
                       k_end > k_begin && (size_t)M * (size_t)K < ((size_t)1 << 32) &&
                       (size_t)GF_BK * (size_t)NB < ((size_t)1 << 32) && !(force_generic && force_generic[0] == '1');
@@ -1666,12 +1709,12 @@ hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int
             int dev = 0;
             if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
         }
-        int bm = ((long)((M + 255) / 256) * tiles_n * 2 >= 3L * cus) ? 256 : 128;
+        int bm = (splits == 1 && (long)((M + 255) / 256) * tiles_n * 2 >= 3L * cus) ? 256 : 128;
         if (bm_env) bm = std::atoi(bm_env) == 128 ? 128 : 256;
         const int wgn = wgn_env && std::atoi(wgn_env) == 2 ? 2 : 4;
         int bk = 128;
         if (bk_env && std::atoi(bk_env) == 256 && bm == 128 && (k_end - k_begin) % 256 == 0) bk = 256;
-        const dim3 grid(((M + bm - 1) / bm) * tiles_n);
+        const dim3 grid(((M + bm - 1) / bm) * tiles_n, splits);
         // 128-row tiles run the software-pipelined kernel (measured faster on MI355X); 256-row tiles
         // keep gemm_fast_kernel, whose wave tile leaves no registers for a second fragment set.
         static const int pipe_env = [] {
@@ -1686,7 +1729,7 @@ hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int
         if (pipe) {
 #define TX_GP_LAUNCH(BM_, WGN_, NS_, BK_)                                                                      \
     hipLaunchKernelGGL((gemm_pipe_kernel<BM_, WGN_, NS_, BK_, 8, GF_BNB>), grid, dim3(GF_THREADS), 0, st, A, B, C, M, \
-                       K, N, tiles_n, k_begin, k_end, accumulate, vs, os)
+                       K, N, tiles_n, k_begin, k_end, accumulate, vs, k_split, os)
             if (bk == 256 && wgn == 4) TX_GP_LAUNCH(128, 4, 3, 256);
             else if (bk == 256) TX_GP_LAUNCH(128, 2, 3, 256);
             else if (wgn == 4 && pipe_ns == 4) TX_GP_LAUNCH(128, 4, 4, 128);
@@ -1698,7 +1741,7 @@ hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int
         }
 #define TX_GF_LAUNCH(BM_, WGN_, NS_, BK_)                                                                         \
     hipLaunchKernelGGL((gemm_fast_kernel<BM_, WGN_, NS_, BK_>), grid, dim3(GF_THREADS), 0, st, A, B, C, M, K, N, \
-                       tiles_n, k_begin, k_end, accumulate, vs, os)
+                       tiles_n, k_begin, k_end, accumulate, vs, k_split, os)
         if (bm == 256 && wgn == 4) TX_GF_LAUNCH(256, 4, 3, 128);
         else if (bm == 256) TX_GF_LAUNCH(256, 2, 3, 128);
         else if (bk == 256 && wgn == 4) TX_GF_LAUNCH(128, 4, 3, 256);
@@ -1710,7 +1753,17 @@ hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int
     }
     const bool aw = (NB % 4 == 0) && ((uintptr_t)B % 4 == 0);
     const bool aa = (K % 16 == 0) && ((uintptr_t)A % 16 == 0);
-    return launch_gemm_t<128, 64>(A, B, C, M, K, N, aw, aa, k_begin, k_end, accumulate, st, os);
+    return launch_gemm_t<128, 64>(A, B, C, M, K, N, aw, aa, k_begin, k_end, accumulate, st, os, splits, k_split);
+}
+
+hipError_t launch_splitk_reduce(const int32_t* P, int32_t* C, int M, int N, int splits, const OutScale& os,
+                                hipStream_t st) {
+    const size_t n4 = (size_t)M * (size_t)N / 4;
+    if (n4 == 0) return hipSuccess;
+    const int vec = ((uintptr_t)(os.Y ? (const void*)os.Y : (const void*)C) % 16) == 0;
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n4 + 63) / 64)), dim3(256), 0, st, P, C, n4, splits, vec,
+                       os, N);
+    return hipGetLastError();
 }
 
 hipError_t launch_dequant(const int32_t* C, const OutScale& os, int M, int N, hipStream_t st) {

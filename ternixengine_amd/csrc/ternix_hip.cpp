@@ -99,7 +99,7 @@ struct SkinnyPlan {
     int tb, kw, splits, sps;
 };
 
-SkinnyPlan plan_skinny(int M, int K, int N) {
+SkinnyPlan plan_skinny(int M, int K, int N, bool generic = false) {
     const int NB = N / 4;
     const int nsteps = (K + 63) / 64;
     const int mgroups = M <= 16 ? 1 : (M + 31) / 32;
@@ -108,13 +108,21 @@ SkinnyPlan plan_skinny(int M, int K, int N) {
     // the grid within one workgroup per CU (a CU holding two of them finishes last).  With several
     // rows the partial sums ([splits][M][N] int32, written and read back once) are capped at about
     // the weight bytes (K*N/4): splits <= K / (32 M).
-    SkinnyPlan p{1, 1, 1, nsteps};
-    const long col_wgs = (NB + 255) / 256;
+    // Above 4 rows two waves share each 64-byte slab (alternate k-steps, summed in LDS), which halves
+    // the cross-workgroup splits -- and the partial sums, 4 bytes per row and column per split -- for
+    // the same number of workgroups (measured on MI355X, cfg3 M=16: 13.9 vs 15.4 us up, 14.1 vs 15.4
+    // us down).
+    const int kw = M > 4 ? 2 : 1;
+    SkinnyPlan p{1, kw, 1, nsteps};
+    const long col_wgs = (NB + 256 / kw - 1) / (256 / kw);
     const long wgs = col_wgs * mgroups;
     const long target = cu_count();
     if (wgs < target) {
         long splits = target / wgs;
-        const long traffic_cap = std::max(1L, (long)K / (32L * M));
+        // The generic kernel (ragged or unaligned shapes) has a serial dword-load loop per k-step, so
+        // it wants at least 32 splits whatever the partial-sum traffic (measured: M=17 K=4093 N=1028
+        // 19.5 us with 32 splits vs 39 us with 7).
+        const long traffic_cap = std::max(generic ? 32L : 1L, (long)K / (32L * M));
         if (splits > traffic_cap) splits = traffic_cap;
         if (splits > nsteps) splits = nsteps;
         if (splits > 1) p.splits = (int)splits;
@@ -145,7 +153,9 @@ SkinnyPlan plan_skinny(int M, int K, int N) {
 hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int K, int N, hipStream_t st,
                       const ternix_hip::OutScale& os = ternix_hip::OutScale{},
                       const ternix_hip::ActQuant& aq = ternix_hip::ActQuant{}) {
-    const SkinnyPlan p = plan_skinny(M, K, N);
+    const bool generic = !(K % 64 == 0 && (N / 4) % 64 == 0 && reinterpret_cast<uintptr_t>(dB) % 16 == 0 &&
+                           (aq.mode != 0 || reinterpret_cast<uintptr_t>(dA) % 16 == 0));
+    const SkinnyPlan p = plan_skinny(M, K, N, generic);
     // Fused activation quantisation needs the short kernel with a split; the caller falls back to the
     // standalone quantisation launch when this returns hipErrorInvalidValue.
     if (aq.mode != 0 && !ternix_hip::skinny_short_ok(dB, M, K, N, p.sps, p.splits)) return hipErrorInvalidValue;
@@ -157,9 +167,41 @@ hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
     return ternix_hip::launch_skinny(dA, dB, dC, M, K, N, p.tb, p.kw, p.splits, p.sps, partials, st, os, aq);
 }
 
+// Split-K for GEMMs with too few output tiles to fill the chip (mid-size M against a long K, e.g.
+// cfg3 M=64, the worst case M=256): each split covers a contiguous k-range of whole 128-row stages,
+// the partial tiles go through the same workspace and reduce launch as the skinny path.
+int gemm_splits(int M, int K, int N) {
+    static const int env = [] {
+        const char* e = std::getenv("TERNIX_GEMM_SPLITS");  // experiments only
+        return e ? std::atoi(e) : 0;
+    }();
+    const long tiles = (long)((M + 127) / 128) * (long)((N / 4 + 63) / 64);
+    const long cus = cu_count();
+    long splits = env > 0 ? env : (tiles * 2 <= cus ? cus / tiles : 1);
+    splits = std::min<long>(splits, std::max(1, K / 256));  // at least two 128-row stages per split
+    return (int)std::max<long>(1, std::min<long>(splits, 16));
+}
+
 hipError_t run_gemm(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int K, int N, hipStream_t st,
                     const ternix_hip::OutScale& os = ternix_hip::OutScale{}) {
-    if (K <= ternix_hip::kMaxKPerAccumulator) return ternix_hip::launch_gemm(dA, dB, dC, M, K, N, 0, K, 0, st, os);
+    if (K <= ternix_hip::kMaxKPerAccumulator) {
+        int splits = gemm_splits(M, K, N);
+        if (splits > 1) {
+            const int unit = K % 128 == 0 ? 128 : 64;
+            const int k_split = ((K + splits - 1) / splits + unit - 1) / unit * unit;
+            splits = (K + k_split - 1) / k_split;
+            const size_t need = (size_t)splits * (size_t)M * (size_t)N * sizeof(int32_t);
+            int32_t* partials = (splits > 1 && need <= kWorkspaceMax) ? static_cast<int32_t*>(workspace(st, need))
+                                                                       : nullptr;
+            if (partials) {
+                hipError_t e = ternix_hip::launch_gemm(dA, dB, partials, M, K, N, 0, K, 0, st, ternix_hip::OutScale{},
+                                                       splits, k_split);
+                if (e != hipSuccess) return e;
+                return ternix_hip::launch_splitk_reduce(partials, dC, M, N, splits, os, st);
+            }
+        }
+        return ternix_hip::launch_gemm(dA, dB, dC, M, K, N, 0, K, 0, st, os);
+    }
     if (dC == nullptr) return hipErrorInvalidValue;  // scaled call without int scratch
     int acc = 0;
     for (long k0 = 0; k0 < K; k0 += ternix_hip::kMaxKPerAccumulator) {
@@ -183,7 +225,11 @@ int dispatch(Path path, const int8_t* dA, const uint8_t* dB, int32_t* dC, int64_
     if (trivial) return (int)hipSuccess;
     const int M = (int)M64, K = (int)K64, N = (int)N64;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    if (path == Path::Auto) path = M <= kSkinnyMaxM ? Path::Skinny : Path::Gemm;
+    static const int auto_skinny_max = [] {
+        const char* e = std::getenv("TERNIX_SKINNY_MAX_M");  // experiments only
+        return e ? std::atoi(e) : kSkinnyMaxM;
+    }();
+    if (path == Path::Auto) path = M <= auto_skinny_max ? Path::Skinny : Path::Gemm;
     switch (path) {
         case Path::Skinny: e = run_skinny(dA, dB, dC, M, K, N, st); break;
         case Path::Gemm: e = run_gemm(dA, dB, dC, M, K, N, st); break;
