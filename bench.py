@@ -44,7 +44,7 @@ def parse():
                     help="untimed sustained load before each GPU measurement (clock ramp)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["all", "gemv", "gemm", "bigm1", "pack", "layer", "ffn"], default="all")
+    ap.add_argument("--only", choices=["all", "gemv", "gemm", "bigm1", "pack", "layer", "ffn", "configs"], default="all")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run 4 device-to-device copies of 256 MiB (the runtime's copy kernel), the "
                          "known-size reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -324,6 +324,29 @@ def bench_ffn(args, stream, lib):
             "gbs": moved / (ms / args.steps * 1e-3) / 1e9, "finite": bool(np.isfinite(y).all())}
 
 
+def bench_configs(args, stream, lib):
+    """Every BASELINE configuration through ternix_hip_mul_mat_ternary (automatic kernel choice),
+    outputs checked against the committed digests: time per call, effective GB/s (M*K + K*N/4 + 4*M*N)
+    and TOPS (2*M*N*K).  Weights rotate over >= 512 MiB of distinct copies (cold, as in a model's
+    layer sequence)."""
+    from ternixengine_amd import configs
+    fn = lib.ternix_hip_mul_mat_ternary
+    out = []
+    for name, case in configs.CASES.items():
+        w = case.K * case.N // 4
+        copies = min(64, max(2, -(-POOL_MIN_BYTES // w)))
+        p = Problem(case, copies)
+        steps = 20 if case.ops > 1e11 else 60
+        prewarm(lambda i: launch(fn, p, i % copies, stream), 0.1, stream)
+        ms = time_launches(lambda i: launch(fn, p, i % copies, stream), steps, 3, stream)
+        us = ms / steps * 1e3
+        out.append({"name": name, "shape": [case.M, case.K, case.N], "us": round(us, 2),
+                    "gbs": round(case.bytes_algorithmic / (us * 1e-6) / 1e9, 1),
+                    "tops": round(case.ops / (us * 1e-6) / 1e12, 1), "verified": verify(p)})
+        del p
+    return out
+
+
 def cpu_baseline(seconds):
     """Reference avx2_blocked (oracle/_ref) or the oracle's restatement, one thread, on the cfg2 pair."""
     from ternixengine_amd import configs
@@ -379,6 +402,8 @@ def main():
         res["layer"] = bench_layer(args, stream, lib)
     if args.only in ("all", "ffn"):
         res["ffn"] = bench_ffn(args, stream, lib)
+    if args.only in ("all", "configs"):
+        res["configs"] = bench_configs(args, stream, lib)
     g = res.get("gemv")
     line = {
         "metric": METRIC,
@@ -427,6 +452,8 @@ def main():
         line["layer_boundary"] = {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in res["layer"].items()}
     if "ffn" in res:
         line["ffn_decode"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in res["ffn"].items()}
+    if "configs" in res:
+        line["all_configs"] = res["configs"]
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
         line["cpu_baseline"]["value"] = round(line["cpu_baseline"]["value"], 3)
