@@ -1726,6 +1726,18 @@ hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int
             const char* e = std::getenv("TERNIX_GEMM_NS");
             return e && std::atoi(e) == 4 ? 4 : 3;
         }();
+        static const int small_m_max = [] {
+            const char* e = std::getenv("TERNIX_GEMM_SMALLM");  // experiments only
+            return e ? std::atoi(e) : 64;
+        }();
+        if (M <= small_m_max) {
+            // Small M (64 rows or fewer): four-wave workgroups on 64-row tiles, so no MFMA row or A
+            // byte is spent on padding rows; the caller splits K to fill the chip.
+            const dim3 grid64((unsigned)(((M + 63) / 64) * tiles_n), splits);
+            hipLaunchKernelGGL((gemm_pipe_kernel<64, 4, 3, 128, 4, 64>), grid64, dim3(256), 0, st, A, B, C, M, K, N,
+                               tiles_n, k_begin, k_end, accumulate, vs, k_split, os);
+            return hipGetLastError();
+        }
         if (pipe) {
 #define TX_GP_LAUNCH(BM_, WGN_, NS_, BK_)                                                                      \
     hipLaunchKernelGGL((gemm_pipe_kernel<BM_, WGN_, NS_, BK_, 8, GF_BNB>), grid, dim3(GF_THREADS), 0, st, A, B, C, M, \

@@ -175,7 +175,8 @@ int gemm_splits(int M, int K, int N) {
         const char* e = std::getenv("TERNIX_GEMM_SPLITS");  // experiments only
         return e ? std::atoi(e) : 0;
     }();
-    const long tiles = (long)((M + 127) / 128) * (long)((N / 4 + 63) / 64);
+    const int bm = M <= 64 ? 64 : 128;  // the tile height launch_gemm picks
+    const long tiles = (long)((M + bm - 1) / bm) * (long)((N / 4 + 63) / 64);
     const long cus = cu_count();
     long splits = env > 0 ? env : (tiles * 2 <= cus ? cus / tiles : 1);
     splits = std::min<long>(splits, std::max(1, K / 256));  // at least two 128-row stages per split
