@@ -52,9 +52,14 @@ struct ActQuant {
     float* rs_out = nullptr;
 };
 bool skinny_short_ok(const uint8_t* B, int M, int K, int N, int steps_per_split, int splits);
+// True when the DMA-staged skinny kernel can run this call: M <= 16, K % 64 == 0, N % 256 == 0,
+// 16-byte aligned A and W, 1..16 k-steps per split.
+bool skinny_dma_ok(const int8_t* A, const uint8_t* B, int M, int K, int N, int steps_per_split);
+// dma_ns (2..4) selects the DMA-staged kernel with that many LDS stages (its own plan: tb and kw are
+// ignored, aq must be unset, skinny_dma_ok must hold; hipErrorInvalidValue otherwise).
 hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int tb, int kw,
                          int splits, int steps_per_split, int32_t* partials, hipStream_t st,
-                         const OutScale& os = OutScale{}, const ActQuant& aq = ActQuant{});
+                         const OutScale& os = OutScale{}, const ActQuant& aq = ActQuant{}, int dma_ns = 0);
 // LDS-tiled MFMA GEMM over k-rows [k_begin, k_end); accumulate != 0 adds into C instead of storing.
 // With os.Y set the tile epilogue writes the dequantised floats instead (accumulate must be 0).
 // splits > 1: split-K over gridDim.y, each workgroup row of the grid covering k_split k-rows (a

@@ -1404,6 +1404,187 @@ void gemm_pipe_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ 
 }
 
 // ------------------------------------------------------------------------------------------------
+// DMA-staged skinny kernel (M <= 16 per m-group, long weight streams).
+//
+// The register-staged skinny kernels read each weight row as 64-byte pieces, one per wave, so every
+// load instruction touches 16 rows x half a cache line and only PD k-steps fit in a wave's registers.
+// Here the workgroup's weight strip (256 bytes of each row, 1024 outputs) goes global -> LDS with
+// global_load_lds_dwordx4: one instruction reads 4 whole rows of the strip (full 128-byte lines),
+// no registers hold data in flight, and NS-1 k-steps (16 KB each) are in flight per workgroup, small
+// enough for two workgroups per CU.  The activation slice of the k-range (16 rows, clamped, up to
+// 16*NAD 16-byte chunks per row) is DMA'd once at the start in k-chunk-major order, so the 16 rows
+// one fragment read touches are 256 contiguous bytes.
+//   * Stage layout: 64 rows x 16 chunks of 16 bytes; chunk c of row r sits at position
+//     c ^ sd_swz(r), chosen per lane when the DMA address is formed.  sd_swz spreads the 8 rows that
+//     one 16-lane group of a transposing read touches over 8 positions (32 banks) and gives the next
+//     16-row group the other 32 banks.
+//   * B fragments: ds_read_b64_tr_b8 as in gemm_pipe_kernel -- lane q gets byte-column q of its
+//     16-byte group for 16 k-rows (two reads); wave w owns groups 4w..4w+3 (a 64-byte slab).
+//   * Decode: shift form, field j of every byte moved to bits 6-7 (values 64*w), result >> 6.
+// Step it: wait for this wave's DMAs of step it (static vmcnt while later steps are in flight,
+// vmcnt(0) in the last NS-1 steps), barrier, issue step it+NS-1 into the buffer read at step it-1,
+// read fragments, MFMAs.  Outputs and modes are those of the other skinny kernels.
+// ------------------------------------------------------------------------------------------------
+constexpr int SD_BNB = 256;                  // strip bytes per row (per workgroup)
+constexpr int SD_STAGE = 64 * SD_BNB;        // one k-step
+constexpr int SD_NL = SD_STAGE / 16 / 256;   // DMA instructions per thread per k-step
+
+__device__ __forceinline__ int sd_swz(int r) { return (r & 7) | (((r >> 4) & 1) << 3); }
+
+template <int NS, int NAD, bool LOW_M>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+void skinny_dma_kernel(SkinnyArgs args) {
+    static_assert(NS >= 2 && NS <= 4, "2 to 4 stages");
+    __shared__ __attribute__((aligned(16))) uint8_t sW0[SD_STAGE];
+    __shared__ __attribute__((aligned(16))) uint8_t sW1[SD_STAGE];
+    __shared__ __attribute__((aligned(16))) uint8_t sW2[NS > 2 ? SD_STAGE : 16];
+    __shared__ __attribute__((aligned(16))) uint8_t sW3[NS > 3 ? SD_STAGE : 16];
+    __shared__ __attribute__((aligned(16))) int8_t sA[NAD * 256 * 16];
+    auto stage_w = [&](int i) -> uint8_t* { return i == 0 ? sW0 : (i == 1 ? sW1 : (i == 2 ? sW2 : sW3)); };
+
+    const int8_t* __restrict__ A = args.A;
+    const uint8_t* __restrict__ B = args.B;
+    const int M = args.M, K = args.K, NB = args.N >> 2;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int q = lane & 15, kb = lane >> 4;
+    int cx, sy;
+    {
+        const int lin = xcd_linear(blockIdx.x + gridDim.x * blockIdx.y, gridDim.x * gridDim.y);
+        cx = lin % gridDim.x;
+        sy = lin / gridDim.x;
+    }
+    const int bc0 = cx * SD_BNB;
+    const int m0 = blockIdx.z * 16;
+    const int s_begin = sy * args.steps_per_split;
+    const int nst = min(K >> 6, s_begin + args.steps_per_split) - s_begin;  // >= 1 (planner)
+
+    // Activation slice: position j = 16 c + r holds 16-byte chunk c of row r (rows clamped to the
+    // m-group, chunks to the k-range).
+    {
+        const int a_rows = min(16, M - m0);
+        const int8_t* abase = A + (size_t)m0 * (size_t)K + (size_t)s_begin * 64;
+#pragma unroll
+        for (int u = 0; u < NAD; ++u) {
+            const int j = u * 256 + tid;
+            const int c = min(j >> 4, nst * 4 - 1), r = min(j & 15, a_rows - 1);
+            lds_dma16(abase + (size_t)r * (size_t)K + c * 16, sA + (u * 256 + wave * 64) * 16);
+        }
+    }
+    uint32_t w_off[SD_NL];
+#pragma unroll
+    for (int p = 0; p < SD_NL; ++p) {
+        const int slot = (p * 4 + wave) * 64 + lane;
+        const int r = slot >> 4, pos = slot & 15;
+        const int col = min(bc0 + (pos ^ sd_swz(r)) * 16, NB - 16);  // past the last column: re-read, unused
+        w_off[p] = (uint32_t)r * (uint32_t)NB + (uint32_t)col;
+    }
+    auto issue = [&](int st, int buf) {
+        const uint8_t* wbase = B + (size_t)(s_begin + st) * 64 * (size_t)NB;
+        uint8_t* wdst = stage_w(buf);
+#pragma unroll
+        for (int p = 0; p < SD_NL; ++p) lds_dma16(wbase + w_off[p], wdst + (p * 4 + wave) * 1024);
+    };
+    uint32_t w_lane[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const int r0 = kb * 16 + (q >> 1);
+        w_lane[g] = (uint32_t)(r0 * SD_BNB + 16 * ((wave * 4 + g) ^ sd_swz(r0)) + 8 * (q & 1));
+    }
+    const uint32_t a_lane = lds_u32(sA) + (uint32_t)((kb * 16 + q) * 16);
+
+    v4i acc[4][4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[g][j] = v4i{0, 0, 0, 0};
+
+    auto step = [&](int it, int buf) {
+        const uint32_t wb = lds_u32(stage_w(buf));
+        uint64_t lo[4], hi[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            lo[g] = lds_read_tr8_asm(wb + w_lane[g]);
+            hi[g] = lds_read_tr8_asm(wb + w_lane[g] + 8 * SD_BNB);
+        }
+        v4i a = lds_read_b128_asm(a_lane + (uint32_t)(it * 64 * 16));
+        TX_LGKMCNT0();
+        __asm__ volatile("" : "+v"(a));
+#pragma unroll
+        for (int g = 0; g < 4; ++g) __asm__ volatile("" : "+v"(lo[g]), "+v"(hi[g]));
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const uint32_t x4[4] = {(uint32_t)lo[g], (uint32_t)(lo[g] >> 32), (uint32_t)hi[g], (uint32_t)(hi[g] >> 32)};
+            v4i bfr[4];
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) {
+                const uint32_t x = x4[r4];
+                bfr[0][r4] = (int)((x << 6) & 0xC0C0C0C0u);
+                bfr[1][r4] = (int)((x << 4) & 0xC0C0C0C0u);
+                bfr[2][r4] = (int)((x << 2) & 0xC0C0C0C0u);
+                bfr[3][r4] = (int)(x & 0xC0C0C0C0u);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[g][j] = mfma_i8(a, bfr[j], acc[g][j]);
+        }
+    };
+
+    // Prologue: NS-1 steps in flight (the activation slice DMA went first).
+#pragma unroll
+    for (int p = 0; p < NS - 1; ++p)
+        if (p < nst) issue(p, p);
+    int it = 0;
+    // Steady state: step it+NS-1 exists, so exactly NS-1 steps are outstanding at each wait.
+    for (; it + NS - 1 < nst; ++it) {
+        TX_VMCNT((NS - 2) * SD_NL);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        issue(it + NS - 1, (it + NS - 1) % NS);
+        step(it, it % NS);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    for (; it < nst; ++it) {
+        TX_VMCNT(0);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        step(it, it % NS);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // Epilogue: lane (q, kb) holds rows 4kb+i of byte-columns bc0 + 16(4 wave + g) + q.
+    if (LOW_M && kb != 0) return;
+    int32_t* out_base = args.mode == SK_PARTIAL ? args.P + (size_t)sy * (size_t)M * (size_t)args.N : args.C;
+    const bool vec = args.mode == SK_PARTIAL || args.vec_store;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int row = m0 + 4 * kb + i;
+        if (row >= M) continue;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int bcol = bc0 + (wave * 4 + g) * 16 + q;
+            if (bcol >= NB) continue;
+            const v4i v = {acc[g][0][i] >> 6, acc[g][1][i] >> 6, acc[g][2][i] >> 6, acc[g][3][i] >> 6};
+            if (args.mode == SK_STORE && args.os.Y) {
+                store_scaled(args.os, row, args.N, 4 * bcol, v, args.vec_store);
+                continue;
+            }
+            int32_t* out = out_base + (size_t)row * (size_t)args.N + 4 * bcol;
+            if (args.mode == SK_ATOMIC) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    if (v[j] != 0) atomicAdd(out + j, v[j]);
+            } else if (vec) {
+                *reinterpret_cast<v4i*>(out) = v;
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) out[j] = v[j];
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
 // Naive kernel: one work-item per output, weights decoded per k from global memory with
 // w = (b & 1) - (b & 2) (the reference decode2, src/cuda_kernels.cu:40-54).
 // ------------------------------------------------------------------------------------------------
@@ -1475,6 +1656,22 @@ hipError_t launch_generic(const SkinnyArgs& a, dim3 grid, hipStream_t st) {
     else if (a.aligned_w) hipLaunchKernelGGL((skinny_generic_kernel<MT, LOW_M, true, false>), grid, block, 0, st, a);
     else if (a.aligned_a) hipLaunchKernelGGL((skinny_generic_kernel<MT, LOW_M, false, true>), grid, block, 0, st, a);
     else hipLaunchKernelGGL((skinny_generic_kernel<MT, LOW_M, false, false>), grid, block, 0, st, a);
+    return hipGetLastError();
+}
+
+template <int NS, bool LOW_M>
+void launch_dma_ns(const SkinnyArgs& a, dim3 grid, hipStream_t st) {
+    const int sps = a.steps_per_split;
+    if (sps <= 4) hipLaunchKernelGGL((skinny_dma_kernel<NS, 1, LOW_M>), grid, dim3(256), 0, st, a);
+    else if (sps <= 8) hipLaunchKernelGGL((skinny_dma_kernel<NS, 2, LOW_M>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((skinny_dma_kernel<NS, 4, LOW_M>), grid, dim3(256), 0, st, a);
+}
+
+hipError_t launch_dma(const SkinnyArgs& a, dim3 grid, int ns, hipStream_t st) {
+    const bool low = a.M <= 4;
+    if (ns == 2) low ? launch_dma_ns<2, true>(a, grid, st) : launch_dma_ns<2, false>(a, grid, st);
+    else if (ns == 3) low ? launch_dma_ns<3, true>(a, grid, st) : launch_dma_ns<3, false>(a, grid, st);
+    else low ? launch_dma_ns<4, true>(a, grid, st) : launch_dma_ns<4, false>(a, grid, st);
     return hipGetLastError();
 }
 
@@ -1616,6 +1813,14 @@ hipError_t launch_zero(int32_t* C, size_t n, hipStream_t st) {
     return hipGetLastError();
 }
 
+// skinny_dma_kernel: one m-group of <= 16 rows, whole 64-row k-steps, 16-byte aligned operands, an
+// activation slice of <= 16 steps per split.
+bool skinny_dma_ok(const int8_t* A, const uint8_t* B, int M, int K, int N, int steps_per_split) {
+    const int NB = N >> 2;
+    return M <= 16 && (K % 64 == 0) && (NB % 64 == 0) && ((uintptr_t)B % 16 == 0) && ((uintptr_t)A % 16 == 0) &&
+           steps_per_split >= 1 && steps_per_split <= 16 && (NB < (1 << 26));
+}
+
 bool skinny_fast_ok(const int8_t* A, const uint8_t* B, int M, int K, int N, int steps_per_split) {
     const int NB = N >> 2;
     return (K % 64 == 0) && (NB % 64 == 0) && ((uintptr_t)B % 16 == 0) && ((uintptr_t)A % 16 == 0) &&
@@ -1630,7 +1835,7 @@ bool skinny_short_ok(const uint8_t* B, int M, int K, int N, int steps_per_split,
 
 hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int tb, int kw,
                          int splits, int steps_per_split, int32_t* partials, hipStream_t st, const OutScale& os,
-                         const ActQuant& aq) {
+                         const ActQuant& aq, int dma_ns) {
     const int NB = N >> 2;
     const int mode = splits <= 1 ? SK_STORE : (partials ? SK_PARTIAL : SK_ATOMIC);
     if (mode == SK_ATOMIC && C == nullptr) return hipErrorInvalidValue;  // scaled call without int scratch
@@ -1652,7 +1857,12 @@ hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, i
         const char* e = std::getenv("TERNIX_SKINNY_SHORT");
         return e && e[0] == '0';
     }();
-    if (aq.mode != 0) {
+    if (dma_ns != 0 && (aq.mode != 0 || dma_ns < 2 || dma_ns > 4 || !skinny_dma_ok(A, B, M, K, N, steps_per_split)))
+        return hipErrorInvalidValue;
+    if (dma_ns != 0) {
+        const dim3 grid((NB + SD_BNB - 1) / SD_BNB, splits, mgroups);
+        e = launch_dma(a, grid, dma_ns, st);
+    } else if (aq.mode != 0) {
         // Fused activation quantisation: only on the short kernel with a split (see skinny_short_kernel).
         a.X = aq.X;
         a.G = aq.G;

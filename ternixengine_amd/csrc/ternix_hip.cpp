@@ -97,7 +97,33 @@ hipError_t validate(const void* dA, const void* dB, const void* dC, int64_t M, i
 // reduce launch) with sps k-steps each.
 struct SkinnyPlan {
     int tb, kw, splits, sps;
+    int dma;  // > 0: skinny_dma_kernel with this many LDS stages
 };
+
+// Plan of the DMA-staged skinny kernel (one m-group of <= 16 rows, 256-byte column strips): the
+// largest split count that keeps the grid within one workgroup per CU, capped, with several rows, so
+// the partial sums stay below half the weight bytes.  Returns dma = 0 when the k-range per split
+// would exceed the kernel's activation slice (16 k-steps).
+SkinnyPlan plan_skinny_dma(int M, int K, int N, int ns) {
+    const int nsteps = K / 64;
+    const long col_wgs = (N / 4 + 255) / 256;
+    const long cus = cu_count();
+    long splits = std::max(1L, cus / col_wgs);
+    splits = std::min(splits, std::max(1L, (long)K / (32L * M)));
+    splits = std::min<long>(splits, nsteps);
+    int sps = (int)((nsteps + splits - 1) / splits);
+    while (col_wgs * ((nsteps + sps - 1) / sps) > std::max(cus, col_wgs)) ++sps;  // no second wave
+    SkinnyPlan p{1, 1, (nsteps + sps - 1) / sps, sps, ns};
+    if (const char* env = std::getenv("TERNIX_SKINNY_PLAN")) {  // experiments: "tb,kw,splits"
+        int etb = 0, ekw = 0, esp = 0;
+        if (std::sscanf(env, "%d,%d,%d", &etb, &ekw, &esp) == 3 && esp >= 1) {
+            p.sps = (nsteps + esp - 1) / esp;
+            p.splits = (nsteps + p.sps - 1) / p.sps;
+        }
+    }
+    if (p.sps > 16 || p.sps > ternix_hip::kMaxKPerAccumulator / 64) p.dma = 0;
+    return p;
+}
 
 SkinnyPlan plan_skinny(int M, int K, int N, bool generic = false) {
     const int NB = N / 4;
@@ -113,7 +139,7 @@ SkinnyPlan plan_skinny(int M, int K, int N, bool generic = false) {
     // the same number of workgroups (measured on MI355X, cfg3 M=16: 13.9 vs 15.4 us up, 14.1 vs 15.4
     // us down).
     const int kw = M > 4 ? 2 : 1;
-    SkinnyPlan p{1, kw, 1, nsteps};
+    SkinnyPlan p{1, kw, 1, nsteps, 0};
     const long col_wgs = (NB + 256 / kw - 1) / (256 / kw);
     const long wgs = col_wgs * mgroups;
     const long target = cu_count();
@@ -155,7 +181,18 @@ hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
                       const ternix_hip::ActQuant& aq = ternix_hip::ActQuant{}) {
     const bool generic = !(K % 64 == 0 && (N / 4) % 64 == 0 && reinterpret_cast<uintptr_t>(dB) % 16 == 0 &&
                            (aq.mode != 0 || reinterpret_cast<uintptr_t>(dA) % 16 == 0));
-    const SkinnyPlan p = plan_skinny(M, K, N, generic);
+    // DMA-staged kernel: TERNIX_SKINNY_DMA=0 disables it, 2..4 sets its stage count (experiments).
+    static const int dma_env = [] {
+        const char* e = std::getenv("TERNIX_SKINNY_DMA");
+        return e ? std::atoi(e) : -1;
+    }();
+    SkinnyPlan p{0, 0, 0, 0, 0};
+    if (!generic && aq.mode == 0 && M <= 16 && dma_env != 0 &&
+        ternix_hip::skinny_dma_ok(dA, dB, M, K, N, 1)) {
+        p = plan_skinny_dma(M, K, N, dma_env >= 2 && dma_env <= 4 ? dma_env : 3);
+        if (p.splits <= 1) p.dma = 0;  // the kernel writes partials or atomics only through a split
+    }
+    if (p.dma == 0) p = plan_skinny(M, K, N, generic);
     // Fused activation quantisation needs the short kernel with a split; the caller falls back to the
     // standalone quantisation launch when this returns hipErrorInvalidValue.
     if (aq.mode != 0 && !ternix_hip::skinny_short_ok(dB, M, K, N, p.sps, p.splits)) return hipErrorInvalidValue;
@@ -164,7 +201,7 @@ hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
         const size_t need = (size_t)p.splits * (size_t)M * (size_t)N * sizeof(int32_t);
         if (need <= kWorkspaceMax) partials = static_cast<int32_t*>(workspace(st, need));
     }
-    return ternix_hip::launch_skinny(dA, dB, dC, M, K, N, p.tb, p.kw, p.splits, p.sps, partials, st, os, aq);
+    return ternix_hip::launch_skinny(dA, dB, dC, M, K, N, p.tb, p.kw, p.splits, p.sps, partials, st, os, aq, p.dma);
 }
 
 // Split-K for GEMMs with too few output tiles to fill the chip (mid-size M against a long K, e.g.
