@@ -59,7 +59,10 @@ bool skinny_dma_ok(const int8_t* A, const uint8_t* B, int M, int K, int N, int s
 // ignored, aq must be unset, skinny_dma_ok must hold; hipErrorInvalidValue otherwise).
 hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int tb, int kw,
                          int splits, int steps_per_split, int32_t* partials, hipStream_t st,
-                         const OutScale& os = OutScale{}, const ActQuant& aq = ActQuant{}, int dma_ns = 0);
+                         const OutScale& os = OutScale{}, const ActQuant& aq = ActQuant{}, int dma_ns = 0,
+                         int n_out = 0);
+// (n_out > 0: a padded problem -- N is the padded column count of A x W, and C / os.Y has n_out <= N
+// columns; only with a split-K workspace, whose reduce drops the padding.)
 // LDS-tiled MFMA GEMM over k-rows [k_begin, k_end); accumulate != 0 adds into C instead of storing.
 // With os.Y set the tile epilogue writes the dequantised floats instead (accumulate must be 0).
 // splits > 1: split-K over gridDim.y, each workgroup row of the grid covering k_split k-rows (a
@@ -70,7 +73,14 @@ hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int
                        int k_split = 0);
 // C (or os.Y) = sum over `splits` slabs of P ([splits][M][N] int32).
 hipError_t launch_splitk_reduce(const int32_t* P, int32_t* C, int M, int N, int splits, const OutScale& os,
-                                hipStream_t st);
+                                hipStream_t st, int n_in = 0);
+// (n_in > N: the partials have n_in columns per row, of which the first N are summed into C.)
+// Padded copy of up to two row sets in one launch (ragged shapes): rows of len bytes at src_pitch
+// into dst rows of dst_pitch bytes (dst 16-byte aligned, dst_pitch % 16 == 0), zero-filled past len
+// and for rows rows..dst_rows-1.  dst1 == nullptr: one set only.
+hipError_t launch_pad_rows(const uint8_t* src0, uint8_t* dst0, int rows0, int dst_rows0, int src_pitch0, int len0,
+                           int dst_pitch0, const uint8_t* src1, uint8_t* dst1, int rows1, int dst_rows1,
+                           int src_pitch1, int len1, int dst_pitch1, hipStream_t st);
 // In-place-capable conversion of an int32 C to the dequantised float Y (Y may alias C).
 hipError_t launch_dequant(const int32_t* C, const OutScale& os, int M, int N, hipStream_t st);
 // Per-row RMSNorm (reference rms_norm_scalar, src/simd_math.cpp:7-12): out = x * inv * w with

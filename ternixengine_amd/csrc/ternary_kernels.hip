@@ -1613,21 +1613,24 @@ __global__ __launch_bounds__(256) void zero_kernel(int32_t* __restrict__ C, size
 // (lane = group); its 4 waves take splits s = w, w+4, ... with all their loads issued at once (one
 // memory round trip for up to 64 splits), then add in LDS.  Integer addition is exact, so the order
 // does not change the result.
+// P: [splits][M][n_in] int32 (slab stride slab4 16-byte units); C / os.Y: M x N (N <= n_in: the
+// columns past N of a padded problem are dropped).
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const int32_t* __restrict__ P, int32_t* __restrict__ C,
                                                             size_t n4, int splits, int vec_store, OutScale os,
-                                                            int N) {
+                                                            int N, int n_in, size_t slab4) {
     __shared__ v4i part[3][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const size_t i = (size_t)blockIdx.x * 64 + lane;
     const size_t ic = i < n4 ? i : n4 - 1;
-    const v4i* src = reinterpret_cast<const v4i*>(P) + ic;
+    const size_t si = n_in == N ? ic : (4 * ic / (size_t)N) * (size_t)(n_in / 4) + (4 * ic % (size_t)N) / 4;
+    const v4i* src = reinterpret_cast<const v4i*>(P) + si;
     v4i sum = {0, 0, 0, 0};
     for (int s0 = wave; s0 < splits; s0 += 64) {
         v4i v[16];
 #pragma unroll
         for (int u = 0; u < 16; ++u) {
             const int s = s0 + 4 * u;
-            v[u] = s < splits ? src[(size_t)s * n4] : v4i{0, 0, 0, 0};
+            v[u] = s < splits ? src[(size_t)s * slab4] : v4i{0, 0, 0, 0};
         }
 #pragma unroll
         for (int u = 0; u < 16; ++u) sum += v[u];
@@ -1835,9 +1838,10 @@ bool skinny_short_ok(const uint8_t* B, int M, int K, int N, int steps_per_split,
 
 hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int tb, int kw,
                          int splits, int steps_per_split, int32_t* partials, hipStream_t st, const OutScale& os,
-                         const ActQuant& aq, int dma_ns) {
+                         const ActQuant& aq, int dma_ns, int n_out) {
     const int NB = N >> 2;
     const int mode = splits <= 1 ? SK_STORE : (partials ? SK_PARTIAL : SK_ATOMIC);
+    if (n_out > 0 && (mode != SK_PARTIAL || n_out > N || n_out % 4 != 0)) return hipErrorInvalidValue;
     if (mode == SK_ATOMIC && C == nullptr) return hipErrorInvalidValue;  // scaled call without int scratch
     if (aq.mode != 0 && !skinny_short_ok(B, M, K, N, steps_per_split, splits)) return hipErrorInvalidValue;
     if (mode == SK_ATOMIC) {
@@ -1891,8 +1895,11 @@ hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, i
     if (mode == SK_ATOMIC && scaled) return launch_dequant(C, os, M, N, st);  // C: alias of os.Y or scratch
     if (mode != SK_PARTIAL) return e;
     const size_t n4 = (size_t)M * (size_t)N / 4;
-    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n4 + 63) / 64)), dim3(256), 0, st, partials, C, n4,
-                       splits, vec_store, os, N);
+    const int n_c = n_out > 0 ? n_out : N;
+    const size_t n4c = (size_t)M * (size_t)n_c / 4;
+    const int vec_c = n_out > 0 ? ((uintptr_t)(scaled ? (const void*)os.Y : (const void*)C) % 16) == 0 : vec_store;
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n4c + 63) / 64)), dim3(256), 0, st, partials, C, n4c,
+                       splits, vec_c, os, n_c, N, n4);
     return hipGetLastError();
 }
 
@@ -1979,12 +1986,77 @@ hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int
 }
 
 hipError_t launch_splitk_reduce(const int32_t* P, int32_t* C, int M, int N, int splits, const OutScale& os,
-                                hipStream_t st) {
+                                hipStream_t st, int n_in) {
+    if (n_in <= 0) n_in = N;
     const size_t n4 = (size_t)M * (size_t)N / 4;
     if (n4 == 0) return hipSuccess;
     const int vec = ((uintptr_t)(os.Y ? (const void*)os.Y : (const void*)C) % 16) == 0;
     hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n4 + 63) / 64)), dim3(256), 0, st, P, C, n4, splits, vec,
-                       os, N);
+                       os, N, n_in, (size_t)M * (size_t)n_in / 4);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------------------------------------
+// Padded copy for ragged shapes: rows of `len` bytes at pitch src_pitch (any alignment) into rows of
+// dst_pitch bytes (16-byte aligned, dst_pitch % 16 == 0), zero-filled past len and for the rows
+// rows..dst_rows-1.  Each thread writes one 16-byte chunk from five aligned dword loads and
+// v_alignbyte; an aligned dword holding at least one byte of the source buffer never crosses a page
+// the buffer does not touch, so loads stay within the buffer's pages (dwords starting past its last
+// byte are not loaded).
+// ------------------------------------------------------------------------------------------------
+struct PadJob {
+    const uint8_t* src;
+    uint8_t* dst;
+    int rows, dst_rows, src_pitch, len, dst_pitch;
+    size_t chunks;  // dst_rows * dst_pitch / 16
+};
+
+__device__ __forceinline__ void pad_chunk(const PadJob& j, size_t idx) {
+    const int cpr = j.dst_pitch >> 4;
+    const int r = (int)(idx / (size_t)cpr), c = (int)(idx % (size_t)cpr);
+    v4i out = {0, 0, 0, 0};
+    const int n = min(max(j.len - 16 * c, 0), 16);  // source bytes in this chunk
+    if (r < j.rows && n > 0) {
+        const uint8_t* p = j.src + (size_t)r * (size_t)j.src_pitch + 16 * c;
+        const uint8_t* end = j.src + (size_t)(j.rows - 1) * (size_t)j.src_pitch + j.len;
+        const uint32_t* pa = reinterpret_cast<const uint32_t*>((uintptr_t)p & ~(uintptr_t)3);
+        const uint32_t sh = (uint32_t)((uintptr_t)p & 3);
+        uint32_t d[5];
+#pragma unroll
+        for (int k = 0; k < 5; ++k) d[k] = reinterpret_cast<const uint8_t*>(pa + k) < end ? pa[k] : 0u;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            uint32_t v = __builtin_amdgcn_alignbyte(d[m + 1], d[m], sh);
+            const int keep = min(max(n - 4 * m, 0), 4);  // bytes of this dword inside the row
+            v = keep >= 4 ? v : (keep == 0 ? 0u : (v & ((1u << (8 * keep)) - 1u)));
+            out[m] = (int)v;
+        }
+    }
+    *reinterpret_cast<v4i*>(j.dst + (size_t)r * (size_t)j.dst_pitch + 16 * c) = out;
+}
+
+__global__ __launch_bounds__(256) void pad_rows_kernel(PadJob j0, PadJob j1) {
+    const size_t total = j0.chunks + j1.chunks;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (size_t)gridDim.x * 256) {
+        if (i < j0.chunks) pad_chunk(j0, i);
+        else pad_chunk(j1, i - j0.chunks);
+    }
+}
+
+hipError_t launch_pad_rows(const uint8_t* src0, uint8_t* dst0, int rows0, int dst_rows0, int src_pitch0, int len0,
+                           int dst_pitch0, const uint8_t* src1, uint8_t* dst1, int rows1, int dst_rows1,
+                           int src_pitch1, int len1, int dst_pitch1, hipStream_t st) {
+    if (dst_pitch0 % 16 != 0 || (uintptr_t)dst0 % 16 != 0 || len0 > dst_pitch0 || rows0 > dst_rows0 ||
+        (dst1 && (dst_pitch1 % 16 != 0 || (uintptr_t)dst1 % 16 != 0 || len1 > dst_pitch1 || rows1 > dst_rows1)))
+        return hipErrorInvalidValue;
+    const PadJob j0{src0, dst0, rows0, dst_rows0, src_pitch0, len0, dst_pitch0,
+                    (size_t)dst_rows0 * (size_t)dst_pitch0 / 16};
+    const PadJob j1{src1, dst1, rows1, dst_rows1, src_pitch1, len1, dst_pitch1,
+                    dst1 ? (size_t)dst_rows1 * (size_t)dst_pitch1 / 16 : 0};
+    const size_t total = j0.chunks + j1.chunks;
+    if (total == 0) return hipSuccess;
+    const unsigned blocks = (unsigned)std::min<size_t>((total + 255) / 256, 8192);
+    hipLaunchKernelGGL(pad_rows_kernel, dim3(blocks), dim3(256), 0, st, j0, j1);
     return hipGetLastError();
 }
 

@@ -95,6 +95,9 @@ hipError_t validate(const void* dA, const void* dB, const void* dC, int64_t M, i
 // Split-K plan of the skinny kernels: tb (64- or 128-byte column slab per wave), kw (waves per slab
 // inside a workgroup of 4 waves), `splits` workgroups along K (splits > 1 adds the partial-sum
 // reduce launch) with sps k-steps each.
+// Split count whose partial sums stay within 4 MiB: allowed whatever the weight size (small N).
+long partials_floor(int M, int N) { return (4L << 20) / std::max(1L, 4L * M * N); }
+
 struct SkinnyPlan {
     int tb, kw, splits, sps;
     int dma;  // > 0: skinny_dma_kernel with this many LDS stages
@@ -109,7 +112,7 @@ SkinnyPlan plan_skinny_dma(int M, int K, int N, int ns) {
     const long col_wgs = (N / 4 + 255) / 256;
     const long cus = cu_count();
     long splits = std::max(1L, cus / col_wgs);
-    splits = std::min(splits, std::max(1L, (long)K / (32L * M)));
+    splits = std::min(splits, std::max({1L, (long)K / (32L * M), partials_floor(M, N)}));
     splits = std::min<long>(splits, nsteps);
     int sps = (int)((nsteps + splits - 1) / splits);
     while (col_wgs * ((nsteps + sps - 1) / sps) > std::max(cus, col_wgs)) ++sps;  // no second wave
@@ -133,7 +136,7 @@ SkinnyPlan plan_skinny(int M, int K, int N, bool generic = false) {
     // contiguous bytes of every weight row per workgroup), and K split into as many ranges as keep
     // the grid within one workgroup per CU (a CU holding two of them finishes last).  With several
     // rows the partial sums ([splits][M][N] int32, written and read back once) are capped at about
-    // the weight bytes (K*N/4): splits <= K / (32 M).
+    // the weight bytes (K*N/4): splits <= K / (32 M), or 4 MiB of partials when that allows more.
     // Above 4 rows two waves share each 64-byte slab (alternate k-steps, summed in LDS), which halves
     // the cross-workgroup splits -- and the partial sums, 4 bytes per row and column per split -- for
     // the same number of workgroups (measured on MI355X, cfg3 M=16: 13.9 vs 15.4 us up, 14.1 vs 15.4
@@ -148,7 +151,7 @@ SkinnyPlan plan_skinny(int M, int K, int N, bool generic = false) {
         // The generic kernel (ragged or unaligned shapes) has a serial dword-load loop per k-step, so
         // it wants at least 32 splits whatever the partial-sum traffic (measured: M=17 K=4093 N=1028
         // 19.5 us with 32 splits vs 39 us with 7).
-        const long traffic_cap = std::max(generic ? 32L : 1L, (long)K / (32L * M));
+        const long traffic_cap = std::max({generic ? 32L : 1L, (long)K / (32L * M), partials_floor(M, N)});
         if (splits > traffic_cap) splits = traffic_cap;
         if (splits > nsteps) splits = nsteps;
         if (splits > 1) p.splits = (int)splits;
@@ -252,6 +255,80 @@ hipError_t run_gemm(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int
     return os.Y ? ternix_hip::launch_dequant(dC, os, M, N, st) : hipSuccess;
 }
 
+// Ragged shapes (K % 64 != 0 or N % 256 != 0) and misaligned operands on the automatic paths: one
+// launch copies W into a padded K' x N'/4 layout (K' = K rounded up to 128, N'/4 to 64 bytes, zeros in
+// the padding) and A into rows of K' bytes, inside the split-K workspace; the aligned kernels then run
+// on the padded problem with split-K, and the reduce writes only the N real columns (zero weights
+// and zero activations in the padding add nothing, so the sums are those of the original problem).
+// Returns hipErrorNotSupported, before launching anything, when this does not apply (no split,
+// graph capture without a large enough workspace, sizes past the workspace cap); the caller then
+// runs the generic kernels.
+hipError_t run_padded(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int K, int N, hipStream_t st,
+                      const ternix_hip::OutScale& os, bool skinny) {
+    const int NB = N / 4;
+    const long Kp = ((long)K + 127) / 128 * 128;
+    const long NBp = ((long)NB + 63) / 64 * 64;
+    const long Np = 4 * NBp;
+    if (K == 0 || Kp > INT_MAX || Np > INT_MAX || Kp * NBp >= (1L << 32)) return hipErrorNotSupported;
+    SkinnyPlan p{0, 0, 0, 0, 0};
+    int splits = 1, k_split = 0;
+    if (skinny) {
+        if (M <= 16) p = plan_skinny_dma(M, (int)Kp, (int)Np, 3);
+        if (p.dma == 0) p = plan_skinny(M, (int)Kp, (int)Np);
+        splits = p.splits;
+    } else {
+        splits = gemm_splits(M, (int)Kp, (int)Np);
+        if (splits > 1) {
+            k_split = (int)(((Kp + splits - 1) / splits + 127) / 128 * 128);
+            splits = (int)((Kp + k_split - 1) / k_split);
+        }
+    }
+    if (splits <= 1) return hipErrorNotSupported;
+    auto up = [](size_t b) { return (b + 255) & ~size_t(255); };
+    const size_t w_bytes = up((size_t)Kp * (size_t)NBp);
+    const size_t a_bytes = up((size_t)M * (size_t)Kp);
+    const size_t p_bytes = (size_t)splits * (size_t)M * (size_t)Np * sizeof(int32_t);
+    if (w_bytes + a_bytes + p_bytes > kWorkspaceMax) return hipErrorNotSupported;
+    uint8_t* ws = static_cast<uint8_t*>(workspace(st, w_bytes + a_bytes + p_bytes));
+    if (ws == nullptr) return hipErrorNotSupported;
+    uint8_t* Wp = ws;
+    int8_t* Ap = reinterpret_cast<int8_t*>(ws + w_bytes);
+    int32_t* P = reinterpret_cast<int32_t*>(ws + w_bytes + a_bytes);
+    hipError_t e = ternix_hip::launch_pad_rows(dB, Wp, K, (int)Kp, NB, NB, (int)NBp,
+                                               reinterpret_cast<const uint8_t*>(dA), reinterpret_cast<uint8_t*>(Ap),
+                                               M, M, K, K, (int)Kp, st);
+    if (e != hipSuccess) return e;
+    if (skinny)
+        return ternix_hip::launch_skinny(Ap, Wp, dC, M, (int)Kp, (int)Np, p.tb, p.kw, p.splits, p.sps, P, st, os,
+                                         ternix_hip::ActQuant{}, p.dma, N);
+    e = ternix_hip::launch_gemm(Ap, Wp, P, M, (int)Kp, (int)Np, 0, (int)Kp, 0, st, ternix_hip::OutScale{}, splits,
+                                k_split);
+    if (e != hipSuccess) return e;
+    return ternix_hip::launch_splitk_reduce(P, dC, M, N, splits, os, st, (int)Np);
+}
+
+// The aligned kernels need 16-byte aligned operands, N/4 % 64 == 0 and whole k-steps: 64 rows for
+// the skinny kernels, 128 for the pipelined GEMM.
+bool needs_padding(const int8_t* dA, const uint8_t* dB, int K, int N, bool skinny) {
+    return !(K % (skinny ? 64 : 128) == 0 && (N / 4) % 64 == 0 && reinterpret_cast<uintptr_t>(dB) % 16 == 0 &&
+             reinterpret_cast<uintptr_t>(dA) % 16 == 0);
+}
+
+// Automatic path for one call: the padded copy for ragged or misaligned shapes when it applies,
+// else the skinny kernels up to kSkinnyMaxM rows and the GEMM above.
+hipError_t run_auto(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int K, int N, hipStream_t st,
+                    const ternix_hip::OutScale& os, int skinny_max) {
+    static const bool pad_off = [] {
+        const char* e = std::getenv("TERNIX_RAGGED_PAD");  // experiments: 0 keeps the generic kernels
+        return e && e[0] == '0';
+    }();
+    if (!pad_off && needs_padding(dA, dB, K, N, M <= skinny_max)) {
+        const hipError_t e = run_padded(dA, dB, dC, M, K, N, st, os, M <= skinny_max);
+        if (e != hipErrorNotSupported) return e;
+    }
+    return M <= skinny_max ? run_skinny(dA, dB, dC, M, K, N, st, os) : run_gemm(dA, dB, dC, M, K, N, st, os);
+}
+
 enum class Path { Auto, Skinny, Gemm, Naive };
 
 int dispatch(Path path, const int8_t* dA, const uint8_t* dB, int32_t* dC, int64_t M64, int64_t K64, int64_t N64,
@@ -267,7 +344,7 @@ int dispatch(Path path, const int8_t* dA, const uint8_t* dB, int32_t* dC, int64_
         const char* e = std::getenv("TERNIX_SKINNY_MAX_M");  // experiments only
         return e ? std::atoi(e) : kSkinnyMaxM;
     }();
-    if (path == Path::Auto) path = M <= auto_skinny_max ? Path::Skinny : Path::Gemm;
+    if (path == Path::Auto) return (int)run_auto(dA, dB, dC, M, K, N, st, ternix_hip::OutScale{}, auto_skinny_max);
     switch (path) {
         case Path::Skinny: e = run_skinny(dA, dB, dC, M, K, N, st); break;
         case Path::Gemm: e = run_gemm(dA, dB, dC, M, K, N, st); break;
@@ -365,7 +442,7 @@ int ternix_hip_mul_mat_ternary_dequant(const int8_t* dA, const uint8_t* dB, floa
     // The int32 C never exists in memory on the fused paths; where one is needed (atomic split-K, K
     // chunks) it is kept in dY itself (same size) and converted in place.
     int32_t* c_alias = reinterpret_cast<int32_t*>(dY);
-    e = m <= kSkinnyMaxM ? run_skinny(dA, dB, c_alias, m, k, n, st, os) : run_gemm(dA, dB, c_alias, m, k, n, st, os);
+    e = run_auto(dA, dB, c_alias, m, k, n, st, os, kSkinnyMaxM);
     return (int)e;
 }
 
@@ -386,7 +463,7 @@ int ternix_hip_mul_mat_ternary_swiglu(const int8_t* dA, const uint8_t* dB, float
     os.rs = dRowScale;
     os.ws = w_scale;
     os.swiglu = 1;
-    e = m <= kSkinnyMaxM ? run_skinny(dA, dB, dScratch, m, k, n, st, os) : run_gemm(dA, dB, dScratch, m, k, n, st, os);
+    e = run_auto(dA, dB, dScratch, m, k, n, st, os, kSkinnyMaxM);
     return (int)e;
 }
 
