@@ -142,6 +142,7 @@ def verify(prob):
 
 def bench_gemv_pair(args, stream, lib):
     from ternixengine_amd import configs
+    from ternixengine_amd import hip_runtime as hr
     up, down = configs.CASES["cfg2_up"], configs.CASES["cfg2_down"]
     pair_w = up.K * up.N // 4 + down.K * down.N // 4
     copies = max(2, -(-POOL_MIN_BYTES // pair_w))
@@ -158,6 +159,19 @@ def bench_gemv_pair(args, stream, lib):
     bytes_step = up.bytes_algorithmic + down.bytes_algorithmic
     ms_eager = time_launches(step, args.steps, args.warmup, stream, graph=False)
     ok = ok and verify(pu) and verify(pd)
+    # per-launch time: events around each single call, synchronised (includes dispatch)
+    per_launch = {}
+    for name, pr in (("up", pu), ("down", pd)):
+        ts = []
+        for i in range(60):
+            e0, e1 = hr.Event(), hr.Event()
+            e0.record(stream)
+            launch(fn, pr, i % copies, stream)
+            e1.record(stream)
+            e1.synchronize()
+            ts.append(e0.elapsed_ms(e1) * 1e3)
+        per_launch[name] = round(statistics.median(ts), 3)
+    ok = ok and verify(pu) and verify(pd)
     # hot-cache variant (same weights every step) for reference only
     ms_hot = time_launches(lambda i: (launch(fn, pu, 0, stream), launch(fn, pd, 0, stream)), args.steps,
                            args.warmup, stream)
@@ -168,6 +182,7 @@ def bench_gemv_pair(args, stream, lib):
         "gbs_eager_launches": bytes_step / (ms_eager / args.steps * 1e-3) / 1e9,
         "gbs_hot_cache": bytes_step / (ms_hot / args.steps * 1e-3) / 1e9,
         "launch_us": ms / args.steps / 2 * 1e3,
+        "single_launch_median_us": per_launch,
         "pool_copies": copies,
         "pool_bytes": copies * pair_w,
         "verified": ok,
@@ -377,6 +392,52 @@ def cpu_baseline(seconds):
                       f"{med * 1e3:.2f} ms/pair, mul_mat_ternary_avx2_blocked, 1 thread, ~{seconds:.0f} s"}
 
 
+def cpu_baseline_all_cores(seconds, threads=None):
+    """The same reference kernel on all host cores (up to 16, the GPU box's CPU share): each thread owns
+    a column slice of every weight matrix, re-strided to its own K x (N_t/4) array (N_t % 8 == 0, the
+    AVX2 kernels' contract), and runs the cfg2 pair over its slice; ctypes releases the GIL during the
+    foreign calls.  Per-pair time = wall time / repetitions."""
+    import threading
+    from ternixengine_amd import configs
+    ref_so = os.path.join(ROOT, "oracle", "_ref", "libternix_ref.so")
+    vp, sz = ctypes.c_void_p, ctypes.c_size_t
+    if os.path.exists(ref_so):
+        fn, kind = ctypes.CDLL(ref_so).ref_mm_avx2_blocked, "reference"
+    else:
+        fn, kind = ctypes.CDLL(os.path.join(ROOT, "oracle", "liboracle.so")).oracle_mm_avx2_blocked, "port"
+    fn.argtypes = [vp, vp, vp, sz, sz, sz]
+    t = threads or max(1, min(16, os.cpu_count() or 1))
+    cases = [configs.CASES["cfg2_up"], configs.CASES["cfg2_down"]]
+    work = [[] for _ in range(t)]  # per thread: (a, w slice, out slice, M, K, N_t)
+    for c in cases:
+        a, wp = configs.gen_a(c), configs.gen_w_packed(c).reshape(c.K, c.N // 4)
+        per = -(-c.N // t // 8) * 8
+        for i in range(t):
+            n0, n1 = i * per, min(c.N, (i + 1) * per)
+            if n1 > n0:
+                ws = np.ascontiguousarray(wp[:, n0 // 4:n1 // 4])
+                work[i].append((a, ws, np.empty((c.M, n1 - n0), np.int32), c.M, c.K, n1 - n0))
+
+    def one_pass(items):
+        for a, ws, out, m, k, n in items:
+            fn(a.ctypes.data_as(vp), ws.ctypes.data_as(vp), out.ctypes.data_as(vp), m, k, n)
+
+    t0 = time.perf_counter()
+    one_pass([x for w in work for x in w])  # single-thread pass: sizes the repetition count
+    reps = max(3, int(seconds / max(time.perf_counter() - t0, 1e-6) * 2))  # ~seconds at 2x, less if faster
+    ths = [threading.Thread(target=lambda w=w: [one_pass(w) for _ in range(reps)]) for w in work]
+    t0 = time.perf_counter()
+    for th in ths:
+        th.start()
+    for th in ths:
+        th.join()
+    per_pair = (time.perf_counter() - t0) / reps
+    bytes_step = sum(c.bytes_algorithmic for c in cases)
+    return {"value": round(bytes_step / per_pair / 1e9, 3), "unit": "GB/s", "cores": t, "kind": kind,
+            "sample": f"{reps} cfg2 FFN pairs on {t} threads (column slices), {per_pair * 1e3:.3f} ms/pair, "
+                      "mul_mat_ternary_avx2_blocked"}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -457,6 +518,7 @@ def main():
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
         line["cpu_baseline"]["value"] = round(line["cpu_baseline"]["value"], 3)
+        line["cpu_baseline_all_cores"] = cpu_baseline_all_cores(min(5.0, args.cpu_seconds))
     print(json.dumps(line), flush=True)
 
 
