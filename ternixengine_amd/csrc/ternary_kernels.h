@@ -63,6 +63,9 @@ hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, i
                          int n_out = 0);
 // (n_out > 0: a padded problem -- N is the padded column count of A x W, and C / os.Y has n_out <= N
 // columns; only with a split-K workspace, whose reduce drops the padding.)
+// True when launch_gemm runs this M <= 64 shape on 64 x 64 tiles (K % 256 == 0, N/4 % 16 == 0, at
+// most one tile per CU); split-K k-ranges must then be multiples of 256.
+bool gemm_narrow_wanted(int M, int K, int N);
 // LDS-tiled MFMA GEMM over k-rows [k_begin, k_end); accumulate != 0 adds into C instead of storing.
 // With os.Y set the tile epilogue writes the dequantised floats instead (accumulate must be 0).
 // splits > 1: split-K over gridDim.y, each workgroup row of the grid covering k_split k-rows (a

@@ -957,7 +957,7 @@ __device__ __forceinline__ int gf_swz_w(int r) { return ((r >> 1) & 3) ^ ((r >> 
 // 8 rows of one transposing read on distinct banks by their pitch alone and flip the chunk for the
 // second 16-row half of a wave's k-block, which is read in the same pass.
 template <int BNB>
-__device__ __forceinline__ int swz_w(int r) { return BNB == 64 ? gf_swz_w(r) : ((r >> 4) & 1); }
+__device__ __forceinline__ int swz_w(int r) { return BNB == 64 ? gf_swz_w(r) : (BNB == 32 ? ((r >> 4) & 1) : 0); }
 
 template <int BM, int WGN, int NS, int BK>
 __global__ __launch_bounds__(GF_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
@@ -1903,6 +1903,27 @@ hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, i
     return hipGetLastError();
 }
 
+// Narrow 64 x 64 tiles for M <= 64 when they alone fill at most one workgroup per CU (measured on
+// MI355X: cfg3 M=64 up 18.0 -> 13.4 us with no K split, 4096^2 at M=64 16.2 -> 9.9 us; with more
+// tiles than CUs, e.g. N = 28672, the 256-column tiles are faster).  TERNIX_GEMM_NARROW=0 / 1 turns
+// the choice off / on regardless (experiments).
+bool gemm_narrow_wanted(int M, int K, int N) {
+    static const int env = [] {
+        const char* e = std::getenv("TERNIX_GEMM_NARROW");
+        return e ? std::atoi(e) : -1;
+    }();
+    const int NB = N >> 2;
+    if (env == 0 || M > 64 || NB % 16 != 0 || K % 256 != 0) return false;
+    if (env > 0) return true;
+    int cus = 256, dev = 0;
+    if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    return (long)((M + 63) / 64) * (NB / 16) <= cus;
+}
+
+bool gemm_narrow_ok(int M, int K, int N, int k_len, int splits, int k_split) {
+    return gemm_narrow_wanted(M, K, N) && k_len % 256 == 0 && (splits == 1 || k_split % 256 == 0);
+}
+
 hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int k_begin, int k_end,
                        int accumulate, hipStream_t st, const OutScale& os, int splits, int k_split) {
     const int NB = N >> 2;
@@ -1947,6 +1968,14 @@ hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int
             const char* e = std::getenv("TERNIX_GEMM_SMALLM");  // experiments only
             return e ? std::atoi(e) : 64;
         }();
+        if (M <= small_m_max && gemm_narrow_ok(M, K, N, k_end - k_begin, splits, k_split)) {
+            // 64 x 64 output tiles (16 bytes of every weight row): enough workgroups without a K
+            // split where the 256-column tiles would need one; one m-tile per wave, 256-deep stages.
+            const dim3 gridn((unsigned)(((M + 63) / 64) * (NB / 16)), splits);
+            hipLaunchKernelGGL((gemm_pipe_kernel<64, 1, 3, 256, 4, 16>), gridn, dim3(256), 0, st, A, B, C, M, K, N,
+                               NB / 16, k_begin, k_end, accumulate, vs, k_split, os);
+            return hipGetLastError();
+        }
         if (M <= small_m_max) {
             // Small M (64 rows or fewer): four-wave workgroups on 64-row tiles, so no MFMA row or A
             // byte is spent on padding rows; the caller splits K to fill the chip.

@@ -216,7 +216,8 @@ int gemm_splits(int M, int K, int N) {
         return e ? std::atoi(e) : 0;
     }();
     const int bm = M <= 64 ? 64 : 128;  // the tile height launch_gemm picks
-    const long tiles = (long)((M + bm - 1) / bm) * (long)((N / 4 + 63) / 64);
+    const bool narrow = ternix_hip::gemm_narrow_wanted(M, K, N);  // 64-column tiles instead of 256
+    const long tiles = (long)((M + bm - 1) / bm) * (long)((N / 4 + 63) / 64) * (narrow ? 4 : 1);
     const long cus = cu_count();
     long splits = env > 0 ? env : (tiles * 2 <= cus ? cus / tiles : 1);
     splits = std::min<long>(splits, std::max(1, K / 256));  // at least two 128-row stages per split
@@ -228,7 +229,8 @@ hipError_t run_gemm(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int
     if (K <= ternix_hip::kMaxKPerAccumulator) {
         int splits = gemm_splits(M, K, N);
         if (splits > 1) {
-            const int unit = K % 128 == 0 ? 128 : 64;
+            // whole stages per split: 256 rows for the narrow tiles, 128 for the others
+            const int unit = ternix_hip::gemm_narrow_wanted(M, K, N) ? 256 : (K % 128 == 0 ? 128 : 64);
             const int k_split = ((K + splits - 1) / splits + unit - 1) / unit * unit;
             splits = (K + k_split - 1) / k_split;
             const size_t need = (size_t)splits * (size_t)M * (size_t)N * sizeof(int32_t);
@@ -279,7 +281,8 @@ hipError_t run_padded(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
     } else {
         splits = gemm_splits(M, (int)Kp, (int)Np);
         if (splits > 1) {
-            k_split = (int)(((Kp + splits - 1) / splits + 127) / 128 * 128);
+            const long unit = ternix_hip::gemm_narrow_wanted(M, (int)Kp, (int)Np) ? 256 : 128;
+            k_split = (int)(((Kp + splits - 1) / splits + unit - 1) / unit * unit);
             splits = (int)((Kp + k_split - 1) / k_split);
         }
     }
