@@ -287,6 +287,8 @@ hipError_t run_padded(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
         }
     }
     if (splits <= 1) return hipErrorNotSupported;
+    // Each split's k-range must fit one int32 accumulator (the skinny plans guarantee it).
+    if (!skinny && k_split > ternix_hip::kMaxKPerAccumulator) return hipErrorNotSupported;
     auto up = [](size_t b) { return (b + 255) & ~size_t(255); };
     const size_t w_bytes = up((size_t)Kp * (size_t)NBp);
     const size_t a_bytes = up((size_t)M * (size_t)Kp);

@@ -307,3 +307,35 @@ def test_graph_survives_workspace_growth(oracle):
         assert (dc.download(np.int32, (1, small.N)) == expect).all(), rep
     got = d2c.download(np.int32, (m, n))
     assert (got[:2] == oracle.mm("scalar", a2[:2], w2, n)).all()
+
+
+def test_padded_path_graph_replay(oracle):
+    """Ragged and misaligned shapes on the automatic path (padded copy in the stream's workspace, aligned
+    kernels, padding-dropping reduce) captured into a hipGraph after one eager call has sized the
+    workspace; every replay, with eager work on the stream between replays, gives the oracle's C."""
+    s = hr.Stream()
+    rng = np.random.default_rng(21)
+    shapes = ((1, 1000, 3076, 0), (17, 4093, 1028, 0), (129, 1001, 516, 0), (3, 4096, 1024, 3), (40, 512, 256, 1))
+    for m, k, n, off in shapes:
+        a = rng.integers(-128, 128, size=(m, k), dtype=np.int8)
+        wp = rng.integers(0, 256, size=(k, n // 4), dtype=np.uint8)
+        wp &= 0xFF ^ ((wp & 0xAA) & ~((wp & 0x55) << 1) & 0xAA)  # clear code 10 fields (10 -> 00)
+        expect = oracle.mm("scalar", a, wp, n)
+        da, db, dc = hr.DeviceBuffer(a.nbytes + 16), hr.DeviceBuffer(wp.nbytes + 16), hr.DeviceBuffer(4 * m * n)
+        hr.check(hr._load().hipMemcpy(ctypes.c_void_p(da.value + off), a.ctypes.data_as(ctypes.c_void_p), a.nbytes,
+                                      hr.H2D), "A")
+        hr.check(hr._load().hipMemcpy(ctypes.c_void_p(db.value + off), wp.ctypes.data_as(ctypes.c_void_p),
+                                      wp.nbytes, hr.H2D), "W")
+        call = lambda: tx.mul_mat_ternary(da.value + off, db.value + off, dc.value, m, k, n, stream=s.handle)
+        log(f"[padded graph] M={m} K={k} N={n} offset={off}")
+        assert call() == 0
+        s.synchronize()
+        assert (dc.download(np.int32, (m, n)) == expect).all(), "eager"
+        g = hr.Graph(s, call)
+        for rep in range(3):
+            dc.upload(np.full(m * n, GARBAGE, np.int32))
+            g.launch()
+            s.synchronize()
+            assert (dc.download(np.int32, (m, n)) == expect).all(), (m, k, n, rep)
+            assert call() == 0  # eager work between replays
+            s.synchronize()
