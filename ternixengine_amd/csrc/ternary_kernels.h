@@ -55,8 +55,11 @@ bool skinny_short_ok(const uint8_t* B, int M, int K, int N, int steps_per_split,
 // True when the DMA-staged skinny kernel can run this call: M <= 16, K % 64 == 0, N % 256 == 0,
 // 16-byte aligned A and W, 1..16 k-steps per split.
 bool skinny_dma_ok(const int8_t* A, const uint8_t* B, int M, int K, int N, int steps_per_split);
+// ... and can also quantise the activations in its prologue (aq_mode 1 or 2): K <= 8192, splits > 1.
+bool skinny_dma_aq_ok(int aq_mode, int K, int splits);
 // dma_ns (2..4) selects the DMA-staged kernel with that many LDS stages (its own plan: tb and kw are
-// ignored, aq must be unset, skinny_dma_ok must hold; hipErrorInvalidValue otherwise).
+// ignored; skinny_dma_ok and skinny_dma_aq_ok must hold, hipErrorInvalidValue otherwise; with aq set
+// it runs 3 stages).
 hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int tb, int kw,
                          int splits, int steps_per_split, int32_t* partials, hipStream_t st,
                          const OutScale& os = OutScale{}, const ActQuant& aq = ActQuant{}, int dma_ns = 0,

@@ -1431,7 +1431,7 @@ constexpr int SD_NL = SD_STAGE / 16 / 256;   // DMA instructions per thread per 
 
 __device__ __forceinline__ int sd_swz(int r) { return (r & 7) | (((r >> 4) & 1) << 3); }
 
-template <int NS, int NAD, bool LOW_M>
+template <int NS, int NAD, bool LOW_M, int AQ = 0>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 void skinny_dma_kernel(SkinnyArgs args) {
     static_assert(NS >= 2 && NS <= 4, "2 to 4 stages");
@@ -1461,9 +1461,21 @@ void skinny_dma_kernel(SkinnyArgs args) {
     const int nst = min(K >> 6, s_begin + args.steps_per_split) - s_begin;  // >= 1 (planner)
 
     // Activation slice: position j = 16 c + r holds 16-byte chunk c of row r (rows clamped to the
-    // m-group, chunks to the k-range).
-    {
-        const int a_rows = min(16, M - m0);
+    // m-group, chunks to the k-range).  AQ > 0: built below from the fp32 rows instead.
+    const int a_rows = min(16, M - m0);
+    float xv[AQ ? kRowRegs : 1], gv[AQ == 2 ? kRowRegs : 1];
+    auto load_row = [&](int r) {  // elements k = tid + 256 j of row m0 + r (K <= 256 * kRowRegs)
+        const float* x = args.X + (size_t)(m0 + r) * (size_t)K;
+#pragma unroll
+        for (int j = 0; j < (AQ ? kRowRegs : 0); ++j) {
+            const int k = tid + 256 * j;
+            xv[j] = k < K ? x[k] : 0.0f;
+            if constexpr (AQ == 2) gv[j] = k < K ? args.G[k] : 0.0f;
+        }
+    };
+    if constexpr (AQ != 0) {
+        load_row(0);  // before the weight DMAs, so waiting for it does not wait for them
+    } else {
         const int8_t* abase = A + (size_t)m0 * (size_t)K + (size_t)s_begin * 64;
 #pragma unroll
         for (int u = 0; u < NAD; ++u) {
@@ -1534,6 +1546,41 @@ void skinny_dma_kernel(SkinnyArgs args) {
 #pragma unroll
     for (int p = 0; p < NS - 1; ++p)
         if (p < nst) issue(p, p);
+    if constexpr (AQ != 0) {
+        // Fused activation quantisation (the rule and accumulation order of quantize_rows_kernel /
+        // rmsnorm_kernel, from row_stats.h, so the int8 values are bit-identical to theirs): every
+        // workgroup computes its rows' statistics from registers and writes the int8 values of its
+        // own k-range into the slice layout; workgroup (0, 0) stores the row scales for the reduce.
+        __shared__ float red[4];
+        const int kbase = s_begin * 64, krange = nst * 64;
+        for (int r = 0; r < a_rows; ++r) {  // uniform: every thread takes part in the reductions
+            if (r > 0) load_row(r);
+            float inv = 1.0f;
+            if constexpr (AQ == 2) {
+                float ss = 0.0f;
+#pragma unroll
+                for (int j = 0; j < kRowRegs; ++j) ss = fmaf(xv[j], xv[j], ss);  // +0 past K changes nothing
+                ss = row_block_sum(ss, red);
+                inv = 1.0f / sqrtf(ss / (float)K + args.eps);
+            }
+            auto val = [&](int j) {
+                if constexpr (AQ == 2) return xv[j] * inv * gv[j];
+                else return xv[j];
+            };
+            float amax = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kRowRegs; ++j) amax = fmaxf(amax, fabsf(val(j)));
+            const float am = fmaxf(row_block_max(amax, red), 1e-5f);
+            const float sc = 127.0f / am;
+            if (tid == 0 && cx == 0 && sy == 0) args.rs_out[m0 + r] = am / 127.0f;
+#pragma unroll
+            for (int j = 0; j < kRowRegs; ++j) {
+                const int kk = tid + 256 * j - kbase;
+                if (kk >= 0 && kk < krange) sA[((kk >> 4) * 16 + r) * 16 + (kk & 15)] = (int8_t)quantize_value(val(j), sc);
+            }
+        }
+        TX_LGKMCNT0();  // this thread's slice bytes are written; the first step's barrier publishes them
+    }
     int it = 0;
     // Steady state: step it+NS-1 exists, so exactly NS-1 steps are outstanding at each wait.
     for (; it + NS - 1 < nst; ++it) {
@@ -1662,17 +1709,20 @@ hipError_t launch_generic(const SkinnyArgs& a, dim3 grid, hipStream_t st) {
     return hipGetLastError();
 }
 
-template <int NS, bool LOW_M>
+template <int NS, bool LOW_M, int AQ = 0>
 void launch_dma_ns(const SkinnyArgs& a, dim3 grid, hipStream_t st) {
     const int sps = a.steps_per_split;
-    if (sps <= 4) hipLaunchKernelGGL((skinny_dma_kernel<NS, 1, LOW_M>), grid, dim3(256), 0, st, a);
-    else if (sps <= 8) hipLaunchKernelGGL((skinny_dma_kernel<NS, 2, LOW_M>), grid, dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((skinny_dma_kernel<NS, 4, LOW_M>), grid, dim3(256), 0, st, a);
+    if (sps <= 4) hipLaunchKernelGGL((skinny_dma_kernel<NS, 1, LOW_M, AQ>), grid, dim3(256), 0, st, a);
+    else if (sps <= 8) hipLaunchKernelGGL((skinny_dma_kernel<NS, 2, LOW_M, AQ>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((skinny_dma_kernel<NS, 4, LOW_M, AQ>), grid, dim3(256), 0, st, a);
 }
 
-hipError_t launch_dma(const SkinnyArgs& a, dim3 grid, int ns, hipStream_t st) {
+// Fused activation quantisation (aq 1 or 2) runs with 3 stages only.
+hipError_t launch_dma(const SkinnyArgs& a, dim3 grid, int ns, int aq, hipStream_t st) {
     const bool low = a.M <= 4;
-    if (ns == 2) low ? launch_dma_ns<2, true>(a, grid, st) : launch_dma_ns<2, false>(a, grid, st);
+    if (aq == 1) low ? launch_dma_ns<3, true, 1>(a, grid, st) : launch_dma_ns<3, false, 1>(a, grid, st);
+    else if (aq == 2) low ? launch_dma_ns<3, true, 2>(a, grid, st) : launch_dma_ns<3, false, 2>(a, grid, st);
+    else if (ns == 2) low ? launch_dma_ns<2, true>(a, grid, st) : launch_dma_ns<2, false>(a, grid, st);
     else if (ns == 3) low ? launch_dma_ns<3, true>(a, grid, st) : launch_dma_ns<3, false>(a, grid, st);
     else low ? launch_dma_ns<4, true>(a, grid, st) : launch_dma_ns<4, false>(a, grid, st);
     return hipGetLastError();
@@ -1816,6 +1866,12 @@ hipError_t launch_zero(int32_t* C, size_t n, hipStream_t st) {
     return hipGetLastError();
 }
 
+// Fused activation quantisation on the DMA kernel: whole rows in registers (K <= 256 * kRowRegs) and a
+// split, whose reduce launch applies the row scales the kernel stores.
+bool skinny_dma_aq_ok(int aq_mode, int K, int splits) {
+    return aq_mode == 0 || (K <= 256 * kRowRegs && splits > 1);
+}
+
 // skinny_dma_kernel: one m-group of <= 16 rows, whole 64-row k-steps, 16-byte aligned operands, an
 // activation slice of <= 16 steps per split.
 bool skinny_dma_ok(const int8_t* A, const uint8_t* B, int M, int K, int N, int steps_per_split) {
@@ -1861,11 +1917,16 @@ hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, i
         const char* e = std::getenv("TERNIX_SKINNY_SHORT");
         return e && e[0] == '0';
     }();
-    if (dma_ns != 0 && (aq.mode != 0 || dma_ns < 2 || dma_ns > 4 || !skinny_dma_ok(A, B, M, K, N, steps_per_split)))
+    if (dma_ns != 0 && (!skinny_dma_aq_ok(aq.mode, K, splits) || dma_ns < 2 || dma_ns > 4 ||
+                        !skinny_dma_ok(A, B, M, K, N, steps_per_split)))
         return hipErrorInvalidValue;
     if (dma_ns != 0) {
         const dim3 grid((NB + SD_BNB - 1) / SD_BNB, splits, mgroups);
-        e = launch_dma(a, grid, dma_ns, st);
+        a.X = aq.X;
+        a.G = aq.G;
+        a.eps = aq.eps;
+        a.rs_out = aq.rs_out;
+        e = launch_dma(a, grid, aq.mode != 0 ? 3 : dma_ns, aq.mode, st);
     } else if (aq.mode != 0) {
         // Fused activation quantisation: only on the short kernel with a split (see skinny_short_kernel).
         a.X = aq.X;

@@ -190,15 +190,16 @@ hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
         return e ? std::atoi(e) : -1;
     }();
     SkinnyPlan p{0, 0, 0, 0, 0};
-    if (!generic && aq.mode == 0 && M <= 16 && dma_env != 0 &&
-        ternix_hip::skinny_dma_ok(dA, dB, M, K, N, 1)) {
+    if (!generic && M <= 16 && dma_env != 0 && ternix_hip::skinny_dma_ok(dA, dB, M, K, N, 1)) {
         p = plan_skinny_dma(M, K, N, dma_env >= 2 && dma_env <= 4 ? dma_env : 3);
         if (p.splits <= 1) p.dma = 0;  // the kernel writes partials or atomics only through a split
+        if (!ternix_hip::skinny_dma_aq_ok(aq.mode, K, p.splits)) p.dma = 0;
     }
     if (p.dma == 0) p = plan_skinny(M, K, N, generic);
-    // Fused activation quantisation needs the short kernel with a split; the caller falls back to the
-    // standalone quantisation launch when this returns hipErrorInvalidValue.
-    if (aq.mode != 0 && !ternix_hip::skinny_short_ok(dB, M, K, N, p.sps, p.splits)) return hipErrorInvalidValue;
+    // Fused activation quantisation needs the DMA or the short kernel with a split; the caller falls
+    // back to the standalone quantisation launch when this returns hipErrorInvalidValue.
+    if (aq.mode != 0 && p.dma == 0 && !ternix_hip::skinny_short_ok(dB, M, K, N, p.sps, p.splits))
+        return hipErrorInvalidValue;
     int32_t* partials = nullptr;
     if (p.splits > 1) {
         const size_t need = (size_t)p.splits * (size_t)M * (size_t)N * sizeof(int32_t);
