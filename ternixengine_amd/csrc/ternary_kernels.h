@@ -66,6 +66,8 @@ hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, i
                          int n_out = 0);
 // (n_out > 0: a padded problem -- N is the padded column count of A x W, and C / os.Y has n_out <= N
 // columns; only with a split-K workspace, whose reduce drops the padding.)
+// Compute units of the current device (cached per device).
+int device_cu_count();
 // True when launch_gemm runs this M <= 64 shape on 64 x 64 tiles (K % 256 == 0, N/4 % 16 == 0, at
 // most one tile per CU); split-K k-ranges must then be multiples of 256.
 bool gemm_narrow_wanted(int M, int K, int N);

@@ -36,6 +36,8 @@
 #include <stdint.h>
 #include <stdlib.h>
 
+#include <atomic>
+
 #include "row_stats.h"
 #include "ternary_kernels.h"
 
@@ -1964,6 +1966,18 @@ hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, i
     return hipGetLastError();
 }
 
+// Compute units of the current device, read once per device (the attribute query is not free).
+int device_cu_count() {
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    int n = cache[dev].load(std::memory_order_relaxed);
+    if (n > 0) return n;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev].store(n, std::memory_order_relaxed);
+    return n;
+}
+
 // Narrow 64 x 64 tiles for M <= 64 when they alone fill at most one workgroup per CU (measured on
 // MI355X: cfg3 M=64 up 18.0 -> 13.4 us with no K split, 4096^2 at M=64 16.2 -> 9.9 us; with more
 // tiles than CUs, e.g. N = 28672, the 256-column tiles are faster).  TERNIX_GEMM_NARROW=0 / 1 turns
@@ -1976,9 +1990,7 @@ bool gemm_narrow_wanted(int M, int K, int N) {
     const int NB = N >> 2;
     if (env == 0 || M > 64 || NB % 16 != 0 || K % 256 != 0) return false;
     if (env > 0) return true;
-    int cus = 256, dev = 0;
-    if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    return (long)((M + 63) / 64) * (NB / 16) <= cus;
+    return (long)((M + 63) / 64) * (NB / 16) <= device_cu_count();
 }
 
 bool gemm_narrow_ok(int M, int K, int N, int k_len, int splits, int k_split) {
@@ -1988,7 +2000,8 @@ bool gemm_narrow_ok(int M, int K, int N, int k_len, int splits, int k_split) {
 hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int k_begin, int k_end,
                        int accumulate, hipStream_t st, const OutScale& os, int splits, int k_split) {
     const int NB = N >> 2;
-    const char* force_generic = std::getenv("TERNIX_GEMM_GENERIC");
+    // Experiment switches, read once per process.
+    static const char* const force_generic = std::getenv("TERNIX_GEMM_GENERIC");
     if (splits < 1) splits = 1;
     const bool fast = (K % GF_BK == 0) && ((k_end - k_begin) % GF_BK == 0) && (k_begin % GF_BK == 0) &&
                       (splits == 1 || k_split % GF_BK == 0) &&
@@ -1998,16 +2011,12 @@ hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int
     if (fast) {
         const int vs = ((uintptr_t)(os.Y ? (const void*)os.Y : (const void*)C) % 16) == 0;
         const int tiles_n = NB / GF_BNB;
-        const char* bm_env = std::getenv("TERNIX_GEMM_BM");
-        const char* wgn_env = std::getenv("TERNIX_GEMM_WGN");
-        const char* bk_env = std::getenv("TERNIX_GEMM_BK");
+        static const char* const bm_env = std::getenv("TERNIX_GEMM_BM");
+        static const char* const wgn_env = std::getenv("TERNIX_GEMM_WGN");
+        static const char* const bk_env = std::getenv("TERNIX_GEMM_BK");
         // Measured on MI355X (cfg4 shapes): 256-row tiles only when they still give >= 1.5 tiles per
         // CU, else 128-row tiles; 8 waves as 2 (M) x 4 (N); 128-deep stages.
-        int cus = 256;
-        {
-            int dev = 0;
-            if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-        }
+        const int cus = device_cu_count();
         int bm = (splits == 1 && (long)((M + 255) / 256) * tiles_n * 2 >= 3L * cus) ? 256 : 128;
         if (bm_env) bm = std::atoi(bm_env) == 128 ? 128 : 256;
         const int wgn = wgn_env && std::atoi(wgn_env) == 2 ? 2 : 4;

@@ -23,20 +23,8 @@
 namespace {
 
 constexpr int kSkinnyMaxM = 32;
-constexpr int kMaxDevices = 64;
 
-// Compute-unit count per device, read once (hipDeviceGetAttribute is not free on a hot path).
-std::atomic<int> g_cu_count[kMaxDevices];
-
-int cu_count() {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
-    int n = g_cu_count[dev].load(std::memory_order_relaxed);
-    if (n > 0) return n;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    g_cu_count[dev].store(n, std::memory_order_relaxed);
-    return n;
-}
+int cu_count() { return ternix_hip::device_cu_count(); }
 
 // ---- split-K workspace -------------------------------------------------------------------------
 // The skinny kernel's split-K writes one partial C per split into a device workspace that the
