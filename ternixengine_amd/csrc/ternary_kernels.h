@@ -68,6 +68,13 @@ hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, i
 // columns; only with a split-K workspace, whose reduce drops the padding.)
 // Compute units of the current device (cached per device).
 int device_cu_count();
+// Wave-pipelined skinny kernel (M <= 16, K % 64 == 0, N/4 % sw == 0, aligned A and W): sw = 16 or
+// 32 bytes of weight row per workgroup, nsw = 2 or 4 ring slots per wave; splits == 1 stores C
+// directly, splits > 1 goes through `partials` and the reduce launch like launch_skinny.
+bool skinny_wave_ok(const int8_t* A, const uint8_t* B, int M, int K, int N, int sw);
+hipError_t launch_skinny_wave(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int sw, int nsw,
+                              int splits, int steps_per_split, int32_t* partials, hipStream_t st,
+                              const OutScale& os = OutScale{});
 // True when launch_gemm runs this M <= 64 shape on 64 x 64 tiles (K % 256 == 0, N/4 % 16 == 0, at
 // most one tile per CU); split-K k-ranges must then be multiples of 256.
 bool gemm_narrow_wanted(int M, int K, int N);

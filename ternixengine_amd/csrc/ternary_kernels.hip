@@ -1634,6 +1634,188 @@ void skinny_dma_kernel(SkinnyArgs args) {
 }
 
 // ------------------------------------------------------------------------------------------------
+// Wave-pipelined skinny kernel (M <= 16 per m-group): no barrier in the k-loop.
+//
+// A workgroup owns SW bytes of every weight row (4 * SW outputs) and its four waves take alternate
+// 64-row k-steps of the workgroup's k-range.  Each wave streams its own steps global -> LDS with
+// global_load_lds_dwordx4 into a private ring of NSW slots (64 x SW bytes each) and reads them back
+// with ds_read_b64_tr_b8 itself, so only the wave's own vmcnt orders the ring: no workgroup barrier
+// until the four waves' sums are combined at the end.  The activation fragment of a step (16 rows,
+// clamped, 16 bytes per lane) is loaded with the step's DMAs.  Narrow strips give many workgroups
+// without a K split, so a wide-N GEMV can store C directly (one launch, no reduce).
+//   * SW = 32: chunk c of row r at position c ^ ((r / 16) % 2) (the two 16-lane groups of a
+//     transposing read use different banks); SW = 16: row r at position r ^ (8 ((r / 16) % 2)).
+// Loads are issued for the same number of steps on every wave (clamped addresses past the range, no
+// MFMAs for them), so the vmcnt waits are static.
+// ------------------------------------------------------------------------------------------------
+template <int SW, int NSW, bool LOW_M>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+void skinny_wave_kernel(SkinnyArgs args) {
+    static_assert(SW == 16 || SW == 32, "16- or 32-byte strips");
+    constexpr int G = SW / 16;                 // 16-byte column groups per strip
+    constexpr int SLOT = 64 * SW;              // bytes per ring slot (one k-step)
+    constexpr int NL = SLOT / 1024;            // DMA instructions per step per wave
+    constexpr int RED = 3 * 64 * 16 * G * 4;   // cross-wave reduction buffer (waves 1-3)
+    constexpr int RING = 4 * NSW * SLOT;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[RING > RED ? RING : RED];
+
+    const int8_t* __restrict__ A = args.A;
+    const uint8_t* __restrict__ B = args.B;
+    const int M = args.M, K = args.K, NB = args.N >> 2;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int q = lane & 15, kb = lane >> 4;
+    int cx, sy;
+    {
+        const int lin = xcd_linear(blockIdx.x + gridDim.x * blockIdx.y, gridDim.x * gridDim.y);
+        cx = lin % gridDim.x;
+        sy = lin / gridDim.x;
+    }
+    const int bc0 = cx * SW;
+    const int m0 = blockIdx.z * 16;
+    const int s_begin = sy * args.steps_per_split;
+    const int nst = min(K >> 6, s_begin + args.steps_per_split) - s_begin;  // >= 1
+    const int iters = ((nst + 3) / 4 + NSW - 1) / NSW * NSW;                  // per wave, padded
+    uint8_t* ring = lds + wave * NSW * SLOT;
+
+    // DMA lane mapping: instruction p, lane l -> LDS byte 1024 p + 16 l of the slot.
+    uint32_t w_off[NL];
+#pragma unroll
+    for (int p = 0; p < NL; ++p) {
+        const int pos = p * 64 + lane;  // 16-byte position in the slot
+        int r, c;
+        if (SW == 32) {
+            r = pos >> 1;
+            c = (pos & 1) ^ ((r >> 4) & 1);
+        } else {
+            r = pos ^ (((pos >> 4) & 1) << 3);
+            c = 0;
+        }
+        w_off[p] = (uint32_t)r * (uint32_t)NB + (uint32_t)(bc0 + 16 * c);
+    }
+    const int8_t* a_row = A + (size_t)(m0 + min(q, M - m0 - 1)) * (size_t)K + kb * 16;
+    const int s_last = s_begin + nst - 1;
+    v4i a_ring[NSW];
+    auto issue = [&](int it, int slot_c, v4i& a_dst) {
+        const int s = min(s_begin + wave + 4 * it, s_last);
+        const uint8_t* wbase = B + (size_t)s * 64 * (size_t)NB;
+        uint8_t* dst = ring + slot_c * SLOT;
+#pragma unroll
+        for (int p = 0; p < NL; ++p) lds_dma16(wbase + w_off[p], dst + p * 1024);
+        a_dst = *reinterpret_cast<const v4i*>(a_row + (size_t)s * 64);
+    };
+    // Transposing-read addresses: lane q reads byte-column q of group g, rows 16 kb + q/2 (+8).
+    uint32_t w_lo[G], w_hi[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const int r = kb * 16 + (q >> 1), r8 = r + 8;
+        if (SW == 32) {
+            w_lo[g] = (uint32_t)(r * 32 + 16 * (g ^ ((r >> 4) & 1)) + 8 * (q & 1));
+            w_hi[g] = (uint32_t)(r8 * 32 + 16 * (g ^ ((r8 >> 4) & 1)) + 8 * (q & 1));
+        } else {
+            w_lo[g] = (uint32_t)((r ^ (((r >> 4) & 1) << 3)) * 16 + 8 * (q & 1));
+            w_hi[g] = (uint32_t)((r8 ^ (((r8 >> 4) & 1) << 3)) * 16 + 8 * (q & 1));
+        }
+    }
+
+    v4i acc[G][4];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[g][j] = v4i{0, 0, 0, 0};
+
+#pragma unroll
+    for (int p = 0; p < NSW - 1; ++p) issue(p, p, a_ring[p]);
+    for (int it0 = 0; it0 < iters; it0 += NSW) {
+#pragma unroll
+        for (int p = 0; p < NSW; ++p) {
+            const int it = it0 + p;
+            issue(it + NSW - 1, (p + NSW - 1) % NSW, a_ring[(p + NSW - 1) % NSW]);
+            TX_VMCNT((NSW - 1) * (NL + 1));  // step `it` (DMAs and activation load) has landed
+            if (wave + 4 * it < nst) {       // wave-uniform
+                const uint32_t base = lds_u32(ring + p * SLOT);
+                uint64_t lo[G], hi[G];
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    lo[g] = lds_read_tr8_asm(base + w_lo[g]);
+                    hi[g] = lds_read_tr8_asm(base + w_hi[g]);
+                }
+                TX_LGKMCNT0();
+#pragma unroll
+                for (int g = 0; g < G; ++g) __asm__ volatile("" : "+v"(lo[g]), "+v"(hi[g]));
+                const v4i a = a_ring[p];
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    const uint32_t x4[4] = {(uint32_t)lo[g], (uint32_t)(lo[g] >> 32), (uint32_t)hi[g],
+                                            (uint32_t)(hi[g] >> 32)};
+                    v4i bfr[4];
+#pragma unroll
+                    for (int r4 = 0; r4 < 4; ++r4) {
+                        const uint32_t x = x4[r4];
+                        bfr[0][r4] = (int)((x << 6) & 0xC0C0C0C0u);
+                        bfr[1][r4] = (int)((x << 4) & 0xC0C0C0C0u);
+                        bfr[2][r4] = (int)((x << 2) & 0xC0C0C0C0u);
+                        bfr[3][r4] = (int)(x & 0xC0C0C0C0u);
+                    }
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) acc[g][j] = mfma_i8(a, bfr[j], acc[g][j]);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    TX_VMCNT(0);  // the padding loads into the ring have landed before the ring is reused
+
+    // Sum the four waves: waves 1-3 put, wave 0 adds and stores.
+    __syncthreads();
+    if (wave > 0) {
+        v4i* r = reinterpret_cast<v4i*>(lds) + (wave - 1) * 64 * 4 * G;
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) r[(g * 4 + j) * 64 + lane] = acc[g][j];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int w = 0; w < 3; ++w) {
+        const v4i* r = reinterpret_cast<const v4i*>(lds) + w * 64 * 4 * G;
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[g][j] += r[(g * 4 + j) * 64 + lane];
+    }
+    if (LOW_M && kb != 0) return;
+    int32_t* out_base = args.mode == SK_PARTIAL ? args.P + (size_t)sy * (size_t)M * (size_t)args.N : args.C;
+    const bool vec = args.mode == SK_PARTIAL || args.vec_store;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int row = m0 + 4 * kb + i;
+        if (row >= M) continue;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const int bcol = bc0 + 16 * g + q;
+            const v4i v = {acc[g][0][i] >> 6, acc[g][1][i] >> 6, acc[g][2][i] >> 6, acc[g][3][i] >> 6};
+            if (args.mode == SK_STORE && args.os.Y) {
+                store_scaled(args.os, row, args.N, 4 * bcol, v, args.vec_store);
+                continue;
+            }
+            int32_t* out = out_base + (size_t)row * (size_t)args.N + 4 * bcol;
+            if (args.mode == SK_ATOMIC) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    if (v[j] != 0) atomicAdd(out + j, v[j]);
+            } else if (vec) {
+                *reinterpret_cast<v4i*>(out) = v;
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) out[j] = v[j];
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
 // Naive kernel: one work-item per output, weights decoded per k from global memory with
 // w = (b & 1) - (b & 2) (the reference decode2, src/cuda_kernels.cu:40-54).
 // ------------------------------------------------------------------------------------------------
@@ -1995,6 +2177,46 @@ bool gemm_narrow_wanted(int M, int K, int N) {
 
 bool gemm_narrow_ok(int M, int K, int N, int k_len, int splits, int k_split) {
     return gemm_narrow_wanted(M, K, N) && k_len % 256 == 0 && (splits == 1 || k_split % 256 == 0);
+}
+
+bool skinny_wave_ok(const int8_t* A, const uint8_t* B, int M, int K, int N, int sw) {
+    const int NB = N >> 2;
+    return M <= 16 && (sw == 16 || sw == 32) && K % 64 == 0 && NB % sw == 0 && (uintptr_t)B % 16 == 0 &&
+           (uintptr_t)A % 16 == 0 && NB < (1 << 26);
+}
+
+hipError_t launch_skinny_wave(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int sw, int nsw,
+                              int splits, int steps_per_split, int32_t* partials, hipStream_t st, const OutScale& os) {
+    if (!skinny_wave_ok(A, B, M, K, N, sw) || nsw < 2 || nsw > 4 || steps_per_split < 1) return hipErrorInvalidValue;
+    const int NB = N >> 2;
+    const int mode = splits <= 1 ? SK_STORE : (partials ? SK_PARTIAL : SK_ATOMIC);
+    if (mode == SK_ATOMIC && C == nullptr) return hipErrorInvalidValue;
+    if (mode == SK_ATOMIC) {
+        const hipError_t e = launch_zero(C, (size_t)M * (size_t)N, st);
+        if (e != hipSuccess) return e;
+    }
+    const bool scaled = os.Y != nullptr;
+    const int vec_store = ((uintptr_t)(scaled ? (const void*)os.Y : (const void*)C) % 16) == 0;
+    SkinnyArgs a{A, B, C, partials, M, K, N, steps_per_split, splits, mode, vec_store, 1, 1,
+                 mode == SK_STORE ? os : OutScale{}};
+    const dim3 grid(NB / sw, splits, (M + 15) / 16), block(256);
+    const bool low = M <= 4;
+#define TX_SW_LAUNCH(SW_, NSW_)                                                              \
+    do {                                                                                      \
+        if (low) hipLaunchKernelGGL((skinny_wave_kernel<SW_, NSW_, true>), grid, block, 0, st, a);  \
+        else hipLaunchKernelGGL((skinny_wave_kernel<SW_, NSW_, false>), grid, block, 0, st, a);     \
+    } while (0)
+    if (sw == 32 && nsw == 4) TX_SW_LAUNCH(32, 4);
+    else if (sw == 32) TX_SW_LAUNCH(32, 2);
+    else if (nsw == 4) TX_SW_LAUNCH(16, 4);
+    else if (nsw == 3) TX_SW_LAUNCH(16, 3);
+    else TX_SW_LAUNCH(16, 2);
+#undef TX_SW_LAUNCH
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    if (mode == SK_ATOMIC && scaled) return launch_dequant(C, os, M, N, st);
+    if (mode != SK_PARTIAL) return e;
+    return launch_splitk_reduce(partials, C, M, N, splits, os, st);
 }
 
 hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int k_begin, int k_end,

@@ -172,6 +172,40 @@ hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
                       const ternix_hip::ActQuant& aq = ternix_hip::ActQuant{}) {
     const bool generic = !(K % 64 == 0 && (N / 4) % 64 == 0 && reinterpret_cast<uintptr_t>(dB) % 16 == 0 &&
                            (aq.mode != 0 || reinterpret_cast<uintptr_t>(dA) % 16 == 0));
+    // Wave-pipelined kernel (16-byte strips, 2 ring slots per wave), measured on MI355X against the
+    // DMA-staged kernel: with K <= 4096 in one launch, no K split and no reduce (cfg1 6.26 -> 5.64 us,
+    // cfg2 up 6.94 -> 6.29, cfg3 M=4 up 11.62 -> 10.41, M=16 up 14.27 -> 11.45); for 4 < M <= 16 with
+    // longer K, split about every 21 k-steps, whose partials are far fewer than the DMA kernel's
+    // (cfg3 M=16 down 14.59 -> 12.78 us).  TERNIX_SKINNY_WAVE="sw,nsw,splits" forces a plan, "0"
+    // turns the kernel off (experiments).
+    if (aq.mode == 0 && !generic && ternix_hip::skinny_wave_ok(dA, dB, M, K, N, 16)) {
+        const int nsteps = K / 64;
+        int sw = 16, nsw = 2, sp = 0;
+        if (K <= 4096) sp = 1;
+        else if (M > 4) sp = std::max(2, std::min(16, nsteps / 21));
+        if (const char* env = std::getenv("TERNIX_SKINNY_WAVE")) {
+            int esw = 0, ensw = 0, esp = 0;
+            if (std::sscanf(env, "%d,%d,%d", &esw, &ensw, &esp) == 3 && esp >= 1 &&
+                ternix_hip::skinny_wave_ok(dA, dB, M, K, N, esw)) {
+                sw = esw;
+                nsw = ensw;
+                sp = esp;
+            } else {
+                sp = 0;
+            }
+        }
+        if (sp > 0) {
+            const int sps = (nsteps + sp - 1) / sp;
+            const int splits = (nsteps + sps - 1) / sps;
+            int32_t* partials = nullptr;
+            if (splits > 1) {
+                const size_t need = (size_t)splits * (size_t)M * (size_t)N * sizeof(int32_t);
+                if (need <= kWorkspaceMax) partials = static_cast<int32_t*>(workspace(st, need));
+            }
+            if (sps * 64 <= ternix_hip::kMaxKPerAccumulator && (splits == 1 || partials || dC))
+                return ternix_hip::launch_skinny_wave(dA, dB, dC, M, K, N, sw, nsw, splits, sps, partials, st, os);
+        }
+    }
     // DMA-staged kernel: TERNIX_SKINNY_DMA=0 disables it, 2..4 sets its stage count (experiments).
     static const int dma_env = [] {
         const char* e = std::getenv("TERNIX_SKINNY_DMA");
