@@ -211,6 +211,7 @@ struct SkinnyArgs {
     const float* G;
     float eps;
     float* rs_out;
+    int n_out;            // skinny_wave_kernel, store mode: C / os.Y has n_out <= N columns (0: N)
 };
 
 // One k-step of MFMA work for one 16-row x 4-byte-column block: raw[r] is the dword of row r.
@@ -1788,6 +1789,8 @@ void skinny_wave_kernel(SkinnyArgs args) {
     if (LOW_M && kb != 0) return;
     int32_t* out_base = args.mode == SK_PARTIAL ? args.P + (size_t)sy * (size_t)M * (size_t)args.N : args.C;
     const bool vec = args.mode == SK_PARTIAL || args.vec_store;
+    // Store mode writes n_out columns at pitch n_out (a padded problem's real columns).
+    const int NO = (args.mode == SK_STORE && args.n_out > 0) ? args.n_out : args.N;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int row = m0 + 4 * kb + i;
@@ -1795,12 +1798,13 @@ void skinny_wave_kernel(SkinnyArgs args) {
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             const int bcol = bc0 + 16 * g + q;
+            if (4 * bcol >= NO) continue;
             const v4i v = {acc[g][0][i] >> 6, acc[g][1][i] >> 6, acc[g][2][i] >> 6, acc[g][3][i] >> 6};
             if (args.mode == SK_STORE && args.os.Y) {
-                store_scaled(args.os, row, args.N, 4 * bcol, v, args.vec_store);
+                store_scaled(args.os, row, NO, 4 * bcol, v, args.vec_store);
                 continue;
             }
-            int32_t* out = out_base + (size_t)row * (size_t)args.N + 4 * bcol;
+            int32_t* out = out_base + (size_t)row * (size_t)NO + 4 * bcol;
             if (args.mode == SK_ATOMIC) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
@@ -2186,10 +2190,12 @@ bool skinny_wave_ok(const int8_t* A, const uint8_t* B, int M, int K, int N, int 
 }
 
 hipError_t launch_skinny_wave(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int sw, int nsw,
-                              int splits, int steps_per_split, int32_t* partials, hipStream_t st, const OutScale& os) {
+                              int splits, int steps_per_split, int32_t* partials, hipStream_t st, const OutScale& os,
+                              int n_out) {
     if (!skinny_wave_ok(A, B, M, K, N, sw) || nsw < 2 || nsw > 4 || steps_per_split < 1) return hipErrorInvalidValue;
     const int NB = N >> 2;
     const int mode = splits <= 1 ? SK_STORE : (partials ? SK_PARTIAL : SK_ATOMIC);
+    if (n_out > 0 && (mode == SK_ATOMIC || n_out > N || n_out % 4 != 0)) return hipErrorInvalidValue;
     if (mode == SK_ATOMIC && C == nullptr) return hipErrorInvalidValue;
     if (mode == SK_ATOMIC) {
         const hipError_t e = launch_zero(C, (size_t)M * (size_t)N, st);
@@ -2199,6 +2205,7 @@ hipError_t launch_skinny_wave(const int8_t* A, const uint8_t* B, int32_t* C, int
     const int vec_store = ((uintptr_t)(scaled ? (const void*)os.Y : (const void*)C) % 16) == 0;
     SkinnyArgs a{A, B, C, partials, M, K, N, steps_per_split, splits, mode, vec_store, 1, 1,
                  mode == SK_STORE ? os : OutScale{}};
+    a.n_out = n_out;
     const dim3 grid(NB / sw, splits, (M + 15) / 16), block(256);
     const bool low = M <= 4;
 #define TX_SW_LAUNCH(SW_, NSW_)                                                              \
@@ -2216,7 +2223,8 @@ hipError_t launch_skinny_wave(const int8_t* A, const uint8_t* B, int32_t* C, int
     if (e != hipSuccess) return e;
     if (mode == SK_ATOMIC && scaled) return launch_dequant(C, os, M, N, st);
     if (mode != SK_PARTIAL) return e;
-    return launch_splitk_reduce(partials, C, M, N, splits, os, st);
+    return n_out > 0 ? launch_splitk_reduce(partials, C, M, n_out, splits, os, st, N)
+                     : launch_splitk_reduce(partials, C, M, N, splits, os, st);
 }
 
 hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int k_begin, int k_end,

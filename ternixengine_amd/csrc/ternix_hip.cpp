@@ -167,6 +167,15 @@ SkinnyPlan plan_skinny(int M, int K, int N, bool generic = false) {
     return p;
 }
 
+// TERNIX_SKINNY_WAVE=0 switches the wave-pipelined skinny kernel off (experiments).
+bool wave_kernel_enabled() {
+    static const bool on = [] {
+        const char* e = std::getenv("TERNIX_SKINNY_WAVE");
+        return !(e && e[0] == '0' && e[1] == '\0');
+    }();
+    return on;
+}
+
 hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int K, int N, hipStream_t st,
                       const ternix_hip::OutScale& os = ternix_hip::OutScale{},
                       const ternix_hip::ActQuant& aq = ternix_hip::ActQuant{}) {
@@ -297,7 +306,11 @@ hipError_t run_padded(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
     if (K == 0 || Kp > INT_MAX || Np > INT_MAX || Kp * NBp >= (1L << 32)) return hipErrorNotSupported;
     SkinnyPlan p{0, 0, 0, 0, 0};
     int splits = 1, k_split = 0;
-    if (skinny) {
+    // Short K at M <= 16: the wave-pipelined kernel in one launch, writing the N real columns itself.
+    const bool wave = skinny && M <= 16 && Kp <= 4096 && wave_kernel_enabled();
+    if (wave) {
+        splits = 1;
+    } else if (skinny) {
         if (M <= 16) p = plan_skinny_dma(M, (int)Kp, (int)Np, 3);
         if (p.dma == 0) p = plan_skinny(M, (int)Kp, (int)Np);
         splits = p.splits;
@@ -309,13 +322,13 @@ hipError_t run_padded(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
             splits = (int)((Kp + k_split - 1) / k_split);
         }
     }
-    if (splits <= 1) return hipErrorNotSupported;
+    if (splits <= 1 && !wave) return hipErrorNotSupported;
     // Each split's k-range must fit one int32 accumulator (the skinny plans guarantee it).
     if (!skinny && k_split > ternix_hip::kMaxKPerAccumulator) return hipErrorNotSupported;
     auto up = [](size_t b) { return (b + 255) & ~size_t(255); };
     const size_t w_bytes = up((size_t)Kp * (size_t)NBp);
     const size_t a_bytes = up((size_t)M * (size_t)Kp);
-    const size_t p_bytes = (size_t)splits * (size_t)M * (size_t)Np * sizeof(int32_t);
+    const size_t p_bytes = wave ? 0 : (size_t)splits * (size_t)M * (size_t)Np * sizeof(int32_t);
     if (w_bytes + a_bytes + p_bytes > kWorkspaceMax) return hipErrorNotSupported;
     uint8_t* ws = static_cast<uint8_t*>(workspace(st, w_bytes + a_bytes + p_bytes));
     if (ws == nullptr) return hipErrorNotSupported;
@@ -326,6 +339,9 @@ hipError_t run_padded(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
                                                reinterpret_cast<const uint8_t*>(dA), reinterpret_cast<uint8_t*>(Ap),
                                                M, M, K, K, (int)Kp, st);
     if (e != hipSuccess) return e;
+    if (wave)
+        return ternix_hip::launch_skinny_wave(Ap, Wp, dC, M, (int)Kp, (int)Np, 16, 2, 1, (int)(Kp / 64), nullptr, st,
+                                              os, N);
     if (skinny)
         return ternix_hip::launch_skinny(Ap, Wp, dC, M, (int)Kp, (int)Np, p.tb, p.kw, p.splits, p.sps, P, st, os,
                                          ternix_hip::ActQuant{}, p.dma, N);
