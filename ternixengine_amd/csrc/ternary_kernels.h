@@ -68,7 +68,7 @@ hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, i
 // columns; only with a split-K workspace, whose reduce drops the padding.)
 // Compute units of the current device (cached per device).
 int device_cu_count();
-// Wave-pipelined skinny kernel (M <= 16, K % 64 == 0, N/4 % sw == 0, aligned A and W): sw = 16 or
+// Wave-pipelined skinny kernel (M <= 32, K % 64 == 0, N/4 % sw == 0, aligned A and W): sw = 16 or
 // 32 bytes of weight row per workgroup, nsw = 2 or 4 ring slots per wave; splits == 1 stores C
 // directly, splits > 1 goes through `partials` and the reduce launch like launch_skinny.
 bool skinny_wave_ok(const int8_t* A, const uint8_t* B, int M, int K, int N, int sw);

@@ -2185,7 +2185,7 @@ bool gemm_narrow_ok(int M, int K, int N, int k_len, int splits, int k_split) {
 
 bool skinny_wave_ok(const int8_t* A, const uint8_t* B, int M, int K, int N, int sw) {
     const int NB = N >> 2;
-    return M <= 16 && (sw == 16 || sw == 32) && K % 64 == 0 && NB % sw == 0 && (uintptr_t)B % 16 == 0 &&
+    return M <= 32 && (sw == 16 || sw == 32) && K % 64 == 0 && NB % sw == 0 && (uintptr_t)B % 16 == 0 &&
            (uintptr_t)A % 16 == 0 && NB < (1 << 26);
 }
 

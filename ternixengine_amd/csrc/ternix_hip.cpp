@@ -176,6 +176,14 @@ bool wave_kernel_enabled() {
     return on;
 }
 
+int wave_max_m() {
+    static const int m = [] {
+        const char* e = std::getenv("TERNIX_WAVE_MAX_M");  // experiments
+        return e ? std::atoi(e) : 32;
+    }();
+    return m;
+}
+
 hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int K, int N, hipStream_t st,
                       const ternix_hip::OutScale& os = ternix_hip::OutScale{},
                       const ternix_hip::ActQuant& aq = ternix_hip::ActQuant{}) {
@@ -187,7 +195,7 @@ hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
     // longer K, split about every 21 k-steps, whose partials are far fewer than the DMA kernel's
     // (cfg3 M=16 down 14.59 -> 12.78 us).  TERNIX_SKINNY_WAVE="sw,nsw,splits" forces a plan, "0"
     // turns the kernel off (experiments).
-    if (aq.mode == 0 && !generic && ternix_hip::skinny_wave_ok(dA, dB, M, K, N, 16)) {
+    if (aq.mode == 0 && !generic && M <= wave_max_m() && ternix_hip::skinny_wave_ok(dA, dB, M, K, N, 16)) {
         const int nsteps = K / 64;
         int sw = 16, nsw = 2, sp = 0;
         if (K <= 4096) sp = 1;
@@ -307,7 +315,7 @@ hipError_t run_padded(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
     SkinnyPlan p{0, 0, 0, 0, 0};
     int splits = 1, k_split = 0;
     // Short K at M <= 16: the wave-pipelined kernel in one launch, writing the N real columns itself.
-    const bool wave = skinny && M <= 16 && Kp <= 4096 && wave_kernel_enabled();
+    const bool wave = skinny && M <= wave_max_m() && Kp <= 4096 && wave_kernel_enabled();
     if (wave) {
         splits = 1;
     } else if (skinny) {

@@ -339,3 +339,17 @@ def test_padded_path_graph_replay(oracle):
             assert (dc.download(np.int32, (m, n)) == expect).all(), (m, k, n, rep)
             assert call() == 0  # eager work between replays
             s.synchronize()
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 64, 1024), (1, 2560, 1024), (3, 4032, 2048), (4, 4096, 512), (8, 1024, 4096),
+                                   (16, 4096, 1024), (17, 2048, 1024), (24, 4096, 512), (32, 2560, 1024),
+                                   (12, 8192, 512), (20, 6144, 1024), (2, 8192, 256)])
+def test_wave_kernel_shapes(oracle, m, k, n):
+    """Shapes the wave-pipelined skinny kernel takes on the automatic path: one launch for K <= 4096
+    (1, 2 or 3 m-groups, 1-row and 4-row groups, one k-step), a few K splits for 4 < M with longer K;
+    and M <= 4 with long K, which stays on the DMA-staged kernel."""
+    rng = np.random.default_rng(m * 7 + k)
+    a = rng.integers(-128, 128, size=(m, k), dtype=np.int8)
+    wp = rng.integers(0, 256, size=(k, n // 4), dtype=np.uint8)
+    log(f"[wave] M={m} K={k} N={n}")
+    assert (run("auto", a, wp, n) == oracle.mm("scalar_mt", a, wp, n)).all()
