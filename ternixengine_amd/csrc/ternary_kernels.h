@@ -74,8 +74,10 @@ int device_cu_count();
 bool skinny_wave_ok(const int8_t* A, const uint8_t* B, int M, int K, int N, int sw);
 hipError_t launch_skinny_wave(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int sw, int nsw,
                               int splits, int steps_per_split, int32_t* partials, hipStream_t st,
-                              const OutScale& os = OutScale{}, int n_out = 0);
-// (n_out > 0: a padded problem -- C / os.Y has n_out <= N columns; not with the atomic mode.)
+                              const OutScale& os = OutScale{}, int n_out = 0, const ActQuant& aq = ActQuant{});
+// (n_out > 0: a padded problem -- C / os.Y has n_out <= N columns; not with the atomic mode.
+// aq set: the activations are quantised in the kernel from aq.X (splits == 1, K <= 4096, sw 16,
+// nsw 2); the dequantising epilogue then uses the kernel's own row scales.)
 // True when launch_gemm runs this M <= 64 shape on 64 x 64 tiles (K % 256 == 0, N/4 % 16 == 0, at
 // most one tile per CU); split-K k-ranges must then be multiples of 256.
 bool gemm_narrow_wanted(int M, int K, int N);

@@ -80,8 +80,12 @@ __device__ __forceinline__ int xcd_linear(int id, int total) {
 // With os.swiglu the four values are two interleaved (gate, up) pairs and the stored row is N/2 wide:
 // h[col/2 + p] = silu(y[2p]) * y[2p+1], silu(g) = g / (1 + exp(-g)) (reference src/simd_math.cpp:40-46).
 typedef float v2f __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void store_scaled_f(const OutScale& os, float f, int row, int N, int col, v4i c, int vec);
 __device__ __forceinline__ void store_scaled(const OutScale& os, int row, int N, int col, v4i c, int vec) {
-    const float f = os.rs[row] * os.ws;
+    store_scaled_f(os, os.rs[row] * os.ws, row, N, col, c, vec);
+}
+// As store_scaled with the combined scale f = row_scale * w_scale given.
+__device__ __forceinline__ void store_scaled_f(const OutScale& os, float f, int row, int N, int col, v4i c, int vec) {
     const v4f y = {(float)c[0] * f, (float)c[1] * f, (float)c[2] * f, (float)c[3] * f};
     if (os.swiglu) {
         const v2f h = {(y[0] / (1.0f + expf(-y[0]))) * y[1], (y[2] / (1.0f + expf(-y[2]))) * y[3]};
@@ -1649,16 +1653,19 @@ void skinny_dma_kernel(SkinnyArgs args) {
 // Loads are issued for the same number of steps on every wave (clamped addresses past the range, no
 // MFMAs for them), so the vmcnt waits are static.
 // ------------------------------------------------------------------------------------------------
-template <int SW, int NSW, bool LOW_M>
+template <int SW, int NSW, bool LOW_M, int AQ = 0>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 void skinny_wave_kernel(SkinnyArgs args) {
     static_assert(SW == 16 || SW == 32, "16- or 32-byte strips");
+    constexpr int QK = 4096;                   // AQ: whole rows of K <= QK quantised into LDS
     constexpr int G = SW / 16;                 // 16-byte column groups per strip
     constexpr int SLOT = 64 * SW;              // bytes per ring slot (one k-step)
     constexpr int NL = SLOT / 1024;            // DMA instructions per step per wave
     constexpr int RED = 3 * 64 * 16 * G * 4;   // cross-wave reduction buffer (waves 1-3)
     constexpr int RING = 4 * NSW * SLOT;
     __shared__ __attribute__((aligned(16))) uint8_t lds[RING > RED ? RING : RED];
+    __shared__ __attribute__((aligned(16))) int8_t qbuf[AQ ? 16 : 1][AQ ? QK : 16];
+    __shared__ float rscale[16];
 
     const int8_t* __restrict__ A = args.A;
     const uint8_t* __restrict__ B = args.B;
@@ -1694,7 +1701,8 @@ void skinny_wave_kernel(SkinnyArgs args) {
         }
         w_off[p] = (uint32_t)r * (uint32_t)NB + (uint32_t)(bc0 + 16 * c);
     }
-    const int8_t* a_row = A + (size_t)(m0 + min(q, M - m0 - 1)) * (size_t)K + kb * 16;
+    const int a_rows = min(16, M - m0);
+    const int8_t* a_row = A + (size_t)(m0 + min(q, a_rows - 1)) * (size_t)K + kb * 16;
     const int s_last = s_begin + nst - 1;
     v4i a_ring[NSW];
     auto issue = [&](int it, int slot_c, v4i& a_dst) {
@@ -1703,8 +1711,24 @@ void skinny_wave_kernel(SkinnyArgs args) {
         uint8_t* dst = ring + slot_c * SLOT;
 #pragma unroll
         for (int p = 0; p < NL; ++p) lds_dma16(wbase + w_off[p], dst + p * 1024);
-        a_dst = *reinterpret_cast<const v4i*>(a_row + (size_t)s * 64);
+        if constexpr (AQ == 0) a_dst = *reinterpret_cast<const v4i*>(a_row + (size_t)s * 64);
     };
+    // AQ > 0 (one launch, whole rows): every workgroup quantises its m-group's fp32 rows itself (the
+    // rule and accumulation order of quantize_rows_kernel / rmsnorm_kernel, from row_stats.h, so the
+    // int8 values and scales are bit-identical to theirs) into qbuf, and dequantises its outputs with
+    // its own copy of the row scales; workgroup 0 also stores them to rs_out.
+    constexpr int QR = AQ ? QK / 256 : 1;
+    float xv[QR], gv[AQ == 2 ? QR : 1];
+    auto load_row = [&](int r) {
+        const float* x = args.X + (size_t)(m0 + r) * (size_t)K;
+#pragma unroll
+        for (int j = 0; j < (AQ ? QR : 0); ++j) {
+            const int k = tid + 256 * j;
+            xv[j] = k < K ? x[k] : 0.0f;
+            if constexpr (AQ == 2) gv[j] = k < K ? args.G[k] : 0.0f;
+        }
+    };
+    if constexpr (AQ != 0) load_row(0);  // before the weight DMAs, so waiting for it does not wait for them
     // Transposing-read addresses: lane q reads byte-column q of group g, rows 16 kb + q/2 (+8).
     uint32_t w_lo[G], w_hi[G];
 #pragma unroll
@@ -1727,12 +1751,46 @@ void skinny_wave_kernel(SkinnyArgs args) {
 
 #pragma unroll
     for (int p = 0; p < NSW - 1; ++p) issue(p, p, a_ring[p]);
+    if constexpr (AQ != 0) {
+        __shared__ float red[4];
+        for (int r = 0; r < a_rows; ++r) {  // uniform: every thread takes part in the reductions
+            if (r > 0) load_row(r);
+            float inv = 1.0f;
+            if constexpr (AQ == 2) {
+                float ss = 0.0f;
+#pragma unroll
+                for (int j = 0; j < QR; ++j) ss = fmaf(xv[j], xv[j], ss);  // +0 past K changes nothing
+                ss = row_block_sum(ss, red);
+                inv = 1.0f / sqrtf(ss / (float)K + args.eps);
+            }
+            auto val = [&](int j) {
+                if constexpr (AQ == 2) return xv[j] * inv * gv[j];
+                else return xv[j];
+            };
+            float amax = 0.0f;
+#pragma unroll
+            for (int j = 0; j < QR; ++j) amax = fmaxf(amax, fabsf(val(j)));
+            const float am = fmaxf(row_block_max(amax, red), 1e-5f);
+            const float sc = 127.0f / am;
+            if (tid == 0) {
+                rscale[r] = am / 127.0f;
+                if (cx == 0 && sy == 0) args.rs_out[m0 + r] = am / 127.0f;
+            }
+#pragma unroll
+            for (int j = 0; j < QR; ++j) {
+                const int k = tid + 256 * j;
+                if (k < K) qbuf[r][k] = (int8_t)quantize_value(val(j), sc);
+            }
+        }
+        __syncthreads();  // qbuf and rscale complete
+    }
+    constexpr int VPS = NL + (AQ ? 0 : 1);  // vector memory operations per step and wave
     for (int it0 = 0; it0 < iters; it0 += NSW) {
 #pragma unroll
         for (int p = 0; p < NSW; ++p) {
             const int it = it0 + p;
             issue(it + NSW - 1, (p + NSW - 1) % NSW, a_ring[(p + NSW - 1) % NSW]);
-            TX_VMCNT((NSW - 1) * (NL + 1));  // step `it` (DMAs and activation load) has landed
+            TX_VMCNT((NSW - 1) * VPS);       // step `it` (DMAs and activation load) has landed
             if (wave + 4 * it < nst) {       // wave-uniform
                 const uint32_t base = lds_u32(ring + p * SLOT);
                 uint64_t lo[G], hi[G];
@@ -1744,7 +1802,11 @@ void skinny_wave_kernel(SkinnyArgs args) {
                 TX_LGKMCNT0();
 #pragma unroll
                 for (int g = 0; g < G; ++g) __asm__ volatile("" : "+v"(lo[g]), "+v"(hi[g]));
-                const v4i a = a_ring[p];
+                v4i a;
+                if constexpr (AQ != 0)
+                    a = *reinterpret_cast<const v4i*>(&qbuf[min(q, a_rows - 1)][(s_begin + wave + 4 * it) * 64 + kb * 16]);
+                else
+                    a = a_ring[p];
 #pragma unroll
                 for (int g = 0; g < G; ++g) {
                     const uint32_t x4[4] = {(uint32_t)lo[g], (uint32_t)(lo[g] >> 32), (uint32_t)hi[g],
@@ -1801,7 +1863,8 @@ void skinny_wave_kernel(SkinnyArgs args) {
             if (4 * bcol >= NO) continue;
             const v4i v = {acc[g][0][i] >> 6, acc[g][1][i] >> 6, acc[g][2][i] >> 6, acc[g][3][i] >> 6};
             if (args.mode == SK_STORE && args.os.Y) {
-                store_scaled(args.os, row, NO, 4 * bcol, v, args.vec_store);
+                if constexpr (AQ != 0) store_scaled_f(args.os, rscale[row - m0] * args.os.ws, row, NO, 4 * bcol, v, args.vec_store);
+                else store_scaled(args.os, row, NO, 4 * bcol, v, args.vec_store);
                 continue;
             }
             int32_t* out = out_base + (size_t)row * (size_t)NO + 4 * bcol;
@@ -2191,8 +2254,12 @@ bool skinny_wave_ok(const int8_t* A, const uint8_t* B, int M, int K, int N, int 
 
 hipError_t launch_skinny_wave(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int sw, int nsw,
                               int splits, int steps_per_split, int32_t* partials, hipStream_t st, const OutScale& os,
-                              int n_out) {
+                              int n_out, const ActQuant& aq) {
     if (!skinny_wave_ok(A, B, M, K, N, sw) || nsw < 2 || nsw > 4 || steps_per_split < 1) return hipErrorInvalidValue;
+    // Fused activation quantisation: one launch over whole rows (K <= 4096), 16-byte strips, 2 slots.
+    if (aq.mode != 0 && (splits != 1 || K > 4096 || sw != 16 || nsw != 2 || n_out > 0 || aq.X == nullptr ||
+                         aq.rs_out == nullptr || (aq.mode == 2 && aq.G == nullptr)))
+        return hipErrorInvalidValue;
     const int NB = N >> 2;
     const int mode = splits <= 1 ? SK_STORE : (partials ? SK_PARTIAL : SK_ATOMIC);
     if (n_out > 0 && (mode == SK_ATOMIC || n_out > N || n_out % 4 != 0)) return hipErrorInvalidValue;
@@ -2206,6 +2273,10 @@ hipError_t launch_skinny_wave(const int8_t* A, const uint8_t* B, int32_t* C, int
     SkinnyArgs a{A, B, C, partials, M, K, N, steps_per_split, splits, mode, vec_store, 1, 1,
                  mode == SK_STORE ? os : OutScale{}};
     a.n_out = n_out;
+    a.X = aq.X;
+    a.G = aq.G;
+    a.eps = aq.eps;
+    a.rs_out = aq.rs_out;
     const dim3 grid(NB / sw, splits, (M + 15) / 16), block(256);
     const bool low = M <= 4;
 #define TX_SW_LAUNCH(SW_, NSW_)                                                              \
@@ -2213,7 +2284,13 @@ hipError_t launch_skinny_wave(const int8_t* A, const uint8_t* B, int32_t* C, int
         if (low) hipLaunchKernelGGL((skinny_wave_kernel<SW_, NSW_, true>), grid, block, 0, st, a);  \
         else hipLaunchKernelGGL((skinny_wave_kernel<SW_, NSW_, false>), grid, block, 0, st, a);     \
     } while (0)
-    if (sw == 32 && nsw == 4) TX_SW_LAUNCH(32, 4);
+    if (aq.mode == 1) {
+        if (low) hipLaunchKernelGGL((skinny_wave_kernel<16, 2, true, 1>), grid, block, 0, st, a);
+        else hipLaunchKernelGGL((skinny_wave_kernel<16, 2, false, 1>), grid, block, 0, st, a);
+    } else if (aq.mode == 2) {
+        if (low) hipLaunchKernelGGL((skinny_wave_kernel<16, 2, true, 2>), grid, block, 0, st, a);
+        else hipLaunchKernelGGL((skinny_wave_kernel<16, 2, false, 2>), grid, block, 0, st, a);
+    } else if (sw == 32 && nsw == 4) TX_SW_LAUNCH(32, 4);
     else if (sw == 32) TX_SW_LAUNCH(32, 2);
     else if (nsw == 4) TX_SW_LAUNCH(16, 4);
     else if (nsw == 3) TX_SW_LAUNCH(16, 3);

@@ -195,7 +195,10 @@ hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
     // longer K, split about every 21 k-steps, whose partials are far fewer than the DMA kernel's
     // (cfg3 M=16 down 14.59 -> 12.78 us).  TERNIX_SKINNY_WAVE="sw,nsw,splits" forces a plan, "0"
     // turns the kernel off (experiments).
-    if (aq.mode == 0 && !generic && M <= wave_max_m() && ternix_hip::skinny_wave_ok(dA, dB, M, K, N, 16)) {
+    // With fused activation quantisation (K <= 4096) it quantises whole rows itself and dequantises with
+    // its own row scales: the FFN block's gate/up GEMV becomes one launch.
+    if (!generic && M <= wave_max_m() && ternix_hip::skinny_wave_ok(dA, dB, M, K, N, 16) &&
+        (aq.mode == 0 || (K <= 4096 && M <= 16))) {
         const int nsteps = K / 64;
         int sw = 16, nsw = 2, sp = 0;
         if (K <= 4096) sp = 1;
@@ -219,8 +222,10 @@ hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
                 const size_t need = (size_t)splits * (size_t)M * (size_t)N * sizeof(int32_t);
                 if (need <= kWorkspaceMax) partials = static_cast<int32_t*>(workspace(st, need));
             }
-            if (sps * 64 <= ternix_hip::kMaxKPerAccumulator && (splits == 1 || partials || dC))
-                return ternix_hip::launch_skinny_wave(dA, dB, dC, M, K, N, sw, nsw, splits, sps, partials, st, os);
+            if (sps * 64 <= ternix_hip::kMaxKPerAccumulator && (splits == 1 || partials || dC) &&
+                (aq.mode == 0 || (splits == 1 && sw == 16 && nsw == 2)))
+                return ternix_hip::launch_skinny_wave(dA, dB, dC, M, K, N, sw, nsw, splits, sps, partials, st, os, 0,
+                                                      aq);
         }
     }
     // DMA-staged kernel: TERNIX_SKINNY_DMA=0 disables it, 2..4 sets its stage count (experiments).
