@@ -216,6 +216,7 @@ struct SkinnyArgs {
     float eps;
     float* rs_out;
     int n_out;            // skinny_wave_kernel, store mode: C / os.Y has n_out <= N columns (0: N)
+    int line_units;       // skinny_wave_kernel: block -> strip mapping by 128-byte line units
 };
 
 // One k-step of MFMA work for one 16-row x 4-byte-column block: raw[r] is the dword of row r.
@@ -1673,11 +1674,26 @@ void skinny_wave_kernel(SkinnyArgs args) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int q = lane & 15, kb = lane >> 4;
+    // Block -> (strip, split): the hardware deals block ids round-robin to the 8 XCDs (XCD = id % 8).
+    // The 128 / SW strips that share each 128-byte line of a weight row form one unit, and all
+    // blocks of a unit sit on one XCD, so the line is fetched into one L2 only; ids past the last
+    // unit, or strips past the last column, have no work.
+    constexpr int SPL = 128 / SW;  // strips per 128-byte line
+    const int n_strips = NB / SW, lines = (n_strips + SPL - 1) / SPL;
     int cx, sy;
-    {
-        const int lin = xcd_linear(blockIdx.x + gridDim.x * blockIdx.y, gridDim.x * gridDim.y);
-        cx = lin % gridDim.x;
-        sy = lin / gridDim.x;
+    if (args.line_units) {
+        const int b = blockIdx.x, t = b >> 3;
+        const int u = (b & 7) + 8 * (t / SPL);  // unit: (split, line group)
+        sy = u / lines;
+        cx = (u % lines) * SPL + t % SPL;
+        if (sy >= args.splits || cx >= n_strips) return;  // whole workgroup: no barrier reached yet
+    } else {
+        // contiguous strip ranges per XCD (balanced; lines at range ends are fetched by two L2s)
+        const int total = n_strips * args.splits;
+        if ((int)blockIdx.x >= total) return;
+        const int lin = xcd_linear(blockIdx.x, total);
+        cx = lin % n_strips;
+        sy = lin / n_strips;
     }
     const int bc0 = cx * SW;
     const int m0 = blockIdx.z * 16;
@@ -2277,7 +2293,17 @@ hipError_t launch_skinny_wave(const int8_t* A, const uint8_t* B, int32_t* C, int
     a.G = aq.G;
     a.eps = aq.eps;
     a.rs_out = aq.rs_out;
-    const dim3 grid(NB / sw, splits, (M + 15) / 16), block(256);
+    // Line units: 8 XCDs x (128 / sw) strips x enough rounds for every (split, line-group) unit.
+    // Measured on MI355X (cold weights): line units help the one-launch shapes (cfg1 5.76 -> 5.24 us,
+    // cfg2 up 6.75 -> 6.5, ragged 17x4093x1028 13.1 -> 11.5) and cost 2 % with a K split.
+    static const int lu_env = [] {
+        const char* e = std::getenv("TERNIX_WAVE_LINES");  // experiments: 0 / 1 forces the mapping
+        return e ? std::atoi(e) : -1;
+    }();
+    a.line_units = lu_env >= 0 ? lu_env : (splits == 1);
+    const int spl = 128 / sw, units = splits * ((NB / sw + spl - 1) / spl);
+    const unsigned gx = a.line_units ? (unsigned)(8 * spl * ((units + 7) / 8)) : (unsigned)((NB / sw) * splits);
+    const dim3 grid(gx, 1, (M + 15) / 16), block(256);
     const bool low = M <= 4;
 #define TX_SW_LAUNCH(SW_, NSW_)                                                              \
     do {                                                                                      \
