@@ -4,16 +4,25 @@
 // weight (k, n) in bits 2*(n%4) of byte k*NB + n/4; 00 = 0, 01 = +1, 11 = -1 (10 decodes as -2,
 // like the reference's scalar and CUDA decode, src/mul_mat_ternary.cpp:53, src/cuda_kernels.cu:40).
 //
-// Both fast kernels feed v_mfma_i32_16x16x64_i8.  The int8 MFMA reduces along K inside a lane
-// (lane l holds 16 K-consecutive bytes of one row of A and of one column of B, K-block l/16),
+// Every matmul kernel here feeds v_mfma_i32_16x16x64_i8.  The int8 MFMA reduces along K inside a
+// lane (lane l holds 16 K-consecutive bytes of one row of A and of one column of B, K-block l/16),
 // while the packed layout runs along N.  The kernels therefore
 //   1. gather, per lane, one packed byte-column (= 4 output columns) over 16 consecutive k-rows:
-//      four dwords, each holding 4 k-rows x 4 fields (a 4x4 byte transpose with v_perm_b32);
+//      with the gfx950 transposing LDS read ds_read_b64_tr_b8 from a row-major LDS stage (the
+//      DMA-staged and wave-pipelined GEMVs, the pipelined GEMM), or with a 4x4 byte transpose in
+//      registers (v_perm_b32; the register-staged GEMVs and the older GEMM kernels);
 //   2. split every dword into four MFMA B-operand dwords, one per 2-bit field j, without any
 //      per-weight work (a handful of bitwise ops per 16 weights, see "Field decode" below);
 //   3. run one MFMA per field: MFMA column i of field j is output column 4*(byte-col_i) + j.
 // Which k-rows a lane's 16 bytes hold only has to agree between A and B, so the natural row order
 // is used for both and A fragments are plain 16-byte loads.
+//
+// Kernel families (the launch layer, ternix_hip.cpp, picks one per call):
+//   skinny_wave_kernel    M <= 32: 16-byte weight strips, per-wave DMA rings, one launch for K <= 4096
+//   skinny_dma_kernel     M <= 16, long K: 256-byte strips staged by DMA, split-K + reduce
+//   skinny_short/fast/generic_kernel  register-staged GEMVs (fallbacks, fused FFN prologue)
+//   gemm_pipe_kernel / gemm_fast_kernel / gemm_kernel  LDS-tiled MFMA GEMMs (M > 32)
+//   splitk_reduce_kernel, pad_rows_kernel, quantize / dequant kernels: the steps around them
 //
 // Field decode.  Let x be 4 bytes (4 k-rows), each holding fields f0..f3 (bits 0-1 .. 6-7).
 //   * "shift" form: (x << (6-2j)) & 0xC0C0C0C0 puts field j in the top two bits of each byte, so
@@ -24,10 +33,10 @@
 //     4^j * (R - A.W) with R the row sum of A over the same k range, so A.W = R - (S >> 2j).
 //     One shared XOR plus one AND per field; field 3 uses the shift form with shift 0 (one AND).
 //     R itself comes from one extra MFMA against an all-ones B per k-step, shared by all tiles.
-// The complement form costs 5 VALU ops per 16 weights and needs R (one MFMA per k-step shared by
-// all columns of the wave); the shift form costs 7 ops and needs nothing else.  The skinny kernel,
-// which has few A rows to amortise the decode over, uses the complement form; the GEMM, where the
-// extra R MFMA per m-tile would cost 25% of MFMA issue, uses the shift form.
+// The complement form costs 5 VALU ops per 16 weights and needs R; the shift form costs 7 ops and
+// needs nothing else.  The register-staged GEMVs use the complement form; the DMA-staged and
+// wave-pipelined GEMVs and the GEMMs use the shift form (the decode is not what limits them, and the
+// R MFMA would add a sixteenth to the MFMA issue of a GEMM m-tile).
 // Accumulator bound: each k-row adds at most 64*128 = 8192 in magnitude to a scaled accumulator
 // (16384 for the out-of-domain code 10, byte -128 times activation -128); the launch layer splits K
 // so that no accumulator sums more than kMaxKPerAccumulator = 2^17 - 128 k-rows.
