@@ -36,7 +36,7 @@
 // The complement form costs 5 VALU ops per 16 weights and needs R; the shift form costs 7 ops and
 // needs nothing else.  The register-staged GEMVs use the complement form; the DMA-staged and
 // wave-pipelined GEMVs and the GEMMs use the shift form (the decode is not what limits them, and the
-// R MFMA would add a sixteenth to the MFMA issue of a GEMM m-tile).
+// R MFMA per m-tile would add a quarter to a GEMM wave's MFMA issue).
 // Accumulator bound: each k-row adds at most 64*128 = 8192 in magnitude to a scaled accumulator
 // (16384 for the out-of-domain code 10, byte -128 times activation -128); the launch layer splits K
 // so that no accumulator sums more than kMaxKPerAccumulator = 2^17 - 128 k-rows.
