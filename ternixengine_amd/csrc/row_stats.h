@@ -1,7 +1,7 @@
 // row_stats.h -- per-row statistics of fp32 activations shared by every kernel that normalises or
-// quantises a row (ffn_kernels.hip, and the skinny GEMV's fused activation prologue in
-// ternary_kernels.hip).  All of them run 256-thread workgroups and use exactly these loops, so the
-// same row gives the same bits whichever kernel computes it:
+// quantises a row (ffn_kernels.hip, quantize_rows_kernel in layer_kernels.hip, and the skinny GEMVs'
+// fused activation prologue in skinny_kernels.hip).  All of them run 256-thread workgroups and use
+// exactly these loops, so the same row gives the same bits whichever kernel computes it:
 //   sum of squares: per-thread fmaf over k = tid, tid + 256, ..., then a fixed butterfly and a fixed
 //   4-wave combine; RMSNorm inv = 1 / sqrt(ss / K + eps) (reference src/simd_math.cpp:7-12);
 //   absmax of the (optionally normalised) row: a max-reduction, exact in any order;

@@ -1,176 +1,17 @@
-// ternary_kernels.hip -- gfx950 (CDNA4) kernels for C[M,N] int32 = A[M,K] int8 x W[K,N] ternary.
-//
-// Weight layout (the contract, reference src/bitpack.cpp:5-15): row-major K x NB bytes, NB = N/4,
-// weight (k, n) in bits 2*(n%4) of byte k*NB + n/4; 00 = 0, 01 = +1, 11 = -1 (10 decodes as -2,
-// like the reference's scalar and CUDA decode, src/mul_mat_ternary.cpp:53, src/cuda_kernels.cu:40).
-//
-// Every matmul kernel here feeds v_mfma_i32_16x16x64_i8.  The int8 MFMA reduces along K inside a
-// lane (lane l holds 16 K-consecutive bytes of one row of A and of one column of B, K-block l/16),
-// while the packed layout runs along N.  The kernels therefore
-//   1. gather, per lane, one packed byte-column (= 4 output columns) over 16 consecutive k-rows:
-//      with the gfx950 transposing LDS read ds_read_b64_tr_b8 from a row-major LDS stage (the
-//      DMA-staged and wave-pipelined GEMVs, the pipelined GEMM), or with a 4x4 byte transpose in
-//      registers (v_perm_b32; the register-staged GEMVs and the older GEMM kernels);
-//   2. split every dword into four MFMA B-operand dwords, one per 2-bit field j, without any
-//      per-weight work (a handful of bitwise ops per 16 weights, see "Field decode" below);
-//   3. run one MFMA per field: MFMA column i of field j is output column 4*(byte-col_i) + j.
-// Which k-rows a lane's 16 bytes hold only has to agree between A and B, so the natural row order
-// is used for both and A fragments are plain 16-byte loads.
-//
-// Kernel families (the launch layer, ternix_hip.cpp, picks one per call):
-//   skinny_wave_kernel    M <= 32: 16-byte weight strips, per-wave DMA rings, one launch for K <= 4096
-//   skinny_dma_kernel     M <= 16, long K: 256-byte strips staged by DMA, split-K + reduce
-//   skinny_short/fast/generic_kernel  register-staged GEMVs (fallbacks, fused FFN prologue)
-//   gemm_pipe_kernel / gemm_fast_kernel / gemm_kernel  LDS-tiled MFMA GEMMs (M > 32)
-//   splitk_reduce_kernel, pad_rows_kernel, quantize / dequant kernels: the steps around them
-//
-// Field decode.  Let x be 4 bytes (4 k-rows), each holding fields f0..f3 (bits 0-1 .. 6-7).
-//   * "shift" form: (x << (6-2j)) & 0xC0C0C0C0 puts field j in the top two bits of each byte, so
-//     the signed byte is 64*w (01 -> 0x40 = +64, 11 -> 0xC0 = -64, 10 -> 0x80 = -128 = -2*64).
-//     MFMA then yields 64*(A.W); the result is an exact arithmetic shift right by 6.
-//   * "complement" form (fields 0..2): z = x ^ 0x55555555 flips each field's low bit, so
-//     z & (3 << 2j) per byte equals 4^j * (1 - w) (00 -> 1, 01 -> 0, 11 -> 2, 10 -> 3).  MFMA gives
-//     4^j * (R - A.W) with R the row sum of A over the same k range, so A.W = R - (S >> 2j).
-//     One shared XOR plus one AND per field; field 3 uses the shift form with shift 0 (one AND).
-//     R itself comes from one extra MFMA against an all-ones B per k-step, shared by all tiles.
-// The complement form costs 5 VALU ops per 16 weights and needs R; the shift form costs 7 ops and
-// needs nothing else.  The register-staged GEMVs use the complement form; the DMA-staged and
-// wave-pipelined GEMVs and the GEMMs use the shift form (the decode is not what limits them, and the
-// R MFMA per m-tile would add a quarter to a GEMM wave's MFMA issue).
-// Accumulator bound: each k-row adds at most 64*128 = 8192 in magnitude to a scaled accumulator
-// (16384 for the out-of-domain code 10, byte -128 times activation -128); the launch layer splits K
-// so that no accumulator sums more than kMaxKPerAccumulator = 2^17 - 128 k-rows.
+// skinny_kernels.hip -- gfx950 GEMV / small-M kernels (M <= 32) for the ternary matmul: the
+// wave-pipelined, DMA-staged and register-staged skinny kernels, their split-K reduce and launchers.
+// Shared helpers, the weight layout and the decode forms are described in kernel_common.h.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <stdlib.h>
 
-#include <atomic>
-
+#include "kernel_common.h"
 #include "row_stats.h"
 #include "ternary_kernels.h"
 
 namespace ternix_hip {
 namespace {
-
-typedef int v4i __attribute__((ext_vector_type(4)));
-typedef float v4f __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ v4i mfma_i8(v4i a, v4i b, v4i c) {
-    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
-}
-
-// 4x4 byte transpose.  r0..r3 are four rows (byte b of r_i = byte-column b of row i); on return
-// c_b holds byte-column b of the four rows, row i in byte i.  v_perm_b32 picks bytes of {S0,S1}:
-// selector 0-3 = bytes of the second operand, 4-7 = bytes of the first.
-__device__ __forceinline__ void transpose4x4(uint32_t r0, uint32_t r1, uint32_t r2, uint32_t r3,
-                                             uint32_t& c0, uint32_t& c1, uint32_t& c2, uint32_t& c3) {
-    const uint32_t t01l = __builtin_amdgcn_perm(r1, r0, 0x05010400u);  // r0.b0 r1.b0 r0.b1 r1.b1
-    const uint32_t t01h = __builtin_amdgcn_perm(r1, r0, 0x07030602u);  // r0.b2 r1.b2 r0.b3 r1.b3
-    const uint32_t t23l = __builtin_amdgcn_perm(r3, r2, 0x05010400u);
-    const uint32_t t23h = __builtin_amdgcn_perm(r3, r2, 0x07030602u);
-    c0 = __builtin_amdgcn_perm(t23l, t01l, 0x05040100u);
-    c1 = __builtin_amdgcn_perm(t23l, t01l, 0x07060302u);
-    c2 = __builtin_amdgcn_perm(t23h, t01h, 0x05040100u);
-    c3 = __builtin_amdgcn_perm(t23h, t01h, 0x07060302u);
-}
-
-// Block ids are dealt round-robin over the 8 XCDs (XCD = id % 8).  xcd_linear(id, total) renumbers
-// them so that each XCD's blocks get consecutive numbers: XCD x holds ids x, x+8, ... and receives
-// the numbers [prefix(x), prefix(x) + count(x)).  A bijection on [0, total) for any total; it only
-// steers which blocks share an XCD's L2 and does not affect results.
-__device__ __forceinline__ int xcd_linear(int id, int total) {
-    const int q = total >> 3, r = total & 7, x = id & 7;
-    return x * q + min(x, r) + (id >> 3);
-}
-
-// Dequantising store of four consecutive outputs of one row: y = (float)c * (rs[row] * ws), the scale
-// product rounded once, then one rounding per output (the CPU oracle uses the same two steps).
-// With os.swiglu the four values are two interleaved (gate, up) pairs and the stored row is N/2 wide:
-// h[col/2 + p] = silu(y[2p]) * y[2p+1], silu(g) = g / (1 + exp(-g)) (reference src/simd_math.cpp:40-46).
-typedef float v2f __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ void store_scaled_f(const OutScale& os, float f, int row, int N, int col, v4i c, int vec);
-__device__ __forceinline__ void store_scaled(const OutScale& os, int row, int N, int col, v4i c, int vec) {
-    store_scaled_f(os, os.rs[row] * os.ws, row, N, col, c, vec);
-}
-// As store_scaled with the combined scale f = row_scale * w_scale given.
-__device__ __forceinline__ void store_scaled_f(const OutScale& os, float f, int row, int N, int col, v4i c, int vec) {
-    const v4f y = {(float)c[0] * f, (float)c[1] * f, (float)c[2] * f, (float)c[3] * f};
-    if (os.swiglu) {
-        const v2f h = {(y[0] / (1.0f + expf(-y[0]))) * y[1], (y[2] / (1.0f + expf(-y[2]))) * y[3]};
-        float* out = os.Y + (size_t)row * (size_t)(N / 2) + col / 2;
-        if (vec) {
-            __builtin_nontemporal_store(h, reinterpret_cast<v2f*>(out));
-        } else {
-            out[0] = h[0];
-            out[1] = h[1];
-        }
-        return;
-    }
-    float* out = os.Y + (size_t)row * (size_t)N + col;
-    if (vec) {
-        __builtin_nontemporal_store(y, reinterpret_cast<v4f*>(out));
-    } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) out[j] = y[j];
-    }
-}
-
-// ------------------------------------------------------------------------------------------------
-// Loads with optional bounds / alignment handling.
-// ------------------------------------------------------------------------------------------------
-
-// Four packed bytes of row `row` starting at byte-column `bc` (bc % 4 == 0).  ALIGNED: NB % 4 == 0
-// and B is 4-byte aligned, so the dword is entirely inside or entirely outside the row.
-template <bool ALIGNED>
-__device__ __forceinline__ uint32_t load_w4(const uint8_t* __restrict__ B, int row, int bc, int K, int NB) {
-    if (row >= K) return 0u;
-    const uint8_t* p = B + (size_t)row * (size_t)NB + bc;
-    if (ALIGNED) {
-        return bc < NB ? *reinterpret_cast<const uint32_t*>(p) : 0u;
-    } else {
-        uint32_t v = 0;
-#pragma unroll
-        for (int b = 0; b < 4; ++b)
-            if (bc + b < NB) v |= (uint32_t)p[b] << (8 * b);
-        return v;
-    }
-}
-
-// 16 activation bytes of row m starting at k (k % 16 == 0).  ALIGNED: K % 16 == 0 and A is 16-byte
-// aligned, so the chunk is entirely inside or outside the row.
-template <bool ALIGNED>
-__device__ __forceinline__ v4i load_a16(const int8_t* __restrict__ A, int m, int k, int M, int K) {
-    v4i r = {0, 0, 0, 0};
-    if (m >= M) return r;
-    const int8_t* p = A + (size_t)m * (size_t)K + k;
-    if (ALIGNED) {
-        if (k < K) r = *reinterpret_cast<const v4i*>(p);
-    } else {
-        uint32_t w[4] = {0u, 0u, 0u, 0u};
-#pragma unroll
-        for (int b = 0; b < 16; ++b)
-            if (k + b < K) w[b >> 2] |= (uint32_t)(uint8_t)p[b] << (8 * (b & 3));
-        r = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
-    }
-    return r;
-}
-
-// As load_a16 but rows end at k_end <= K (k_end % 64 == 0 or k_end == K, so an aligned chunk is
-// still entirely inside or outside).
-template <bool ALIGNED>
-__device__ __forceinline__ v4i load_a16_range(const int8_t* __restrict__ A, int m, int k, int M, int K, int k_end) {
-    if (k >= k_end) return v4i{0, 0, 0, 0};
-    if (ALIGNED || k + 16 <= k_end) return load_a16<ALIGNED>(A, m, k, M, K);
-    v4i r = {0, 0, 0, 0};
-    if (m >= M) return r;
-    const int8_t* p = A + (size_t)m * (size_t)K + k;
-    uint32_t w[4] = {0u, 0u, 0u, 0u};
-#pragma unroll
-    for (int b = 0; b < 16; ++b)
-        if (k + b < k_end) w[b >> 2] |= (uint32_t)(uint8_t)p[b] << (8 * (b & 3));
-    return v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
-}
 
 // ------------------------------------------------------------------------------------------------
 // Skinny split-K kernels (decode shapes, M <= 32).
@@ -738,689 +579,6 @@ __global__ __launch_bounds__(64 * SK_WAVES) void skinny_generic_kernel(SkinnyArg
 }
 
 // ------------------------------------------------------------------------------------------------
-// LDS-tiled GEMM (prefill shapes).
-//
-// Workgroup tile BM x (4*BNB) outputs, BNB packed byte-columns, k-step 64.  4 waves in a 2 x 2 grid,
-// wave tile (BM/2) rows x (BNB/2) byte-columns; per k-step a wave issues (BM/32) x (BNB/32) x 4
-// MFMAs.  A tile in LDS: BM rows x 64 bytes, 16-byte chunks XOR-swizzled by (row/4)%4 so the 16 rows
-// read by one ds_read_b128 land on distinct banks.  W tile in LDS is stored transposed (byte-column
-// major, the 64 k-rows of a byte-column contiguous, pitch 80 bytes) so a lane's B fragment is one
-// ds_read_b128; the transpose is done in registers (v_perm) between the global load and the LDS
-// store.  Two LDS stages: global loads of step s+1 are issued before the MFMAs of step s.
-// ------------------------------------------------------------------------------------------------
-
-constexpr int GM_THREADS = 256;
-constexpr int WT_PITCH = 80;  // bytes per transposed byte-column (64 k-rows + 16 pad)
-
-template <int BM, int BNB, bool ALIGNED_W, bool ALIGNED_A>
-__global__ __launch_bounds__(GM_THREADS) void gemm_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ B,
-                                                          int32_t* __restrict__ C, int M, int K, int N,
-                                                          int tiles_n, int k_begin, int k_end, int accumulate,
-                                                          int vec_store, int k_split, OutScale os) {
-    if (gridDim.y > 1) {  // split-K: this workgroup's k-range, partial tile in slab blockIdx.y
-        k_begin += (int)blockIdx.y * k_split;
-        k_end = min(k_end, k_begin + k_split);
-        C += (size_t)blockIdx.y * (size_t)M * (size_t)N;
-    }
-    constexpr int WM = BM / 2;            // rows per wave
-    constexpr int WB = BNB / 2;           // byte-columns per wave
-    constexpr int MT = WM / 16;           // m-tiles per wave
-    constexpr int GT = WB / 16;           // 16-byte-column groups per wave
-    constexpr int A_CHUNKS = BM * 4;      // 16-byte chunks per A stage
-    constexpr int A_PER_T = A_CHUNKS / GM_THREADS;
-    constexpr int W_JOBS = (BNB / 4) * 16;  // (dword column, row quad) jobs per W stage
-    constexpr int W_PER_T = (W_JOBS + GM_THREADS - 1) / GM_THREADS;
-    static_assert(A_CHUNKS % GM_THREADS == 0, "A tile must split evenly");
-
-    __shared__ __attribute__((aligned(16))) int8_t sA[2][BM * 64];
-    __shared__ __attribute__((aligned(16))) uint8_t sW[2][BNB * WT_PITCH];
-
-    const int NB = N >> 2;
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int q = lane & 15, kb = lane >> 4;
-
-    // Block -> tile: consecutive block ids are dealt round-robin over the 8 XCDs; regroup so that
-    // each XCD works on a contiguous run of tiles (neighbouring tiles share A rows / W columns in
-    // that XCD's L2).
-    const int nblocks = gridDim.x;
-    const int bid = blockIdx.x;
-    const int per_xcd = (nblocks + 7) >> 3;
-    const int xcd = bid & 7, slot = bid >> 3;
-    int tile = xcd * per_xcd + slot;
-    if ((nblocks & 7) != 0) tile = bid;  // uneven split: keep the plain order
-    const int tm = tile / tiles_n, tn = tile % tiles_n;
-    const int row0 = tm * BM;
-    const int bc0 = tn * BNB;
-    // k-steps cover [k_begin, k_end); k_begin % 64 == 0.  Loads treat k >= k_end as zero.
-    const int nsteps = (k_end - k_begin + 63) >> 6;
-
-    v4i areg[A_PER_T];
-    uint32_t wreg[W_PER_T][4];
-
-    auto gload = [&](int s) {
-        const int k0 = k_begin + s * 64;
-#pragma unroll
-        for (int p = 0; p < A_PER_T; ++p) {
-            const int c = tid + p * GM_THREADS;
-            const int r = c >> 2, ch = c & 3;
-            areg[p] = load_a16_range<ALIGNED_A>(A, row0 + r, k0 + ch * 16, M, K, k_end);
-        }
-#pragma unroll
-        for (int p = 0; p < W_PER_T; ++p) {
-            const int job = tid + p * GM_THREADS;
-            if (job < W_JOBS) {
-                const int dc = job % (BNB / 4), rq = job / (BNB / 4);
-#pragma unroll
-                for (int r = 0; r < 4; ++r) wreg[p][r] = load_w4<ALIGNED_W>(B, k0 + 4 * rq + r, bc0 + 4 * dc, k_end, NB);
-            }
-        }
-    };
-    auto sstore = [&](int buf) {
-#pragma unroll
-        for (int p = 0; p < A_PER_T; ++p) {
-            const int c = tid + p * GM_THREADS;
-            const int r = c >> 2, ch = c & 3;
-            const int sw = ch ^ ((r >> 2) & 3);
-            *reinterpret_cast<v4i*>(&sA[buf][r * 64 + sw * 16]) = areg[p];
-        }
-#pragma unroll
-        for (int p = 0; p < W_PER_T; ++p) {
-            const int job = tid + p * GM_THREADS;
-            if (job < W_JOBS) {
-                const int dc = job % (BNB / 4), rq = job / (BNB / 4);
-                uint32_t c0, c1, c2, c3;
-                transpose4x4(wreg[p][0], wreg[p][1], wreg[p][2], wreg[p][3], c0, c1, c2, c3);
-                uint8_t* base = &sW[buf][(4 * dc) * WT_PITCH + 4 * rq];
-                *reinterpret_cast<uint32_t*>(base) = c0;
-                *reinterpret_cast<uint32_t*>(base + WT_PITCH) = c1;
-                *reinterpret_cast<uint32_t*>(base + 2 * WT_PITCH) = c2;
-                *reinterpret_cast<uint32_t*>(base + 3 * WT_PITCH) = c3;
-            }
-        }
-    };
-
-    v4i acc[MT][GT][4];
-#pragma unroll
-    for (int t = 0; t < MT; ++t)
-#pragma unroll
-        for (int g = 0; g < GT; ++g)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) acc[t][g][j] = v4i{0, 0, 0, 0};
-
-    if (nsteps > 0) {
-        gload(0);
-        sstore(0);
-    }
-    __syncthreads();
-
-    for (int s = 0; s < nsteps; ++s) {
-        const int buf = s & 1;
-        if (s + 1 < nsteps) gload(s + 1);
-
-        // B fragments for this wave: GT groups of 16 byte-columns, 16 k-rows each.
-        v4i bfr[GT][4];
-#pragma unroll
-        for (int g = 0; g < GT; ++g) {
-            const int col = wn * WB + g * 16 + q;
-            const v4i x4 = *reinterpret_cast<const v4i*>(&sW[buf][col * WT_PITCH + kb * 16]);
-#pragma unroll
-            for (int rq = 0; rq < 4; ++rq) {
-                const uint32_t x = (uint32_t)x4[rq];
-                bfr[g][0][rq] = (int)((x << 6) & 0xC0C0C0C0u);
-                bfr[g][1][rq] = (int)((x << 4) & 0xC0C0C0C0u);
-                bfr[g][2][rq] = (int)((x << 2) & 0xC0C0C0C0u);
-                bfr[g][3][rq] = (int)(x & 0xC0C0C0C0u);
-            }
-        }
-#pragma unroll
-        for (int t = 0; t < MT; ++t) {
-            const int r = wm * WM + t * 16 + q;
-            const int sw = kb ^ ((r >> 2) & 3);
-            const v4i a = *reinterpret_cast<const v4i*>(&sA[buf][r * 64 + sw * 16]);
-#pragma unroll
-            for (int g = 0; g < GT; ++g)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) acc[t][g][j] = mfma_i8(a, bfr[g][j], acc[t][g][j]);
-        }
-
-        if (s + 1 < nsteps) sstore(buf ^ 1);
-        __syncthreads();
-    }
-
-    // Epilogue: element i of tile (t, g, j) is row 4*kb + i of m-tile t, column 4*(byte-col) + j.
-#pragma unroll
-    for (int t = 0; t < MT; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int row = row0 + wm * WM + t * 16 + 4 * kb + i;
-            if (row >= M) continue;
-#pragma unroll
-            for (int g = 0; g < GT; ++g) {
-                const int bcol = bc0 + wn * WB + g * 16 + q;
-                if (bcol >= NB) continue;
-                v4i v = {acc[t][g][0][i] >> 6, acc[t][g][1][i] >> 6, acc[t][g][2][i] >> 6, acc[t][g][3][i] >> 6};
-                if (os.Y) {  // dequantised float output: y = c * (row_scale[row] * w_scale)
-                    store_scaled(os, row, N, 4 * bcol, v, vec_store);
-                    continue;
-                }
-                int32_t* out = C + (size_t)row * (size_t)N + 4 * bcol;
-                if (vec_store) {
-                    if (accumulate) v += *reinterpret_cast<const v4i*>(out);
-                    __builtin_nontemporal_store(v, reinterpret_cast<v4i*>(out));  // streamed, not re-read
-                } else {
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) out[j] = accumulate ? out[j] + v[j] : v[j];
-                }
-            }
-        }
-}
-
-// ------------------------------------------------------------------------------------------------
-// Pipelined LDS-tiled GEMM (prefill shapes; K % 128 == 0, NB % 64 == 0, aligned A and W).
-//
-// Workgroup = 8 waves (8/WGN along M x WGN along N) on a BM x 64-byte-column tile (BM x 256
-// outputs); wave tile BM*WGN/8 rows x 64/WGN byte-columns, i.e. m-tiles x 16-byte-column groups x
-// 4 fields of 16x16 MFMA outputs.  Each decoded weight fragment feeds all m-tiles of the wave.
-// K advances in stages of 128 (two MFMA k-steps), NS LDS stages deep.
-//   * A and W both go global -> LDS with direct 16-byte loads (global_load_lds_dwordx4): no
-//     registers held, so NS-1 stages are in flight while one is consumed.  Each wave instruction
-//     fills 64 consecutive 16-byte LDS slots; the bank-conflict swizzles are applied by choosing
-//     which global chunk each lane loads.
-//   * A rows (128 bytes per stage): chunk c of row r at position c ^ ((r/2) % 8), so the 16 rows of
-//     one ds_read_b128 fragment read fall on distinct banks.
-//   * W rows stay row-major (64 bytes = 4 chunks per stage row): chunk c of row r at position
-//     c ^ ((r/2) % 4) ^ ((r/16) % 2).  The first term spreads the 8 rows one 16-lane group reads over
-//     32 banks; the second gives the group of the next 16 rows (the other half of the wave's k-block,
-//     read in the same pass) the other 32 banks (measured: no LDS bank conflicts left).
-//     B fragments are read with ds_read_b64_tr_b8, which transposes bytes within
-//     each 16-lane group: result lane j, byte i = byte (j % 8) of the 8 bytes addressed by lane
-//     2i + j/8.  Lane x addresses k-row (x/2) at byte offset 8*(x%2) of its 16-byte-column group,
-//     so lane q receives byte-column q of 8 consecutive k-rows; two reads give the 16 k-rows of its
-//     MFMA B operand, with no VALU transpose and no transposed stores.
-// Stage s: wait until stage s has landed (vmcnt with a static count: every thread issues the same
-// loads each stage, tails are clamped), raw s_barrier, issue stage s+NS-1, then the MFMAs of stage
-// s.  A buffer is refilled only after the barrier that follows its last read.
-// ------------------------------------------------------------------------------------------------
-
-#define TX_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 0xF) | (((n) >> 4) << 14) | (7 << 4) | (0xF << 8))
-#define TX_LGKMCNT0() __builtin_amdgcn_s_waitcnt((0xF) | (3 << 14) | (7 << 4) | (0 << 8))
-
-// 16 bytes per lane from global memory straight into LDS: lane l of the wave writes lds + 16*l.
-// (A plain device function, so the kernel templates that call it instantiate cleanly for the host.)
-__device__ __forceinline__ void lds_dma16(const void* gsrc, void* lds) {
-    __builtin_amdgcn_global_load_lds(gsrc, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
-}
-
-// Transposing 8-byte LDS read (see above).  Issued as inline assembly: the compiler then neither
-// waits for the LDS DMA in flight into other stage buffers before it (it cannot tell they do not
-// alias) nor for its own result -- the caller waits with lgkmcnt before using the value.
-__device__ __forceinline__ uint64_t lds_read_tr8(const void* lds) {
-    uint64_t v;
-    const uint32_t addr = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)lds;
-    __asm__ volatile("ds_read_b64_tr_b8 %0, %1" : "=v"(v) : "v"(addr));
-    return v;
-}
-
-constexpr int GF_THREADS = 512;
-constexpr int GF_BK = 128;
-constexpr int GF_BNB = 64;
-
-__device__ __forceinline__ int gf_swz_a(int r) { return (r >> 1) & 7; }
-__device__ __forceinline__ int gf_swz_w(int r) { return ((r >> 1) & 3) ^ ((r >> 4) & 1); }
-// W swizzle for a given stage-row width: 64-byte rows as gf_swz_w; 32-byte rows (two chunks) keep the
-// 8 rows of one transposing read on distinct banks by their pitch alone and flip the chunk for the
-// second 16-row half of a wave's k-block, which is read in the same pass.
-template <int BNB>
-__device__ __forceinline__ int swz_w(int r) { return BNB == 64 ? gf_swz_w(r) : (BNB == 32 ? ((r >> 4) & 1) : 0); }
-
-template <int BM, int WGN, int NS, int BK>
-__global__ __launch_bounds__(GF_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
-void gemm_fast_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ B, int32_t* __restrict__ C, int M,
-                      int K, int N, int tiles_n, int k_begin, int k_end, int accumulate, int vec_store,
-                      int k_split, OutScale os) {
-    if (gridDim.y > 1) {  // split-K: this workgroup's k-range, partial tile in slab blockIdx.y
-        k_begin += (int)blockIdx.y * k_split;
-        k_end = min(k_end, k_begin + k_split);
-        C += (size_t)blockIdx.y * (size_t)M * (size_t)N;
-    }
-    constexpr int WGM = 8 / WGN;             // waves along M
-    constexpr int WM = BM / WGM;             // rows per wave
-    constexpr int MT = WM / 16;              // m-tiles per wave
-    constexpr int GT = 4 / WGN;              // 16-byte-column groups per wave
-    constexpr int KS = BK / 64;              // MFMA k-steps per stage
-    constexpr int CPR = BK / 16;             // 16-byte A chunks per row per stage
-    constexpr int A_STAGE = BM * BK;         // bytes
-    constexpr int W_STAGE = BK * GF_BNB;     // bytes
-    constexpr int NA = A_STAGE / 16 / GF_THREADS;  // A loads per thread per stage
-    constexpr int NW = W_STAGE / 16 / GF_THREADS;  // W loads per thread per stage
-    // Separate arrays per stage: the compiler tracks in-flight LDS DMA per array, so reads of one
-    // stage do not wait for loads into the others.
-    __shared__ __attribute__((aligned(16))) int8_t sA0[A_STAGE];
-    __shared__ __attribute__((aligned(16))) int8_t sA1[A_STAGE];
-    __shared__ __attribute__((aligned(16))) int8_t sA2[A_STAGE];
-    __shared__ __attribute__((aligned(16))) int8_t sA3[NS > 3 ? A_STAGE : 16];
-    __shared__ __attribute__((aligned(16))) uint8_t sW0[W_STAGE];
-    __shared__ __attribute__((aligned(16))) uint8_t sW1[W_STAGE];
-    __shared__ __attribute__((aligned(16))) uint8_t sW2[W_STAGE];
-    __shared__ __attribute__((aligned(16))) uint8_t sW3[NS > 3 ? W_STAGE : 16];
-    auto stage_a = [&](int i) -> int8_t* { return i == 0 ? sA0 : (i == 1 ? sA1 : (i == 2 ? sA2 : sA3)); };
-    auto stage_w = [&](int i) -> uint8_t* { return i == 0 ? sW0 : (i == 1 ? sW1 : (i == 2 ? sW2 : sW3)); };
-
-    const int NB = N >> 2;
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave / WGN, wn = wave % WGN;
-    const int q = lane & 15, kb = lane >> 4;
-
-    // Block -> tile, XCD-aware: each XCD gets a contiguous run of tile numbers (xcd_linear).
-    // Grouped order: consecutive tile numbers walk 4 row bands before moving to the next column
-    // band, so each XCD's contiguous run of tiles is a ~4 x 8 block (A read by ~2 XCDs and W by
-    // ~4, instead of W by all 8).
-    int tm, tn;
-    {
-        const int t = xcd_linear(blockIdx.x, gridDim.x);
-        const int tiles_m = gridDim.x / tiles_n;
-        constexpr int GM = 4;
-        const int first_m = (t / (GM * tiles_n)) * GM;
-        const int gm = min(tiles_m - first_m, GM);
-        const int local = t % (GM * tiles_n);
-        tm = first_m + local % gm;
-        tn = local / gm;
-    }
-    const int row0 = tm * BM;
-    const int bc0 = tn * GF_BNB;
-    const int nst = (k_end - k_begin) / BK;  // stages
-
-    // Load geometry.  Instruction p of wave w fills 16-byte slots (p*8 + w)*64 + lane.  32-bit lane
-    // offsets (M*K and K*NB < 2^32, checked by the launcher) from wave-uniform bases.
-    uint32_t a_off[NA];
-#pragma unroll
-    for (int p = 0; p < NA; ++p) {
-        const int slot = (p * 8 + wave) * 64 + lane;
-        const int r = slot / CPR, pos = slot % CPR;
-        const int grow = min(row0 + r, M - 1);  // rows past M load row M-1; never stored
-        a_off[p] = (uint32_t)grow * (uint32_t)K + (uint32_t)(((pos & ~7) | ((pos & 7) ^ gf_swz_a(r))) * 16);
-    }
-    uint32_t w_off[NW];
-#pragma unroll
-    for (int p = 0; p < NW; ++p) {
-        const int slot = (p * 8 + wave) * 64 + lane;
-        const int r = slot >> 2, pos = slot & 3;
-        w_off[p] = (uint32_t)r * (uint32_t)NB + (uint32_t)(bc0 + (pos ^ gf_swz_w(r)) * 16);
-    }
-    auto issue = [&](int st, int buf) {
-        const int sc = min(st, nst - 1);  // clamped: keeps the per-stage load count static
-        const int8_t* abase = A + k_begin + (size_t)sc * BK;
-        int8_t* adst = stage_a(buf);
-#pragma unroll
-        for (int p = 0; p < NA; ++p) lds_dma16(abase + a_off[p], adst + (p * 8 + wave) * 1024);
-        const uint8_t* wbase = B + (size_t)(k_begin + sc * BK) * (size_t)NB;
-        uint8_t* wdst = stage_w(buf);
-#pragma unroll
-        for (int p = 0; p < NW; ++p) lds_dma16(wbase + w_off[p], wdst + (p * 8 + wave) * 1024);
-    };
-
-    v4i acc[MT][GT][4];
-#pragma unroll
-    for (int t = 0; t < MT; ++t)
-#pragma unroll
-        for (int g = 0; g < GT; ++g)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) acc[t][g][j] = v4i{0, 0, 0, 0};
-
-    auto compute = [&](int buf) {
-        const int8_t* a_st = stage_a(buf);
-        const uint8_t* w_st = stage_w(buf);
-#pragma unroll
-        for (int kk = 0; kk < KS; ++kk) {
-            v4i a[MT];
-#pragma unroll
-            for (int t = 0; t < MT; ++t) {
-                const int r = wm * WM + t * 16 + q;
-                const int c = kk * 4 + kb;  // chunk; the swizzle permutes within groups of 8
-                a[t] = *reinterpret_cast<const v4i*>(a_st + r * BK + 16 * ((c & ~7) | ((c & 7) ^ gf_swz_a(r))));
-            }
-#pragma unroll
-            for (int g = 0; g < GT; ++g) {
-                const int cg = wn * GT + g;  // 16-byte column group within the tile
-                const int r0 = kk * 64 + kb * 16 + (q >> 1);
-                const int r1 = r0 + 8;
-                uint64_t lo = lds_read_tr8(w_st + r0 * GF_BNB + 16 * (cg ^ gf_swz_w(r0)) + 8 * (q & 1));
-                uint64_t hi = lds_read_tr8(w_st + r1 * GF_BNB + 16 * (cg ^ gf_swz_w(r1)) + 8 * (q & 1));
-                // The wait names the results, so no use of them can be scheduled before it.
-                __asm__ volatile("s_waitcnt lgkmcnt(0)" : "+v"(lo), "+v"(hi));
-                const uint32_t x4[4] = {(uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32)};
-                v4i bfr[4];
-#pragma unroll
-                for (int r4 = 0; r4 < 4; ++r4) {
-                    const uint32_t x = x4[r4];
-                    bfr[0][r4] = (int)((x << 6) & 0xC0C0C0C0u);
-                    bfr[1][r4] = (int)((x << 4) & 0xC0C0C0C0u);
-                    bfr[2][r4] = (int)((x << 2) & 0xC0C0C0C0u);
-                    bfr[3][r4] = (int)(x & 0xC0C0C0C0u);
-                }
-#pragma unroll
-                for (int t = 0; t < MT; ++t)
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) acc[t][g][j] = mfma_i8(a[t], bfr[j], acc[t][g][j]);
-            }
-        }
-    };
-
-    // Prologue: stages 0 .. NS-2 in flight.
-#pragma unroll
-    for (int p = 0; p < NS - 1; ++p) issue(p, p);
-
-    // h is always a literal at the call sites, so after inlining every buffer index is a constant;
-    // the main loop has no conditions, so the compiler counts the loads in flight exactly as the
-    // waits assume.
-    auto stage = [&](int st, int h) {
-        TX_VMCNT((NS - 2) * (NA + NW));  // stage st has landed (the NS-2 later stages may not)
-        __builtin_amdgcn_s_barrier();
-        __builtin_amdgcn_sched_barrier(0);
-        issue(st + NS - 1, (h + NS - 1) % NS);
-        compute(h % NS);
-        TX_LGKMCNT0();  // this stage's LDS reads are done before the next barrier
-        __builtin_amdgcn_sched_barrier(0);
-    };
-    int s = 0;
-    for (; s + NS <= nst; s += NS) {
-        stage(s + 0, 0);
-        stage(s + 1, 1);
-        stage(s + 2, 2);
-        if (NS > 3) stage(s + 3, 3);
-    }
-    if (s + 0 < nst) stage(s + 0, 0);
-    if (s + 1 < nst) stage(s + 1, 1);
-    if (NS > 3 && s + 2 < nst) stage(s + 2, 2);
-    TX_VMCNT(0);  // no LDS DMA may land after the workgroup exits
-
-    // Epilogue: element i of tile (t, g, j) is row 4*kb + i of m-tile t, column 4*(byte-col) + j.
-#pragma unroll
-    for (int t = 0; t < MT; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int row = row0 + wm * WM + t * 16 + 4 * kb + i;
-            if (row >= M) continue;
-#pragma unroll
-            for (int g = 0; g < GT; ++g) {
-                const int bcol = bc0 + (wn * GT + g) * 16 + q;
-                v4i v = {acc[t][g][0][i] >> 6, acc[t][g][1][i] >> 6, acc[t][g][2][i] >> 6, acc[t][g][3][i] >> 6};
-                if (os.Y) {  // dequantised float output: y = c * (row_scale[row] * w_scale)
-                    store_scaled(os, row, N, 4 * bcol, v, vec_store);
-                    continue;
-                }
-                int32_t* out = C + (size_t)row * (size_t)N + 4 * bcol;
-                if (vec_store) {
-                    if (accumulate) v += *reinterpret_cast<const v4i*>(out);
-                    __builtin_nontemporal_store(v, reinterpret_cast<v4i*>(out));  // streamed, not re-read
-                } else {
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) out[j] = accumulate ? out[j] + v[j] : v[j];
-                }
-            }
-        }
-}
-
-// ------------------------------------------------------------------------------------------------
-// Software-pipelined variant of the LDS-tiled GEMM.  Same tiles, LDS layouts and DMA as
-// gemm_fast_kernel; the difference is the order of work inside a wave:
-//   * every LDS fragment read is inline assembly, so the only LDS waits are the explicit ones;
-//   * the fragments of the next MFMA k-step are read while the MFMAs of the current one run
-//     (two register sets, alternating);
-//   * the stage barrier (stage s+1 landed everywhere, stage s free for reuse) and the DMA issue of
-//     stage s+NS happen before the last k-step's MFMAs of stage s, and the first fragments of
-//     stage s+1 are read right after it, so the MFMA pipe never waits for a fresh stage's reads.
-// NS stages are in flight: NS-1 DMA stages ahead of the one being read.
-// ------------------------------------------------------------------------------------------------
-__device__ __forceinline__ v4i lds_read_b128_asm(uint32_t addr) {
-    v4i v;
-    __asm__ volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
-    return v;
-}
-__device__ __forceinline__ uint64_t lds_read_tr8_asm(uint32_t addr) {
-    uint64_t v;
-    __asm__ volatile("ds_read_b64_tr_b8 %0, %1" : "=v"(v) : "v"(addr));
-    return v;
-}
-__device__ __forceinline__ uint32_t lds_u32(const void* p) {
-    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
-}
-
-template <int MT, int GT>
-struct PipeFrag {
-    v4i a[MT];
-    uint64_t lo[GT], hi[GT];
-};
-
-template <int BM, int WGN, int NS, int BK, int NWV, int BNB>
-__global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2)))
-void gemm_pipe_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ B, int32_t* __restrict__ C, int M,
-                      int K, int N, int tiles_n, int k_begin, int k_end, int accumulate, int vec_store,
-                      int k_split, OutScale os) {
-    if (gridDim.y > 1) {  // split-K: this workgroup's k-range, partial tile in slab blockIdx.y
-        k_begin += (int)blockIdx.y * k_split;
-        k_end = min(k_end, k_begin + k_split);
-        C += (size_t)blockIdx.y * (size_t)M * (size_t)N;
-    }
-    constexpr int THR = 64 * NWV;           // threads per workgroup
-    constexpr int CW = BNB / 16;            // 16-byte chunks per W stage row
-    constexpr int WGM = NWV / WGN;
-    constexpr int WM = BM / WGM;
-    constexpr int MT = WM / 16;
-    constexpr int GT = CW / WGN;
-    constexpr int KS = BK / 64;
-    constexpr int CPR = BK / 16;
-    constexpr int A_STAGE = BM * BK;
-    constexpr int W_STAGE = BK * BNB;
-    constexpr int NA = A_STAGE / 16 / THR;
-    constexpr int NW = W_STAGE / 16 / THR;
-    static_assert(KS % 2 == 0, "fragment sets alternate per k-step");
-    static_assert(NA >= 1 && NW >= 1 && GT >= 1, "tile too small for the workgroup");
-    __shared__ __attribute__((aligned(16))) int8_t sA0[A_STAGE];
-    __shared__ __attribute__((aligned(16))) int8_t sA1[A_STAGE];
-    __shared__ __attribute__((aligned(16))) int8_t sA2[A_STAGE];
-    __shared__ __attribute__((aligned(16))) int8_t sA3[NS > 3 ? A_STAGE : 16];
-    __shared__ __attribute__((aligned(16))) uint8_t sW0[W_STAGE];
-    __shared__ __attribute__((aligned(16))) uint8_t sW1[W_STAGE];
-    __shared__ __attribute__((aligned(16))) uint8_t sW2[W_STAGE];
-    __shared__ __attribute__((aligned(16))) uint8_t sW3[NS > 3 ? W_STAGE : 16];
-    auto stage_a = [&](int i) -> int8_t* { return i == 0 ? sA0 : (i == 1 ? sA1 : (i == 2 ? sA2 : sA3)); };
-    auto stage_w = [&](int i) -> uint8_t* { return i == 0 ? sW0 : (i == 1 ? sW1 : (i == 2 ? sW2 : sW3)); };
-
-    const int NB = N >> 2;
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave / WGN, wn = wave % WGN;
-    const int q = lane & 15, kb = lane >> 4;
-
-    const int tiles_m = (M + BM - 1) / BM;
-    int tm, tn;
-    {
-        const int t = xcd_linear(blockIdx.x, gridDim.x);
-        constexpr int GM = 4;
-        const int first_m = (t / (GM * tiles_n)) * GM;
-        const int gm = min(tiles_m - first_m, GM);
-        const int local = t % (GM * tiles_n);
-        tm = first_m + local % gm;
-        tn = local / gm;
-    }
-    const int row0 = tm * BM;
-    const int bc0 = tn * BNB;
-    const int nst = (k_end - k_begin) / BK;
-
-    uint32_t a_off[NA];
-#pragma unroll
-    for (int p = 0; p < NA; ++p) {
-        const int slot = (p * NWV + wave) * 64 + lane;
-        const int r = slot / CPR, pos = slot % CPR;
-        const int grow = min(row0 + r, M - 1);
-        a_off[p] = (uint32_t)grow * (uint32_t)K + (uint32_t)(((pos & ~7) | ((pos & 7) ^ gf_swz_a(r))) * 16);
-    }
-    uint32_t w_off[NW];
-#pragma unroll
-    for (int p = 0; p < NW; ++p) {
-        const int slot = (p * NWV + wave) * 64 + lane;
-        const int r = slot / CW, pos = slot % CW;
-        w_off[p] = (uint32_t)r * (uint32_t)NB + (uint32_t)(bc0 + (pos ^ swz_w<BNB>(r)) * 16);
-    }
-    auto issue = [&](int st, int buf) {
-        const int sc = min(st, nst - 1);
-        const int8_t* abase = A + k_begin + (size_t)sc * BK;
-        int8_t* adst = stage_a(buf);
-#pragma unroll
-        for (int p = 0; p < NA; ++p) lds_dma16(abase + a_off[p], adst + (p * NWV + wave) * 1024);
-        const uint8_t* wbase = B + (size_t)(k_begin + sc * BK) * (size_t)NB;
-        uint8_t* wdst = stage_w(buf);
-#pragma unroll
-        for (int p = 0; p < NW; ++p) lds_dma16(wbase + w_off[p], wdst + (p * NWV + wave) * 1024);
-    };
-
-    // Per-lane fragment offsets inside a stage.  A: row wm*WM + 16t + q, chunk kk*4 + kb (the swizzle
-    // depends on the row only through (row/2) % 8, the same for all t).  W: k-row 64kk + 16kb + q/2
-    // (+8 for the second read), 16-byte group wn*GT + g (swizzle through (row/2) % 4, the same for all
-    // kk and for the +8 row).
-    uint32_t a_lane[KS];
-#pragma unroll
-    for (int kk = 0; kk < KS; ++kk) {
-        const int r = wm * WM + q;
-        const int c = kk * 4 + kb;
-        a_lane[kk] = (uint32_t)(r * BK + 16 * ((c & ~7) | ((c & 7) ^ gf_swz_a(r))));
-    }
-    uint32_t w_lane[GT];
-#pragma unroll
-    for (int g = 0; g < GT; ++g) {
-        const int cg = wn * GT + g;
-        const int r0 = kb * 16 + (q >> 1);
-        w_lane[g] = (uint32_t)(r0 * BNB + 16 * (cg ^ swz_w<BNB>(r0)) + 8 * (q & 1));
-    }
-    auto read = [&](PipeFrag<MT, GT>& f, int buf, int kk) {
-        const uint32_t ab = lds_u32(stage_a(buf)) + a_lane[kk];
-#pragma unroll
-        for (int t = 0; t < MT; ++t) f.a[t] = lds_read_b128_asm(ab + (uint32_t)(t * 16 * BK));
-        const uint32_t wb = lds_u32(stage_w(buf)) + (uint32_t)(kk * 64 * BNB);
-#pragma unroll
-        for (int g = 0; g < GT; ++g) {
-            f.lo[g] = lds_read_tr8_asm(wb + w_lane[g]);
-            f.hi[g] = lds_read_tr8_asm(wb + w_lane[g] + 8 * BNB);
-        }
-    };
-    // All LDS reads issued so far have returned; the empty asm statements tie each fragment register
-    // to that point, so no use of them is scheduled before it.
-    auto wait_frag = [&](PipeFrag<MT, GT>& f) {
-        TX_LGKMCNT0();
-#pragma unroll
-        for (int t = 0; t < MT; ++t) __asm__ volatile("" : "+v"(f.a[t]));
-#pragma unroll
-        for (int g = 0; g < GT; ++g) __asm__ volatile("" : "+v"(f.lo[g]), "+v"(f.hi[g]));
-    };
-
-    v4i acc[MT][GT][4];
-#pragma unroll
-    for (int t = 0; t < MT; ++t)
-#pragma unroll
-        for (int g = 0; g < GT; ++g)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) acc[t][g][j] = v4i{0, 0, 0, 0};
-
-    auto mfmas = [&](const PipeFrag<MT, GT>& f) {
-#pragma unroll
-        for (int g = 0; g < GT; ++g) {
-            const uint32_t x4[4] = {(uint32_t)f.lo[g], (uint32_t)(f.lo[g] >> 32), (uint32_t)f.hi[g],
-                                    (uint32_t)(f.hi[g] >> 32)};
-            v4i bfr[4];
-#pragma unroll
-            for (int r4 = 0; r4 < 4; ++r4) {
-                const uint32_t x = x4[r4];
-                bfr[0][r4] = (int)((x << 6) & 0xC0C0C0C0u);
-                bfr[1][r4] = (int)((x << 4) & 0xC0C0C0C0u);
-                bfr[2][r4] = (int)((x << 2) & 0xC0C0C0C0u);
-                bfr[3][r4] = (int)(x & 0xC0C0C0C0u);
-            }
-#pragma unroll
-            for (int t = 0; t < MT; ++t)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) acc[t][g][j] = mfma_i8(f.a[t], bfr[j], acc[t][g][j]);
-        }
-    };
-
-    PipeFrag<MT, GT> f0, f1;
-    // Prologue: all NS stages in flight, wait for stage 0, first fragments.
-#pragma unroll
-    for (int p = 0; p < NS; ++p) issue(p, p);
-    TX_VMCNT((NS - 1) * (NA + NW));
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_sched_barrier(0);
-    read(f0, 0, 0);
-
-    // One stage in buffer h (a literal at every call site).  Fragment set f0 serves even k-steps.
-    auto stage = [&](int st, int h) {
-#pragma unroll
-        for (int kk = 0; kk < KS; ++kk) {
-            PipeFrag<MT, GT>& cur = (kk & 1) ? f1 : f0;
-            PipeFrag<MT, GT>& nxt = (kk & 1) ? f0 : f1;
-            wait_frag(cur);
-            __builtin_amdgcn_sched_barrier(0);
-            if (kk + 1 < KS) {
-                read(nxt, h, kk + 1);
-            } else if (st + 1 < nst) {
-                TX_VMCNT((NS - 2) * (NA + NW));  // stage st+1 has landed (NS-2 later stages may not)
-                __builtin_amdgcn_s_barrier();     // ... everywhere, and every wave is done reading stage st
-                __builtin_amdgcn_sched_barrier(0);
-                issue(st + NS, h);
-                read(nxt, (h + 1) % NS, 0);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-            mfmas(cur);
-            // keep the next k-step's wait below these MFMAs (it would otherwise be hoisted among them
-            // and wait for the reads just issued)
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    };
-    int s = 0;
-    for (; s + NS <= nst; s += NS) {
-        stage(s + 0, 0);
-        stage(s + 1, 1);
-        stage(s + 2, 2);
-        if (NS > 3) stage(s + 3, 3);
-    }
-    if (s + 0 < nst) stage(s + 0, 0);
-    if (s + 1 < nst) stage(s + 1, 1);
-    if (NS > 3 && s + 2 < nst) stage(s + 2, 2);
-    TX_VMCNT(0);  // no LDS DMA may land after the workgroup exits
-
-#pragma unroll
-    for (int t = 0; t < MT; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int row = row0 + wm * WM + t * 16 + 4 * kb + i;
-            if (row >= M) continue;
-#pragma unroll
-            for (int g = 0; g < GT; ++g) {
-                const int bcol = bc0 + (wn * GT + g) * 16 + q;
-                v4i v = {acc[t][g][0][i] >> 6, acc[t][g][1][i] >> 6, acc[t][g][2][i] >> 6, acc[t][g][3][i] >> 6};
-                if (os.Y) {  // dequantised float output: y = c * (row_scale[row] * w_scale)
-                    store_scaled(os, row, N, 4 * bcol, v, vec_store);
-                    continue;
-                }
-                int32_t* out = C + (size_t)row * (size_t)N + 4 * bcol;
-                if (vec_store) {
-                    if (accumulate) v += *reinterpret_cast<const v4i*>(out);
-                    __builtin_nontemporal_store(v, reinterpret_cast<v4i*>(out));  // streamed, not re-read
-                } else {
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) out[j] = accumulate ? out[j] + v[j] : v[j];
-                }
-            }
-        }
-}
-
-// ------------------------------------------------------------------------------------------------
 // DMA-staged skinny kernel (M <= 16 per m-group, long weight streams).
 //
 // The register-staged skinny kernels read each weight row as 64-byte pieces, one per wave, so every
@@ -1907,31 +1065,6 @@ void skinny_wave_kernel(SkinnyArgs args) {
     }
 }
 
-// ------------------------------------------------------------------------------------------------
-// Naive kernel: one work-item per output, weights decoded per k from global memory with
-// w = (b & 1) - (b & 2) (the reference decode2, src/cuda_kernels.cu:40-54).
-// ------------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void naive_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ B,
-                                                    int32_t* __restrict__ C, int M, int K, int N) {
-    const int col = blockIdx.x * 64 + (threadIdx.x & 63);
-    const int row = blockIdx.y * 4 + (threadIdx.x >> 6);
-    if (row >= M || col >= N) return;
-    const int NB = N >> 2;
-    const int shift = (col & 3) * 2;
-    int acc = 0;
-    for (int k = 0; k < K; ++k) {
-        const unsigned bits = (B[(size_t)k * NB + (col >> 2)] >> shift) & 3u;
-        acc += (int)A[(size_t)row * K + k] * ((int)(bits & 1u) - (int)(bits & 2u));
-    }
-    C[(size_t)row * N + col] = acc;
-}
-
-__global__ __launch_bounds__(256) void zero_kernel(int32_t* __restrict__ C, size_t n) {
-    size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-    const size_t stride = (size_t)gridDim.x * 256;
-    for (; i < n; i += stride) C[i] = 0;
-}
-
 // C[m][n] = sum over splits of P[s][m][n].  A workgroup owns 64 consecutive groups of 4 outputs
 // (lane = group); its 4 waves take splits s = w, w+4, ... with all their loads issued at once (one
 // memory round trip for up to 64 splits), then add in LDS.  Integer addition is exact, so the order
@@ -2043,104 +1176,7 @@ hipError_t launch_fast_kw(const SkinnyArgs& a, int kw, dim3 grid, hipStream_t st
     return launch_fast_t<MT, TB, 1, PD, LOW_M>(a, grid, st);
 }
 
-template <int BM, int BNB>
-hipError_t launch_gemm_t(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, bool aw, bool aa,
-                         int kb, int ke, int acc, hipStream_t st, const OutScale& os, int splits, int k_split) {
-    const int NB = N >> 2;
-    const int tiles_m = (M + BM - 1) / BM, tiles_n = (NB + BNB - 1) / BNB;
-    const dim3 grid(tiles_m * tiles_n, splits), block(GM_THREADS);
-    const int vs = ((uintptr_t)(os.Y ? (const void*)os.Y : (const void*)C) % 16) == 0;
-    if (aw && aa)
-        hipLaunchKernelGGL((gemm_kernel<BM, BNB, true, true>), grid, block, 0, st, A, B, C, M, K, N, tiles_n, kb, ke, acc, vs, k_split, os);
-    else if (aw)
-        hipLaunchKernelGGL((gemm_kernel<BM, BNB, true, false>), grid, block, 0, st, A, B, C, M, K, N, tiles_n, kb, ke, acc, vs, k_split, os);
-    else if (aa)
-        hipLaunchKernelGGL((gemm_kernel<BM, BNB, false, true>), grid, block, 0, st, A, B, C, M, K, N, tiles_n, kb, ke, acc, vs, k_split, os);
-    else
-        hipLaunchKernelGGL((gemm_kernel<BM, BNB, false, false>), grid, block, 0, st, A, B, C, M, K, N, tiles_n, kb, ke, acc, vs, k_split, os);
-    return hipGetLastError();
-}
-
-// ------------------------------------------------------------------------------------------------
-// Activation quantisation and dequantisation (the steps either side of the matmul in a BitNet b1.58
-// layer; the reference leaves them as a stub, scripts/quantize.py:5, README.md:203).
-//   quantize_rows_kernel: one workgroup per row; absmax by a max-reduction (exact, order-free),
-//     s = 127 / max(absmax, 1e-5), q = clamp(rint(x * s), -128, 127) (round half to even),
-//     row_scale = max(absmax, 1e-5) / 127 -- IEEE division and multiplication, no contraction, so the
-//     CPU restatement reproduces every bit.
-//   dequant_kernel: y = (float)c * (row_scale[m] * w_scale) for an int32 C (Y may alias C: each
-//     element is read before the same element is written by the same thread).
-// Both are HBM streams (quantise: 4 bytes read + 1 written per element, twice over the row if it
-// does not stay in cache; dequantise: 4 + 4 bytes per output).
-// ------------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void dequant_kernel(const int32_t* C, OutScale os, int N, size_t items, int vec) {
-    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= items) return;
-    const size_t e = 4 * i;
-    const int row = (int)(e / (size_t)N), col = (int)(e % (size_t)N);
-    v4i c;
-    if (vec) {
-        c = reinterpret_cast<const v4i*>(C)[i];
-    } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) c[j] = C[e + j];
-    }
-    store_scaled(os, row, N, col, c, vec);
-}
-
-__global__ __launch_bounds__(256) void quantize_rows_kernel(const float* __restrict__ X, int8_t* __restrict__ Q,
-                                                            float* __restrict__ row_scale, int K, int vec) {
-    __shared__ float red[4];
-    const int m = blockIdx.x;
-    const float* x = X + (size_t)m * (size_t)K;
-    int8_t* q = Q + (size_t)m * (size_t)K;
-    float amax = 0.0f;
-    if (vec) {
-        for (int c = threadIdx.x; c < K / 4; c += 256) {
-            const v4f v = reinterpret_cast<const v4f*>(x)[c];
-            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
-        }
-    } else {
-        for (int c = threadIdx.x; c < K; c += 256) amax = fmaxf(amax, fabsf(x[c]));
-    }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
-    __syncthreads();
-    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    const float a = fmaxf(amax, 1e-5f);
-    const float s = 127.0f / a;
-    if (threadIdx.x == 0) row_scale[m] = a / 127.0f;
-    auto qz = [&](float v) -> int {
-        const float r = rintf(v * s);
-        return (int)fminf(fmaxf(r, -128.0f), 127.0f);
-    };
-    if (vec) {
-        for (int c = threadIdx.x; c < K / 16; c += 256) {
-            const v4f* src = reinterpret_cast<const v4f*>(x) + 4 * c;
-            v4i out;
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const v4f v = src[u];
-                out[u] = (int)((uint32_t)(qz(v[0]) & 0xFF) | ((uint32_t)(qz(v[1]) & 0xFF) << 8) |
-                               ((uint32_t)(qz(v[2]) & 0xFF) << 16) | ((uint32_t)(qz(v[3]) & 0xFF) << 24));
-            }
-            reinterpret_cast<v4i*>(q)[c] = out;
-        }
-    } else {
-        for (int c = threadIdx.x; c < K; c += 256) q[c] = (int8_t)qz(x[c]);
-    }
-}
-
 }  // namespace
-
-hipError_t launch_zero(int32_t* C, size_t n, hipStream_t st) {
-    if (n == 0) return hipSuccess;
-    size_t blocks = (n + 255) / 256;
-    if (blocks > 4096) blocks = 4096;
-    hipLaunchKernelGGL(zero_kernel, dim3((unsigned)blocks), dim3(256), 0, st, C, n);
-    return hipGetLastError();
-}
 
 // Fused activation quantisation on the DMA kernel: whole rows in registers (K <= 256 * kRowRegs) and a
 // split, whose reduce launch applies the row scales the kernel stores.
@@ -2240,37 +1276,6 @@ hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, i
     return hipGetLastError();
 }
 
-// Compute units of the current device, read once per device (the attribute query is not free).
-int device_cu_count() {
-    static std::atomic<int> cache[64];
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    int n = cache[dev].load(std::memory_order_relaxed);
-    if (n > 0) return n;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cache[dev].store(n, std::memory_order_relaxed);
-    return n;
-}
-
-// Narrow 64 x 64 tiles for M <= 64 when they alone fill at most one workgroup per CU (measured on
-// MI355X: cfg3 M=64 up 18.0 -> 13.4 us with no K split, 4096^2 at M=64 16.2 -> 9.9 us; with more
-// tiles than CUs, e.g. N = 28672, the 256-column tiles are faster).  TERNIX_GEMM_NARROW=0 / 1 turns
-// the choice off / on regardless (experiments).
-bool gemm_narrow_wanted(int M, int K, int N) {
-    static const int env = [] {
-        const char* e = std::getenv("TERNIX_GEMM_NARROW");
-        return e ? std::atoi(e) : -1;
-    }();
-    const int NB = N >> 2;
-    if (env == 0 || M > 64 || NB % 16 != 0 || K % 256 != 0) return false;
-    if (env > 0) return true;
-    return (long)((M + 63) / 64) * (NB / 16) <= device_cu_count();
-}
-
-bool gemm_narrow_ok(int M, int K, int N, int k_len, int splits, int k_split) {
-    return gemm_narrow_wanted(M, K, N) && k_len % 256 == 0 && (splits == 1 || k_split % 256 == 0);
-}
-
 bool skinny_wave_ok(const int8_t* A, const uint8_t* B, int M, int K, int N, int sw) {
     const int NB = N >> 2;
     return M <= 32 && (sw == 16 || sw == 32) && K % 64 == 0 && NB % sw == 0 && (uintptr_t)B % 16 == 0 &&
@@ -2339,99 +1344,6 @@ hipError_t launch_skinny_wave(const int8_t* A, const uint8_t* B, int32_t* C, int
                      : launch_splitk_reduce(partials, C, M, N, splits, os, st);
 }
 
-hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int k_begin, int k_end,
-                       int accumulate, hipStream_t st, const OutScale& os, int splits, int k_split) {
-    const int NB = N >> 2;
-    // Experiment switches, read once per process.
-    static const char* const force_generic = std::getenv("TERNIX_GEMM_GENERIC");
-    if (splits < 1) splits = 1;
-    const bool fast = (K % GF_BK == 0) && ((k_end - k_begin) % GF_BK == 0) && (k_begin % GF_BK == 0) &&
-                      (splits == 1 || k_split % GF_BK == 0) &&
-                      (NB % GF_BNB == 0) && ((uintptr_t)A % 16 == 0) && ((uintptr_t)B % 16 == 0) &&
-                      k_end > k_begin && (size_t)M * (size_t)K < ((size_t)1 << 32) &&
-                      (size_t)GF_BK * (size_t)NB < ((size_t)1 << 32) && !(force_generic && force_generic[0] == '1');
-    if (fast) {
-        const int vs = ((uintptr_t)(os.Y ? (const void*)os.Y : (const void*)C) % 16) == 0;
-        const int tiles_n = NB / GF_BNB;
-        static const char* const bm_env = std::getenv("TERNIX_GEMM_BM");
-        static const char* const wgn_env = std::getenv("TERNIX_GEMM_WGN");
-        static const char* const bk_env = std::getenv("TERNIX_GEMM_BK");
-        // Measured on MI355X (cfg4 shapes): 256-row tiles only when they still give >= 1.5 tiles per
-        // CU, else 128-row tiles; 8 waves as 2 (M) x 4 (N); 128-deep stages.
-        const int cus = device_cu_count();
-        int bm = (splits == 1 && (long)((M + 255) / 256) * tiles_n * 2 >= 3L * cus) ? 256 : 128;
-        if (bm_env) bm = std::atoi(bm_env) == 128 ? 128 : 256;
-        const int wgn = wgn_env && std::atoi(wgn_env) == 2 ? 2 : 4;
-        int bk = 128;
-        if (bk_env && std::atoi(bk_env) == 256 && bm == 128 && (k_end - k_begin) % 256 == 0) bk = 256;
-        const dim3 grid(((M + bm - 1) / bm) * tiles_n, splits);
-        // 128-row tiles run the software-pipelined kernel (measured faster on MI355X); 256-row tiles
-        // keep gemm_fast_kernel, whose wave tile leaves no registers for a second fragment set.
-        static const int pipe_env = [] {
-            const char* e = std::getenv("TERNIX_GEMM_PIPE");
-            return e ? std::atoi(e) : -1;
-        }();
-        const int pipe = pipe_env >= 0 ? (pipe_env == 1 && bm == 256 ? 0 : pipe_env) : (bm == 128 ? 1 : 0);
-        static const int pipe_ns = [] {
-            const char* e = std::getenv("TERNIX_GEMM_NS");
-            return e && std::atoi(e) == 4 ? 4 : 3;
-        }();
-        static const int small_m_max = [] {
-            const char* e = std::getenv("TERNIX_GEMM_SMALLM");  // experiments only
-            return e ? std::atoi(e) : 64;
-        }();
-        if (M <= small_m_max && gemm_narrow_ok(M, K, N, k_end - k_begin, splits, k_split)) {
-            // 64 x 64 output tiles (16 bytes of every weight row): enough workgroups without a K
-            // split where the 256-column tiles would need one; one m-tile per wave, 256-deep stages.
-            const dim3 gridn((unsigned)(((M + 63) / 64) * (NB / 16)), splits);
-            hipLaunchKernelGGL((gemm_pipe_kernel<64, 1, 3, 256, 4, 16>), gridn, dim3(256), 0, st, A, B, C, M, K, N,
-                               NB / 16, k_begin, k_end, accumulate, vs, k_split, os);
-            return hipGetLastError();
-        }
-        // One round of 128-row tiles with a short k-range (cfg4 4096^2): two co-resident workgroups
-        // of 64-row tiles per CU instead, whose barriers and final stores overlap each other's work
-        // (measured on MI355X: 29.5 -> 27.9 us; with long K or several rounds the 128-row tiles win).
-        const long tiles128 = (long)((M + 127) / 128) * tiles_n;
-        const bool short_round = splits == 1 && bm == 128 && !bm_env && tiles128 <= cus &&
-                                 2 * tiles128 >= cus && (k_end - k_begin) <= 4096;
-        if (M <= small_m_max || short_round) {
-            // Small M (64 rows or fewer): four-wave workgroups on 64-row tiles, so no MFMA row or A
-            // byte is spent on padding rows; the caller splits K to fill the chip.
-            const dim3 grid64((unsigned)(((M + 63) / 64) * tiles_n), splits);
-            hipLaunchKernelGGL((gemm_pipe_kernel<64, 4, 3, 128, 4, 64>), grid64, dim3(256), 0, st, A, B, C, M, K, N,
-                               tiles_n, k_begin, k_end, accumulate, vs, k_split, os);
-            return hipGetLastError();
-        }
-        if (pipe) {
-#define TX_GP_LAUNCH(BM_, WGN_, NS_, BK_)                                                                      \
-    hipLaunchKernelGGL((gemm_pipe_kernel<BM_, WGN_, NS_, BK_, 8, GF_BNB>), grid, dim3(GF_THREADS), 0, st, A, B, C, M, \
-                       K, N, tiles_n, k_begin, k_end, accumulate, vs, k_split, os)
-            if (bk == 256 && wgn == 4) TX_GP_LAUNCH(128, 4, 3, 256);
-            else if (bk == 256) TX_GP_LAUNCH(128, 2, 3, 256);
-            else if (wgn == 4 && pipe_ns == 4) TX_GP_LAUNCH(128, 4, 4, 128);
-            else if (wgn == 4) TX_GP_LAUNCH(128, 4, 3, 128);
-            else if (pipe_ns == 4) TX_GP_LAUNCH(128, 2, 4, 128);
-            else TX_GP_LAUNCH(128, 2, 3, 128);
-#undef TX_GP_LAUNCH
-            return hipGetLastError();
-        }
-#define TX_GF_LAUNCH(BM_, WGN_, NS_, BK_)                                                                         \
-    hipLaunchKernelGGL((gemm_fast_kernel<BM_, WGN_, NS_, BK_>), grid, dim3(GF_THREADS), 0, st, A, B, C, M, K, N, \
-                       tiles_n, k_begin, k_end, accumulate, vs, k_split, os)
-        if (bm == 256 && wgn == 4) TX_GF_LAUNCH(256, 4, 3, 128);
-        else if (bm == 256) TX_GF_LAUNCH(256, 2, 3, 128);
-        else if (bk == 256 && wgn == 4) TX_GF_LAUNCH(128, 4, 3, 256);
-        else if (bk == 256) TX_GF_LAUNCH(128, 2, 3, 256);
-        else if (wgn == 4) TX_GF_LAUNCH(128, 4, 4, 128);
-        else TX_GF_LAUNCH(128, 2, 4, 128);
-#undef TX_GF_LAUNCH
-        return hipGetLastError();
-    }
-    const bool aw = (NB % 4 == 0) && ((uintptr_t)B % 4 == 0);
-    const bool aa = (K % 16 == 0) && ((uintptr_t)A % 16 == 0);
-    return launch_gemm_t<128, 64>(A, B, C, M, K, N, aw, aa, k_begin, k_end, accumulate, st, os, splits, k_split);
-}
-
 hipError_t launch_splitk_reduce(const int32_t* P, int32_t* C, int M, int N, int splits, const OutScale& os,
                                 hipStream_t st, int n_in) {
     if (n_in <= 0) n_in = N;
@@ -2440,92 +1352,6 @@ hipError_t launch_splitk_reduce(const int32_t* P, int32_t* C, int M, int N, int 
     const int vec = ((uintptr_t)(os.Y ? (const void*)os.Y : (const void*)C) % 16) == 0;
     hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n4 + 63) / 64)), dim3(256), 0, st, P, C, n4, splits, vec,
                        os, N, n_in, (size_t)M * (size_t)n_in / 4);
-    return hipGetLastError();
-}
-
-// ------------------------------------------------------------------------------------------------
-// Padded copy for ragged shapes: rows of `len` bytes at pitch src_pitch (any alignment) into rows of
-// dst_pitch bytes (16-byte aligned, dst_pitch % 16 == 0), zero-filled past len and for the rows
-// rows..dst_rows-1.  Each thread writes one 16-byte chunk from five aligned dword loads and
-// v_alignbyte; an aligned dword holding at least one byte of the source buffer never crosses a page
-// the buffer does not touch, so loads stay within the buffer's pages (dwords starting past its last
-// byte are not loaded).
-// ------------------------------------------------------------------------------------------------
-struct PadJob {
-    const uint8_t* src;
-    uint8_t* dst;
-    int rows, dst_rows, src_pitch, len, dst_pitch;
-    size_t chunks;  // dst_rows * dst_pitch / 16
-};
-
-__device__ __forceinline__ void pad_chunk(const PadJob& j, size_t idx) {
-    const int cpr = j.dst_pitch >> 4;
-    const int r = (int)(idx / (size_t)cpr), c = (int)(idx % (size_t)cpr);
-    v4i out = {0, 0, 0, 0};
-    const int n = min(max(j.len - 16 * c, 0), 16);  // source bytes in this chunk
-    if (r < j.rows && n > 0) {
-        const uint8_t* p = j.src + (size_t)r * (size_t)j.src_pitch + 16 * c;
-        const uint8_t* end = j.src + (size_t)(j.rows - 1) * (size_t)j.src_pitch + j.len;
-        const uint32_t* pa = reinterpret_cast<const uint32_t*>((uintptr_t)p & ~(uintptr_t)3);
-        const uint32_t sh = (uint32_t)((uintptr_t)p & 3);
-        uint32_t d[5];
-#pragma unroll
-        for (int k = 0; k < 5; ++k) d[k] = reinterpret_cast<const uint8_t*>(pa + k) < end ? pa[k] : 0u;
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            uint32_t v = __builtin_amdgcn_alignbyte(d[m + 1], d[m], sh);
-            const int keep = min(max(n - 4 * m, 0), 4);  // bytes of this dword inside the row
-            v = keep >= 4 ? v : (keep == 0 ? 0u : (v & ((1u << (8 * keep)) - 1u)));
-            out[m] = (int)v;
-        }
-    }
-    *reinterpret_cast<v4i*>(j.dst + (size_t)r * (size_t)j.dst_pitch + 16 * c) = out;
-}
-
-__global__ __launch_bounds__(256) void pad_rows_kernel(PadJob j0, PadJob j1) {
-    const size_t total = j0.chunks + j1.chunks;
-    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (size_t)gridDim.x * 256) {
-        if (i < j0.chunks) pad_chunk(j0, i);
-        else pad_chunk(j1, i - j0.chunks);
-    }
-}
-
-hipError_t launch_pad_rows(const uint8_t* src0, uint8_t* dst0, int rows0, int dst_rows0, int src_pitch0, int len0,
-                           int dst_pitch0, const uint8_t* src1, uint8_t* dst1, int rows1, int dst_rows1,
-                           int src_pitch1, int len1, int dst_pitch1, hipStream_t st) {
-    if (dst_pitch0 % 16 != 0 || (uintptr_t)dst0 % 16 != 0 || len0 > dst_pitch0 || rows0 > dst_rows0 ||
-        (dst1 && (dst_pitch1 % 16 != 0 || (uintptr_t)dst1 % 16 != 0 || len1 > dst_pitch1 || rows1 > dst_rows1)))
-        return hipErrorInvalidValue;
-    const PadJob j0{src0, dst0, rows0, dst_rows0, src_pitch0, len0, dst_pitch0,
-                    (size_t)dst_rows0 * (size_t)dst_pitch0 / 16};
-    const PadJob j1{src1, dst1, rows1, dst_rows1, src_pitch1, len1, dst_pitch1,
-                    dst1 ? (size_t)dst_rows1 * (size_t)dst_pitch1 / 16 : 0};
-    const size_t total = j0.chunks + j1.chunks;
-    if (total == 0) return hipSuccess;
-    const unsigned blocks = (unsigned)std::min<size_t>((total + 255) / 256, 8192);
-    hipLaunchKernelGGL(pad_rows_kernel, dim3(blocks), dim3(256), 0, st, j0, j1);
-    return hipGetLastError();
-}
-
-hipError_t launch_dequant(const int32_t* C, const OutScale& os, int M, int N, hipStream_t st) {
-    const size_t n = (size_t)M * (size_t)N;
-    if (n == 0) return hipSuccess;
-    const int vec = ((uintptr_t)C % 16 == 0) && ((uintptr_t)os.Y % 16 == 0);
-    const size_t items = n / 4;
-    hipLaunchKernelGGL(dequant_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, st, C, os, N, items, vec);
-    return hipGetLastError();
-}
-
-hipError_t launch_quantize_rows(const float* X, int8_t* Q, float* row_scale, int M, int K, hipStream_t st) {
-    if (M == 0) return hipSuccess;
-    const int vec = (K % 16 == 0) && ((uintptr_t)X % 16 == 0) && ((uintptr_t)Q % 16 == 0);
-    hipLaunchKernelGGL(quantize_rows_kernel, dim3((unsigned)M), dim3(256), 0, st, X, Q, row_scale, K, vec);
-    return hipGetLastError();
-}
-
-hipError_t launch_naive(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, hipStream_t st) {
-    const dim3 grid((N + 63) / 64, (M + 3) / 4);
-    hipLaunchKernelGGL(naive_kernel, grid, dim3(256), 0, st, A, B, C, M, K, N);
     return hipGetLastError();
 }
 
