@@ -83,6 +83,16 @@ hipError_t validate(const void* dA, const void* dB, const void* dC, int64_t M, i
 // Split-K plan of the skinny kernels: tb (64- or 128-byte column slab per wave), kw (waves per slab
 // inside a workgroup of 4 waves), `splits` workgroups along K (splits > 1 adds the partial-sum
 // reduce launch) with sps k-steps each.
+// Experiment switches, read once per process (a lookup per call would cost host time on every launch).
+const char* skinny_plan_env() {  // "tb,kw,splits": forces the skinny split plan
+    static const char* const e = std::getenv("TERNIX_SKINNY_PLAN");
+    return e;
+}
+const char* skinny_wave_env() {  // "sw,nsw,splits" forces a wave-kernel plan, "0" turns it off
+    static const char* const e = std::getenv("TERNIX_SKINNY_WAVE");
+    return e;
+}
+
 // Split count whose partial sums stay within 4 MiB: allowed whatever the weight size (small N).
 long partials_floor(int M, int N) { return (4L << 20) / std::max(1L, 4L * M * N); }
 
@@ -105,7 +115,7 @@ SkinnyPlan plan_skinny_dma(int M, int K, int N, int ns) {
     int sps = (int)((nsteps + splits - 1) / splits);
     while (col_wgs * ((nsteps + sps - 1) / sps) > std::max(cus, col_wgs)) ++sps;  // no second wave
     SkinnyPlan p{1, 1, (nsteps + sps - 1) / sps, sps, ns};
-    if (const char* env = std::getenv("TERNIX_SKINNY_PLAN")) {  // experiments: "tb,kw,splits"
+    if (const char* env = skinny_plan_env()) {  // experiments: "tb,kw,splits"
         int etb = 0, ekw = 0, esp = 0;
         if (std::sscanf(env, "%d,%d,%d", &etb, &ekw, &esp) == 3 && esp >= 1) {
             p.sps = (nsteps + esp - 1) / esp;
@@ -145,7 +155,7 @@ SkinnyPlan plan_skinny(int M, int K, int N, bool generic = false) {
         if (splits > 1) p.splits = (int)splits;
     }
     // Tuning override for experiments: TERNIX_SKINNY_PLAN="tb,kw,splits".
-    if (const char* env = std::getenv("TERNIX_SKINNY_PLAN")) {
+    if (const char* env = skinny_plan_env()) {
         int etb = 0, ekw = 0, esp = 0;
         if (std::sscanf(env, "%d,%d,%d", &etb, &ekw, &esp) == 3 && (etb == 1 || etb == 2) &&
             (ekw == 1 || ekw == 2 || ekw == 4) && esp >= 1) {
@@ -203,7 +213,7 @@ hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
         int sw = 16, nsw = 2, sp = 0;
         if (K <= 4096) sp = 1;
         else if (M > 4) sp = std::max(2, std::min(16, nsteps / 21));
-        if (const char* env = std::getenv("TERNIX_SKINNY_WAVE")) {
+        if (const char* env = skinny_wave_env()) {
             int esw = 0, ensw = 0, esp = 0;
             if (std::sscanf(env, "%d,%d,%d", &esw, &ensw, &esp) == 3 && esp >= 1 &&
                 ternix_hip::skinny_wave_ok(dA, dB, M, K, N, esw)) {
