@@ -44,7 +44,8 @@ def parse():
                     help="untimed sustained load before each GPU measurement (clock ramp)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["all", "gemv", "gemm", "bigm1", "pack", "layer", "ffn", "configs"], default="all")
+    ap.add_argument("--only", choices=["all", "gemv", "gemm", "bigm1", "pack", "layer", "ffn", "configs", "tile64"],
+                    default="all")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run 4 device-to-device copies of 256 MiB (the runtime's copy kernel), the "
                          "known-size reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -362,6 +363,66 @@ def bench_configs(args, stream, lib):
     return out
 
 
+def to_tile64(prob, lib):
+    """Convert the problem's weight copies to the tile-64 layout on the device (untimed)."""
+    from ternixengine_amd import hip_runtime as hr
+    c = prob.case
+    tiled = []
+    for d in prob.dW:
+        t = hr.DeviceBuffer(c.K * c.N // 4)
+        st = lib.ternix_hip_interleave_weights_tile64(t.value, d.value, c.K, c.N, None)
+        if st != 0:
+            raise RuntimeError(f"tile-64 conversion failed: {st}")
+        tiled.append(t)
+    hr.synchronize()
+    prob.dW = tiled
+
+
+TILE64_CASES = ["cfg1", "cfg2_up", "cfg2_down", "cfg3_m4_up", "cfg3_m4_down", "cfg3_m16_up", "cfg3_m16_down",
+                "cfg3_m64_up", "cfg3_m64_down", "cfg5_big_m1", "cfg4_4096x4096"]
+
+
+def bench_tile64(args, stream, lib):
+    """The opt-in tile-64 weight layout (ternix_hip_mul_mat_ternary_tile64) on the headline pair and on
+    the decode-shaped configurations, measured exactly like the contract-layout numbers (same cold
+    weight pools, graphs, prewarm) and checked against the same digests."""
+    from ternixengine_amd import configs
+    fn = lib.ternix_hip_mul_mat_ternary_tile64
+    up, down = configs.CASES["cfg2_up"], configs.CASES["cfg2_down"]
+    pair_w = up.K * up.N // 4 + down.K * down.N // 4
+    copies = max(2, -(-POOL_MIN_BYTES // pair_w))
+    pu, pd = Problem(up, copies), Problem(down, copies)
+    to_tile64(pu, lib)
+    to_tile64(pd, lib)
+
+    def step(i):
+        launch(fn, pu, i % copies, stream)
+        launch(fn, pd, i % copies, stream)
+
+    prewarm(step, args.prewarm_s, stream)
+    ms = time_launches(step, args.steps, args.warmup, stream)
+    ok = verify(pu) and verify(pd)
+    bytes_step = up.bytes_algorithmic + down.bytes_algorithmic
+    out = {"gemv_pair_gbs": round(bytes_step / (ms / args.steps * 1e-3) / 1e9, 2),
+           "gemv_pair_ms_per_step": round(ms / args.steps, 5), "verified": ok, "configs": []}
+    del pu, pd
+    for name in TILE64_CASES:
+        case = configs.CASES[name]
+        w = case.K * case.N // 4
+        cp = min(64, max(2, -(-POOL_MIN_BYTES // w)))
+        p = Problem(case, cp)
+        to_tile64(p, lib)
+        steps = 20 if case.ops > 1e11 else 60
+        prewarm(lambda i: launch(fn, p, i % cp, stream), 0.1, stream)
+        ms = time_launches(lambda i: launch(fn, p, i % cp, stream), steps, 3, stream)
+        us = ms / steps * 1e3
+        out["configs"].append({"name": name, "us": round(us, 2),
+                               "gbs": round(case.bytes_algorithmic / (us * 1e-6) / 1e9, 1),
+                               "tops": round(case.ops / (us * 1e-6) / 1e12, 1), "verified": verify(p)})
+        del p
+    return out
+
+
 def cpu_baseline(seconds):
     """Reference avx2_blocked (oracle/_ref) or the oracle's restatement, one thread, on the cfg2 pair."""
     from ternixengine_amd import configs
@@ -465,6 +526,8 @@ def main():
         res["ffn"] = bench_ffn(args, stream, lib)
     if args.only in ("all", "configs"):
         res["configs"] = bench_configs(args, stream, lib)
+    if args.only in ("all", "tile64"):
+        res["tile64"] = bench_tile64(args, stream, lib)
     g = res.get("gemv")
     line = {
         "metric": METRIC,
@@ -515,6 +578,8 @@ def main():
         line["ffn_decode"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in res["ffn"].items()}
     if "configs" in res:
         line["all_configs"] = res["configs"]
+    if "tile64" in res:
+        line["tile64_layout"] = res["tile64"]
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
         line["cpu_baseline"]["value"] = round(line["cpu_baseline"]["value"], 3)

@@ -119,6 +119,14 @@ void ternix_unpack_ternary_weights(int8_t* unpacked, const uint8_t* packed, size
 /* interleave_weights_offline (reference src/bitpack.cpp:29-33): identity copy
  * of size/4 bytes (the K x N/4 layout is consumed as is by every kernel). */
 void ternix_interleave_weights_offline(uint8_t* interleaved, const uint8_t* packed, size_t size);
+/* Opt-in pre-permuted layout ("tile-64"), the MI355X form of the offline
+ * interleave the reference reserves (src/bitpack.cpp:29-33 keeps it the identity;
+ * no reference kernel reads a permuted layout).  The K x N/4 packed matrix is cut
+ * into 16-byte column strips c (64 weight columns) and 64-row k-steps s; block
+ * (c, s) is 1 KB at byte offset (c * K/64 + s) * 1024 and holds row r of the step
+ * at 16-byte position r ^ (8 * ((r / 16) % 2)).  Requires K % 64 == 0,
+ * (N/4) % 16 == 0, out != packed; returns 0, or 1 (hipErrorInvalidValue). */
+int ternix_interleave_weights_tile64(uint8_t* out, const uint8_t* packed, size_t K, size_t N);
 
 /* ---- quantised layer boundary (BitNet b1.58 scheme; no reference counterpart: the
  *      reference leaves weight and activation quantisation as a stub, scripts/quantize.py:5,
@@ -200,6 +208,16 @@ int ternix_hip_unpack_ternary_weights(int8_t* dW, const uint8_t* dPacked, size_t
 /* interleave_weights_offline on device memory (reference src/bitpack.cpp:29-33):
  * the identity, a device-to-device copy of size/4 bytes (none when dOut == dPacked). */
 int ternix_hip_interleave_weights_offline(uint8_t* dOut, const uint8_t* dPacked, size_t size, void* stream);
+/* ternix_interleave_weights_tile64 on device memory (one coalesced permutation copy);
+ * K % 64 == 0, (N/4) % 16 == 0, 16-byte aligned, dOut != dPacked, K * N/4 < 2^32. */
+int ternix_hip_interleave_weights_tile64(uint8_t* dOut, const uint8_t* dPacked, int64_t K, int64_t N, void* stream);
+/* ternix_hip_mul_mat_ternary on tile-64 weights dWt (same C = A x W, same status
+ * contract); K % 128 == 0, N % 256 == 0, dA and dWt 16-byte aligned, K * N/4 < 2^32.
+ * Each wave's weight read is one contiguous 1 KB block, which the LDS transposing
+ * reads consume without a swizzle: the decode-shaped calls (M <= 32) run faster than
+ * on the row-major layout. */
+int ternix_hip_mul_mat_ternary_tile64(const int8_t* dA, const uint8_t* dWt, int32_t* dC, int64_t M, int64_t K,
+                                      int64_t N, void* stream);
 
 #ifdef __cplusplus
 }

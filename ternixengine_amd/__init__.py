@@ -16,6 +16,10 @@ RuntimeError("HIP error: ...") for device errors.  The GIL is released during de
 Device-pointer access (no copies) is `mul_mat_ternary(dA, dB, dC, M, K, N, stream=None, path="auto")`
 with integer device addresses, mirroring the C-ABI in include/ternix/ternix_hip.h; the weight format
 on device memory is `pack_ternary_device` / `unpack_ternary_device`.
+
+Opt-in pre-permuted weights: `interleave_tile64(packed)` (host) / `interleave_tile64_device` rewrite the
+(K, N/4) packed matrix as 1 KB blocks of 64 k-rows x 16 bytes, which `ternary_matmul_tile64` and
+`mul_mat_ternary(..., path="tile64")` consume (same results, faster decode-shaped calls).
 """
 import ctypes
 
@@ -26,14 +30,14 @@ from ._lib import LibraryNotBuilt, load as _load  # noqa: F401
 
 __all__ = ["pack_ternary", "unpack_ternary", "ternary_matmul", "mul_mat_ternary", "pack_ternary_device",
            "unpack_ternary_device", "quantize_weights_absmean", "quantize_activations", "ternary_matmul_dequant", "rms_norm", "swiglu",
-           "ffn_forward",
+           "ffn_forward", "interleave_tile64", "interleave_tile64_device", "ternary_matmul_tile64",
            "has_cuda", "has_hip", "HIP_IMPLS", "ternix_error"]
 
 has_cuda = False
 HIP_IMPLS = {"hip": 0, "hip_naive": 1, "hip_gemv": 2, "hip_gemm": 3, "hip_tiled": 4}
 _PATHS = {"auto": "ternix_hip_mul_mat_ternary", "gemv": "ternix_hip_mul_mat_ternary_gemv",
           "gemm": "ternix_hip_mul_mat_ternary_gemm", "tiled": "ternix_hip_mul_mat_ternary_tiled",
-          "naive": "ternix_hip_mul_mat_ternary_naive"}
+          "naive": "ternix_hip_mul_mat_ternary_naive", "tile64": "ternix_hip_mul_mat_ternary_tile64"}
 
 
 def _has_hip():
@@ -166,6 +170,44 @@ def ternary_matmul_dequant(a, b_packed, row_scale, w_scale):
         raise RuntimeError(f"HIP error: {ternix_error(status)}")
     hr.synchronize()
     return dy.download(np.float32, (m, n))
+
+
+def interleave_tile64(packed):
+    """(K, N/4) packed weights -> the same bytes in the tile-64 layout (flat uint8, K*N/4 bytes):
+    block (strip c, k-step s) of 64 rows x 16 bytes at (c * K/64 + s) * 1024, row r of the step at
+    16-byte position r ^ (8 * ((r / 16) % 2)).  Needs K % 64 == 0 and (N/4) % 16 == 0."""
+    p = np.ascontiguousarray(np.asarray(packed).astype(np.uint8, copy=False))
+    if p.ndim != 2:
+        raise ValueError("interleave_tile64 expects a 2-D (K, N/4) array")
+    k, nb = p.shape
+    out = np.empty(k * nb, dtype=np.uint8)
+    if _load().ternix_interleave_weights_tile64(_ptr(out), _ptr(p), k, nb * 4) != 0:
+        raise ValueError("interleave_tile64 needs K % 64 == 0 and (N/4) % 16 == 0")
+    return out
+
+
+def interleave_tile64_device(d_out, d_packed, K, N, stream=None):
+    """Device-memory tile-64 conversion (asynchronous on `stream`); returns the hipError_t status."""
+    return _load().ternix_hip_interleave_weights_tile64(d_out, d_packed, int(K), int(N), stream)
+
+
+def ternary_matmul_tile64(a, w_tile64, n):
+    """C = A (M,K int8) @ W on the GPU, W given in the tile-64 layout (interleave_tile64) with N
+    columns -> (M, N) int32.  Needs K % 128 == 0 and N % 256 == 0."""
+    from . import hip_runtime as hr
+    a = np.ascontiguousarray(np.asarray(a).astype(np.int8, copy=False))
+    wt = np.ascontiguousarray(np.asarray(w_tile64).astype(np.uint8, copy=False)).reshape(-1)
+    if a.ndim != 2:
+        raise ValueError("A must be (M, K)")
+    m, k = a.shape
+    n = int(n)
+    if n % 4 != 0 or wt.size != k * (n // 4):
+        raise ValueError("w_tile64 must hold K * N/4 bytes")
+    da, dw = hr.DeviceBuffer.from_array(a), hr.DeviceBuffer.from_array(wt)
+    dc = hr.DeviceBuffer(max(4 * m * n, 4))
+    _check(_load().ternix_hip_mul_mat_ternary_tile64(da.value, dw.value, dc.value, m, k, n, None))
+    hr.synchronize()
+    return dc.download(np.int32, (m, n))
 
 
 def _check(status):

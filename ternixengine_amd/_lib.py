@@ -28,7 +28,8 @@ def load():
     i8p = ctypes.c_void_p
     i64 = ctypes.c_int64
     for name in ("ternix_hip_mul_mat_ternary", "ternix_hip_mul_mat_ternary_gemv", "ternix_hip_mul_mat_ternary_gemm",
-                 "ternix_hip_mul_mat_ternary_tiled", "ternix_hip_mul_mat_ternary_naive"):
+                 "ternix_hip_mul_mat_ternary_tiled", "ternix_hip_mul_mat_ternary_naive",
+                 "ternix_hip_mul_mat_ternary_tile64"):
         f = getattr(lib, name)
         f.argtypes = [i8p, i8p, i8p, i64, i64, i64, ctypes.c_void_p]
         f.restype = ctypes.c_int
@@ -47,6 +48,10 @@ def load():
         f.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
         f.restype = ctypes.c_int
     vp = ctypes.c_void_p
+    lib.ternix_interleave_weights_tile64.argtypes = [vp, vp, ctypes.c_size_t, ctypes.c_size_t]
+    lib.ternix_interleave_weights_tile64.restype = ctypes.c_int
+    lib.ternix_hip_interleave_weights_tile64.argtypes = [vp, vp, i64, i64, vp]
+    lib.ternix_hip_interleave_weights_tile64.restype = ctypes.c_int
     lib.ternix_hip_quantize_activations.argtypes = [vp, vp, vp, i64, i64, vp]
     lib.ternix_hip_quantize_activations.restype = ctypes.c_int
     lib.ternix_hip_mul_mat_ternary_dequant.argtypes = [vp, vp, vp, i64, i64, i64, vp, ctypes.c_float, vp]

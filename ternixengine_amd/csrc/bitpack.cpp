@@ -106,4 +106,19 @@ void ternix_interleave_weights_offline(uint8_t* interleaved, const uint8_t* pack
     ternix::interleave_weights_offline(interleaved, packed, size);
 }
 
+int ternix_interleave_weights_tile64(uint8_t* out, const uint8_t* packed, size_t K, size_t N) {
+    const size_t NB = N / 4;
+    if (N % 4 != 0 || K % 64 != 0 || NB % 16 != 0) return 1;  // hipErrorInvalidValue
+    if (K * NB == 0) return 0;
+    if (out == nullptr || packed == nullptr || out == packed) return 1;
+    const size_t nK = K / 64, strips = NB / 16;
+    for (size_t r = 0; r < K; ++r)
+        for (size_t c = 0; c < strips; ++c) {
+            // block (c, r / 64), row position r % 64 ^ (8 * ((r % 64 / 16) % 2)), 16 bytes per row
+            const size_t rr = r % 64, pos = rr ^ (((rr >> 4) & 1) << 3);
+            std::memcpy(out + ((c * nK + r / 64) * 64 + pos) * 16, packed + r * NB + c * 16, 16);
+        }
+    return 0;
+}
+
 }  // extern "C"

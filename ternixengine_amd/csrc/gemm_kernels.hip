@@ -236,7 +236,7 @@ template <int BM, int WGN, int NS, int BK>
 __global__ __launch_bounds__(GF_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
 void gemm_fast_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ B, int32_t* __restrict__ C, int M,
                       int K, int N, int tiles_n, int k_begin, int k_end, int accumulate, int vec_store,
-                      int k_split, OutScale os) {
+                      int k_split, OutScale os, int tiled) {
     if (gridDim.y > 1) {  // split-K: this workgroup's k-range, partial tile in slab blockIdx.y
         k_begin += (int)blockIdx.y * k_split;
         k_end = min(k_end, k_begin + k_split);
@@ -306,7 +306,8 @@ void gemm_fast_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ 
     for (int p = 0; p < NW; ++p) {
         const int slot = (p * 8 + wave) * 64 + lane;
         const int r = slot >> 2, pos = slot & 3;
-        w_off[p] = (uint32_t)r * (uint32_t)NB + (uint32_t)(bc0 + (pos ^ gf_swz_w(r)) * 16);
+        w_off[p] = tiled ? tile64_offset((bc0 >> 4) + (pos ^ gf_swz_w(r)), r, K >> 6)
+                         : (uint32_t)r * (uint32_t)NB + (uint32_t)(bc0 + (pos ^ gf_swz_w(r)) * 16);
     }
     auto issue = [&](int st, int buf) {
         const int sc = min(st, nst - 1);  // clamped: keeps the per-stage load count static
@@ -314,7 +315,8 @@ void gemm_fast_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ 
         int8_t* adst = stage_a(buf);
 #pragma unroll
         for (int p = 0; p < NA; ++p) lds_dma16(abase + a_off[p], adst + (p * 8 + wave) * 1024);
-        const uint8_t* wbase = B + (size_t)(k_begin + sc * BK) * (size_t)NB;
+        const uint8_t* wbase = tiled ? B + (size_t)((k_begin + sc * BK) >> 6) * 1024
+                                     : B + (size_t)(k_begin + sc * BK) * (size_t)NB;
         uint8_t* wdst = stage_w(buf);
 #pragma unroll
         for (int p = 0; p < NW; ++p) lds_dma16(wbase + w_off[p], wdst + (p * 8 + wave) * 1024);
@@ -443,7 +445,7 @@ template <int BM, int WGN, int NS, int BK, int NWV, int BNB>
 __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2)))
 void gemm_pipe_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ B, int32_t* __restrict__ C, int M,
                       int K, int N, int tiles_n, int k_begin, int k_end, int accumulate, int vec_store,
-                      int k_split, OutScale os) {
+                      int k_split, OutScale os, int tiled) {
     if (gridDim.y > 1) {  // split-K: this workgroup's k-range, partial tile in slab blockIdx.y
         k_begin += (int)blockIdx.y * k_split;
         k_end = min(k_end, k_begin + k_split);
@@ -509,7 +511,8 @@ void gemm_pipe_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ 
     for (int p = 0; p < NW; ++p) {
         const int slot = (p * NWV + wave) * 64 + lane;
         const int r = slot / CW, pos = slot % CW;
-        w_off[p] = (uint32_t)r * (uint32_t)NB + (uint32_t)(bc0 + (pos ^ swz_w<BNB>(r)) * 16);
+        w_off[p] = tiled ? tile64_offset((bc0 >> 4) + (pos ^ swz_w<BNB>(r)), r, K >> 6)
+                         : (uint32_t)r * (uint32_t)NB + (uint32_t)(bc0 + (pos ^ swz_w<BNB>(r)) * 16);
     }
     auto issue = [&](int st, int buf) {
         const int sc = min(st, nst - 1);
@@ -517,7 +520,8 @@ void gemm_pipe_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ 
         int8_t* adst = stage_a(buf);
 #pragma unroll
         for (int p = 0; p < NA; ++p) lds_dma16(abase + a_off[p], adst + (p * NWV + wave) * 1024);
-        const uint8_t* wbase = B + (size_t)(k_begin + sc * BK) * (size_t)NB;
+        const uint8_t* wbase = tiled ? B + (size_t)((k_begin + sc * BK) >> 6) * 1024
+                                     : B + (size_t)(k_begin + sc * BK) * (size_t)NB;
         uint8_t* wdst = stage_w(buf);
 #pragma unroll
         for (int p = 0; p < NW; ++p) lds_dma16(wbase + w_off[p], wdst + (p * NWV + wave) * 1024);
@@ -702,7 +706,7 @@ bool gemm_narrow_ok(int M, int K, int N, int k_len, int splits, int k_split) {
 }
 
 hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int k_begin, int k_end,
-                       int accumulate, hipStream_t st, const OutScale& os, int splits, int k_split) {
+                       int accumulate, hipStream_t st, const OutScale& os, int splits, int k_split, int tiled) {
     const int NB = N >> 2;
     // Experiment switches, read once per process.
     static const char* const force_generic = std::getenv("TERNIX_GEMM_GENERIC");
@@ -711,7 +715,10 @@ hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int
                       (splits == 1 || k_split % GF_BK == 0) &&
                       (NB % GF_BNB == 0) && ((uintptr_t)A % 16 == 0) && ((uintptr_t)B % 16 == 0) &&
                       k_end > k_begin && (size_t)M * (size_t)K < ((size_t)1 << 32) &&
-                      (size_t)GF_BK * (size_t)NB < ((size_t)1 << 32) && !(force_generic && force_generic[0] == '1');
+                      (size_t)GF_BK * (size_t)NB < ((size_t)1 << 32) &&
+                      (tiled || !(force_generic && force_generic[0] == '1'));
+    // The tile-64 layout is read by the LDS-DMA GEMMs only (whole 128-row stages, at most 4 GiB of W).
+    if (tiled && (!fast || (size_t)K * (size_t)NB >= ((size_t)1 << 32))) return hipErrorInvalidValue;
     if (fast) {
         const int vs = ((uintptr_t)(os.Y ? (const void*)os.Y : (const void*)C) % 16) == 0;
         const int tiles_n = NB / GF_BNB;
@@ -747,7 +754,7 @@ hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int
             // split where the 256-column tiles would need one; one m-tile per wave, 256-deep stages.
             const dim3 gridn((unsigned)(((M + 63) / 64) * (NB / 16)), splits);
             hipLaunchKernelGGL((gemm_pipe_kernel<64, 1, 3, 256, 4, 16>), gridn, dim3(256), 0, st, A, B, C, M, K, N,
-                               NB / 16, k_begin, k_end, accumulate, vs, k_split, os);
+                               NB / 16, k_begin, k_end, accumulate, vs, k_split, os, tiled);
             return hipGetLastError();
         }
         // One round of 128-row tiles with a short k-range (cfg4 4096^2): two co-resident workgroups
@@ -761,13 +768,13 @@ hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int
             // byte is spent on padding rows; the caller splits K to fill the chip.
             const dim3 grid64((unsigned)(((M + 63) / 64) * tiles_n), splits);
             hipLaunchKernelGGL((gemm_pipe_kernel<64, 4, 3, 128, 4, 64>), grid64, dim3(256), 0, st, A, B, C, M, K, N,
-                               tiles_n, k_begin, k_end, accumulate, vs, k_split, os);
+                               tiles_n, k_begin, k_end, accumulate, vs, k_split, os, tiled);
             return hipGetLastError();
         }
         if (pipe) {
 #define TX_GP_LAUNCH(BM_, WGN_, NS_, BK_)                                                                      \
     hipLaunchKernelGGL((gemm_pipe_kernel<BM_, WGN_, NS_, BK_, 8, GF_BNB>), grid, dim3(GF_THREADS), 0, st, A, B, C, M, \
-                       K, N, tiles_n, k_begin, k_end, accumulate, vs, k_split, os)
+                       K, N, tiles_n, k_begin, k_end, accumulate, vs, k_split, os, tiled)
             if (bk == 256 && wgn == 4) TX_GP_LAUNCH(128, 4, 3, 256);
             else if (bk == 256) TX_GP_LAUNCH(128, 2, 3, 256);
             else if (wgn == 4 && pipe_ns == 4) TX_GP_LAUNCH(128, 4, 4, 128);
@@ -779,7 +786,7 @@ hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int
         }
 #define TX_GF_LAUNCH(BM_, WGN_, NS_, BK_)                                                                         \
     hipLaunchKernelGGL((gemm_fast_kernel<BM_, WGN_, NS_, BK_>), grid, dim3(GF_THREADS), 0, st, A, B, C, M, K, N, \
-                       tiles_n, k_begin, k_end, accumulate, vs, k_split, os)
+                       tiles_n, k_begin, k_end, accumulate, vs, k_split, os, tiled)
         if (bm == 256 && wgn == 4) TX_GF_LAUNCH(256, 4, 3, 128);
         else if (bm == 256) TX_GF_LAUNCH(256, 2, 3, 128);
         else if (bk == 256 && wgn == 4) TX_GF_LAUNCH(128, 4, 3, 256);

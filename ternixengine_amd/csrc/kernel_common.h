@@ -206,5 +206,15 @@ __device__ __forceinline__ uint32_t lds_u32(const void* p) {
     return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
 }
 
+// Tile-64 weight layout (opt-in, written by ternix_hip_interleave_weights): the K x NB packed matrix
+// as 1 KB blocks of 64 k-rows x 16 bytes; block (strip c, k-step s) starts at byte (c * K/64 + s) * 1024
+// and row r of the block sits at 16-byte position r ^ (8 * ((r / 16) % 2)) (the map is its own
+// inverse).  A wave's 64-lane DMA of one block is 1 KB contiguous and lands in LDS already in the
+// bank-spread order the transposing reads want.
+__device__ __forceinline__ int tile64_pos(int r) { return r ^ (((r >> 4) & 1) << 3); }
+__device__ __forceinline__ uint32_t tile64_offset(int strip, int row, int nK) {
+    return ((uint32_t)strip * (uint32_t)nK + (uint32_t)(row >> 6)) * 1024u + (uint32_t)tile64_pos(row & 63) * 16u;
+}
+
 }  // namespace
 }  // namespace ternix_hip

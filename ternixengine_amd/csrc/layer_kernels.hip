@@ -111,6 +111,16 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const float* __restr
     }
 }
 
+// Tile-64 layout conversion (kernel_common.h): a permutation copy, one 16-byte chunk per thread,
+// read row-major (coalesced) and written to its block position.
+__global__ __launch_bounds__(256) void tile64_kernel(const uint8_t* __restrict__ W, uint8_t* __restrict__ Wt,
+                                                     int nK, int strips, size_t chunks) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < chunks; i += (size_t)gridDim.x * 256) {
+        const int r = (int)(i / (size_t)strips), c = (int)(i % (size_t)strips);
+        *reinterpret_cast<v4i*>(Wt + tile64_offset(c, r, nK)) = *reinterpret_cast<const v4i*>(W + i * 16);
+    }
+}
+
 }  // namespace
 
 hipError_t launch_zero(int32_t* C, size_t n, hipStream_t st) {
@@ -210,6 +220,18 @@ hipError_t launch_quantize_rows(const float* X, int8_t* Q, float* row_scale, int
     if (M == 0) return hipSuccess;
     const int vec = (K % 16 == 0) && ((uintptr_t)X % 16 == 0) && ((uintptr_t)Q % 16 == 0);
     hipLaunchKernelGGL(quantize_rows_kernel, dim3((unsigned)M), dim3(256), 0, st, X, Q, row_scale, K, vec);
+    return hipGetLastError();
+}
+
+hipError_t launch_tile64(const uint8_t* W, uint8_t* Wt, int K, int N, hipStream_t st) {
+    const int NB = N >> 2;
+    if (K % 64 != 0 || NB % 16 != 0 || (uintptr_t)W % 16 != 0 || (uintptr_t)Wt % 16 != 0 ||
+        (size_t)K * (size_t)NB >= ((size_t)1 << 32))
+        return hipErrorInvalidValue;
+    const size_t chunks = (size_t)K * (size_t)NB / 16;
+    if (chunks == 0) return hipSuccess;
+    const unsigned blocks = (unsigned)std::min<size_t>((chunks + 255) / 256, 16384);
+    hipLaunchKernelGGL(tile64_kernel, dim3(blocks), dim3(256), 0, st, W, Wt, K / 64, NB / 16, chunks);
     return hipGetLastError();
 }
 

@@ -67,6 +67,7 @@ struct SkinnyArgs {
     float* rs_out;
     int n_out;            // skinny_wave_kernel, store mode: C / os.Y has n_out <= N columns (0: N)
     int line_units;       // skinny_wave_kernel: block -> strip mapping by 128-byte line units
+    int tiled;            // skinny_wave_kernel: W in the tile-64 layout (kernel_common.h)
 };
 
 // One k-step of MFMA work for one 16-row x 4-byte-column block: raw[r] is the dword of row r.
@@ -890,10 +891,14 @@ void skinny_wave_kernel(SkinnyArgs args) {
     v4i a_ring[NSW];
     auto issue = [&](int it, int slot_c, v4i& a_dst) {
         const int s = min(s_begin + wave + 4 * it, s_last);
-        const uint8_t* wbase = B + (size_t)s * 64 * (size_t)NB;
         uint8_t* dst = ring + slot_c * SLOT;
+        if (SW == 16 && args.tiled) {  // one contiguous 1 KB block, already in LDS order
+            lds_dma16(B + ((size_t)cx * (size_t)(K >> 6) + (size_t)s) * 1024 + lane * 16, dst);
+        } else {
+            const uint8_t* wbase = B + (size_t)s * 64 * (size_t)NB;
 #pragma unroll
-        for (int p = 0; p < NL; ++p) lds_dma16(wbase + w_off[p], dst + p * 1024);
+            for (int p = 0; p < NL; ++p) lds_dma16(wbase + w_off[p], dst + p * 1024);
+        }
         if constexpr (AQ == 0) a_dst = *reinterpret_cast<const v4i*>(a_row + (size_t)s * 64);
     };
     // AQ > 0 (one launch, whole rows): every workgroup quantises its m-group's fp32 rows itself (the
@@ -1284,7 +1289,8 @@ bool skinny_wave_ok(const int8_t* A, const uint8_t* B, int M, int K, int N, int 
 
 hipError_t launch_skinny_wave(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int sw, int nsw,
                               int splits, int steps_per_split, int32_t* partials, hipStream_t st, const OutScale& os,
-                              int n_out, const ActQuant& aq) {
+                              int n_out, const ActQuant& aq, int tiled) {
+    if (tiled && (sw != 16 || n_out > 0)) return hipErrorInvalidValue;
     if (!skinny_wave_ok(A, B, M, K, N, sw) || nsw < 2 || nsw > 4 || steps_per_split < 1) return hipErrorInvalidValue;
     // Fused activation quantisation: one launch over whole rows (K <= 4096), 16-byte strips, 2 slots.
     if (aq.mode != 0 && (splits != 1 || K > 4096 || sw != 16 || nsw != 2 || n_out > 0 || aq.X == nullptr ||
@@ -1303,6 +1309,7 @@ hipError_t launch_skinny_wave(const int8_t* A, const uint8_t* B, int32_t* C, int
     SkinnyArgs a{A, B, C, partials, M, K, N, steps_per_split, splits, mode, vec_store, 1, 1,
                  mode == SK_STORE ? os : OutScale{}};
     a.n_out = n_out;
+    a.tiled = tiled;
     a.X = aq.X;
     a.G = aq.G;
     a.eps = aq.eps;

@@ -74,8 +74,10 @@ int device_cu_count();
 bool skinny_wave_ok(const int8_t* A, const uint8_t* B, int M, int K, int N, int sw);
 hipError_t launch_skinny_wave(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int sw, int nsw,
                               int splits, int steps_per_split, int32_t* partials, hipStream_t st,
-                              const OutScale& os = OutScale{}, int n_out = 0, const ActQuant& aq = ActQuant{});
-// (n_out > 0: a padded problem -- C / os.Y has n_out <= N columns; not with the atomic mode.
+                              const OutScale& os = OutScale{}, int n_out = 0, const ActQuant& aq = ActQuant{},
+                              int tiled = 0);
+// (tiled != 0: W is in the tile-64 layout of launch_interleave_weights, sw must be 16.
+// n_out > 0: a padded problem -- C / os.Y has n_out <= N columns; not with the atomic mode.
 // aq set: the activations are quantised in the kernel from aq.X (splits == 1, K <= 4096, sw 16,
 // nsw 2); the dequantising epilogue then uses the kernel's own row scales.)
 // True when launch_gemm runs this M <= 64 shape on 64 x 64 tiles (K % 256 == 0, N/4 % 16 == 0, at
@@ -88,11 +90,16 @@ bool gemm_narrow_wanted(int M, int K, int N);
 // (accumulate must be 0 and os unset; launch_splitk_reduce finishes the sum).
 hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int k_begin,
                        int k_end, int accumulate, hipStream_t st, const OutScale& os = OutScale{}, int splits = 1,
-                       int k_split = 0);
+                       int k_split = 0, int tiled = 0);
+// (tiled != 0: W in the tile-64 layout; needs K % 128 == 0, N/4 % 64 == 0, aligned operands, k-ranges
+// of whole 128-row stages, K * N/4 < 2^32; hipErrorInvalidValue otherwise.)
 // C (or os.Y) = sum over `splits` slabs of P ([splits][M][N] int32).
 hipError_t launch_splitk_reduce(const int32_t* P, int32_t* C, int M, int N, int splits, const OutScale& os,
                                 hipStream_t st, int n_in = 0);
 // (n_in > N: the partials have n_in columns per row, of which the first N are summed into C.)
+// Tile-64 weight layout (opt-in; kernel_common.h): Wt = the K x N/4 packed W as 1 KB blocks of 64
+// k-rows x 16 bytes.  K % 64 == 0, N/4 % 16 == 0, 16-byte aligned, Wt != W.
+hipError_t launch_tile64(const uint8_t* W, uint8_t* Wt, int K, int N, hipStream_t st);
 // Padded copy of up to two row sets in one launch (ragged shapes): rows of len bytes at src_pitch
 // into dst rows of dst_pitch bytes (dst 16-byte aligned, dst_pitch % 16 == 0), zero-filled past len
 // and for rows rows..dst_rows-1.  dst1 == nullptr: one set only.

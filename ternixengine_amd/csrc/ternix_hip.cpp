@@ -194,25 +194,45 @@ int wave_max_m() {
     return m;
 }
 
+// K split of the wave-pipelined kernel (one workgroup per 16-byte strip, m-group and split): enough
+// workgroups for about 2.75 per CU, and for M <= 4 up to 7 per CU, one per 8 KB of weights (more
+// weight loads in flight per CU on the large decode matrices, where the extra partial sums cost
+// little); at least two k-steps per split.  Measured on MI355X with cold weights (512 MiB pools):
+// cfg2 up 9.35 -> 8.5 us against no split, cfg3 M=4 up 13.5 -> 12.0, tile-64 cfg5 big 17.8 -> 15.3.
+// TERNIX_WAVE_TARGET overrides the workgroup target (experiments).
+int wave_splits(int M, int K, int N) {
+    static const long env = [] {
+        const char* e = std::getenv("TERNIX_WAVE_TARGET");
+        return e ? std::atol(e) : 0L;
+    }();
+    const long nsteps = K / 64, units = (long)(N / 4 / 16) * ((M + 15) / 16), cus = cu_count();
+    long target = cus * 11 / 4;
+    if (M <= 4) target = std::max(target, std::min(7 * cus, (long)K * (N / 4) / 8192));
+    if (env > 0) target = env;
+    long sp = (target + units / 2) / std::max(1L, units);
+    sp = std::min(sp, std::max(1L, nsteps / 2));
+    return (int)std::max(1L, std::min(16L, sp));
+}
+
 hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int K, int N, hipStream_t st,
                       const ternix_hip::OutScale& os = ternix_hip::OutScale{},
                       const ternix_hip::ActQuant& aq = ternix_hip::ActQuant{}) {
     const bool generic = !(K % 64 == 0 && (N / 4) % 64 == 0 && reinterpret_cast<uintptr_t>(dB) % 16 == 0 &&
                            (aq.mode != 0 || reinterpret_cast<uintptr_t>(dA) % 16 == 0));
     // Wave-pipelined kernel (16-byte strips, 2 ring slots per wave), measured on MI355X against the
-    // DMA-staged kernel: with K <= 4096 in one launch, no K split and no reduce (cfg1 6.26 -> 5.64 us,
-    // cfg2 up 6.94 -> 6.29, cfg3 M=4 up 11.62 -> 10.41, M=16 up 14.27 -> 11.45); for 4 < M <= 16 with
-    // longer K, split about every 21 k-steps, whose partials are far fewer than the DMA kernel's
-    // (cfg3 M=16 down 14.59 -> 12.78 us).  TERNIX_SKINNY_WAVE="sw,nsw,splits" forces a plan, "0"
-    // turns the kernel off (experiments).
+    // DMA-staged kernel: faster for K <= 4096 (cfg1 6.26 -> 5.64 us, cfg2 up 6.94 -> 6.29, cfg3 M=4
+    // up 11.62 -> 10.41, M=16 up 14.27 -> 11.45) and for 4 < M <= 32 with longer K, whose partials
+    // are far fewer than the DMA kernel's (cfg3 M=16 down 14.59 -> 12.78 us); K split by wave_splits.
+    // M <= 4 with K > 4096 stays on the DMA kernel (cold cfg2 down 7.8 us against 9.0 at best).
+    // TERNIX_SKINNY_WAVE="sw,nsw,splits" forces a plan, "0" turns the kernel off (experiments).
     // With fused activation quantisation (K <= 4096) it quantises whole rows itself and dequantises with
     // its own row scales: the FFN block's gate/up GEMV becomes one launch.
     if (!generic && M <= wave_max_m() && ternix_hip::skinny_wave_ok(dA, dB, M, K, N, 16) &&
         (aq.mode == 0 || (K <= 4096 && M <= 16))) {
         const int nsteps = K / 64;
         int sw = 16, nsw = 2, sp = 0;
-        if (K <= 4096) sp = 1;
-        else if (M > 4) sp = std::max(2, std::min(16, nsteps / 21));
+        if (aq.mode != 0) sp = 1;
+        else if (K <= 4096 || M > 4) sp = wave_splits(M, K, N);
         if (const char* env = skinny_wave_env()) {
             int esw = 0, ensw = 0, esp = 0;
             if (std::sscanf(env, "%d,%d,%d", &esw, &ensw, &esp) == 3 && esp >= 1 &&
@@ -280,7 +300,7 @@ int gemm_splits(int M, int K, int N) {
 }
 
 hipError_t run_gemm(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int K, int N, hipStream_t st,
-                    const ternix_hip::OutScale& os = ternix_hip::OutScale{}) {
+                    const ternix_hip::OutScale& os = ternix_hip::OutScale{}, int tiled = 0) {
     if (K <= ternix_hip::kMaxKPerAccumulator) {
         int splits = gemm_splits(M, K, N);
         if (splits > 1) {
@@ -293,18 +313,19 @@ hipError_t run_gemm(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int
                                                                        : nullptr;
             if (partials) {
                 hipError_t e = ternix_hip::launch_gemm(dA, dB, partials, M, K, N, 0, K, 0, st, ternix_hip::OutScale{},
-                                                       splits, k_split);
+                                                       splits, k_split, tiled);
                 if (e != hipSuccess) return e;
                 return ternix_hip::launch_splitk_reduce(partials, dC, M, N, splits, os, st);
             }
         }
-        return ternix_hip::launch_gemm(dA, dB, dC, M, K, N, 0, K, 0, st, os);
+        return ternix_hip::launch_gemm(dA, dB, dC, M, K, N, 0, K, 0, st, os, 1, 0, tiled);
     }
     if (dC == nullptr) return hipErrorInvalidValue;  // scaled call without int scratch
     int acc = 0;
     for (long k0 = 0; k0 < K; k0 += ternix_hip::kMaxKPerAccumulator) {
         const long k1 = k0 + ternix_hip::kMaxKPerAccumulator < K ? k0 + ternix_hip::kMaxKPerAccumulator : K;
-        const hipError_t e = ternix_hip::launch_gemm(dA, dB, dC, M, K, N, (int)k0, (int)k1, acc, st);
+        const hipError_t e = ternix_hip::launch_gemm(dA, dB, dC, M, K, N, (int)k0, (int)k1, acc, st,
+                                                     ternix_hip::OutScale{}, 1, 0, tiled);
         if (e != hipSuccess) return e;
         acc = 1;
     }
@@ -394,6 +415,33 @@ hipError_t run_auto(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int
         if (e != hipErrorNotSupported) return e;
     }
     return M <= skinny_max ? run_skinny(dA, dB, dC, M, K, N, st, os) : run_gemm(dA, dB, dC, M, K, N, st, os);
+}
+
+// Tile-64 weights (the opt-in pre-permuted layout): M <= 32 runs the wave-pipelined kernel, whose
+// per-wave DMA of one 1 KB block is a single contiguous read, K split by wave_splits at every K
+// (the contiguous reads make it faster than the DMA kernel for long K too: cold cfg2 down 6.7 us
+// against 7.8 on the row-major layout; TERNIX_SKINNY_WAVE="16,2,splits" forces the split count,
+// experiments).  Larger M runs the LDS-DMA GEMMs with the contract layout's split-K planning.
+hipError_t run_tile64(const int8_t* dA, const uint8_t* dWt, int32_t* dC, int M, int K, int N, hipStream_t st) {
+    if (M <= 32) {
+        const int nsteps = K / 64;
+        int sp = wave_splits(M, K, N);
+        if (const char* env = skinny_wave_env()) {
+            int esw = 0, ensw = 0, esp = 0;
+            if (std::sscanf(env, "%d,%d,%d", &esw, &ensw, &esp) == 3 && esp >= 1) sp = esp;
+        }
+        const int sps = (nsteps + sp - 1) / sp;
+        const int splits = (nsteps + sps - 1) / sps;
+        if (sps * 64 > ternix_hip::kMaxKPerAccumulator) return hipErrorInvalidValue;
+        int32_t* partials = nullptr;
+        if (splits > 1) {
+            const size_t need = (size_t)splits * (size_t)M * (size_t)N * sizeof(int32_t);
+            if (need <= kWorkspaceMax) partials = static_cast<int32_t*>(workspace(st, need));
+        }
+        return ternix_hip::launch_skinny_wave(dA, dWt, dC, M, K, N, 16, 2, splits, sps, partials, st,
+                                              ternix_hip::OutScale{}, 0, ternix_hip::ActQuant{}, 1);
+    }
+    return run_gemm(dA, dWt, dC, M, K, N, st, ternix_hip::OutScale{}, 1);
 }
 
 enum class Path { Auto, Skinny, Gemm, Naive };
@@ -674,6 +722,26 @@ int ternix_hip_interleave_weights_offline(uint8_t* dOut, const uint8_t* dPacked,
     if (dOut == nullptr || dPacked == nullptr) return (int)hipErrorInvalidValue;
     if (dOut == dPacked) return (int)hipSuccess;
     return (int)hipMemcpyAsync(dOut, dPacked, nbytes, hipMemcpyDeviceToDevice, static_cast<hipStream_t>(stream));
+}
+
+int ternix_hip_interleave_weights_tile64(uint8_t* dOut, const uint8_t* dPacked, int64_t K, int64_t N, void* stream) {
+    if (K < 0 || N < 0 || N % 4 != 0 || K % 64 != 0 || (N / 4) % 16 != 0 || K > INT_MAX || N > INT_MAX)
+        return (int)hipErrorInvalidValue;
+    if (K == 0 || N == 0) return (int)hipSuccess;
+    if (dOut == nullptr || dPacked == nullptr || dOut == dPacked) return (int)hipErrorInvalidValue;
+    return (int)ternix_hip::launch_tile64(dPacked, dOut, (int)K, (int)N, static_cast<hipStream_t>(stream));
+}
+
+int ternix_hip_mul_mat_ternary_tile64(const int8_t* dA, const uint8_t* dWt, int32_t* dC, int64_t M, int64_t K,
+                                      int64_t N, void* stream) {
+    bool trivial = false;
+    hipError_t e = validate(dA, dWt, dC, M, K, N, &trivial);
+    if (e != hipSuccess) return (int)e;
+    if (K % 128 != 0 || N % 256 != 0 || (size_t)K * (size_t)(N / 4) >= ((size_t)1 << 32) ||
+        reinterpret_cast<uintptr_t>(dA) % 16 != 0 || reinterpret_cast<uintptr_t>(dWt) % 16 != 0)
+        return (int)hipErrorInvalidValue;
+    if (trivial) return (int)hipSuccess;
+    return (int)run_tile64(dA, dWt, dC, (int)M, (int)K, (int)N, static_cast<hipStream_t>(stream));
 }
 
 const char* ternix_hip_error_string(int status) {
