@@ -406,6 +406,17 @@ def bench_tile64(args, stream, lib):
     out = {"gemv_pair_gbs": round(bytes_step / (ms / args.steps * 1e-3) / 1e9, 2),
            "gemv_pair_ms_per_step": round(ms / args.steps, 5), "verified": ok, "configs": []}
     del pu, pd
+    # the conversion itself (offline, once per weight matrix): cfg5 big, read + write
+    from ternixengine_amd import hip_runtime as hr
+    big = configs.CASES["cfg5_big_m1"]
+    src = hr.DeviceBuffer.from_array(configs.gen_w_packed(big))
+    dst = hr.DeviceBuffer(big.K * big.N // 4)
+    conv = lambda i: lib.ternix_hip_interleave_weights_tile64(dst.value, src.value, big.K, big.N, stream.handle)
+    prewarm(conv, 0.1, stream)
+    ms = time_launches(conv, 20, 2, stream)
+    us = ms / 20 * 1e3
+    out["convert_cfg5_big"] = {"us": round(us, 2), "gbs": round(2 * big.K * big.N // 4 / (us * 1e-6) / 1e9, 1)}
+    del src, dst
     for name in TILE64_CASES:
         case = configs.CASES[name]
         w = case.K * case.N // 4
@@ -552,7 +563,7 @@ def main():
         line["roofline"] = {"bound": "hbm", "achieved": round(g["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                             "frac": round(g["gbs"] / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(),
                             "algorithmic_bytes": g["bytes_per_step"] // 2,
-                            "kernel": "skinny_wave_kernel (up, one launch) / skinny_dma_kernel + splitk_reduce_kernel (down); one ternix_hip_mul_mat_ternary call each, M=1",
+                            "kernel": "skinny_wave_kernel + splitk_reduce_kernel (up) / skinny_dma_kernel + splitk_reduce_kernel (down); one ternix_hip_mul_mat_ternary call each, M=1",
                             "avg_launch_us": round(g["launch_us"], 3)}
         line["gemv_detail"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in g.items()}
     if "bigm1" in res:

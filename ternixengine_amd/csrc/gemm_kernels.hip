@@ -232,11 +232,11 @@ __device__ __forceinline__ int gf_swz_w(int r) { return ((r >> 1) & 3) ^ ((r >> 
 template <int BNB>
 __device__ __forceinline__ int swz_w(int r) { return BNB == 64 ? gf_swz_w(r) : (BNB == 32 ? ((r >> 4) & 1) : 0); }
 
-template <int BM, int WGN, int NS, int BK>
+template <int BM, int WGN, int NS, int BK, bool TILED>
 __global__ __launch_bounds__(GF_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
 void gemm_fast_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ B, int32_t* __restrict__ C, int M,
                       int K, int N, int tiles_n, int k_begin, int k_end, int accumulate, int vec_store,
-                      int k_split, OutScale os, int tiled) {
+                      int k_split, OutScale os) {
     if (gridDim.y > 1) {  // split-K: this workgroup's k-range, partial tile in slab blockIdx.y
         k_begin += (int)blockIdx.y * k_split;
         k_end = min(k_end, k_begin + k_split);
@@ -306,7 +306,7 @@ void gemm_fast_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ 
     for (int p = 0; p < NW; ++p) {
         const int slot = (p * 8 + wave) * 64 + lane;
         const int r = slot >> 2, pos = slot & 3;
-        w_off[p] = tiled ? tile64_offset((bc0 >> 4) + (pos ^ gf_swz_w(r)), r, K >> 6)
+        w_off[p] = TILED ? tile64_offset((bc0 >> 4) + (pos ^ gf_swz_w(r)), r, K >> 6)
                          : (uint32_t)r * (uint32_t)NB + (uint32_t)(bc0 + (pos ^ gf_swz_w(r)) * 16);
     }
     auto issue = [&](int st, int buf) {
@@ -315,7 +315,7 @@ void gemm_fast_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ 
         int8_t* adst = stage_a(buf);
 #pragma unroll
         for (int p = 0; p < NA; ++p) lds_dma16(abase + a_off[p], adst + (p * 8 + wave) * 1024);
-        const uint8_t* wbase = tiled ? B + (size_t)((k_begin + sc * BK) >> 6) * 1024
+        const uint8_t* wbase = TILED ? B + (size_t)((k_begin + sc * BK) >> 6) * 1024
                                      : B + (size_t)(k_begin + sc * BK) * (size_t)NB;
         uint8_t* wdst = stage_w(buf);
 #pragma unroll
@@ -441,11 +441,11 @@ struct PipeFrag {
     uint64_t lo[GT], hi[GT];
 };
 
-template <int BM, int WGN, int NS, int BK, int NWV, int BNB>
+template <int BM, int WGN, int NS, int BK, int NWV, int BNB, bool TILED>
 __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2)))
 void gemm_pipe_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ B, int32_t* __restrict__ C, int M,
                       int K, int N, int tiles_n, int k_begin, int k_end, int accumulate, int vec_store,
-                      int k_split, OutScale os, int tiled) {
+                      int k_split, OutScale os) {
     if (gridDim.y > 1) {  // split-K: this workgroup's k-range, partial tile in slab blockIdx.y
         k_begin += (int)blockIdx.y * k_split;
         k_end = min(k_end, k_begin + k_split);
@@ -511,7 +511,7 @@ void gemm_pipe_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ 
     for (int p = 0; p < NW; ++p) {
         const int slot = (p * NWV + wave) * 64 + lane;
         const int r = slot / CW, pos = slot % CW;
-        w_off[p] = tiled ? tile64_offset((bc0 >> 4) + (pos ^ swz_w<BNB>(r)), r, K >> 6)
+        w_off[p] = TILED ? tile64_offset((bc0 >> 4) + (pos ^ swz_w<BNB>(r)), r, K >> 6)
                          : (uint32_t)r * (uint32_t)NB + (uint32_t)(bc0 + (pos ^ swz_w<BNB>(r)) * 16);
     }
     auto issue = [&](int st, int buf) {
@@ -520,7 +520,7 @@ void gemm_pipe_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ 
         int8_t* adst = stage_a(buf);
 #pragma unroll
         for (int p = 0; p < NA; ++p) lds_dma16(abase + a_off[p], adst + (p * NWV + wave) * 1024);
-        const uint8_t* wbase = tiled ? B + (size_t)((k_begin + sc * BK) >> 6) * 1024
+        const uint8_t* wbase = TILED ? B + (size_t)((k_begin + sc * BK) >> 6) * 1024
                                      : B + (size_t)(k_begin + sc * BK) * (size_t)NB;
         uint8_t* wdst = stage_w(buf);
 #pragma unroll
@@ -753,8 +753,12 @@ hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int
             // 64 x 64 output tiles (16 bytes of every weight row): enough workgroups without a K
             // split where the 256-column tiles would need one; one m-tile per wave, 256-deep stages.
             const dim3 gridn((unsigned)(((M + 63) / 64) * (NB / 16)), splits);
-            hipLaunchKernelGGL((gemm_pipe_kernel<64, 1, 3, 256, 4, 16>), gridn, dim3(256), 0, st, A, B, C, M, K, N,
-                               NB / 16, k_begin, k_end, accumulate, vs, k_split, os, tiled);
+            if (tiled)
+                hipLaunchKernelGGL((gemm_pipe_kernel<64, 1, 3, 256, 4, 16, true>), gridn, dim3(256), 0, st, A, B, C, M,
+                                   K, N, NB / 16, k_begin, k_end, accumulate, vs, k_split, os);
+            else
+                hipLaunchKernelGGL((gemm_pipe_kernel<64, 1, 3, 256, 4, 16, false>), gridn, dim3(256), 0, st, A, B, C,
+                                   M, K, N, NB / 16, k_begin, k_end, accumulate, vs, k_split, os);
             return hipGetLastError();
         }
         // One round of 128-row tiles with a short k-range (cfg4 4096^2): two co-resident workgroups
@@ -767,14 +771,24 @@ hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int
             // Small M (64 rows or fewer): four-wave workgroups on 64-row tiles, so no MFMA row or A
             // byte is spent on padding rows; the caller splits K to fill the chip.
             const dim3 grid64((unsigned)(((M + 63) / 64) * tiles_n), splits);
-            hipLaunchKernelGGL((gemm_pipe_kernel<64, 4, 3, 128, 4, 64>), grid64, dim3(256), 0, st, A, B, C, M, K, N,
-                               tiles_n, k_begin, k_end, accumulate, vs, k_split, os, tiled);
+            if (tiled)
+                hipLaunchKernelGGL((gemm_pipe_kernel<64, 4, 3, 128, 4, 64, true>), grid64, dim3(256), 0, st, A, B, C,
+                                   M, K, N, tiles_n, k_begin, k_end, accumulate, vs, k_split, os);
+            else
+                hipLaunchKernelGGL((gemm_pipe_kernel<64, 4, 3, 128, 4, 64, false>), grid64, dim3(256), 0, st, A, B, C,
+                                   M, K, N, tiles_n, k_begin, k_end, accumulate, vs, k_split, os);
             return hipGetLastError();
         }
         if (pipe) {
-#define TX_GP_LAUNCH(BM_, WGN_, NS_, BK_)                                                                      \
-    hipLaunchKernelGGL((gemm_pipe_kernel<BM_, WGN_, NS_, BK_, 8, GF_BNB>), grid, dim3(GF_THREADS), 0, st, A, B, C, M, \
-                       K, N, tiles_n, k_begin, k_end, accumulate, vs, k_split, os, tiled)
+#define TX_GP_LAUNCH(BM_, WGN_, NS_, BK_)                                                                          \
+    do {                                                                                                           \
+        if (tiled)                                                                                                 \
+            hipLaunchKernelGGL((gemm_pipe_kernel<BM_, WGN_, NS_, BK_, 8, GF_BNB, true>), grid, dim3(GF_THREADS), 0, \
+                               st, A, B, C, M, K, N, tiles_n, k_begin, k_end, accumulate, vs, k_split, os);      \
+        else                                                                                                       \
+            hipLaunchKernelGGL((gemm_pipe_kernel<BM_, WGN_, NS_, BK_, 8, GF_BNB, false>), grid, dim3(GF_THREADS), 0, \
+                               st, A, B, C, M, K, N, tiles_n, k_begin, k_end, accumulate, vs, k_split, os);      \
+    } while (0)
             if (bk == 256 && wgn == 4) TX_GP_LAUNCH(128, 4, 3, 256);
             else if (bk == 256) TX_GP_LAUNCH(128, 2, 3, 256);
             else if (wgn == 4 && pipe_ns == 4) TX_GP_LAUNCH(128, 4, 4, 128);
@@ -785,8 +799,14 @@ hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int
             return hipGetLastError();
         }
 #define TX_GF_LAUNCH(BM_, WGN_, NS_, BK_)                                                                         \
-    hipLaunchKernelGGL((gemm_fast_kernel<BM_, WGN_, NS_, BK_>), grid, dim3(GF_THREADS), 0, st, A, B, C, M, K, N, \
-                       tiles_n, k_begin, k_end, accumulate, vs, k_split, os, tiled)
+    do {                                                                                                          \
+        if (tiled)                                                                                                \
+            hipLaunchKernelGGL((gemm_fast_kernel<BM_, WGN_, NS_, BK_, true>), grid, dim3(GF_THREADS), 0, st, A, B, \
+                               C, M, K, N, tiles_n, k_begin, k_end, accumulate, vs, k_split, os);               \
+        else                                                                                                      \
+            hipLaunchKernelGGL((gemm_fast_kernel<BM_, WGN_, NS_, BK_, false>), grid, dim3(GF_THREADS), 0, st, A,  \
+                               B, C, M, K, N, tiles_n, k_begin, k_end, accumulate, vs, k_split, os);            \
+    } while (0)
         if (bm == 256 && wgn == 4) TX_GF_LAUNCH(256, 4, 3, 128);
         else if (bm == 256) TX_GF_LAUNCH(256, 2, 3, 128);
         else if (bk == 256 && wgn == 4) TX_GF_LAUNCH(128, 4, 3, 256);

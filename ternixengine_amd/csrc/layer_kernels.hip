@@ -111,13 +111,20 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const float* __restr
     }
 }
 
-// Tile-64 layout conversion (kernel_common.h): a permutation copy, one 16-byte chunk per thread,
-// read row-major (coalesced) and written to its block position.
-__global__ __launch_bounds__(256) void tile64_kernel(const uint8_t* __restrict__ W, uint8_t* __restrict__ Wt,
-                                                     int nK, int strips, size_t chunks) {
-    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < chunks; i += (size_t)gridDim.x * 256) {
-        const int r = (int)(i / (size_t)strips), c = (int)(i % (size_t)strips);
-        *reinterpret_cast<v4i*>(Wt + tile64_offset(c, r, nK)) = *reinterpret_cast<const v4i*>(W + i * 16);
+// Tile-64 layout conversion (kernel_common.h): a permutation copy.  A workgroup of 8 waves takes one
+// 64-row k-step of 8 adjacent strips; wave w writes block (strip, k-step) of its strip as one
+// contiguous 1 KB store (lane = row), and the 8 waves together read 128 contiguous bytes of each row.
+__global__ __launch_bounds__(512) void tile64_kernel(const uint8_t* __restrict__ W, uint8_t* __restrict__ Wt,
+                                                     int nK, int strips) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int groups = (strips + 7) >> 3;
+    const size_t NB = (size_t)strips * 16;
+    for (size_t u = blockIdx.x; u < (size_t)groups * (size_t)nK; u += gridDim.x) {
+        const int s = (int)(u % (size_t)nK), c = (int)(u / (size_t)nK) * 8 + wave;
+        if (c >= strips) continue;
+        const int r = s * 64 + tile64_pos(lane);  // the row stored at position `lane` of the block
+        *reinterpret_cast<v4i*>(Wt + ((size_t)c * (size_t)nK + (size_t)s) * 1024 + (size_t)lane * 16) =
+            *reinterpret_cast<const v4i*>(W + (size_t)r * NB + (size_t)c * 16);
     }
 }
 
@@ -228,10 +235,10 @@ hipError_t launch_tile64(const uint8_t* W, uint8_t* Wt, int K, int N, hipStream_
     if (K % 64 != 0 || NB % 16 != 0 || (uintptr_t)W % 16 != 0 || (uintptr_t)Wt % 16 != 0 ||
         (size_t)K * (size_t)NB >= ((size_t)1 << 32))
         return hipErrorInvalidValue;
-    const size_t chunks = (size_t)K * (size_t)NB / 16;
-    if (chunks == 0) return hipSuccess;
-    const unsigned blocks = (unsigned)std::min<size_t>((chunks + 255) / 256, 16384);
-    hipLaunchKernelGGL(tile64_kernel, dim3(blocks), dim3(256), 0, st, W, Wt, K / 64, NB / 16, chunks);
+    const size_t units = (size_t)K / 64 * (size_t)((NB / 16 + 7) / 8);
+    if (units == 0) return hipSuccess;
+    const unsigned blocks = (unsigned)std::min<size_t>(units, 65536);
+    hipLaunchKernelGGL(tile64_kernel, dim3(blocks), dim3(512), 0, st, W, Wt, K / 64, NB / 16);
     return hipGetLastError();
 }
 

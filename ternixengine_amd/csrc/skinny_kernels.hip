@@ -1264,10 +1264,11 @@ hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, i
         else if (M <= 16) e = tb == 2 ? launch_fast_kw<1, 2, false>(a, kw, grid, st) : launch_fast_kw<1, 1, false>(a, kw, grid, st);
         else e = launch_fast_kw<2, 1, false>(a, kw, grid, st);
     } else {
-        const dim3 grid((NB + 127) / 128, splits, mgroups);
+        // One 16-row m-group per workgroup at every M (two row tiles per wave would need more than
+        // the 256 VGPRs and spill).
+        const dim3 grid((NB + 127) / 128, splits, (M + 15) / 16);
         if (M <= 4) e = launch_generic<1, true>(a, grid, st);
-        else if (M <= 16) e = launch_generic<1, false>(a, grid, st);
-        else e = launch_generic<2, false>(a, grid, st);
+        else e = launch_generic<1, false>(a, grid, st);
     }
     if (e != hipSuccess) return e;
     if (mode == SK_ATOMIC && scaled) return launch_dequant(C, os, M, N, st);  // C: alias of os.Y or scratch
