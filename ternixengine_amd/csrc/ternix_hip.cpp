@@ -194,24 +194,35 @@ int wave_max_m() {
     return m;
 }
 
-// K split of the wave-pipelined kernel (one workgroup per 16-byte strip, m-group and split): enough
-// workgroups for about 2.75 per CU, and for M <= 4 up to 7 per CU, one per 8 KB of weights (more
-// weight loads in flight per CU on the large decode matrices, where the extra partial sums cost
-// little); at least two k-steps per split.  Measured on MI355X with cold weights (512 MiB pools):
-// cfg2 up 9.35 -> 8.5 us against no split, cfg3 M=4 up 13.5 -> 12.0, tile-64 cfg5 big 17.8 -> 15.3.
+// K split of the wave-pipelined kernel (one workgroup per strip of sw bytes, m-group and split).
+// 16-byte strips (tile-64 weights): enough workgroups for about 2.75 per CU, and for M <= 4 up to 7
+// per CU, one per 8 KB of weights (more weight loads in flight on the large decode matrices, where
+// the extra partial sums cost little).  32-byte strips (row-major weights): about one workgroup per
+// CU.  At least two k-steps per split.  Measured on MI355X with cold weights (512 MiB pools, one
+// box): 16-byte strips cfg2 up 9.35 -> 8.4 us against no split, tile-64 cfg5 big 17.8 -> 15.3 us;
+// 32-byte strips against 16-byte ones, each with its split: cfg1 6.72 -> 6.14 us, cfg2 up 8.41 ->
+// 7.56, cfg3 M=4 up 12.3 -> 10.9, M=16 up 13.8 -> 11.9, M=16 down 13.95 -> 11.8.
 // TERNIX_WAVE_TARGET overrides the workgroup target (experiments).
-int wave_splits(int M, int K, int N) {
+int wave_splits(int M, int K, int N, int sw = 16) {
     static const long env = [] {
         const char* e = std::getenv("TERNIX_WAVE_TARGET");
         return e ? std::atol(e) : 0L;
     }();
-    const long nsteps = K / 64, units = (long)(N / 4 / 16) * ((M + 15) / 16), cus = cu_count();
+    const long nsteps = K / 64, units = (long)(N / 4 / sw) * ((M + 15) / 16), cus = cu_count();
     long target = cus * 11 / 4;
     if (M <= 4) target = std::max(target, std::min(7 * cus, (long)K * (N / 4) / 8192));
+    if (sw == 32) target = cus;
     if (env > 0) target = env;
     long sp = (target + units / 2) / std::max(1L, units);
-    sp = std::min(sp, std::max(1L, nsteps / 2));
-    return (int)std::max(1L, std::min(16L, sp));
+    sp = std::max(1L, std::min(16L, std::min(sp, std::max(1L, nsteps / 2))));
+    // 32-byte strips: at most one workgroup per CU (2 % slack); a CU given a second one finishes last
+    // (cfg3 M=16 down: 8 splits, 256 workgroups 11.8 us; 10 splits, 320 workgroups 15.5 us).
+    while (sw == 32 && sp > 1) {
+        const long sps = (nsteps + sp - 1) / sp;
+        if (units * ((nsteps + sps - 1) / sps) * 50 <= cus * 51) break;
+        --sp;
+    }
+    return (int)sp;
 }
 
 hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int K, int N, hipStream_t st,
@@ -219,20 +230,25 @@ hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
                       const ternix_hip::ActQuant& aq = ternix_hip::ActQuant{}) {
     const bool generic = !(K % 64 == 0 && (N / 4) % 64 == 0 && reinterpret_cast<uintptr_t>(dB) % 16 == 0 &&
                            (aq.mode != 0 || reinterpret_cast<uintptr_t>(dA) % 16 == 0));
-    // Wave-pipelined kernel (16-byte strips, 2 ring slots per wave), measured on MI355X against the
-    // DMA-staged kernel: faster for K <= 4096 (cfg1 6.26 -> 5.64 us, cfg2 up 6.94 -> 6.29, cfg3 M=4
-    // up 11.62 -> 10.41, M=16 up 14.27 -> 11.45) and for 4 < M <= 32 with longer K, whose partials
-    // are far fewer than the DMA kernel's (cfg3 M=16 down 14.59 -> 12.78 us); K split by wave_splits.
-    // M <= 4 with K > 4096 stays on the DMA kernel (cold cfg2 down 7.8 us against 9.0 at best).
+    // Wave-pipelined kernel (32-byte strips, 16-byte with fused quantisation; 2 ring slots per wave),
+    // measured on MI355X (16-byte strips) against the DMA-staged kernel: faster for K <= 4096 (cfg1
+    // 6.26 -> 5.64 us, cfg2 up 6.94 -> 6.29, cfg3 M=4 up 11.62 -> 10.41, M=16 up 14.27 -> 11.45) and
+    // for 4 < M <= 32 with longer K, whose partials are far fewer than the DMA kernel's (cfg3 M=16
+    // down 14.59 -> 12.78 us); strip width and K split as in wave_splits.  M <= 4 with K > 4096 stays
+    // on the DMA kernel (cold cfg2 down 7.8 us against 7.9-9.0 for the wave kernel).
     // TERNIX_SKINNY_WAVE="sw,nsw,splits" forces a plan, "0" turns the kernel off (experiments).
     // With fused activation quantisation (K <= 4096) it quantises whole rows itself and dequantises with
     // its own row scales: the FFN block's gate/up GEMV becomes one launch.
     if (!generic && M <= wave_max_m() && ternix_hip::skinny_wave_ok(dA, dB, M, K, N, 16) &&
         (aq.mode == 0 || (K <= 4096 && M <= 16))) {
+        static const int sw_env = [] {
+            const char* e = std::getenv("TERNIX_WAVE_SW");  // experiments: "16" for 16-byte strips
+            return e && std::atoi(e) == 16 ? 16 : 32;
+        }();
         const int nsteps = K / 64;
-        int sw = 16, nsw = 2, sp = 0;
+        int sw = aq.mode == 0 && ternix_hip::skinny_wave_ok(dA, dB, M, K, N, sw_env) ? sw_env : 16, nsw = 2, sp = 0;
         if (aq.mode != 0) sp = 1;
-        else if (K <= 4096 || M > 4) sp = wave_splits(M, K, N);
+        else if (K <= 4096 || M > 4) sp = wave_splits(M, K, N, sw);
         if (const char* env = skinny_wave_env()) {
             int esw = 0, ensw = 0, esp = 0;
             if (std::sscanf(env, "%d,%d,%d", &esw, &ensw, &esp) == 3 && esp >= 1 &&

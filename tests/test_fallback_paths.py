@@ -10,6 +10,7 @@ import pytest
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 SWITCHES = [
     {"TERNIX_SKINNY_WAVE": "0"},                                                     # DMA-staged GEMVs
+    {"TERNIX_WAVE_SW": "16"},                                                        # 16-byte wave strips
     {"TERNIX_SKINNY_WAVE": "0", "TERNIX_SKINNY_DMA": "0"},                           # short / fast kernels
     {"TERNIX_SKINNY_WAVE": "0", "TERNIX_SKINNY_DMA": "0", "TERNIX_SKINNY_SHORT": "0"},  # fast kernel only
     {"TERNIX_RAGGED_PAD": "0"},                                                      # generic ragged kernels
