@@ -44,7 +44,12 @@ namespace {
 constexpr int SK_WAVES = 4;
 constexpr int kRowRegs = 32;  // fused activation quantisation: row elements per thread (K <= 8192)
 
-enum SkinnyMode { SK_STORE = 0, SK_ATOMIC = 1, SK_PARTIAL = 2 };
+// SK_LAST (skinny_wave_kernel only): every split stores its partial tile with agent-scope
+// (L2 write-through) stores, waits for them, and counts itself on the tile's counter; the last
+// split to arrive sums all partials of the tile (agent-scope loads) and writes C, then resets the
+// counter.  No L2 writeback or invalidate is needed because only those coherent accesses touch the
+// exchanged data, and no second launch is needed.
+enum SkinnyMode { SK_STORE = 0, SK_ATOMIC = 1, SK_PARTIAL = 2, SK_LAST = 3 };
 
 struct SkinnyArgs {
     const int8_t* A;
@@ -68,6 +73,7 @@ struct SkinnyArgs {
     int n_out;            // skinny_wave_kernel, store mode: C / os.Y has n_out <= N columns (0: N)
     int line_units;       // skinny_wave_kernel: block -> strip mapping by 128-byte line units
     int tiled;            // skinny_wave_kernel: W in the tile-64 layout (kernel_common.h)
+    int* cnt;             // SK_LAST: arrival counters, one per (m-group, strip), zero between calls
 };
 
 // One k-step of MFMA work for one 16-row x 4-byte-column block: raw[r] is the dword of row r.
@@ -1027,14 +1033,79 @@ void skinny_wave_kernel(SkinnyArgs args) {
             for (int j = 0; j < 4; ++j) r[(g * 4 + j) * 64 + lane] = acc[g][j];
     }
     __syncthreads();
-    if (wave != 0) return;
+    if (wave != 0 && args.mode != SK_LAST) return;
+    if (wave == 0) {
 #pragma unroll
-    for (int w = 0; w < 3; ++w) {
-        const v4i* r = reinterpret_cast<const v4i*>(lds) + w * 64 * 4 * G;
+        for (int w = 0; w < 3; ++w) {
+            const v4i* r = reinterpret_cast<const v4i*>(lds) + w * 64 * 4 * G;
 #pragma unroll
-        for (int g = 0; g < G; ++g)
+            for (int g = 0; g < G; ++g)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[g][j] += r[(g * 4 + j) * 64 + lane];
+                for (int j = 0; j < 4; ++j) acc[g][j] += r[(g * 4 + j) * 64 + lane];
+        }
+    }
+    if (args.mode == SK_LAST) {
+        __shared__ int s_last;
+        const size_t MN = (size_t)M * (size_t)args.N;
+        int* counter = args.cnt + (size_t)blockIdx.z * (size_t)n_strips + cx;
+        if (wave == 0) {
+            int32_t* mine = args.P + (size_t)sy * MN;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int row = m0 + 4 * kb + i;
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    if ((LOW_M && kb != 0) || row >= M) continue;
+                    int32_t* out = mine + (size_t)row * (size_t)args.N + 4 * (bc0 + 16 * g + q);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        __hip_atomic_store(out + j, acc[g][j][i] >> 6, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+            __builtin_amdgcn_s_waitcnt(0);  // the partial stores are complete, coherent at agent scope
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            if (lane == 0)
+                s_last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                         args.splits - 1;
+        }
+        __syncthreads();
+        if (!s_last) return;  // workgroup-uniform
+        // Last arrival: the whole workgroup sums the tile's partials (its own included) over all
+        // splits, eight splits' loads in flight at a time (indices clamped: the loads are unconditional).
+        const int rows = min(16, M - m0);
+        for (int idx = tid; idx < rows * SW; idx += 256) {
+            const int row = m0 + idx / SW, col = 4 * (bc0 + idx % SW);
+            const size_t off = (size_t)row * (size_t)args.N + col;
+            v4i v = {0, 0, 0, 0};
+            for (int c0 = 0; c0 < args.splits; c0 += 8) {
+                uint64_t lo[8], hi[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const uint64_t* src =
+                        reinterpret_cast<const uint64_t*>(args.P + (size_t)min(c0 + u, args.splits - 1) * MN + off);
+                    lo[u] = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    hi[u] = __hip_atomic_load(src + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    if (c0 + u >= args.splits) continue;
+                    v[0] += (int)(uint32_t)lo[u];
+                    v[1] += (int)(uint32_t)(lo[u] >> 32);
+                    v[2] += (int)(uint32_t)hi[u];
+                    v[3] += (int)(uint32_t)(hi[u] >> 32);
+                }
+            }
+            if (args.os.Y) {
+                store_scaled(args.os, row, args.N, col, v, args.vec_store);
+            } else if (args.vec_store) {
+                *reinterpret_cast<v4i*>(args.C + off) = v;
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) args.C[off + j] = v[j];
+            }
+        }
+        if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
     }
     if (LOW_M && kb != 0) return;
     int32_t* out_base = args.mode == SK_PARTIAL ? args.P + (size_t)sy * (size_t)M * (size_t)args.N : args.C;
@@ -1290,7 +1361,7 @@ bool skinny_wave_ok(const int8_t* A, const uint8_t* B, int M, int K, int N, int 
 
 hipError_t launch_skinny_wave(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int sw, int nsw,
                               int splits, int steps_per_split, int32_t* partials, hipStream_t st, const OutScale& os,
-                              int n_out, const ActQuant& aq, int tiled) {
+                              int n_out, const ActQuant& aq, int tiled, int* counters) {
     if (tiled && (sw != 16 || n_out > 0)) return hipErrorInvalidValue;
     if (!skinny_wave_ok(A, B, M, K, N, sw) || nsw < 2 || nsw > 4 || steps_per_split < 1) return hipErrorInvalidValue;
     // Fused activation quantisation: one launch over whole rows (K <= 4096), 16-byte strips, 2 slots.
@@ -1298,7 +1369,8 @@ hipError_t launch_skinny_wave(const int8_t* A, const uint8_t* B, int32_t* C, int
                          aq.rs_out == nullptr || (aq.mode == 2 && aq.G == nullptr)))
         return hipErrorInvalidValue;
     const int NB = N >> 2;
-    const int mode = splits <= 1 ? SK_STORE : (partials ? SK_PARTIAL : SK_ATOMIC);
+    int mode = splits <= 1 ? SK_STORE : (partials ? SK_PARTIAL : SK_ATOMIC);
+    if (mode == SK_PARTIAL && counters && n_out == 0 && aq.mode == 0) mode = SK_LAST;
     if (n_out > 0 && (mode == SK_ATOMIC || n_out > N || n_out % 4 != 0)) return hipErrorInvalidValue;
     if (mode == SK_ATOMIC && C == nullptr) return hipErrorInvalidValue;
     if (mode == SK_ATOMIC) {
@@ -1308,7 +1380,8 @@ hipError_t launch_skinny_wave(const int8_t* A, const uint8_t* B, int32_t* C, int
     const bool scaled = os.Y != nullptr;
     const int vec_store = ((uintptr_t)(scaled ? (const void*)os.Y : (const void*)C) % 16) == 0;
     SkinnyArgs a{A, B, C, partials, M, K, N, steps_per_split, splits, mode, vec_store, 1, 1,
-                 mode == SK_STORE ? os : OutScale{}};
+                 (mode == SK_STORE || mode == SK_LAST) ? os : OutScale{}};
+    a.cnt = counters;
     a.n_out = n_out;
     a.tiled = tiled;
     a.X = aq.X;

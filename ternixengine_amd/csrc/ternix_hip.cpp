@@ -39,6 +39,7 @@ struct Workspace {
     void* ptr = nullptr;
     size_t bytes = 0;
     std::vector<void*> retired;
+    int* counters = nullptr;  // arrival counters of the single-launch split-K GEMV (zero between calls)
 };
 std::mutex g_ws_mutex;
 std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
@@ -62,6 +63,41 @@ void* workspace(hipStream_t st, size_t bytes) {
     w.ptr = p;
     w.bytes = nb;
     return p;
+}
+
+// Largest split count for which the wave GEMV sums its K splits inside the launch (the last
+// workgroup of each strip to arrive adds the partials) instead of in a reduce launch.  Measured on
+// MI355X, cold weights, one box: with 2-5 splits the single launch wins (cfg2 up 7.7 -> 7.0 us,
+// cfg3 M=4 up 11.1 -> 9.2, tile-64 cfg5 big 15.6 -> 15.0); from about 8 splits the serialised
+// arrivals on each counter cost more than the launch (cfg3 M=16 down 12.1 -> 12.8 us).
+// TERNIX_WAVE_LAST overrides it (experiments; 0 turns the scheme off).
+int last_max_splits() {
+    static const int v = [] {
+        const char* e = std::getenv("TERNIX_WAVE_LAST");
+        return e ? std::atoi(e) : 5;
+    }();
+    return v;
+}
+
+// Arrival counters of the wave GEMV's single-launch split-K (kCounterSlots ints per (device, stream),
+// zeroed once when allocated; every call leaves them zero).  nullptr during graph capture before
+// they exist, when `need` exceeds the slots or for more than last_max_splits() splits: the caller
+// then uses the reduce launch.
+constexpr size_t kCounterSlots = size_t(1) << 16;
+int* arrival_counters(hipStream_t st, size_t need, int splits) {
+    if (splits > last_max_splits() || need > kCounterSlots) return nullptr;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    Workspace& w = g_ws[{dev, st}];
+    if (w.counters) return w.counters;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
+    void* p = nullptr;
+    if (hipMalloc(&p, kCounterSlots * sizeof(int)) != hipSuccess) return nullptr;
+    if (hipMemsetAsync(p, 0, kCounterSlots * sizeof(int), st) != hipSuccess) return nullptr;
+    w.counters = static_cast<int*>(p);
+    return w.counters;
 }
 
 // Shape / pointer validation shared by every device entry point.  Returns hipSuccess when the call
@@ -222,6 +258,9 @@ int wave_splits(int M, int K, int N, int sw = 16) {
         if (units * ((nsteps + sps - 1) / sps) * 50 <= cus * 51) break;
         --sp;
     }
+    // K <= 4096: few enough splits to sum them inside the launch (measured: cfg1 6.27 us with 10
+    // splits and the reduce launch, 5.75 with 5 in one launch; tile-64 cfg2 up 6.88 -> 6.41).
+    if (nsteps <= 64 && last_max_splits() > 0) sp = std::min<long>(sp, last_max_splits());
     return (int)sp;
 }
 
@@ -269,9 +308,12 @@ hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
                 if (need <= kWorkspaceMax) partials = static_cast<int32_t*>(workspace(st, need));
             }
             if (sps * 64 <= ternix_hip::kMaxKPerAccumulator && (splits == 1 || partials || dC) &&
-                (aq.mode == 0 || (splits == 1 && sw == 16 && nsw == 2)))
+                (aq.mode == 0 || (splits == 1 && sw == 16 && nsw == 2))) {
+                int* cnt = (partials && aq.mode == 0)
+                               ? arrival_counters(st, (size_t)(N / 4 / sw) * (size_t)((M + 15) / 16), splits) : nullptr;
                 return ternix_hip::launch_skinny_wave(dA, dB, dC, M, K, N, sw, nsw, splits, sps, partials, st, os, 0,
-                                                      aq);
+                                                      aq, 0, cnt);
+            }
         }
     }
     // DMA-staged kernel: TERNIX_SKINNY_DMA=0 disables it, 2..4 sets its stage count (experiments).
@@ -454,8 +496,9 @@ hipError_t run_tile64(const int8_t* dA, const uint8_t* dWt, int32_t* dC, int M, 
             const size_t need = (size_t)splits * (size_t)M * (size_t)N * sizeof(int32_t);
             if (need <= kWorkspaceMax) partials = static_cast<int32_t*>(workspace(st, need));
         }
+        int* cnt = partials ? arrival_counters(st, (size_t)(N / 4 / 16) * (size_t)((M + 15) / 16), splits) : nullptr;
         return ternix_hip::launch_skinny_wave(dA, dWt, dC, M, K, N, 16, 2, splits, sps, partials, st,
-                                              ternix_hip::OutScale{}, 0, ternix_hip::ActQuant{}, 1);
+                                              ternix_hip::OutScale{}, 0, ternix_hip::ActQuant{}, 1, cnt);
     }
     return run_gemm(dA, dWt, dC, M, K, N, st, ternix_hip::OutScale{}, 1);
 }

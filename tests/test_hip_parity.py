@@ -236,8 +236,9 @@ def test_config_full_size_digest(digests, name):
 
 @pytest.mark.parametrize("capture", [False, True])
 def test_split_k_repeated_launches_exact(oracle, capture):
-    """Split-K partial sums go through the workspace and a reduce launch; every one of many
-    back-to-back launches must be bit-exact.  capture=True records the launches into a hipGraph on
+    """Split-K partial sums go through the workspace and either a reduce launch or, for few splits of
+    the wave GEMV, the last-arriving workgroup of each strip (arrival counters that every call leaves
+    at zero); every one of many back-to-back launches must be bit-exact.  capture=True records the launches into a hipGraph on
     a fresh stream (no workspace can be allocated while capturing, so the split-K falls back to
     zero-fill + atomics) and replays it several times, checking each replay."""
     s = hr.Stream()
@@ -276,6 +277,49 @@ def test_split_k_repeated_launches_exact(oracle, capture):
             assert tx.mul_mat_ternary(da.value, db.value, dc.value, case.M, case.K, case.N, stream=s.handle) == 0
         s.synchronize()
         assert (dc.download(np.int32, (case.M, case.N)) == expect).all(), name
+
+
+def test_single_launch_split_k_interleaved_and_graph(oracle):
+    """The wave GEMV's in-launch split-K sum (cfg1, cfg2 up, cfg3 M=4 up, 24 rows in two m-groups,
+    tile-64 weights) shares one set of arrival counters per stream: calls of different shapes issued
+    back to back without host synchronisation, and a graph of them captured after the counters exist
+    and replayed with eager calls between replays, all give the oracle's C."""
+    s = hr.Stream()
+    rng = np.random.default_rng(33)
+    probs = []
+    for m, k, n, tiled in ((1, 2560, 2560, 0), (1, 2560, 6912, 0), (4, 4096, 11008, 0), (24, 2048, 4096, 0),
+                           (2, 4096, 4096, 1), (1, 2560, 6912, 1)):
+        a = rng.integers(-128, 128, size=(m, k), dtype=np.int8)
+        wp = rng.integers(0, 256, size=(k, n // 4), dtype=np.uint8)
+        expect = oracle.mm("scalar_mt", a, wp, n)
+        w_dev = tx.interleave_tile64(wp) if tiled else wp
+        da, db, dc = hr.DeviceBuffer.from_array(a), hr.DeviceBuffer.from_array(w_dev), hr.DeviceBuffer(4 * m * n)
+        probs.append((m, k, n, "tile64" if tiled else "auto", da, db, dc, expect))
+
+    def issue_all():
+        for m, k, n, path, da, db, dc, _ in probs:
+            assert tx.mul_mat_ternary(da.value, db.value, dc.value, m, k, n, stream=s.handle, path=path) == 0
+
+    def check(tag):
+        for m, k, n, path, _, _, dc, expect in probs:
+            assert (dc.download(np.int32, (m, n)) == expect).all(), (tag, m, k, n, path)
+
+    log("[in-launch split-K] interleaved eager calls")
+    for it in range(40):
+        issue_all()
+    s.synchronize()
+    check("eager")
+    log("[in-launch split-K] graph replays")
+    g = hr.Graph(s, issue_all)
+    for rep in range(4):
+        for _, _, _, _, _, _, dc, _ in probs:
+            dc.upload(np.full(dc.nbytes // 4, GARBAGE, np.int32))
+        g.launch()
+        s.synchronize()
+        check(f"replay {rep}")
+        issue_all()  # eager work between replays
+        s.synchronize()
+        check(f"eager after replay {rep}")
 
 
 def test_graph_survives_workspace_growth(oracle):
