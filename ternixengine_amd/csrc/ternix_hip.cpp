@@ -84,8 +84,15 @@ int last_max_splits() {
 // they exist, when `need` exceeds the slots or for more than last_max_splits() splits: the caller
 // then uses the reduce launch.
 constexpr size_t kCounterSlots = size_t(1) << 16;
-int* arrival_counters(hipStream_t st, size_t need, int splits) {
-    if (splits > last_max_splits() || need > kCounterSlots) return nullptr;
+int* arrival_counters(hipStream_t st, size_t need, int M, int splits, int sps) {
+    // Up to 4 rows with long k-ranges per split (>= 8 steps) also sum up to 8 splits inside the
+    // launch: their workgroups finish far apart, so the arrivals hardly queue (cold cfg3 M=4 down:
+    // 8 splits 9.8 us against 11.5 for the DMA-staged kernel and its reduce launch; 12 splits of
+    // cfg2 down 8.6 us against 7.8 with 8; 16 splits of tile-64 cfg3 M=4 down 12.2 against 9.3 us
+    // with the reduce launch).
+    const int lim = last_max_splits();
+    if (lim <= 0 || (splits > lim && !(M <= 4 && sps >= 8 && splits <= 8)) || need > kCounterSlots)
+        return nullptr;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return nullptr;
     std::lock_guard<std::mutex> lock(g_ws_mutex);
@@ -286,8 +293,19 @@ hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
         }();
         const int nsteps = K / 64;
         int sw = aq.mode == 0 && ternix_hip::skinny_wave_ok(dA, dB, M, K, N, sw_env) ? sw_env : 16, nsw = 2, sp = 0;
+        static const int long_small = [] {
+            const char* e = std::getenv("TERNIX_WAVE_LONG");  // experiments: 0 keeps M <= 4, K > 4096 off it
+            return e ? std::atoi(e) : 1;
+        }();
         if (aq.mode != 0) sp = 1;
         else if (K <= 4096 || M > 4) sp = wave_splits(M, K, N, sw);
+        else if (long_small && sw == 32 && last_max_splits() > 0) {
+            // M <= 4 with long K: only when 32-byte strips split 4 to 8 ways within one round of
+            // workgroups (cfg2 down 7.8 us, as the DMA-staged kernel; cfg3 M=4 down 11.5 -> 9.8 us),
+            // summed inside the launch; wide matrices (cfg5 big: 224 strips) keep the DMA-staged kernel.
+            const int s2 = std::min(8, wave_splits(M, K, N, sw));
+            if (s2 >= 4) sp = s2;
+        }
         if (const char* env = skinny_wave_env()) {
             int esw = 0, ensw = 0, esp = 0;
             if (std::sscanf(env, "%d,%d,%d", &esw, &ensw, &esp) == 3 && esp >= 1 &&
@@ -310,7 +328,8 @@ hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
             if (sps * 64 <= ternix_hip::kMaxKPerAccumulator && (splits == 1 || partials || dC) &&
                 (aq.mode == 0 || (splits == 1 && sw == 16 && nsw == 2))) {
                 int* cnt = (partials && aq.mode == 0)
-                               ? arrival_counters(st, (size_t)(N / 4 / sw) * (size_t)((M + 15) / 16), splits) : nullptr;
+                               ? arrival_counters(st, (size_t)(N / 4 / sw) * (size_t)((M + 15) / 16), M, splits, sps)
+                               : nullptr;
                 return ternix_hip::launch_skinny_wave(dA, dB, dC, M, K, N, sw, nsw, splits, sps, partials, st, os, 0,
                                                       aq, 0, cnt);
             }
@@ -496,7 +515,8 @@ hipError_t run_tile64(const int8_t* dA, const uint8_t* dWt, int32_t* dC, int M, 
             const size_t need = (size_t)splits * (size_t)M * (size_t)N * sizeof(int32_t);
             if (need <= kWorkspaceMax) partials = static_cast<int32_t*>(workspace(st, need));
         }
-        int* cnt = partials ? arrival_counters(st, (size_t)(N / 4 / 16) * (size_t)((M + 15) / 16), splits) : nullptr;
+        int* cnt = partials ? arrival_counters(st, (size_t)(N / 4 / 16) * (size_t)((M + 15) / 16), M, splits, sps)
+                            : nullptr;
         return ternix_hip::launch_skinny_wave(dA, dWt, dC, M, K, N, 16, 2, splits, sps, partials, st,
                                               ternix_hip::OutScale{}, 0, ternix_hip::ActQuant{}, 1, cnt);
     }
