@@ -563,7 +563,7 @@ def main():
         line["roofline"] = {"bound": "hbm", "achieved": round(g["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                             "frac": round(g["gbs"] / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(),
                             "algorithmic_bytes": g["bytes_per_step"] // 2,
-                            "kernel": "skinny_wave_kernel + splitk_reduce_kernel (up) / skinny_dma_kernel + splitk_reduce_kernel (down); one ternix_hip_mul_mat_ternary call each, M=1",
+                            "kernel": "skinny_wave_kernel<32,2> (up: 4 K splits, down: 8, each summed inside the launch); one launch per ternix_hip_mul_mat_ternary call, M=1",
                             "avg_launch_us": round(g["launch_us"], 3)}
         line["gemv_detail"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in g.items()}
     if "bigm1" in res:

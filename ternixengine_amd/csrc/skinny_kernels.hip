@@ -33,10 +33,11 @@ namespace {
 // take alternate k-steps and are summed in LDS.  blockIdx.y splits K further over `splits`
 // workgroups: each stores its partial tile with plain stores in the workspace P[split][M][N] and
 // splitk_reduce_kernel (the next launch on the stream) adds the partials.  Cross-workgroup exchange
-// inside one launch would need device-scope release/acquire fences, which on this multi-XCD part
-// write back and invalidate a whole L2 per workgroup, and same-address device-scope atomics from
-// several XCDs serialise at the memory side; the kernel boundary gives the ordering for free.
-// (SK_ATOMIC, used only when no workspace is available, accumulates into a pre-zeroed C instead.)
+// inside one launch with device-scope release/acquire fences would write back and invalidate a whole
+// L2 per workgroup on this multi-XCD part, and same-address device-scope atomics from several XCDs
+// serialise at the memory side; the kernel boundary gives the ordering for free.  (SK_ATOMIC, used
+// only when no workspace is available, accumulates into a pre-zeroed C instead; SK_LAST, below,
+// exchanges through coherent stores and loads without fences, for the wave kernel's few splits.)
 // LOW_M: at most 4 rows in this m-group, all held by lanes 0-15 (rows 4*kb + i of an MFMA tile), so
 // only those lanes take part in the LDS exchange and the epilogue.
 // ------------------------------------------------------------------------------------------------
