@@ -322,6 +322,27 @@ def test_single_launch_split_k_interleaved_and_graph(oracle):
         check(f"eager after replay {rep}")
 
 
+def test_single_launch_split_k_two_streams(oracle):
+    """Two streams run the in-launch split-K sum concurrently (each stream has its own counters and
+    partials): alternating calls without synchronisation give the oracle's C on both."""
+    s1, s2 = hr.Stream(), hr.Stream()
+    rng = np.random.default_rng(34)
+    jobs = []
+    for s, (m, k, n) in ((s1, (1, 2560, 6912)), (s2, (1, 2560, 6912)), (s1, (4, 4096, 4096)), (s2, (3, 6912, 2560))):
+        a = rng.integers(-128, 128, size=(m, k), dtype=np.int8)
+        wp = rng.integers(0, 256, size=(k, n // 4), dtype=np.uint8)
+        da, db, dc = hr.DeviceBuffer.from_array(a), hr.DeviceBuffer.from_array(wp), hr.DeviceBuffer(4 * m * n)
+        jobs.append((s, m, k, n, da, db, dc, oracle.mm("scalar_mt", a, wp, n)))
+    log("[in-launch split-K] two streams")
+    for it in range(50):
+        for s, m, k, n, da, db, dc, _ in jobs:
+            assert tx.mul_mat_ternary(da.value, db.value, dc.value, m, k, n, stream=s.handle) == 0
+    s1.synchronize()
+    s2.synchronize()
+    for _, m, k, n, _, _, dc, expect in jobs:
+        assert (dc.download(np.int32, (m, n)) == expect).all(), (m, k, n)
+
+
 def test_graph_survives_workspace_growth(oracle):
     """A graph captured while the stream's split-K workspace is small keeps working after a larger
     shape on the same stream grows the workspace (outgrown buffers are retired, never freed)."""
