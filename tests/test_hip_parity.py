@@ -343,6 +343,47 @@ def test_single_launch_split_k_two_streams(oracle):
         assert (dc.download(np.int32, (m, n)) == expect).all(), (m, k, n)
 
 
+def test_host_threads_on_own_streams(oracle):
+    """Four host threads (ctypes releases the GIL) each drive their own stream: the per-(device,
+    stream) workspace, arrival counters and the device-property cache are created concurrently, and
+    every result is exact."""
+    import threading
+    rng = np.random.default_rng(35)
+    shapes = ((1, 2560, 6912), (4, 4096, 4096), (16, 11008, 4096), (64, 4096, 2048), (1, 6912, 2560))
+    cases = []
+    for m, k, n in shapes:
+        a = rng.integers(-128, 128, size=(m, k), dtype=np.int8)
+        wp = rng.integers(0, 256, size=(k, n // 4), dtype=np.uint8)
+        cases.append((m, k, n, hr.DeviceBuffer.from_array(a), hr.DeviceBuffer.from_array(wp),
+                      oracle.mm("scalar_mt", a, wp, n)))
+    errors = []
+
+    def worker(t):
+        try:
+            s = hr.Stream()
+            outs = [hr.DeviceBuffer(4 * m * n) for m, k, n, *_ in cases]
+            for it in range(20):
+                for (m, k, n, da, db, _), dc in zip(cases, outs):
+                    st = tx.mul_mat_ternary(da.value, db.value, dc.value, m, k, n, stream=s.handle)
+                    if st != 0:
+                        errors.append((t, it, m, k, n, st))
+                        return
+            s.synchronize()
+            for (m, k, n, _, _, expect), dc in zip(cases, outs):
+                if not (dc.download(np.int32, (m, n)) == expect).all():
+                    errors.append((t, "mismatch", m, k, n))
+        except Exception as e:  # reported below
+            errors.append((t, repr(e)))
+
+    log("[threads] 4 host threads, own streams")
+    threads = [threading.Thread(target=worker, args=(t,)) for t in range(4)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join()
+    assert not errors, errors
+
+
 def test_graph_survives_workspace_growth(oracle):
     """A graph captured while the stream's split-K workspace is small keeps working after a larger
     shape on the same stream grows the workspace (outgrown buffers are retired, never freed)."""
