@@ -4,7 +4,8 @@
 // It covers what the reference's GPU test checks (tests/test_cuda_matmul.cu:11-43: the naive and
 // tiled host entry points against the scalar CPU kernel, and the tiled shape rejection) and the
 // reference's CPU shape list (tests/test_ternary_matmul.cpp:44-69), plus the device-pointer automatic
-// path on decode / ragged / misaligned shapes, the int8 extreme case and a hipGraph replay.
+// path on decode / ragged / misaligned shapes, the int8 extreme case, a hipGraph replay and the
+// opt-in tile-64 weight layout (host conversion + its entry point).
 // The checker is the CPU oracle (oracle/liboracle.so, a restatement of the reference's scalar
 // kernel): test infrastructure only.  Dependency-free: no test framework, exit status 0 on success.
 //
@@ -213,6 +214,36 @@ void graph_replay() {
     HIP_OK(hipStreamDestroy(st));
 }
 
+// The opt-in tile-64 layout: host conversion, then the tile-64 entry point on device memory.
+void tile64_layout_matches_cpu() {
+    const size_t shapes[][3] = {{1, 2560, 6912}, {4, 4096, 4096}, {24, 2048, 1024}, {64, 4096, 2048}};
+    for (const auto& s : shapes) {
+        const Problem p = make_problem(s[0], s[1], s[2], 31u + (uint32_t)s[0]);
+        const std::vector<int32_t> ref = expected(p);
+        std::vector<uint8_t> wt(p.Wp.size());
+        EXPECT(ternix_interleave_weights_tile64(wt.data(), p.Wp.data(), p.K, p.N) == 0, "conversion");
+        int8_t* dA = nullptr;
+        uint8_t* dW = nullptr;
+        int32_t* dC = nullptr;
+        HIP_OK(hipMalloc(&dA, p.A.size()));
+        HIP_OK(hipMalloc(&dW, wt.size()));
+        HIP_OK(hipMalloc(&dC, ref.size() * sizeof(int32_t)));
+        HIP_OK(hipMemcpy(dA, p.A.data(), p.A.size(), hipMemcpyHostToDevice));
+        HIP_OK(hipMemcpy(dW, wt.data(), wt.size(), hipMemcpyHostToDevice));
+        HIP_OK((hipError_t)ternix_hip_mul_mat_ternary_tile64(dA, dW, dC, (int64_t)p.M, (int64_t)p.K, (int64_t)p.N,
+                                                              nullptr));
+        HIP_OK(hipDeviceSynchronize());
+        std::vector<int32_t> got(ref.size());
+        HIP_OK(hipMemcpy(got.data(), dC, got.size() * sizeof(int32_t), hipMemcpyDeviceToHost));
+        const size_t i = first_mismatch(ref, got);
+        EXPECT(i == ref.size(), "M=%zu K=%zu N=%zu: C[%zu] = %d, expected %d", p.M, p.K, p.N, i,
+               i < got.size() ? got[i] : 0, i < ref.size() ? ref[i] : 0);
+        HIP_OK(hipFree(dA));
+        HIP_OK(hipFree(dW));
+        HIP_OK(hipFree(dC));
+    }
+}
+
 void pack_known_answer() {
     // {1,0,-1,1,-1,0,1,0}: byte 0 = 01 | 00<<2 | 11<<4 | 01<<6 = 0x71, byte 1 = 11 | 00<<2 | 01<<4 | 00<<6 = 0x13.
     const int8_t w[8] = {1, 0, -1, 1, -1, 0, 1, 0};
@@ -237,6 +268,7 @@ int main(int argc, char** argv) {
         {"RaggedAndMisalignedShapes", ragged_and_misaligned_shapes},
         {"ExtremeActivationsDoNotOverflow", extreme_activations_do_not_overflow},
         {"GraphReplay", graph_replay},
+        {"Tile64LayoutMatchesCpu", tile64_layout_matches_cpu},
     };
     if (argc > 1 && std::strcmp(argv[1], "--list") == 0) {
         for (const auto& c : cases) std::printf("%s\n", c.first);

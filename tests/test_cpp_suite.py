@@ -10,7 +10,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 EXE = os.path.join(ROOT, "tests", "cpp", "test_hip_matmul")
 CASES = ["PackKnownAnswer", "NaiveMatchesCpu", "TiledMatchesCpu", "TiledRejectsUnsupportedShape",
          "ReferenceCpuShapes", "DecodeAndPrefillShapes", "RaggedAndMisalignedShapes",
-         "ExtremeActivationsDoNotOverflow", "GraphReplay"]
+         "ExtremeActivationsDoNotOverflow", "GraphReplay", "Tile64LayoutMatchesCpu"]
 
 
 def _exe():
