@@ -371,10 +371,11 @@ int gemm_splits(int M, int K, int N) {
     const bool narrow = ternix_hip::gemm_narrow_wanted(M, K, N);  // 64-column tiles instead of 256
     const long tiles = (long)((M + bm - 1) / bm) * (long)((N / 4 + 63) / 64) * (narrow ? 4 : 1);
     const long cus = cu_count();
-    // K < 4096: the reduce launch and the partial sums cost more than the idle CUs (measured on
-    // MI355X, cold weights, 40-64 rows: 40x1024x4096 7.6 -> 4.9 us without the split, 64x2560x6912
-    // 11.8 -> 8.8 us; at K = 4096 the two are within 5 %, longer K keeps the split).
-    if (env <= 0 && K < 4096) return 1;
+    // K <= 4096: the reduce launch and the partial sums cost more than the idle CUs (measured on
+    // MI355X, cold weights: 40x1024x4096 7.6 -> 4.9 us without the split, 64x2560x6912 11.8 -> 8.8,
+    // 256x1024x11008 31.1 -> 9.7, 256x4096x11008 35.2 -> 25.0; from K = 6144 the split wins:
+    // 128x11008x4096 59.0 -> 22.4 us).
+    if (env <= 0 && K <= 4096) return 1;
     long splits = env > 0 ? env : (tiles * 2 <= cus ? cus / tiles : 1);
     splits = std::min<long>(splits, std::max(1, K / 256));  // at least two 128-row stages per split
     return (int)std::max<long>(1, std::min<long>(splits, 16));
@@ -419,9 +420,9 @@ hipError_t run_gemm(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int
 // the padding) and A into rows of K' bytes, inside the split-K workspace; the aligned kernels then run
 // on the padded problem with split-K, and the reduce writes only the N real columns (zero weights
 // and zero activations in the padding add nothing, so the sums are those of the original problem).
-// Returns hipErrorNotSupported, before launching anything, when this does not apply (no split,
-// graph capture without a large enough workspace, sizes past the workspace cap); the caller then
-// runs the generic kernels.
+// Returns hipErrorNotSupported, before launching anything, when this does not apply (a skinny plan
+// without a split, graph capture without a large enough workspace, sizes past the workspace cap);
+// the caller then runs the generic kernels.
 hipError_t run_padded(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int K, int N, hipStream_t st,
                       const ternix_hip::OutScale& os, bool skinny) {
     const int NB = N / 4;
@@ -447,7 +448,9 @@ hipError_t run_padded(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
             splits = (int)((Kp + k_split - 1) / k_split);
         }
     }
-    if (splits <= 1 && !wave) return hipErrorNotSupported;
+    // The skinny kernels write partials only through a split; the GEMM writes its one slab to the
+    // workspace just the same, and the reduce launch keeps the N real columns.
+    if (splits <= 1 && skinny && !wave) return hipErrorNotSupported;
     // Each split's k-range must fit one int32 accumulator (the skinny plans guarantee it).
     if (!skinny && k_split > ternix_hip::kMaxKPerAccumulator) return hipErrorNotSupported;
     auto up = [](size_t b) { return (b + 255) & ~size_t(255); };
