@@ -102,7 +102,10 @@ int* arrival_counters(hipStream_t st, size_t need, int M, int splits, int sps) {
     if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
     void* p = nullptr;
     if (hipMalloc(&p, kCounterSlots * sizeof(int)) != hipSuccess) return nullptr;
-    if (hipMemsetAsync(p, 0, kCounterSlots * sizeof(int), st) != hipSuccess) return nullptr;
+    if (hipMemsetAsync(p, 0, kCounterSlots * sizeof(int), st) != hipSuccess) {
+        (void)hipFree(p);
+        return nullptr;
+    }
     w.counters = static_cast<int*>(p);
     return w.counters;
 }
