@@ -822,8 +822,9 @@ void skinny_dma_kernel(SkinnyArgs args) {
 // global_load_lds_dwordx4 into a private ring of NSW slots (64 x SW bytes each) and reads them back
 // with ds_read_b64_tr_b8 itself, so only the wave's own vmcnt orders the ring: no workgroup barrier
 // until the four waves' sums are combined at the end.  The activation fragment of a step (16 rows,
-// clamped, 16 bytes per lane) is loaded with the step's DMAs.  Narrow strips give many workgroups
-// without a K split, so a wide-N GEMV can store C directly (one launch, no reduce).
+// clamped, 16 bytes per lane) is loaded with the step's DMAs.  Narrow strips give many workgroups;
+// the host splits K over a few more (blockIdx.x covers strip x split) and, for few splits, the
+// splits are summed inside the launch (SK_LAST), so a decode GEMV is one launch.
 //   * SW = 32: chunk c of row r at position c ^ ((r / 16) % 2) (the two 16-lane groups of a
 //     transposing read use different banks); SW = 16: row r at position r ^ (8 ((r / 16) % 2)).
 // Loads are issued for the same number of steps on every wave (clamped addresses past the range, no
