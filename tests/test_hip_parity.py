@@ -384,6 +384,40 @@ def test_host_threads_on_own_streams(oracle):
     assert not errors, errors
 
 
+def test_random_shapes_all_planners(oracle):
+    """Seeded random shapes across every planner branch (wave GEMV with and without in-launch split
+    sums, DMA-staged GEMV, padded ragged path, narrow and wide GEMMs with and without split-K), on the
+    automatic path and, where the shape allows, on tile-64 weights; each compared with the oracle."""
+    rng = np.random.default_rng(2024)
+    s = hr.Stream()
+    done = 0
+    for t in range(40):
+        m = int(rng.choice([1, 2, 3, 4, 5, 8, 16, 17, 24, 32, 33, 48, 64, 65, 96, 128, 200]))
+        k = int(rng.integers(1, 9000)) if t % 2 else int(rng.integers(1, 70)) * 128
+        n = 4 * int(rng.integers(1, 3000)) if t % 3 else 256 * int(rng.integers(1, 40))
+        if m * k * n > 5e8:
+            continue
+        a = rng.integers(-128, 128, size=(m, k), dtype=np.int8)
+        wp = rng.integers(0, 256, size=(k, n // 4), dtype=np.uint8)
+        wp &= 0xFF ^ ((wp & 0xAA) & ~((wp & 0x55) << 1) & 0xAA)  # no code 10
+        expect = oracle.mm("scalar_mt", a, wp, n)
+        log(f"[random] M={m} K={k} N={n}")
+        da, db, dc = hr.DeviceBuffer.from_array(a), hr.DeviceBuffer.from_array(wp), hr.DeviceBuffer(4 * m * n)
+        dc.upload(np.full(m * n, GARBAGE, np.int32))
+        assert tx.mul_mat_ternary(da.value, db.value, dc.value, m, k, n, stream=s.handle) == 0
+        s.synchronize()
+        assert (dc.download(np.int32, (m, n)) == expect).all(), ("auto", m, k, n)
+        if k % 128 == 0 and n % 256 == 0:
+            dt = hr.DeviceBuffer(wp.nbytes)
+            assert tx.interleave_tile64_device(dt.value, db.value, k, n, s.handle) == 0
+            dc.upload(np.full(m * n, GARBAGE, np.int32))
+            assert tx.mul_mat_ternary(da.value, dt.value, dc.value, m, k, n, stream=s.handle, path="tile64") == 0
+            s.synchronize()
+            assert (dc.download(np.int32, (m, n)) == expect).all(), ("tile64", m, k, n)
+        done += 1
+    assert done >= 20
+
+
 def test_graph_survives_workspace_growth(oracle):
     """A graph captured while the stream's split-K workspace is small keeps working after a larger
     shape on the same stream grows the workspace (outgrown buffers are retired, never freed)."""
