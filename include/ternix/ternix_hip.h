@@ -218,6 +218,10 @@ int ternix_hip_interleave_weights_tile64(uint8_t* dOut, const uint8_t* dPacked, 
  * on the row-major layout. */
 int ternix_hip_mul_mat_ternary_tile64(const int8_t* dA, const uint8_t* dWt, int32_t* dC, int64_t M, int64_t K,
                                       int64_t N, void* stream);
+/* ternix_hip_mul_mat_ternary_dequant on tile-64 weights: Y = (float)C * (dRowScale[m] * w_scale),
+ * fp32 M x N, the scaling fused into the output; same contract as ternix_hip_mul_mat_ternary_tile64. */
+int ternix_hip_mul_mat_ternary_tile64_dequant(const int8_t* dA, const uint8_t* dWt, float* dY, int64_t M, int64_t K,
+                                              int64_t N, const float* dRowScale, float w_scale, void* stream);
 
 #ifdef __cplusplus
 }

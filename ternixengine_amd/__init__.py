@@ -31,6 +31,7 @@ from ._lib import LibraryNotBuilt, load as _load  # noqa: F401
 __all__ = ["pack_ternary", "unpack_ternary", "ternary_matmul", "mul_mat_ternary", "pack_ternary_device",
            "unpack_ternary_device", "quantize_weights_absmean", "quantize_activations", "ternary_matmul_dequant", "rms_norm", "swiglu",
            "ffn_forward", "interleave_tile64", "interleave_tile64_device", "ternary_matmul_tile64",
+           "ternary_matmul_tile64_dequant",
            "has_cuda", "has_hip", "HIP_IMPLS", "ternix_error"]
 
 has_cuda = False
@@ -208,6 +209,29 @@ def ternary_matmul_tile64(a, w_tile64, n):
     _check(_load().ternix_hip_mul_mat_ternary_tile64(da.value, dw.value, dc.value, m, k, n, None))
     hr.synchronize()
     return dc.download(np.int32, (m, n))
+
+
+def ternary_matmul_tile64_dequant(a, w_tile64, n, row_scale, w_scale):
+    """ternary_matmul_dequant on tile-64 weights: (A @ W) * row_scale[:, None] * w_scale as fp32, W in
+    the tile-64 layout with N columns (K % 128 == 0, N % 256 == 0)."""
+    from . import hip_runtime as hr
+    a = np.ascontiguousarray(np.asarray(a).astype(np.int8, copy=False))
+    wt = np.ascontiguousarray(np.asarray(w_tile64).astype(np.uint8, copy=False)).reshape(-1)
+    rs = np.ascontiguousarray(np.asarray(row_scale, dtype=np.float32).reshape(-1))
+    if a.ndim != 2:
+        raise ValueError("A must be (M, K)")
+    m, k = a.shape
+    n = int(n)
+    if n % 4 != 0 or wt.size != k * (n // 4):
+        raise ValueError("w_tile64 must hold K * N/4 bytes")
+    if rs.shape[0] != m:
+        raise ValueError("row_scale must have M entries")
+    da, dw, drs = hr.DeviceBuffer.from_array(a), hr.DeviceBuffer.from_array(wt), hr.DeviceBuffer.from_array(rs)
+    dy = hr.DeviceBuffer(max(4 * m * n, 4))
+    _check(_load().ternix_hip_mul_mat_ternary_tile64_dequant(da.value, dw.value, dy.value, m, k, n, drs.value,
+                                                             float(w_scale), None))
+    hr.synchronize()
+    return dy.download(np.float32, (m, n))
 
 
 def _check(status):

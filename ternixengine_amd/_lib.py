@@ -56,6 +56,8 @@ def load():
     lib.ternix_hip_quantize_activations.restype = ctypes.c_int
     lib.ternix_hip_mul_mat_ternary_dequant.argtypes = [vp, vp, vp, i64, i64, i64, vp, ctypes.c_float, vp]
     lib.ternix_hip_mul_mat_ternary_dequant.restype = ctypes.c_int
+    lib.ternix_hip_mul_mat_ternary_tile64_dequant.argtypes = [vp, vp, vp, i64, i64, i64, vp, ctypes.c_float, vp]
+    lib.ternix_hip_mul_mat_ternary_tile64_dequant.restype = ctypes.c_int
     lib.ternix_quantize_weights_absmean.argtypes = [vp, vp, vp, ctypes.c_size_t]
     lib.ternix_quantize_weights_absmean.restype = ctypes.c_int
     f32 = ctypes.c_float

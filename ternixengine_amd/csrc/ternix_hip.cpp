@@ -509,7 +509,8 @@ hipError_t run_auto(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int
 // (the contiguous reads make it faster than the DMA kernel for long K too: cold cfg2 down 6.7 us
 // against 7.8 on the row-major layout; TERNIX_SKINNY_WAVE="16,2,splits" forces the split count,
 // experiments).  Larger M runs the LDS-DMA GEMMs with the contract layout's split-K planning.
-hipError_t run_tile64(const int8_t* dA, const uint8_t* dWt, int32_t* dC, int M, int K, int N, hipStream_t st) {
+hipError_t run_tile64(const int8_t* dA, const uint8_t* dWt, int32_t* dC, int M, int K, int N, hipStream_t st,
+                      const ternix_hip::OutScale& os = ternix_hip::OutScale{}) {
     if (M <= 32) {
         const int nsteps = K / 64;
         int sp = wave_splits(M, K, N);
@@ -527,10 +528,10 @@ hipError_t run_tile64(const int8_t* dA, const uint8_t* dWt, int32_t* dC, int M, 
         }
         int* cnt = partials ? arrival_counters(st, (size_t)(N / 4 / 16) * (size_t)((M + 15) / 16), M, splits, sps)
                             : nullptr;
-        return ternix_hip::launch_skinny_wave(dA, dWt, dC, M, K, N, 16, 2, splits, sps, partials, st,
-                                              ternix_hip::OutScale{}, 0, ternix_hip::ActQuant{}, 1, cnt);
+        return ternix_hip::launch_skinny_wave(dA, dWt, dC, M, K, N, 16, 2, splits, sps, partials, st, os, 0,
+                                              ternix_hip::ActQuant{}, 1, cnt);
     }
-    return run_gemm(dA, dWt, dC, M, K, N, st, ternix_hip::OutScale{}, 1);
+    return run_gemm(dA, dWt, dC, M, K, N, st, os, 1);
 }
 
 enum class Path { Auto, Skinny, Gemm, Naive };
@@ -831,6 +832,25 @@ int ternix_hip_mul_mat_ternary_tile64(const int8_t* dA, const uint8_t* dWt, int3
         return (int)hipErrorInvalidValue;
     if (trivial) return (int)hipSuccess;
     return (int)run_tile64(dA, dWt, dC, (int)M, (int)K, (int)N, static_cast<hipStream_t>(stream));
+}
+
+int ternix_hip_mul_mat_ternary_tile64_dequant(const int8_t* dA, const uint8_t* dWt, float* dY, int64_t M, int64_t K,
+                                              int64_t N, const float* dRowScale, float w_scale, void* stream) {
+    bool trivial = false;
+    hipError_t e = validate(dA, dWt, dY, M, K, N, &trivial);
+    if (e != hipSuccess) return (int)e;
+    if (K % 128 != 0 || N % 256 != 0 || (size_t)K * (size_t)(N / 4) >= ((size_t)1 << 32) ||
+        reinterpret_cast<uintptr_t>(dA) % 16 != 0 || reinterpret_cast<uintptr_t>(dWt) % 16 != 0)
+        return (int)hipErrorInvalidValue;
+    if (trivial) return (int)hipSuccess;
+    if (dRowScale == nullptr) return (int)hipErrorInvalidValue;
+    ternix_hip::OutScale os;
+    os.Y = dY;
+    os.rs = dRowScale;
+    os.ws = w_scale;
+    // As in ternix_hip_mul_mat_ternary_dequant: an int32 C, where a path needs one, lives in dY.
+    return (int)run_tile64(dA, dWt, reinterpret_cast<int32_t*>(dY), (int)M, (int)K, (int)N,
+                           static_cast<hipStream_t>(stream), os);
 }
 
 const char* ternix_hip_error_string(int status) {

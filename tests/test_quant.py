@@ -163,6 +163,24 @@ def test_gpu_dequant_matmul_matches_oracle(oracle, shape):
 
 
 @gpu
+@pytest.mark.parametrize("shape", [(1, 2560, 6912), (1, 6912, 2560), (4, 4096, 1024), (24, 2048, 1024),
+                                   (64, 1024, 512), (200, 1024, 512)])
+def test_gpu_tile64_dequant_matches_oracle(oracle, shape):
+    """The dequantising matmul on tile-64 weights: the same float outputs, bit for bit."""
+    m, k, n = shape
+    log(f"[tile-64 dequant matmul] M={m} K={k} N={n}")
+    rng = np.random.default_rng(m * 3 + k + n)
+    a = rng.integers(-128, 128, size=(m, k), dtype=np.int8)
+    w = (rng.integers(0, 10, size=(k, n)) // 4 - 1).clip(-1, 1).astype(np.int8)
+    wp = tx.pack_ternary(w)
+    rs = rng.uniform(1e-3, 1.0, size=m).astype(F32)
+    ws = 0.4375
+    y = tx.ternary_matmul_tile64_dequant(a, tx.interleave_tile64(wp), n, rs, ws)
+    yo = oracle_dequant(oracle, _mm_oracle(oracle, a, wp, n), rs, ws)
+    np.testing.assert_array_equal(y, yo)
+
+
+@gpu
 def test_gpu_dequant_long_k_chunks_and_misaligned(oracle):
     """K beyond one accumulator (int32 chunks kept in Y, converted in place) and a Y that is not
     16-byte aligned (scalar stores)."""

@@ -96,6 +96,11 @@ def test_device_entry_points_validate_before_launch():
     assert mm(0x1000, 0x2000, 0x3002, 1, 128, 256, None) == 1      # C misaligned
     assert mm(None, 0x2000, 0x3000, 1, 128, 256, None) == 1
     assert mm(0x1000, 0x2000, 0x3000, -1, 128, 256, None) == 1
+    dq = lib.ternix_hip_mul_mat_ternary_tile64_dequant
+    assert dq(0x1000, 0x2000, 0x3000, 0, 128, 256, 0x4000, 1.0, None) == 0      # M == 0
+    assert dq(0x1000, 0x2000, 0x3000, 1, 64, 256, 0x4000, 1.0, None) == 1      # K % 128
+    assert dq(0x1000, 0x2000, 0x3000, 1, 128, 200, 0x4000, 1.0, None) == 1     # N % 256 (and N % 4)
+    assert dq(0x1000, 0x2000, 0x3000, 1, 128, 256, None, 1.0, None) == 1       # row scales
 
 
 # ---- GPU ----
