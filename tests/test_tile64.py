@@ -5,7 +5,7 @@ The layout is a permutation of the packed K x N/4 bytes (1 KB blocks of 64 k-row
 r ^ (8 * ((r / 16) % 2))).  The host conversion is pinned here against a numpy reshape/transpose
 statement of that permutation; the device conversion must equal the host one byte for byte; the
 matmul on converted weights must equal the CPU oracle on the original packed weights (oracle/,
-a restatement of reference src/cpu_kernels.cpp) and the committed digests of the reference's own
+a restatement of reference src/mul_mat_ternary.cpp) and the committed digests of the reference's own
 outputs, bit for bit.
 """
 import ctypes
@@ -155,8 +155,8 @@ SHAPES = [(m, k, n) for m in (1, 2, 3, 4, 5, 8, 13, 16, 17, 31, 32, 33, 64, 65, 
 @pytest.mark.gpu
 @pytest.mark.parametrize("m,k,n", SHAPES)
 def test_matmul_tile64_matches_oracle(oracle, m, k, n):
-    """Every planner branch: the wave kernel without a K split (K <= 4096), with a split (longer K),
-    low-M and 16-row groups, and the GEMMs (M > 32) with and without split-K."""
+    """Every planner branch: the wave kernel with K splits summed inside the launch and with the
+    reduce launch, low-M and 16-row groups, and the GEMMs (M > 32) with and without split-K."""
     hr = _hr()
     log(f"[tile64 matmul] M={m} K={k} N={n}")
     rng = np.random.default_rng(m * 1000 + k + n)
