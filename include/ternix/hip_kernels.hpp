@@ -41,4 +41,16 @@ inline hipError_t mul_mat_ternary_hip_host(const int8_t* A, const uint8_t* B_pac
         ternix_hip_mul_mat_ternary_host(A, B_packed, C, M, K, N, tiled ? TERNIX_HIP_TILED : TERNIX_HIP_NAIVE));
 }
 
+// Opt-in tile-64 weights (no reference counterpart; the offline re-layout interleave_weights_offline
+// reserves, bitpack.cpp:29-33): convert once, then call the tile-64 matmul with the converted buffer.
+// K % 64 == 0 and N % 64 == 0 for the conversion; K % 128 == 0 and N % 256 == 0 for the matmul.
+inline hipError_t interleave_weights_tile64_hip(uint8_t* dOut, const uint8_t* dPacked, int64_t K, int64_t N,
+                                                hipStream_t stream = nullptr) {
+    return static_cast<hipError_t>(ternix_hip_interleave_weights_tile64(dOut, dPacked, K, N, stream));
+}
+inline hipError_t mul_mat_ternary_hip_tile64(const int8_t* dA, const uint8_t* dWt, int32_t* dC, int64_t M, int64_t K,
+                                             int64_t N, hipStream_t stream = nullptr) {
+    return static_cast<hipError_t>(ternix_hip_mul_mat_ternary_tile64(dA, dWt, dC, M, K, N, stream));
+}
+
 }  // namespace ternix

@@ -230,8 +230,7 @@ void tile64_layout_matches_cpu() {
         HIP_OK(hipMalloc(&dC, ref.size() * sizeof(int32_t)));
         HIP_OK(hipMemcpy(dA, p.A.data(), p.A.size(), hipMemcpyHostToDevice));
         HIP_OK(hipMemcpy(dW, wt.data(), wt.size(), hipMemcpyHostToDevice));
-        HIP_OK((hipError_t)ternix_hip_mul_mat_ternary_tile64(dA, dW, dC, (int64_t)p.M, (int64_t)p.K, (int64_t)p.N,
-                                                              nullptr));
+        HIP_OK(ternix::mul_mat_ternary_hip_tile64(dA, dW, dC, (int64_t)p.M, (int64_t)p.K, (int64_t)p.N));
         HIP_OK(hipDeviceSynchronize());
         std::vector<int32_t> got(ref.size());
         HIP_OK(hipMemcpy(got.data(), dC, got.size() * sizeof(int32_t), hipMemcpyDeviceToHost));
