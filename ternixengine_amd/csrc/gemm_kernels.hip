@@ -767,13 +767,7 @@ hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int
         const long tiles128 = (long)((M + 127) / 128) * tiles_n;
         const bool short_round = splits == 1 && bm == 128 && !bm_env && tiles128 <= cus &&
                                  2 * tiles128 >= cus && (k_end - k_begin) <= 4096;
-        // 256-row tiles whose last round leaves CUs idle while 64-row tiles divide evenly over the CUs
-        // (2048x4096x14336: 448 tiles = 1.75 per CU, against 1792 = 7 per CU): the 64-row tiles, two
-        // workgroups per CU (measured on MI355X: 103.7 -> 100.8 us, three alternating runs).
-        auto balance = [&](long t) { return (double)t / (double)(((t + cus - 1) / cus) * cus); };
-        const long t256 = (long)((M + 255) / 256) * tiles_n, t64 = (long)((M + 63) / 64) * tiles_n;
-        const bool balanced64 = splits == 1 && bm == 256 && !bm_env && balance(t64) >= 1.1 * balance(t256);
-        if (M <= small_m_max || short_round || balanced64) {
+        if (M <= small_m_max || short_round) {
             // Small M (64 rows or fewer): four-wave workgroups on 64-row tiles, so no MFMA row or A
             // byte is spent on padding rows; the caller splits K to fill the chip.
             const dim3 grid64((unsigned)(((M + 63) / 64) * tiles_n), splits);
