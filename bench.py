@@ -336,8 +336,27 @@ def bench_ffn(args, stream, lib):
     ms = time_launches(one, args.steps, args.warmup, stream)
     y = dy.download(np.float32, (m, h))
     moved = per + 4 * m * h * 2 + 4 * h
+    # the same block on tile-64 weights (converted once, untimed), same pools; output compared
+    import ternixengine_amd as tx
+    tgu = [hr.DeviceBuffer.from_array(tx.interleave_tile64(wgu)) for _ in range(copies)]
+    td = [hr.DeviceBuffer.from_array(tx.interleave_tile64(wd)) for _ in range(copies)]
+    dyt = hr.DeviceBuffer(4 * m * h)
+
+    def one_t(i):
+        st = lib.ternix_hip_ffn_forward_tile64(dyt.value, dx.value, dg.value, 1e-5, tgu[i % copies].value, 0.02,
+                                               td[i % copies].value, 0.02, m, h, f, dws.value, nws, stream.handle)
+        if st != 0:
+            raise RuntimeError(f"ffn tile-64 failed: {st}")
+
+    prewarm(one_t, args.prewarm_s / 2, stream)
+    ms_t = time_launches(one_t, args.steps, args.warmup, stream)
+    one(args.steps - 1)
+    one_t(args.steps - 1)
+    stream.synchronize()
+    same = bool((dyt.download(np.float32, (m, h)) == dy.download(np.float32, (m, h))).all())
     return {"us_per_block": ms / args.steps * 1e3, "weight_bytes": per,
-            "gbs": moved / (ms / args.steps * 1e-3) / 1e9, "finite": bool(np.isfinite(y).all())}
+            "gbs": moved / (ms / args.steps * 1e-3) / 1e9, "finite": bool(np.isfinite(y).all()),
+            "tile64_us_per_block": ms_t / args.steps * 1e3, "tile64_equal": same}
 
 
 def bench_configs(args, stream, lib):

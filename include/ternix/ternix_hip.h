@@ -222,6 +222,13 @@ int ternix_hip_mul_mat_ternary_tile64(const int8_t* dA, const uint8_t* dWt, int3
  * fp32 M x N, the scaling fused into the output; same contract as ternix_hip_mul_mat_ternary_tile64. */
 int ternix_hip_mul_mat_ternary_tile64_dequant(const int8_t* dA, const uint8_t* dWt, float* dY, int64_t M, int64_t K,
                                               int64_t N, const float* dRowScale, float w_scale, void* stream);
+/* ternix_hip_ffn_forward with both weight matrices in the tile-64 layout (dWguT: H x 2F, interleaved
+ * (gate, up) columns, dWdT: F x H, each converted by ternix_hip_interleave_weights_tile64): the same
+ * results bit for bit, the same workspace (ternix_hip_ffn_workspace_size).  H % 256 == 0,
+ * F % 128 == 0; no reference counterpart. */
+int ternix_hip_ffn_forward_tile64(float* dY, const float* dX, const float* dNormWeight, float eps,
+                                  const uint8_t* dWguT, float ws_gu, const uint8_t* dWdT, float ws_d, int64_t M,
+                                  int64_t H, int64_t F, void* dWorkspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -31,7 +31,7 @@ from ._lib import LibraryNotBuilt, load as _load  # noqa: F401
 __all__ = ["pack_ternary", "unpack_ternary", "ternary_matmul", "mul_mat_ternary", "pack_ternary_device",
            "unpack_ternary_device", "quantize_weights_absmean", "quantize_activations", "ternary_matmul_dequant", "rms_norm", "swiglu",
            "ffn_forward", "interleave_tile64", "interleave_tile64_device", "ternary_matmul_tile64",
-           "ternary_matmul_tile64_dequant",
+           "ternary_matmul_tile64_dequant", "ffn_forward_tile64",
            "has_cuda", "has_hip", "HIP_IMPLS", "ternix_error"]
 
 has_cuda = False
@@ -284,6 +284,30 @@ def ffn_forward(x, norm_weight, eps, w_gateup_packed, ws_gateup, w_down_packed, 
     dy, dws = hr.DeviceBuffer(max(x.nbytes, 4)), hr.DeviceBuffer(max(nws, 256))
     _check(lib.ternix_hip_ffn_forward(dy.value, dx.value, dg.value, float(eps), dgu.value, float(ws_gateup),
                                       dd.value, float(ws_down), m, h, f, dws.value, nws, None))
+    hr.synchronize()
+    return dy.download(np.float32, (m, h))
+
+
+def ffn_forward_tile64(x, norm_weight, eps, w_gateup_packed, ws_gateup, w_down_packed, ws_down):
+    """ffn_forward with the weights in the tile-64 layout (ternix_hip_ffn_forward_tile64).  Takes the
+    same (K, N/4) packed matrices as ffn_forward and converts them on the host here (a caller keeps the
+    converted copies and calls the C-ABI instead); the result equals ffn_forward's bit for bit."""
+    from . import hip_runtime as hr
+    x = np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+    g = np.ascontiguousarray(np.asarray(norm_weight, dtype=np.float32).reshape(-1))
+    wgu = np.ascontiguousarray(np.asarray(w_gateup_packed, dtype=np.uint8))
+    wd = np.ascontiguousarray(np.asarray(w_down_packed, dtype=np.uint8))
+    m, h = x.shape
+    f = wgu.shape[1] * 2
+    if wgu.shape[0] != h or wd.shape != (f, h // 4) or g.shape[0] != h:
+        raise ValueError("inconsistent FFN shapes")
+    lib = _load()
+    nws = lib.ternix_hip_ffn_workspace_size(m, h, f)
+    dx, dg = hr.DeviceBuffer.from_array(x), hr.DeviceBuffer.from_array(g)
+    dgu, dd = hr.DeviceBuffer.from_array(interleave_tile64(wgu)), hr.DeviceBuffer.from_array(interleave_tile64(wd))
+    dy, dws = hr.DeviceBuffer(max(x.nbytes, 4)), hr.DeviceBuffer(max(nws, 256))
+    _check(lib.ternix_hip_ffn_forward_tile64(dy.value, dx.value, dg.value, float(eps), dgu.value, float(ws_gateup),
+                                             dd.value, float(ws_down), m, h, f, dws.value, nws, None))
     hr.synchronize()
     return dy.download(np.float32, (m, h))
 

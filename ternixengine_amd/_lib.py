@@ -68,6 +68,8 @@ def load():
     lib.ternix_hip_ffn_workspace_size.argtypes = [i64, i64, i64]
     lib.ternix_hip_ffn_workspace_size.restype = ctypes.c_size_t
     lib.ternix_hip_ffn_forward.argtypes = [vp, vp, vp, f32, vp, f32, vp, f32, i64, i64, i64, vp, ctypes.c_size_t, vp]
+    lib.ternix_hip_ffn_forward_tile64.argtypes = lib.ternix_hip_ffn_forward.argtypes
+    lib.ternix_hip_ffn_forward_tile64.restype = ctypes.c_int
     for name in ("ternix_hip_rms_norm", "ternix_hip_rms_norm_quantize", "ternix_hip_swiglu",
                  "ternix_hip_mul_mat_ternary_swiglu", "ternix_hip_ffn_forward"):
         getattr(lib, name).restype = ctypes.c_int

@@ -786,6 +786,61 @@ int ternix_hip_ffn_forward(float* dY, const float* dX, const float* dNormWeight,
     return ternix_hip_mul_mat_ternary_dequant(q2, dWd, dY, M, F, H, rs2, ws_d, stream);
 }
 
+int ternix_hip_ffn_forward_tile64(float* dY, const float* dX, const float* dNormWeight, float eps,
+                                  const uint8_t* dWguT, float ws_gu, const uint8_t* dWdT, float ws_d, int64_t M,
+                                  int64_t H, int64_t F, void* dWorkspace, size_t workspace_bytes, void* stream) {
+    if (M < 0 || H < 0 || F < 0 || M > INT_MAX || H > INT_MAX || 2 * F > INT_MAX) return (int)hipErrorInvalidValue;
+    if (M == 0 || H == 0) return (int)hipSuccess;
+    // The tile-64 matmul contract for both weight matrices: K % 128, N % 256 (H x 2F and F x H).
+    if (H % 256 != 0 || F % 128 != 0 || (2 * F) % 256 != 0 || (size_t)H * (size_t)(2 * F / 4) >= ((size_t)1 << 32) ||
+        (size_t)F * (size_t)(H / 4) >= ((size_t)1 << 32))
+        return (int)hipErrorInvalidValue;
+    const FfnLayout l = ffn_layout(M, H, F);
+    if (dWorkspace == nullptr || workspace_bytes < l.total || reinterpret_cast<uintptr_t>(dWorkspace) % 256 != 0)
+        return (int)hipErrorInvalidValue;
+    if (dY == nullptr || dX == nullptr || dNormWeight == nullptr || dWguT == nullptr || dWdT == nullptr ||
+        reinterpret_cast<uintptr_t>(dWguT) % 16 != 0 || reinterpret_cast<uintptr_t>(dWdT) % 16 != 0)
+        return (int)hipErrorInvalidValue;
+    char* ws = static_cast<char*>(dWorkspace);
+    int8_t* q1 = reinterpret_cast<int8_t*>(ws + l.q1);
+    float* rs1 = reinterpret_cast<float*>(ws + l.rs1);
+    float* h = reinterpret_cast<float*>(ws + l.h);
+    int8_t* q2 = reinterpret_cast<int8_t*>(ws + l.q2);
+    float* rs2 = reinterpret_cast<float*>(ws + l.rs2);
+    int32_t* scratch = reinterpret_cast<int32_t*>(ws + l.scratch);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int m = (int)M, hd = (int)H, f = (int)F;
+    ternix_hip::OutScale os1;
+    os1.Y = h;
+    os1.rs = rs1;
+    os1.ws = ws_gu;
+    os1.swiglu = 1;
+    hipError_t e;
+    if (m <= 16 && hd <= 4096) {
+        // RMSNorm + quantisation of x inside the gate/up GEMV (one launch, whole rows per workgroup).
+        ternix_hip::ActQuant aq1;
+        aq1.mode = 2;
+        aq1.X = dX;
+        aq1.G = dNormWeight;
+        aq1.eps = eps;
+        aq1.rs_out = rs1;
+        e = ternix_hip::launch_skinny_wave(nullptr, dWguT, scratch, m, hd, 2 * f, 16, 2, 1, hd / 64, nullptr, st, os1,
+                                           0, aq1, 1);
+    } else {
+        const int s = ternix_hip_rms_norm_quantize(q1, rs1, dX, dNormWeight, M, H, eps, stream);
+        if (s != 0) return s;
+        e = run_tile64(q1, dWguT, scratch, m, hd, 2 * f, st, os1);
+    }
+    if (e != hipSuccess) return (int)e;
+    e = ternix_hip::launch_quantize_rows(h, q2, rs2, m, f, st);
+    if (e != hipSuccess) return (int)e;
+    ternix_hip::OutScale os2;
+    os2.Y = dY;
+    os2.rs = rs2;
+    os2.ws = ws_d;
+    return (int)run_tile64(q2, dWdT, reinterpret_cast<int32_t*>(dY), m, f, hd, st, os2);
+}
+
 int ternix_hip_quantize_activations(const float* dX, int8_t* dQ, float* dRowScale, int64_t M, int64_t K,
                                     void* stream) {
     if (M < 0 || K < 0 || M > INT_MAX || K > INT_MAX) return (int)hipErrorInvalidValue;

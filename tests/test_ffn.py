@@ -213,11 +213,33 @@ def test_gpu_ffn_forward(oracle, shape):
     assert rel < 0.03, rel   # int8 activation quantisation twice: ~1% relative error
 
 
+@gpu
+@pytest.mark.parametrize("shape", [(1, 2560, 6912), (4, 2560, 6912), (16, 1024, 2816), (24, 512, 1024)])
+def test_gpu_ffn_forward_tile64(shape):
+    """The block on tile-64 weights equals the block on the contract layout, bit for bit (fused
+    RMSNorm + quantisation in the gate/up GEMV for M <= 16, the separate launches above)."""
+    m, hd, f = shape
+    log(f"[ffn tile-64] M={m} H={hd} F={f}")
+    rng = np.random.default_rng(7 * m + hd + f)
+    x = rng.normal(0, 1, (m, hd)).astype(F32)
+    g = rng.normal(1, 0.1, hd).astype(F32)
+    t_gu, t_d = _ffn_weights(rng, hd, f)
+    wgu, wd = tx.pack_ternary(t_gu), tx.pack_ternary(t_d)
+    y = tx.ffn_forward(x, g, 1e-5, wgu, 0.02, wd, 0.03)
+    yt = tx.ffn_forward_tile64(x, g, 1e-5, wgu, 0.02, wd, 0.03)
+    np.testing.assert_array_equal(yt, y)
+
+
 def test_ffn_validation():
     lib = tx._load()
     assert lib.ternix_hip_ffn_workspace_size(1, 2560, 6912) > 0
     # H % 4 and F % 2 are checked before any pointer is used
     assert lib.ternix_hip_ffn_forward(None, None, None, 1e-5, None, 1.0, None, 1.0, 1, 6, 4, None, 0, None) == 1
+    # tile-64: H % 256 and F % 128 are checked before any pointer is used
+    assert lib.ternix_hip_ffn_forward_tile64(None, None, None, 1e-5, None, 1.0, None, 1.0, 1, 2560, 64, None, 0,
+                                             None) == 1
+    assert lib.ternix_hip_ffn_forward_tile64(None, None, None, 1e-5, None, 1.0, None, 1.0, 1, 2500, 6912, None, 0,
+                                             None) == 1
     assert lib.ternix_hip_ffn_forward(None, None, None, 1e-5, None, 1.0, None, 1.0, 1, 8, 3, None, 0, None) == 1
     assert lib.ternix_hip_ffn_forward(None, None, None, 1e-5, None, 1.0, None, 1.0, 1, 8, 4, None, 0, None) == 1
     assert lib.ternix_hip_swiglu(None, None, 1, None) == 0
