@@ -309,6 +309,12 @@ hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
             const int s2 = std::min(8, wave_splits(M, K, N, sw));
             if (s2 >= 4) sp = s2;
         }
+        // Wide matrices leave the wave kernel few splits and long k-ranges per workgroup; beyond 32
+        // k-steps per workgroup the DMA-staged kernel is faster for M <= 16 (measured on MI355X, cold:
+        // 8x8192x28672 31.2 -> 19.1 us, 6x4096x28672 16.9 -> 14.6, 12x6144x16384 17.6 -> 16.6).
+        if (sp > 0 && aq.mode == 0 && M <= 16 && (nsteps + sp - 1) / sp > 32 &&
+            ternix_hip::skinny_dma_ok(dA, dB, M, K, N, 1))
+            sp = 0;
         if (const char* env = skinny_wave_env()) {
             int esw = 0, ensw = 0, esp = 0;
             if (std::sscanf(env, "%d,%d,%d", &esw, &ensw, &esp) == 3 && esp >= 1 &&
