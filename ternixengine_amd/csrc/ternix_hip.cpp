@@ -310,9 +310,11 @@ hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
             if (s2 >= 4) sp = s2;
         }
         // Wide matrices leave the wave kernel few splits and long k-ranges per workgroup; beyond 32
-        // k-steps per workgroup the DMA-staged kernel is faster for M <= 16 (measured on MI355X, cold:
-        // 8x8192x28672 31.2 -> 19.1 us, 6x4096x28672 16.9 -> 14.6, 12x6144x16384 17.6 -> 16.6).
-        if (sp > 0 && aq.mode == 0 && M <= 16 && (nsteps + sp - 1) / sp > 32 &&
+        // k-steps per workgroup (24 for M <= 2) the DMA-staged kernel is faster for M <= 16 (measured
+        // on MI355X, cold: 8x8192x28672 31.2 -> 19.1 us, 6x4096x28672 16.9 -> 14.6, 12x6144x16384
+        // 17.6 -> 16.6, 1x4096x14336 10.2 -> 9.2, 1x14336x4096 10.7 -> 9.6; at 28 steps and M >= 4 the
+        // wave kernel still wins: 4x14336x4096 11.3 against 12.1).
+        if (sp > 0 && aq.mode == 0 && M <= 16 && (nsteps + sp - 1) / sp > (M <= 2 ? 24 : 32) &&
             ternix_hip::skinny_dma_ok(dA, dB, M, K, N, 1))
             sp = 0;
         if (const char* env = skinny_wave_env()) {
