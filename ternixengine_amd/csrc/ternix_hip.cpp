@@ -261,11 +261,12 @@ int wave_splits(int M, int K, int N, int sw = 16) {
     if (env > 0) target = env;
     long sp = (target + units / 2) / std::max(1L, units);
     sp = std::max(1L, std::min(16L, std::min(sp, std::max(1L, nsteps / 2))));
-    // 32-byte strips: at most one workgroup per CU (2 % slack); a CU given a second one finishes last
-    // (cfg3 M=16 down: 8 splits, 256 workgroups 11.8 us; 10 splits, 320 workgroups 15.5 us).
+    // 32-byte strips: at most one workgroup per CU (6 % slack); a CU given a second one finishes last
+    // (cfg3 M=16 down: 8 splits, 256 workgroups 11.8 us; 10 splits, 320 workgroups 15.5 us), while a
+    // few doubled CUs cost less than a smaller split (cfg2 up: 270 workgroups 6.9 us, 216 7.04 us).
     while (sw == 32 && sp > 1) {
         const long sps = (nsteps + sp - 1) / sp;
-        if (units * ((nsteps + sps - 1) / sps) * 50 <= cus * 51) break;
+        if (units * ((nsteps + sps - 1) / sps) * 50 <= cus * 53) break;
         --sp;
     }
     // K <= 4096: few enough splits to sum them inside the launch (measured: cfg1 6.27 us with 10
