@@ -84,6 +84,52 @@ int ternix_hip_mul_mat_ternary_tiled(const int8_t* dA, const uint8_t* dB, int32_
 int ternix_hip_mul_mat_ternary_naive(const int8_t* dA, const uint8_t* dB, int32_t* dC,
                                      int64_t M, int64_t K, int64_t N, void* stream);
 
+/* ---- workspace contract of the automatic path ----
+ * Some plans need device scratch beyond A, B and C: split-K partial sums
+ * ([splits][M][N] int32, K split over workgroups when the output alone cannot fill the
+ * chip: mid-size M against long K, decode shapes with very long K) and, for ragged or
+ * misaligned operands, padded copies of W (K' x N'/4) and A (M x K').  By default the
+ * library owns it (see Workspace above).  Callers that must not allocate on the hot path
+ * size it once with ternix_hip_mul_mat_ternary_workspace_size and pass it in.
+ * No reference counterpart: the reference's device-pointer kernels need no scratch
+ * (src/cuda_kernels.cu:126-140). */
+
+/* Bytes of workspace ternix_hip_mul_mat_ternary_ws needs so that it takes exactly the
+ * plan ternix_hip_mul_mat_ternary would, for 16-byte aligned A and W (as hipMalloc
+ * returns them); 0 when the plan uses none, and for a rejected shape.  The _for form
+ * gives the need for the given operand addresses (only their alignment is used:
+ * misaligned operands are worked on through padded copies, which need more). */
+size_t ternix_hip_mul_mat_ternary_workspace_size(int64_t M, int64_t K, int64_t N);
+size_t ternix_hip_mul_mat_ternary_workspace_size_for(const int8_t* dA, const uint8_t* dB,
+                                                     int64_t M, int64_t K, int64_t N);
+
+/* ternix_hip_mul_mat_ternary with a caller-owned workspace (dWorkspace: 256-byte
+ * aligned, workspace_bytes long; may be NULL with 0 bytes).  Never allocates device
+ * memory.  With at least ternix_hip_mul_mat_ternary_workspace_size(M, K, N) bytes it runs
+ * the automatic plan (except that split sums are never done inside one launch: a
+ * reduce launch adds them); with less it takes a plan that needs no more than given
+ * (for a GEMV with a K split: C is zeroed and the splits add into it with int32 atomics,
+ * exact and order-independent; a ragged shape runs the generic kernels).  Results are
+ * identical either way.  The workspace holds no state between calls; calls sharing one
+ * workspace must be ordered (same stream, or synchronised), as for any buffer two
+ * kernels write.  hipErrorInvalidValue (before any work) for a misaligned workspace. */
+int ternix_hip_mul_mat_ternary_ws(const int8_t* dA, const uint8_t* dB, int32_t* dC,
+                                  int64_t M, int64_t K, int64_t N,
+                                  void* dWorkspace, size_t workspace_bytes, void* stream);
+
+/* Frees the library-owned workspace of (current device, stream) after synchronising
+ * the stream.  The caller guarantees that no hipGraph captured on that stream with
+ * library calls runs again afterwards (it would reference the freed buffers).  The next
+ * call on the stream allocates afresh.  Returns 0 or the hipStreamSynchronize error. */
+int ternix_hip_release_stream(void* stream);
+
+/* Writes a one-line description of the kernel(s) the automatic path would launch for
+ * this call (operand addresses matter only through their alignment; nothing is read or
+ * launched) into buf (len bytes, NUL-terminated).  0, or hipErrorInvalidValue for a
+ * rejected shape or buffer. */
+int ternix_hip_plan_describe(const int8_t* dA, const uint8_t* dB, int64_t M, int64_t K, int64_t N,
+                             char* buf, size_t len);
+
 /* Kernel choice for ternix_hip_mul_mat_ternary_host. */
 enum ternix_hip_variant {
     TERNIX_HIP_AUTO = 0,
@@ -107,6 +153,38 @@ const char* ternix_hip_error_string(int status);
 
 /* Library version as an integer, major*10000 + minor*100 + patch. */
 int ternix_hip_version(void);
+
+/* Number of HIP devices visible to the process (0 when there is none or no
+ * driver); the reference binding's has_cuda probe (pybind11_wrapper.cpp:86-90)
+ * becomes has_hip = ternix_hip_device_count() > 0. */
+int ternix_hip_device_count(void);
+
+/* Test and tuning switches.  The library never reads the environment: its
+ * kernel choice depends only on the call's arguments and the device, unless a
+ * caller sets a switch here.  `key` names a switch and v0..v3 its values (-1:
+ * unset); ternix_hip_debug_reset() clears all of them.  Keys (the planner's
+ * choice is used for an unset value):
+ *   "wave_last" v0      most K splits summed inside one wave-GEMV launch (0: none)
+ *   "skinny_wave" v0..2 0: no wave-pipelined GEMV; else force (strip bytes,
+ *                       ring slots, splits)
+ *   "wave_sw" v0        16: 16-byte wave strips on row-major weights
+ *   "skinny_dma" v0     0: no DMA-staged GEMV; 2..4: its stage count
+ *   "skinny_short" v0   0: no register-staged short GEMV
+ *   "ragged_pad" v0     0: ragged shapes run the generic kernels, not a padded copy
+ *   "gemm_narrow" v0    0 / 1: 64 x 64 GEMM tiles for M <= 64 off / forced
+ *   "gemm_generic" v0   1: the generic GEMM for every GEMM call
+ *   "gemm_splits" v0    GEMM split-K count forced
+ *   "gemm_bm" v0        128 / 256: GEMM tile height forced
+ *   "deep" v0..3        0: no whole-K deep GEMV; else force (strip bytes, waves
+ *                       per workgroup, ring slots, splits)
+ * Returns 0, or 1 (hipErrorInvalidValue) for an unknown key.  Switches are
+ * process-wide; a call running concurrently sees the old or the new value.
+ * No reference counterpart (test hook of this library). */
+int ternix_hip_debug_set(const char* key, int v0, int v1, int v2, int v3);
+void ternix_hip_debug_reset(void);
+/* Number of device allocations the library has made in this process (workspace
+ * buffers, split counters, the host wrapper's temporaries); a test hook. */
+long long ternix_hip_debug_alloc_count(void);
 
 /* ---- weight format (host), C-ABI of reference include/ternix/bitpack.hpp:6-8 ---- */
 

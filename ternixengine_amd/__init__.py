@@ -100,10 +100,8 @@ def ternary_matmul(a, b_packed, impl="hip"):
         raise ValueError(f"unknown impl '{impl}'")
     c = np.empty((m, n), dtype=np.int32)
     status = _load().ternix_hip_mul_mat_ternary_host(_ptr(a), _ptr(b), _ptr(c), m, k, n, HIP_IMPLS[impl])
-    if status != 0:
-        if status == 1:
-            raise ValueError(f"impl '{impl}' rejected shape M={m} K={k} N={n}")
-        raise RuntimeError(f"HIP error: {ternix_error(status)}")
+    if status != 0:  # device-side rejection included, as the reference binding reports it
+        raise RuntimeError(f"HIP error: {ternix_error(status)} (impl '{impl}', M={m} K={k} N={n})")
     return c
 
 

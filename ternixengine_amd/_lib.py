@@ -38,6 +38,23 @@ def load():
     lib.ternix_hip_error_string.argtypes = [ctypes.c_int]
     lib.ternix_hip_error_string.restype = ctypes.c_char_p
     lib.ternix_hip_version.restype = ctypes.c_int
+    lib.ternix_hip_debug_set.argtypes = [ctypes.c_char_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+    lib.ternix_hip_debug_set.restype = ctypes.c_int
+    lib.ternix_hip_debug_reset.argtypes = []
+    lib.ternix_hip_debug_reset.restype = None
+    lib.ternix_hip_debug_alloc_count.argtypes = []
+    lib.ternix_hip_debug_alloc_count.restype = ctypes.c_longlong
+    lib.ternix_hip_mul_mat_ternary_workspace_size.argtypes = [i64, i64, i64]
+    lib.ternix_hip_mul_mat_ternary_workspace_size.restype = ctypes.c_size_t
+    lib.ternix_hip_mul_mat_ternary_workspace_size_for.argtypes = [i8p, i8p, i64, i64, i64]
+    lib.ternix_hip_mul_mat_ternary_workspace_size_for.restype = ctypes.c_size_t
+    lib.ternix_hip_mul_mat_ternary_ws.argtypes = [i8p, i8p, i8p, i64, i64, i64, ctypes.c_void_p, ctypes.c_size_t,
+                                                  ctypes.c_void_p]
+    lib.ternix_hip_mul_mat_ternary_ws.restype = ctypes.c_int
+    lib.ternix_hip_release_stream.argtypes = [ctypes.c_void_p]
+    lib.ternix_hip_release_stream.restype = ctypes.c_int
+    lib.ternix_hip_plan_describe.argtypes = [i8p, i8p, i64, i64, i64, ctypes.c_char_p, ctypes.c_size_t]
+    lib.ternix_hip_plan_describe.restype = ctypes.c_int
     for name in ("ternix_pack_ternary_weights", "ternix_unpack_ternary_weights", "ternix_interleave_weights_offline"):
         f = getattr(lib, name)
         f.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]

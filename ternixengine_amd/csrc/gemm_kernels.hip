@@ -691,10 +691,7 @@ hipError_t launch_gemm_t(const int8_t* A, const uint8_t* B, int32_t* C, int M, i
 // tiles than CUs, e.g. N = 28672, the 256-column tiles are faster).  TERNIX_GEMM_NARROW=0 / 1 turns
 // the choice off / on regardless (experiments).
 bool gemm_narrow_wanted(int M, int K, int N) {
-    static const int env = [] {
-        const char* e = std::getenv("TERNIX_GEMM_NARROW");
-        return e ? std::atoi(e) : -1;
-    }();
+    const int env = debug_get(DBG_GEMM_NARROW);
     const int NB = N >> 2;
     if (env == 0 || M > 64 || NB % 16 != 0 || K % 256 != 0) return false;
     if (env > 0) return true;
@@ -708,47 +705,30 @@ bool gemm_narrow_ok(int M, int K, int N, int k_len, int splits, int k_split) {
 hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int k_begin, int k_end,
                        int accumulate, hipStream_t st, const OutScale& os, int splits, int k_split, int tiled) {
     const int NB = N >> 2;
-    // Experiment switches, read once per process.
-    static const char* const force_generic = std::getenv("TERNIX_GEMM_GENERIC");
+    const bool force_generic = debug_get(DBG_GEMM_GENERIC) == 1;  // tests
     if (splits < 1) splits = 1;
     const bool fast = (K % GF_BK == 0) && ((k_end - k_begin) % GF_BK == 0) && (k_begin % GF_BK == 0) &&
                       (splits == 1 || k_split % GF_BK == 0) &&
                       (NB % GF_BNB == 0) && ((uintptr_t)A % 16 == 0) && ((uintptr_t)B % 16 == 0) &&
                       k_end > k_begin && (size_t)M * (size_t)K < ((size_t)1 << 32) &&
                       (size_t)GF_BK * (size_t)NB < ((size_t)1 << 32) &&
-                      (tiled || !(force_generic && force_generic[0] == '1'));
+                      (tiled || !force_generic);
     // The tile-64 layout is read by the LDS-DMA GEMMs only (whole 128-row stages, at most 4 GiB of W).
     if (tiled && (!fast || (size_t)K * (size_t)NB >= ((size_t)1 << 32))) return hipErrorInvalidValue;
     if (fast) {
         const int vs = ((uintptr_t)(os.Y ? (const void*)os.Y : (const void*)C) % 16) == 0;
         const int tiles_n = NB / GF_BNB;
-        static const char* const bm_env = std::getenv("TERNIX_GEMM_BM");
-        static const char* const wgn_env = std::getenv("TERNIX_GEMM_WGN");
-        static const char* const bk_env = std::getenv("TERNIX_GEMM_BK");
+        const int bm_env = debug_get(DBG_GEMM_BM);
         // Measured on MI355X (cfg4 shapes): 256-row tiles only when they still give >= 1.5 tiles per
         // CU, else 128-row tiles; 8 waves as 2 (M) x 4 (N); 128-deep stages.
         const int cus = device_cu_count();
         int bm = (splits == 1 && (long)((M + 255) / 256) * tiles_n * 2 >= 3L * cus) ? 256 : 128;
-        if (bm_env) bm = std::atoi(bm_env) == 128 ? 128 : 256;
-        const int wgn = wgn_env && std::atoi(wgn_env) == 2 ? 2 : 4;
-        int bk = 128;
-        if (bk_env && std::atoi(bk_env) == 256 && bm == 128 && (k_end - k_begin) % 256 == 0) bk = 256;
+        if (bm_env > 0) bm = bm_env == 128 ? 128 : 256;
         const dim3 grid(((M + bm - 1) / bm) * tiles_n, splits);
         // 128-row tiles run the software-pipelined kernel (measured faster on MI355X); 256-row tiles
         // keep gemm_fast_kernel, whose wave tile leaves no registers for a second fragment set.
-        static const int pipe_env = [] {
-            const char* e = std::getenv("TERNIX_GEMM_PIPE");
-            return e ? std::atoi(e) : -1;
-        }();
-        const int pipe = pipe_env >= 0 ? (pipe_env == 1 && bm == 256 ? 0 : pipe_env) : (bm == 128 ? 1 : 0);
-        static const int pipe_ns = [] {
-            const char* e = std::getenv("TERNIX_GEMM_NS");
-            return e && std::atoi(e) == 4 ? 4 : 3;
-        }();
-        static const int small_m_max = [] {
-            const char* e = std::getenv("TERNIX_GEMM_SMALLM");  // experiments only
-            return e ? std::atoi(e) : 64;
-        }();
+        const int pipe = bm == 128 ? 1 : 0;
+        constexpr int small_m_max = 64;
         if (M <= small_m_max && gemm_narrow_ok(M, K, N, k_end - k_begin, splits, k_split)) {
             // 64 x 64 output tiles (16 bytes of every weight row): enough workgroups without a K
             // split where the 256-column tiles would need one; one m-tile per wave, 256-deep stages.
@@ -765,7 +745,7 @@ hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int
         // of 64-row tiles per CU instead, whose barriers and final stores overlap each other's work
         // (measured on MI355X: 29.5 -> 27.9 us; with long K or several rounds the 128-row tiles win).
         const long tiles128 = (long)((M + 127) / 128) * tiles_n;
-        const bool short_round = splits == 1 && bm == 128 && !bm_env && tiles128 <= cus &&
+        const bool short_round = splits == 1 && bm == 128 && bm_env <= 0 && tiles128 <= cus &&
                                  2 * tiles128 >= cus && (k_end - k_begin) <= 4096;
         if (M <= small_m_max || short_round) {
             // Small M (64 rows or fewer): four-wave workgroups on 64-row tiles, so no MFMA row or A
@@ -789,12 +769,7 @@ hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int
             hipLaunchKernelGGL((gemm_pipe_kernel<BM_, WGN_, NS_, BK_, 8, GF_BNB, false>), grid, dim3(GF_THREADS), 0, \
                                st, A, B, C, M, K, N, tiles_n, k_begin, k_end, accumulate, vs, k_split, os);      \
     } while (0)
-            if (bk == 256 && wgn == 4) TX_GP_LAUNCH(128, 4, 3, 256);
-            else if (bk == 256) TX_GP_LAUNCH(128, 2, 3, 256);
-            else if (wgn == 4 && pipe_ns == 4) TX_GP_LAUNCH(128, 4, 4, 128);
-            else if (wgn == 4) TX_GP_LAUNCH(128, 4, 3, 128);
-            else if (pipe_ns == 4) TX_GP_LAUNCH(128, 2, 4, 128);
-            else TX_GP_LAUNCH(128, 2, 3, 128);
+            TX_GP_LAUNCH(128, 4, 3, 128);
 #undef TX_GP_LAUNCH
             return hipGetLastError();
         }
@@ -807,12 +782,7 @@ hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int
             hipLaunchKernelGGL((gemm_fast_kernel<BM_, WGN_, NS_, BK_, false>), grid, dim3(GF_THREADS), 0, st, A,  \
                                B, C, M, K, N, tiles_n, k_begin, k_end, accumulate, vs, k_split, os);            \
     } while (0)
-        if (bm == 256 && wgn == 4) TX_GF_LAUNCH(256, 4, 3, 128);
-        else if (bm == 256) TX_GF_LAUNCH(256, 2, 3, 128);
-        else if (bk == 256 && wgn == 4) TX_GF_LAUNCH(128, 4, 3, 256);
-        else if (bk == 256) TX_GF_LAUNCH(128, 2, 3, 256);
-        else if (wgn == 4) TX_GF_LAUNCH(128, 4, 4, 128);
-        else TX_GF_LAUNCH(128, 2, 4, 128);
+        TX_GF_LAUNCH(256, 4, 3, 128);
 #undef TX_GF_LAUNCH
         return hipGetLastError();
     }

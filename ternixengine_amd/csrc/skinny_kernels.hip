@@ -75,6 +75,7 @@ struct SkinnyArgs {
     int line_units;       // skinny_wave_kernel: block -> strip mapping by 128-byte line units
     int tiled;            // skinny_wave_kernel: W in the tile-64 layout (kernel_common.h)
     int* cnt;             // SK_LAST: arrival counters, one per (m-group, strip), zero between calls
+    int order;            // SK_LAST: 1 = C++ release/acquire at agent scope, 0 = coherent accesses only
 };
 
 // One k-step of MFMA work for one 16-row x 4-byte-column block: raw[r] is the dword of row r.
@@ -1059,15 +1060,31 @@ void skinny_wave_kernel(SkinnyArgs args) {
                 for (int g = 0; g < G; ++g) {
                     if ((LOW_M && kb != 0) || row >= M) continue;
                     int32_t* out = mine + (size_t)row * (size_t)args.N + 4 * (bc0 + 16 * g + q);
+                    if (args.order) {
+                        *reinterpret_cast<v4i*>(out) =
+                            v4i{acc[g][0][i] >> 6, acc[g][1][i] >> 6, acc[g][2][i] >> 6, acc[g][3][i] >> 6};
+                        continue;
+                    }
 #pragma unroll
                     for (int j = 0; j < 4; ++j)
                         __hip_atomic_store(out + j, acc[g][j][i] >> 6, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 }
             }
-            __builtin_amdgcn_s_waitcnt(0);  // the partial stores are complete, coherent at agent scope
-            __atomic_signal_fence(__ATOMIC_SEQ_CST);
-            if (lane == 0)
-                s_last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+            if (!args.order) {
+                __builtin_amdgcn_s_waitcnt(0);  // the partial stores are complete, coherent at agent scope
+                __atomic_signal_fence(__ATOMIC_SEQ_CST);
+                if (lane == 0)
+                    s_last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                             args.splits - 1;
+            }
+        }
+        if (args.order) {
+            // Release/acquire form: the barrier orders every partial store of the workgroup before
+            // thread 0's agent-scope release, and its acquire (with the barrier after it) orders the
+            // last arriver's loads after every other split's release.
+            __syncthreads();
+            if (tid == 0)
+                s_last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) ==
                          args.splits - 1;
         }
         __syncthreads();
@@ -1303,10 +1320,7 @@ hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, i
     const int mt = M <= 16 ? 1 : 2;
     const int mgroups = (M + 16 * mt - 1) / (16 * mt);
     hipError_t e;
-    static const bool no_short = [] {
-        const char* e = std::getenv("TERNIX_SKINNY_SHORT");
-        return e && e[0] == '0';
-    }();
+    const bool no_short = debug_get(DBG_SKINNY_SHORT) == 0;
     if (dma_ns != 0 && (!skinny_dma_aq_ok(aq.mode, K, splits) || dma_ns < 2 || dma_ns > 4 ||
                         !skinny_dma_ok(A, B, M, K, N, steps_per_split)))
         return hipErrorInvalidValue;
@@ -1384,6 +1398,7 @@ hipError_t launch_skinny_wave(const int8_t* A, const uint8_t* B, int32_t* C, int
     SkinnyArgs a{A, B, C, partials, M, K, N, steps_per_split, splits, mode, vec_store, 1, 1,
                  (mode == SK_STORE || mode == SK_LAST) ? os : OutScale{}};
     a.cnt = counters;
+    a.order = debug_get(DBG_SK_ORDER) == 1;
     a.n_out = n_out;
     a.tiled = tiled;
     a.X = aq.X;
@@ -1393,11 +1408,7 @@ hipError_t launch_skinny_wave(const int8_t* A, const uint8_t* B, int32_t* C, int
     // Line units: 8 XCDs x (128 / sw) strips x enough rounds for every (split, line-group) unit.
     // Measured on MI355X (cold weights): line units help the one-launch shapes (cfg1 5.76 -> 5.24 us,
     // cfg2 up 6.75 -> 6.5, ragged 17x4093x1028 13.1 -> 11.5) and cost 2 % with a K split.
-    static const int lu_env = [] {
-        const char* e = std::getenv("TERNIX_WAVE_LINES");  // experiments: 0 / 1 forces the mapping
-        return e ? std::atoi(e) : -1;
-    }();
-    a.line_units = lu_env >= 0 ? lu_env : (splits == 1);
+    a.line_units = (splits == 1);
     const int spl = 128 / sw, units = splits * ((NB / sw + spl - 1) / spl);
     const unsigned gx = a.line_units ? (unsigned)(8 * spl * ((units + 7) / 8)) : (unsigned)((NB / sw) * splits);
     const dim3 grid(gx, 1, (M + 15) / 16), block(256);

@@ -23,6 +23,26 @@ struct OutScale {
     int swiglu = 0;
 };
 
+// Test and tuning switches (set only through ternix_hip_debug_set; never read from the environment).
+// Each key holds up to four ints; debug_get returns -1 for a value that is not set, and the planners
+// then make their normal choice.
+enum DebugKey : int {
+    DBG_WAVE_LAST = 0,   // [0] largest split count summed inside the wave GEMV launch (0: never)
+    DBG_SKINNY_WAVE,     // [0] == 0: no wave-pipelined GEMV; else (sw, nsw, splits) forced
+    DBG_WAVE_SW,         // [0] strip width of the wave-pipelined GEMV on row-major weights (16 / 32)
+    DBG_SKINNY_DMA,      // [0] == 0: no DMA-staged GEMV; 2..4: its stage count
+    DBG_SKINNY_SHORT,    // [0] == 0: no register-staged short GEMV
+    DBG_RAGGED_PAD,      // [0] == 0: ragged shapes run the generic kernels instead of a padded copy
+    DBG_GEMM_NARROW,     // [0] 0 / 1: 64 x 64 GEMM tiles for M <= 64 off / forced
+    DBG_GEMM_GENERIC,    // [0] == 1: the generic (register-staged) GEMM for every GEMM call
+    DBG_GEMM_SPLITS,     // [0] GEMM split-K count forced
+    DBG_GEMM_BM,         // [0] 128 / 256: GEMM tile height forced
+    DBG_DEEP,            // [0] == 0: no whole-K deep GEMV; else (sw, nw, nsw, splits) forced
+    DBG_SK_ORDER,        // [0] 1: release/acquire (agent scope) for the in-launch split sums
+    DBG_COUNT
+};
+int debug_get(DebugKey key, int idx = 0);
+
 hipError_t launch_zero(int32_t* C, size_t n, hipStream_t st);
 // LDS bytes the skinny fast kernel uses for one workgroup's activation slice (the rows of one
 // m-group x steps_per_split * 64 bytes, each row padded by 16 bytes); the fast kernel runs only up
@@ -97,6 +117,15 @@ hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int
 hipError_t launch_splitk_reduce(const int32_t* P, int32_t* C, int M, int N, int splits, const OutScale& os,
                                 hipStream_t st, int n_in = 0);
 // (n_in > N: the partials have n_in columns per row, of which the first N are summed into C.)
+// Whole-K decode GEMV (skinny_deep.hip): sw = 16 / 32-byte strips, nw = 8 / 16 waves per workgroup,
+// nsw ring slots per wave (skinny_deep_config_ok lists the built combinations).  splits == 1 stores C
+// (or os.Y, n_out columns when n_out > 0) directly; splits > 1 writes [splits][M][N] partials and the
+// reduce launch sums them.  Needs K % 64 == 0, N/4 % sw == 0, 16-byte aligned A and W.
+bool skinny_deep_config_ok(int sw, int nw, int nsw);
+bool skinny_deep_ok(const int8_t* A, const uint8_t* B, int M, int K, int N, int sw);
+hipError_t launch_skinny_deep(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int sw, int nw,
+                              int nsw, int splits, int steps_per_split, int32_t* partials, hipStream_t st,
+                              const OutScale& os = OutScale{}, int n_out = 0, int tiled = 0);
 // Tile-64 weight layout (opt-in; kernel_common.h): Wt = the K x N/4 packed W as 1 KB blocks of 64
 // k-rows x 16 bytes.  K % 64 == 0, N/4 % 16 == 0, 16-byte aligned, Wt != W.
 hipError_t launch_tile64(const uint8_t* W, uint8_t* Wt, int K, int N, hipStream_t st);

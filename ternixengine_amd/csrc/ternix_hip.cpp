@@ -13,12 +13,26 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <cstdarg>
 #include <map>
 #include <mutex>
 #include <utility>
 #include <vector>
 
 #include "ternary_kernels.h"
+
+namespace ternix_hip {
+namespace {
+// Switch values + 1 (0: not set), per key and index; relaxed atomics because a test may set a switch
+// while another thread is inside a call (the call then sees the old or the new value).
+std::atomic<int> g_debug[DBG_COUNT][4];
+}  // namespace
+
+int debug_get(DebugKey key, int idx) {
+    if ((int)key < 0 || (int)key >= DBG_COUNT || idx < 0 || idx > 3) return -1;
+    return g_debug[key][idx].load(std::memory_order_relaxed) - 1;
+}
+}  // namespace ternix_hip
 
 namespace {
 
@@ -43,6 +57,20 @@ struct Workspace {
 };
 std::mutex g_ws_mutex;
 std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
+std::atomic<long long> g_alloc_count{0};  // device allocations made by the library (a test hook)
+
+// Every device allocation of the library goes through here.  A failed hipMalloc leaves its error in
+// the thread's last-error slot, which the launchers read back with hipGetLastError after their
+// launch; the caller falls back to a path that needs no allocation, so the error is cleared here.
+hipError_t lib_malloc(void** p, size_t bytes) {
+    g_alloc_count.fetch_add(1, std::memory_order_relaxed);
+    const hipError_t e = hipMalloc(p, bytes);
+    if (e != hipSuccess) {
+        *p = nullptr;
+        (void)hipGetLastError();
+    }
+    return e;
+}
 
 void* workspace(hipStream_t st, size_t bytes) {
     int dev = 0;
@@ -58,7 +86,7 @@ void* workspace(hipStream_t st, size_t bytes) {
     size_t nb = std::max(bytes, grown);
     nb = (nb + (size_t(1) << 20) - 1) & ~((size_t(1) << 20) - 1);
     void* p = nullptr;
-    if (hipMalloc(&p, nb) != hipSuccess) return nullptr;
+    if (lib_malloc(&p, nb) != hipSuccess) return nullptr;
     if (w.ptr) w.retired.push_back(w.ptr);  // sizes at least double, so retired memory < the live buffer
     w.ptr = p;
     w.bytes = nb;
@@ -70,13 +98,10 @@ void* workspace(hipStream_t st, size_t bytes) {
 // MI355X, cold weights, one box: with 2-5 splits the single launch wins (cfg2 up 7.7 -> 7.0 us,
 // cfg3 M=4 up 11.1 -> 9.2, tile-64 cfg5 big 15.6 -> 15.0); from about 8 splits the serialised
 // arrivals on each counter cost more than the launch (cfg3 M=16 down 12.1 -> 12.8 us).
-// TERNIX_WAVE_LAST overrides it (experiments; 0 turns the scheme off).
+// The DBG_WAVE_LAST switch overrides it (tests; 0 turns the scheme off).
 int last_max_splits() {
-    static const int v = [] {
-        const char* e = std::getenv("TERNIX_WAVE_LAST");
-        return e ? std::atoi(e) : 5;
-    }();
-    return v;
+    const int v = ternix_hip::debug_get(ternix_hip::DBG_WAVE_LAST);
+    return v >= 0 ? v : 5;
 }
 
 // Arrival counters of the wave GEMV's single-launch split-K (kCounterSlots ints per (device, stream),
@@ -101,14 +126,67 @@ int* arrival_counters(hipStream_t st, size_t need, int M, int splits, int sps) {
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
     void* p = nullptr;
-    if (hipMalloc(&p, kCounterSlots * sizeof(int)) != hipSuccess) return nullptr;
-    if (hipMemsetAsync(p, 0, kCounterSlots * sizeof(int), st) != hipSuccess) {
+    if (lib_malloc(&p, kCounterSlots * sizeof(int)) != hipSuccess) return nullptr;
+    // A fill kernel, not hipMemsetAsync (never inside capture here anyway: checked above).
+    if (ternix_hip::launch_zero(static_cast<int32_t*>(p), kCounterSlots, st) != hipSuccess) {
+        (void)hipGetLastError();
         (void)hipFree(p);
         return nullptr;
     }
     w.counters = static_cast<int*>(p);
     return w.counters;
 }
+
+// Execution context of one call: the stream, where split-K partials and padded copies live, and a
+// dry-run mode for planning queries.
+//   * library-owned workspace (default): the per-(device, stream) buffers above;
+//   * caller-owned workspace (ternix_hip_mul_mat_ternary_ws, and the fixed device scratch of
+//     ternix_hip_mul_mat_ternary_noalloc): a request larger than the buffer gets nullptr (the planners
+//     then take a path that needs less), and the in-launch split sum is not used (its counters must be
+//     zero between calls, which only library-owned memory guarantees);
+//   * dry run (ternix_hip_mul_mat_ternary_workspace_size, ternix_hip_plan_describe): the caller-owned
+//     rules with an unbounded buffer; requests are recorded, nothing is launched, and the chosen
+//     kernel is described in `desc`.
+struct Ctx {
+    hipStream_t st = nullptr;
+    char* caller = nullptr;
+    size_t caller_bytes = 0;
+    bool use_caller = false;
+    bool dry = false;
+    size_t need = 0;
+    char desc[192] = {0};
+
+    void* get(size_t bytes) {
+        if (bytes > kWorkspaceMax) return nullptr;
+        if (dry) {
+            need = std::max(need, bytes);
+            return reinterpret_cast<void*>(uintptr_t(4096));  // never dereferenced: nothing launches
+        }
+        if (use_caller) return bytes <= caller_bytes ? caller : nullptr;
+        return workspace(st, bytes);
+    }
+    int* counters(size_t slots, int M, int splits, int sps) {
+        if (dry || use_caller) return nullptr;
+        return arrival_counters(st, slots, M, splits, sps);
+    }
+    void note(const char* fmt, ...) __attribute__((format(printf, 2, 3))) {
+        if (!dry) return;
+        va_list ap;
+        va_start(ap, fmt);
+        std::vsnprintf(desc, sizeof(desc), fmt, ap);
+        va_end(ap);
+    }
+};
+// Library-owned-workspace context of a stream (a fresh temporary per call).
+struct CtxOf {
+    Ctx c;
+    explicit CtxOf(hipStream_t st) { c.st = st; }
+    operator Ctx&() { return c; }
+};
+inline Ctx& ctx_ref(CtxOf&& t) { return t.c; }
+#define ctx_of(st) ctx_ref(CtxOf(st))
+// Launch unless planning only.
+#define TX_LAUNCH(c, expr) ((c).dry ? hipSuccess : (expr))
 
 // Shape / pointer validation shared by every device entry point.  Returns hipSuccess when the call
 // is well formed; *trivial is set when there is nothing to launch (M == 0 or N == 0).
@@ -129,15 +207,6 @@ hipError_t validate(const void* dA, const void* dB, const void* dC, int64_t M, i
 // Split-K plan of the skinny kernels: tb (64- or 128-byte column slab per wave), kw (waves per slab
 // inside a workgroup of 4 waves), `splits` workgroups along K (splits > 1 adds the partial-sum
 // reduce launch) with sps k-steps each.
-// Experiment switches, read once per process (a lookup per call would cost host time on every launch).
-const char* skinny_plan_env() {  // "tb,kw,splits": forces the skinny split plan
-    static const char* const e = std::getenv("TERNIX_SKINNY_PLAN");
-    return e;
-}
-const char* skinny_wave_env() {  // "sw,nsw,splits" forces a wave-kernel plan, "0" turns it off
-    static const char* const e = std::getenv("TERNIX_SKINNY_WAVE");
-    return e;
-}
 
 // Split count whose partial sums stay within 4 MiB: allowed whatever the weight size (small N).
 long partials_floor(int M, int N) { return (4L << 20) / std::max(1L, 4L * M * N); }
@@ -161,13 +230,6 @@ SkinnyPlan plan_skinny_dma(int M, int K, int N, int ns) {
     int sps = (int)((nsteps + splits - 1) / splits);
     while (col_wgs * ((nsteps + sps - 1) / sps) > std::max(cus, col_wgs)) ++sps;  // no second wave
     SkinnyPlan p{1, 1, (nsteps + sps - 1) / sps, sps, ns};
-    if (const char* env = skinny_plan_env()) {  // experiments: "tb,kw,splits"
-        int etb = 0, ekw = 0, esp = 0;
-        if (std::sscanf(env, "%d,%d,%d", &etb, &ekw, &esp) == 3 && esp >= 1) {
-            p.sps = (nsteps + esp - 1) / esp;
-            p.splits = (nsteps + p.sps - 1) / p.sps;
-        }
-    }
     if (p.sps > 16 || p.sps > ternix_hip::kMaxKPerAccumulator / 64) p.dma = 0;
     return p;
 }
@@ -200,16 +262,6 @@ SkinnyPlan plan_skinny(int M, int K, int N, bool generic = false) {
         if (splits > nsteps) splits = nsteps;
         if (splits > 1) p.splits = (int)splits;
     }
-    // Tuning override for experiments: TERNIX_SKINNY_PLAN="tb,kw,splits".
-    if (const char* env = skinny_plan_env()) {
-        int etb = 0, ekw = 0, esp = 0;
-        if (std::sscanf(env, "%d,%d,%d", &etb, &ekw, &esp) == 3 && (etb == 1 || etb == 2) &&
-            (ekw == 1 || ekw == 2 || ekw == 4) && esp >= 1) {
-            p.tb = etb;
-            p.kw = ekw;
-            p.splits = esp;
-        }
-    }
     // Each split's k-range must stay within the accumulator bound and, for the fast kernel, its
     // activation slice within the LDS budget.
     int max_sps = ternix_hip::kMaxKPerAccumulator / 64;
@@ -223,22 +275,10 @@ SkinnyPlan plan_skinny(int M, int K, int N, bool generic = false) {
     return p;
 }
 
-// TERNIX_SKINNY_WAVE=0 switches the wave-pipelined skinny kernel off (experiments).
-bool wave_kernel_enabled() {
-    static const bool on = [] {
-        const char* e = std::getenv("TERNIX_SKINNY_WAVE");
-        return !(e && e[0] == '0' && e[1] == '\0');
-    }();
-    return on;
-}
+// The DBG_SKINNY_WAVE switch set to 0 turns the wave-pipelined skinny kernel off (tests).
+bool wave_kernel_enabled() { return ternix_hip::debug_get(ternix_hip::DBG_SKINNY_WAVE) != 0; }
 
-int wave_max_m() {
-    static const int m = [] {
-        const char* e = std::getenv("TERNIX_WAVE_MAX_M");  // experiments
-        return e ? std::atoi(e) : 32;
-    }();
-    return m;
-}
+constexpr int kWaveMaxM = 32;
 
 // K split of the wave-pipelined kernel (one workgroup per strip of sw bytes, m-group and split).
 // 16-byte strips (tile-64 weights): enough workgroups for about 2.75 per CU, and for M <= 4 up to 7
@@ -248,17 +288,11 @@ int wave_max_m() {
 // box): 16-byte strips cfg2 up 9.35 -> 8.4 us against no split, tile-64 cfg5 big 17.8 -> 15.3 us;
 // 32-byte strips against 16-byte ones, each with its split: cfg1 6.72 -> 6.14 us, cfg2 up 8.41 ->
 // 7.56, cfg3 M=4 up 12.3 -> 10.9, M=16 up 13.8 -> 11.9, M=16 down 13.95 -> 11.8.
-// TERNIX_WAVE_TARGET overrides the workgroup target (experiments).
 int wave_splits(int M, int K, int N, int sw = 16) {
-    static const long env = [] {
-        const char* e = std::getenv("TERNIX_WAVE_TARGET");
-        return e ? std::atol(e) : 0L;
-    }();
     const long nsteps = K / 64, units = (long)(N / 4 / sw) * ((M + 15) / 16), cus = cu_count();
     long target = cus * 11 / 4;
     if (M <= 4) target = std::max(target, std::min(7 * cus, (long)K * (N / 4) / 8192));
     if (sw == 32) target = cus;
-    if (env > 0) target = env;
     long sp = (target + units / 2) / std::max(1L, units);
     sp = std::max(1L, std::min(16L, std::min(sp, std::max(1L, nsteps / 2))));
     // 32-byte strips: at most one workgroup per CU (6 % slack); a CU given a second one finishes last
@@ -275,35 +309,75 @@ int wave_splits(int M, int K, int N, int sw = 16) {
     return (int)sp;
 }
 
-hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int K, int N, hipStream_t st,
+// Plan of the whole-K deep GEMV (skinny_deep.hip); sw == 0 when it does not take the call.  Automatic
+// only on tile-64 weights, for short K (<= 4096) and at most two workgroups per CU: measured on MI355X
+// with cold weights against the split wave kernel, cfg1 5.31 -> 4.77 us, cfg2 up 6.25 -> 5.02, cfg3
+// M=4 up 8.37 -> 6.45, M=16 up 10.68 -> 7.55; the long-K down projections and cfg5 big are slower
+// whole (cfg2 down 6.80 -> 7.12, cfg5 big 14.9 -> 16.9).  On row-major weights only when forced.
+struct DeepPlan {
+    int sw, nw, nsw, splits, sps;
+};
+DeepPlan plan_deep(const int8_t* dA, const uint8_t* dB, int M, int K, int N, bool tiled) {
+    DeepPlan p{0, 0, 0, 1, 0};
+    const int nsteps = K / 64;
+    if (ternix_hip::debug_get(ternix_hip::DBG_DEEP) > 0) {  // forced plan (tests and tuning)
+        p.sw = ternix_hip::debug_get(ternix_hip::DBG_DEEP, 0);
+        p.nw = ternix_hip::debug_get(ternix_hip::DBG_DEEP, 1);
+        p.nsw = ternix_hip::debug_get(ternix_hip::DBG_DEEP, 2);
+        const int sp = std::max(1, ternix_hip::debug_get(ternix_hip::DBG_DEEP, 3));
+        if (M > 16 || !ternix_hip::skinny_deep_config_ok(p.sw, p.nw, p.nsw) ||
+            !ternix_hip::skinny_deep_ok(dA, dB, M, K, N, p.sw))
+            return DeepPlan{0, 0, 0, 1, 0};
+        p.sps = (nsteps + sp - 1) / sp;
+        p.splits = (nsteps + p.sps - 1) / p.sps;
+        if (p.sps * 64 > ternix_hip::kMaxKPerAccumulator) return DeepPlan{0, 0, 0, 1, 0};
+        return p;
+    }
+    if (!tiled || ternix_hip::debug_get(ternix_hip::DBG_DEEP) == 0 || M > 16 || K > 4096 ||
+        !ternix_hip::skinny_deep_ok(dA, dB, M, K, N, 16) || (long)(N / 64) > 2L * cu_count())
+        return p;
+    return DeepPlan{16, 16, 4, 1, nsteps};
+}
+
+hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int K, int N, Ctx& c,
                       const ternix_hip::OutScale& os = ternix_hip::OutScale{},
                       const ternix_hip::ActQuant& aq = ternix_hip::ActQuant{}) {
+    const hipStream_t st = c.st;
+    (void)st;
     const bool generic = !(K % 64 == 0 && (N / 4) % 64 == 0 && reinterpret_cast<uintptr_t>(dB) % 16 == 0 &&
                            (aq.mode != 0 || reinterpret_cast<uintptr_t>(dA) % 16 == 0));
+    if (!generic && aq.mode == 0) {
+        const DeepPlan dp = plan_deep(dA, dB, M, K, N, false);
+        if (dp.sw > 0) {
+            int32_t* partials = nullptr;
+            if (dp.splits > 1) {
+                const size_t need = (size_t)dp.splits * (size_t)M * (size_t)N * sizeof(int32_t);
+                if (need <= kWorkspaceMax) partials = static_cast<int32_t*>(c.get(need));
+            }
+            c.note("skinny_deep_kernel sw=%d nw=%d nsw=%d splits=%d%s", dp.sw, dp.nw, dp.nsw, dp.splits,
+                   dp.splits > 1 ? " + splitk_reduce_kernel" : "");
+            if (dp.splits == 1 || partials)
+                return TX_LAUNCH(c, ternix_hip::launch_skinny_deep(dA, dB, dC, M, K, N, dp.sw, dp.nw, dp.nsw, dp.splits, dp.sps,
+                                                      partials, st, os));
+        }
+    }
     // Wave-pipelined kernel (32-byte strips, 16-byte with fused quantisation; 2 ring slots per wave),
     // measured on MI355X (16-byte strips) against the DMA-staged kernel: faster for K <= 4096 (cfg1
     // 6.26 -> 5.64 us, cfg2 up 6.94 -> 6.29, cfg3 M=4 up 11.62 -> 10.41, M=16 up 14.27 -> 11.45) and
     // for 4 < M <= 32 with longer K, whose partials are far fewer than the DMA kernel's (cfg3 M=16
     // down 14.59 -> 12.78 us); strip width and K split as in wave_splits.  M <= 4 with K > 4096 stays
     // on the DMA kernel (cold cfg2 down 7.8 us against 7.9-9.0 for the wave kernel).
-    // TERNIX_SKINNY_WAVE="sw,nsw,splits" forces a plan, "0" turns the kernel off (experiments).
+    // The DBG_SKINNY_WAVE switch forces a plan (sw, nsw, splits) or turns the kernel off (tests).
     // With fused activation quantisation (K <= 4096) it quantises whole rows itself and dequantises with
     // its own row scales: the FFN block's gate/up GEMV becomes one launch.
-    if (!generic && M <= wave_max_m() && ternix_hip::skinny_wave_ok(dA, dB, M, K, N, 16) &&
+    if (!generic && M <= kWaveMaxM && wave_kernel_enabled() && ternix_hip::skinny_wave_ok(dA, dB, M, K, N, 16) &&
         (aq.mode == 0 || (K <= 4096 && M <= 16))) {
-        static const int sw_env = [] {
-            const char* e = std::getenv("TERNIX_WAVE_SW");  // experiments: "16" for 16-byte strips
-            return e && std::atoi(e) == 16 ? 16 : 32;
-        }();
+        const int sw_env = ternix_hip::debug_get(ternix_hip::DBG_WAVE_SW) == 16 ? 16 : 32;
         const int nsteps = K / 64;
         int sw = aq.mode == 0 && ternix_hip::skinny_wave_ok(dA, dB, M, K, N, sw_env) ? sw_env : 16, nsw = 2, sp = 0;
-        static const int long_small = [] {
-            const char* e = std::getenv("TERNIX_WAVE_LONG");  // experiments: 0 keeps M <= 4, K > 4096 off it
-            return e ? std::atoi(e) : 1;
-        }();
         if (aq.mode != 0) sp = 1;
         else if (K <= 4096 || M > 4) sp = wave_splits(M, K, N, sw);
-        else if (long_small && sw == 32 && last_max_splits() > 0) {
+        else if (sw == 32 && last_max_splits() > 0) {
             // M <= 4 with long K: only when 32-byte strips split 4 to 8 ways within one round of
             // workgroups (cfg2 down 7.8 us, as the DMA-staged kernel; cfg3 M=4 down 11.5 -> 9.8 us),
             // summed inside the launch; wide matrices (cfg5 big: 224 strips) keep the DMA-staged kernel.
@@ -318,10 +392,11 @@ hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
         if (sp > 0 && aq.mode == 0 && M <= 16 && (nsteps + sp - 1) / sp > (M <= 2 ? 24 : 32) &&
             ternix_hip::skinny_dma_ok(dA, dB, M, K, N, 1))
             sp = 0;
-        if (const char* env = skinny_wave_env()) {
-            int esw = 0, ensw = 0, esp = 0;
-            if (std::sscanf(env, "%d,%d,%d", &esw, &ensw, &esp) == 3 && esp >= 1 &&
-                ternix_hip::skinny_wave_ok(dA, dB, M, K, N, esw)) {
+        if (ternix_hip::debug_get(ternix_hip::DBG_SKINNY_WAVE) > 0) {
+            const int esw = ternix_hip::debug_get(ternix_hip::DBG_SKINNY_WAVE, 0),
+                      ensw = ternix_hip::debug_get(ternix_hip::DBG_SKINNY_WAVE, 1),
+                      esp = ternix_hip::debug_get(ternix_hip::DBG_SKINNY_WAVE, 2);
+            if (esp >= 1 && (ensw == 2 || ensw == 4) && ternix_hip::skinny_wave_ok(dA, dB, M, K, N, esw)) {
                 sw = esw;
                 nsw = ensw;
                 sp = esp;
@@ -335,23 +410,22 @@ hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
             int32_t* partials = nullptr;
             if (splits > 1) {
                 const size_t need = (size_t)splits * (size_t)M * (size_t)N * sizeof(int32_t);
-                if (need <= kWorkspaceMax) partials = static_cast<int32_t*>(workspace(st, need));
+                if (need <= kWorkspaceMax) partials = static_cast<int32_t*>(c.get(need));
             }
             if (sps * 64 <= ternix_hip::kMaxKPerAccumulator && (splits == 1 || partials || dC) &&
                 (aq.mode == 0 || (splits == 1 && sw == 16 && nsw == 2))) {
                 int* cnt = (partials && aq.mode == 0)
-                               ? arrival_counters(st, (size_t)(N / 4 / sw) * (size_t)((M + 15) / 16), M, splits, sps)
+                               ? c.counters((size_t)(N / 4 / sw) * (size_t)((M + 15) / 16), M, splits, sps)
                                : nullptr;
-                return ternix_hip::launch_skinny_wave(dA, dB, dC, M, K, N, sw, nsw, splits, sps, partials, st, os, 0,
-                                                      aq, 0, cnt);
+                c.note("skinny_wave_kernel sw=%d nsw=%d splits=%d%s", sw, nsw, splits,
+                       splits == 1 ? "" : (cnt ? " (splits summed in-launch)" : " + splitk_reduce_kernel"));
+                return TX_LAUNCH(c, ternix_hip::launch_skinny_wave(dA, dB, dC, M, K, N, sw, nsw, splits, sps, partials, st, os, 0,
+                                                      aq, 0, cnt));
             }
         }
     }
-    // DMA-staged kernel: TERNIX_SKINNY_DMA=0 disables it, 2..4 sets its stage count (experiments).
-    static const int dma_env = [] {
-        const char* e = std::getenv("TERNIX_SKINNY_DMA");
-        return e ? std::atoi(e) : -1;
-    }();
+    // DMA-staged kernel: the DBG_SKINNY_DMA switch disables it (0) or sets its stage count (2..4).
+    const int dma_env = ternix_hip::debug_get(ternix_hip::DBG_SKINNY_DMA);
     SkinnyPlan p{0, 0, 0, 0, 0};
     if (!generic && M <= 16 && dma_env != 0 && ternix_hip::skinny_dma_ok(dA, dB, M, K, N, 1)) {
         p = plan_skinny_dma(M, K, N, dma_env >= 2 && dma_env <= 4 ? dma_env : 3);
@@ -366,19 +440,18 @@ hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
     int32_t* partials = nullptr;
     if (p.splits > 1) {
         const size_t need = (size_t)p.splits * (size_t)M * (size_t)N * sizeof(int32_t);
-        if (need <= kWorkspaceMax) partials = static_cast<int32_t*>(workspace(st, need));
+        if (need <= kWorkspaceMax) partials = static_cast<int32_t*>(c.get(need));
     }
-    return ternix_hip::launch_skinny(dA, dB, dC, M, K, N, p.tb, p.kw, p.splits, p.sps, partials, st, os, aq, p.dma);
+    c.note("%s splits=%d%s", p.dma ? "skinny_dma_kernel" : (generic ? "skinny_generic_kernel" : "skinny_short/fast_kernel"),
+           p.splits, p.splits > 1 ? " + splitk_reduce_kernel" : "");
+    return TX_LAUNCH(c, ternix_hip::launch_skinny(dA, dB, dC, M, K, N, p.tb, p.kw, p.splits, p.sps, partials, st, os, aq, p.dma));
 }
 
 // Split-K for GEMMs with too few output tiles to fill the chip (mid-size M against a long K, e.g.
 // cfg3 M=64, the worst case M=256): each split covers a contiguous k-range of whole 128-row stages,
 // the partial tiles go through the same workspace and reduce launch as the skinny path.
 int gemm_splits(int M, int K, int N) {
-    static const int env = [] {
-        const char* e = std::getenv("TERNIX_GEMM_SPLITS");  // experiments only
-        return e ? std::atoi(e) : 0;
-    }();
+    const int env = ternix_hip::debug_get(ternix_hip::DBG_GEMM_SPLITS);  // tests
     const int bm = M <= 64 ? 64 : 128;  // the tile height launch_gemm picks
     const bool narrow = ternix_hip::gemm_narrow_wanted(M, K, N);  // 64-column tiles instead of 256
     const long tiles = (long)((M + bm - 1) / bm) * (long)((N / 4 + 63) / 64) * (narrow ? 4 : 1);
@@ -393,8 +466,10 @@ int gemm_splits(int M, int K, int N) {
     return (int)std::max<long>(1, std::min<long>(splits, 16));
 }
 
-hipError_t run_gemm(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int K, int N, hipStream_t st,
+hipError_t run_gemm(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int K, int N, Ctx& c,
                     const ternix_hip::OutScale& os = ternix_hip::OutScale{}, int tiled = 0) {
+    const hipStream_t st = c.st;
+    (void)st;
     if (K <= ternix_hip::kMaxKPerAccumulator) {
         int splits = gemm_splits(M, K, N);
         if (splits > 1) {
@@ -403,23 +478,25 @@ hipError_t run_gemm(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int
             const int k_split = ((K + splits - 1) / splits + unit - 1) / unit * unit;
             splits = (K + k_split - 1) / k_split;
             const size_t need = (size_t)splits * (size_t)M * (size_t)N * sizeof(int32_t);
-            int32_t* partials = (splits > 1 && need <= kWorkspaceMax) ? static_cast<int32_t*>(workspace(st, need))
+            int32_t* partials = (splits > 1 && need <= kWorkspaceMax) ? static_cast<int32_t*>(c.get(need))
                                                                        : nullptr;
             if (partials) {
-                hipError_t e = ternix_hip::launch_gemm(dA, dB, partials, M, K, N, 0, K, 0, st, ternix_hip::OutScale{},
-                                                       splits, k_split, tiled);
+                c.note("gemm (tile by launch_gemm) splits=%d + splitk_reduce_kernel", splits);
+                hipError_t e = TX_LAUNCH(c, ternix_hip::launch_gemm(dA, dB, partials, M, K, N, 0, K, 0, st, ternix_hip::OutScale{},
+                                                       splits, k_split, tiled));
                 if (e != hipSuccess) return e;
-                return ternix_hip::launch_splitk_reduce(partials, dC, M, N, splits, os, st);
+                return TX_LAUNCH(c, ternix_hip::launch_splitk_reduce(partials, dC, M, N, splits, os, st));
             }
         }
-        return ternix_hip::launch_gemm(dA, dB, dC, M, K, N, 0, K, 0, st, os, 1, 0, tiled);
+        c.note("gemm (tile by launch_gemm)");
+        return TX_LAUNCH(c, ternix_hip::launch_gemm(dA, dB, dC, M, K, N, 0, K, 0, st, os, 1, 0, tiled));
     }
     if (dC == nullptr) return hipErrorInvalidValue;  // scaled call without int scratch
     int acc = 0;
     for (long k0 = 0; k0 < K; k0 += ternix_hip::kMaxKPerAccumulator) {
         const long k1 = k0 + ternix_hip::kMaxKPerAccumulator < K ? k0 + ternix_hip::kMaxKPerAccumulator : K;
-        const hipError_t e = ternix_hip::launch_gemm(dA, dB, dC, M, K, N, (int)k0, (int)k1, acc, st,
-                                                     ternix_hip::OutScale{}, 1, 0, tiled);
+        const hipError_t e = TX_LAUNCH(c, ternix_hip::launch_gemm(dA, dB, dC, M, K, N, (int)k0, (int)k1, acc, st,
+                                                     ternix_hip::OutScale{}, 1, 0, tiled));
         if (e != hipSuccess) return e;
         acc = 1;
     }
@@ -435,8 +512,10 @@ hipError_t run_gemm(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int
 // Returns hipErrorNotSupported, before launching anything, when this does not apply (a skinny plan
 // without a split, graph capture without a large enough workspace, sizes past the workspace cap);
 // the caller then runs the generic kernels.
-hipError_t run_padded(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int K, int N, hipStream_t st,
+hipError_t run_padded(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int K, int N, Ctx& c,
                       const ternix_hip::OutScale& os, bool skinny) {
+    const hipStream_t st = c.st;
+    (void)st;
     const int NB = N / 4;
     const long Kp = ((long)K + 127) / 128 * 128;
     const long NBp = ((long)NB + 63) / 64 * 64;
@@ -445,7 +524,7 @@ hipError_t run_padded(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
     SkinnyPlan p{0, 0, 0, 0, 0};
     int splits = 1, k_split = 0;
     // Short K at M <= 16: the wave-pipelined kernel in one launch, writing the N real columns itself.
-    const bool wave = skinny && M <= wave_max_m() && Kp <= 4096 && wave_kernel_enabled();
+    const bool wave = skinny && M <= kWaveMaxM && Kp <= 4096 && wave_kernel_enabled();
     if (wave) {
         splits = 1;
     } else if (skinny) {
@@ -470,25 +549,26 @@ hipError_t run_padded(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
     const size_t a_bytes = up((size_t)M * (size_t)Kp);
     const size_t p_bytes = wave ? 0 : (size_t)splits * (size_t)M * (size_t)Np * sizeof(int32_t);
     if (w_bytes + a_bytes + p_bytes > kWorkspaceMax) return hipErrorNotSupported;
-    uint8_t* ws = static_cast<uint8_t*>(workspace(st, w_bytes + a_bytes + p_bytes));
+    uint8_t* ws = static_cast<uint8_t*>(c.get(w_bytes + a_bytes + p_bytes));
     if (ws == nullptr) return hipErrorNotSupported;
+    c.note("pad_rows_kernel + %s", wave ? "skinny_wave_kernel" : (skinny ? (p.dma ? "skinny_dma_kernel" : "skinny_short/fast_kernel") : "gemm"));
     uint8_t* Wp = ws;
     int8_t* Ap = reinterpret_cast<int8_t*>(ws + w_bytes);
     int32_t* P = reinterpret_cast<int32_t*>(ws + w_bytes + a_bytes);
-    hipError_t e = ternix_hip::launch_pad_rows(dB, Wp, K, (int)Kp, NB, NB, (int)NBp,
+    hipError_t e = TX_LAUNCH(c, ternix_hip::launch_pad_rows(dB, Wp, K, (int)Kp, NB, NB, (int)NBp,
                                                reinterpret_cast<const uint8_t*>(dA), reinterpret_cast<uint8_t*>(Ap),
-                                               M, M, K, K, (int)Kp, st);
+                                               M, M, K, K, (int)Kp, st));
     if (e != hipSuccess) return e;
     if (wave)
-        return ternix_hip::launch_skinny_wave(Ap, Wp, dC, M, (int)Kp, (int)Np, 16, 2, 1, (int)(Kp / 64), nullptr, st,
-                                              os, N);
+        return TX_LAUNCH(c, ternix_hip::launch_skinny_wave(Ap, Wp, dC, M, (int)Kp, (int)Np, 16, 2, 1, (int)(Kp / 64), nullptr, st,
+                                              os, N));
     if (skinny)
-        return ternix_hip::launch_skinny(Ap, Wp, dC, M, (int)Kp, (int)Np, p.tb, p.kw, p.splits, p.sps, P, st, os,
-                                         ternix_hip::ActQuant{}, p.dma, N);
-    e = ternix_hip::launch_gemm(Ap, Wp, P, M, (int)Kp, (int)Np, 0, (int)Kp, 0, st, ternix_hip::OutScale{}, splits,
-                                k_split);
+        return TX_LAUNCH(c, ternix_hip::launch_skinny(Ap, Wp, dC, M, (int)Kp, (int)Np, p.tb, p.kw, p.splits, p.sps, P, st, os,
+                                         ternix_hip::ActQuant{}, p.dma, N));
+    e = TX_LAUNCH(c, ternix_hip::launch_gemm(Ap, Wp, P, M, (int)Kp, (int)Np, 0, (int)Kp, 0, st, ternix_hip::OutScale{}, splits,
+                                k_split));
     if (e != hipSuccess) return e;
-    return ternix_hip::launch_splitk_reduce(P, dC, M, N, splits, os, st, (int)Np);
+    return TX_LAUNCH(c, ternix_hip::launch_splitk_reduce(P, dC, M, N, splits, os, st, (int)Np));
 }
 
 // The aligned kernels need 16-byte aligned operands, N/4 % 64 == 0 and whole k-steps: 64 rows for
@@ -500,71 +580,102 @@ bool needs_padding(const int8_t* dA, const uint8_t* dB, int K, int N, bool skinn
 
 // Automatic path for one call: the padded copy for ragged or misaligned shapes when it applies,
 // else the skinny kernels up to kSkinnyMaxM rows and the GEMM above.
-hipError_t run_auto(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int K, int N, hipStream_t st,
+hipError_t run_auto(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int K, int N, Ctx& c,
                     const ternix_hip::OutScale& os, int skinny_max) {
-    static const bool pad_off = [] {
-        const char* e = std::getenv("TERNIX_RAGGED_PAD");  // experiments: 0 keeps the generic kernels
-        return e && e[0] == '0';
-    }();
+    const hipStream_t st = c.st;
+    (void)st;
+    const bool pad_off = ternix_hip::debug_get(ternix_hip::DBG_RAGGED_PAD) == 0;  // tests: generic kernels
     if (!pad_off && needs_padding(dA, dB, K, N, M <= skinny_max)) {
-        const hipError_t e = run_padded(dA, dB, dC, M, K, N, st, os, M <= skinny_max);
+        const hipError_t e = run_padded(dA, dB, dC, M, K, N, c, os, M <= skinny_max);
         if (e != hipErrorNotSupported) return e;
     }
-    return M <= skinny_max ? run_skinny(dA, dB, dC, M, K, N, st, os) : run_gemm(dA, dB, dC, M, K, N, st, os);
+    return M <= skinny_max ? run_skinny(dA, dB, dC, M, K, N, c, os) : run_gemm(dA, dB, dC, M, K, N, c, os);
 }
 
 // Tile-64 weights (the opt-in pre-permuted layout): M <= 32 runs the wave-pipelined kernel, whose
 // per-wave DMA of one 1 KB block is a single contiguous read, K split by wave_splits at every K
 // (the contiguous reads make it faster than the DMA kernel for long K too: cold cfg2 down 6.7 us
-// against 7.8 on the row-major layout; TERNIX_SKINNY_WAVE="16,2,splits" forces the split count,
-// experiments).  Larger M runs the LDS-DMA GEMMs with the contract layout's split-K planning.
-hipError_t run_tile64(const int8_t* dA, const uint8_t* dWt, int32_t* dC, int M, int K, int N, hipStream_t st,
+// against 7.8 on the row-major layout; the DBG_SKINNY_WAVE switch forces the split count, tests).  Larger M runs the LDS-DMA GEMMs with the contract layout's split-K planning.
+hipError_t run_tile64(const int8_t* dA, const uint8_t* dWt, int32_t* dC, int M, int K, int N, Ctx& c,
                       const ternix_hip::OutScale& os = ternix_hip::OutScale{}) {
+    const hipStream_t st = c.st;
+    (void)st;
+    if (M <= 16) {
+        const DeepPlan dp = plan_deep(dA, dWt, M, K, N, true);
+        if (dp.sw > 0) {
+            int32_t* partials =
+                dp.splits > 1 ? static_cast<int32_t*>(c.get((size_t)dp.splits * M * N * sizeof(int32_t))) : nullptr;
+            c.note("skinny_deep_kernel (tile-64) nw=%d nsw=%d splits=%d%s", dp.nw, dp.nsw, dp.splits,
+                   dp.splits > 1 ? " + splitk_reduce_kernel" : "");
+            if (dp.splits == 1 || partials)
+                return TX_LAUNCH(c, ternix_hip::launch_skinny_deep(dA, dWt, dC, M, K, N, 16, dp.nw, dp.nsw, dp.splits,
+                                                                   dp.sps, partials, st, os, 0, 1));
+        }
+    }
     if (M <= 32) {
         const int nsteps = K / 64;
         int sp = wave_splits(M, K, N);
-        if (const char* env = skinny_wave_env()) {
-            int esw = 0, ensw = 0, esp = 0;
-            if (std::sscanf(env, "%d,%d,%d", &esw, &ensw, &esp) == 3 && esp >= 1) sp = esp;
-        }
+        if (ternix_hip::debug_get(ternix_hip::DBG_SKINNY_WAVE) > 0 && ternix_hip::debug_get(ternix_hip::DBG_SKINNY_WAVE, 2) >= 1)
+            sp = ternix_hip::debug_get(ternix_hip::DBG_SKINNY_WAVE, 2);
         const int sps = (nsteps + sp - 1) / sp;
         const int splits = (nsteps + sps - 1) / sps;
         if (sps * 64 > ternix_hip::kMaxKPerAccumulator) return hipErrorInvalidValue;
         int32_t* partials = nullptr;
         if (splits > 1) {
             const size_t need = (size_t)splits * (size_t)M * (size_t)N * sizeof(int32_t);
-            if (need <= kWorkspaceMax) partials = static_cast<int32_t*>(workspace(st, need));
+            if (need <= kWorkspaceMax) partials = static_cast<int32_t*>(c.get(need));
         }
-        int* cnt = partials ? arrival_counters(st, (size_t)(N / 4 / 16) * (size_t)((M + 15) / 16), M, splits, sps)
+        int* cnt = partials ? c.counters((size_t)(N / 4 / 16) * (size_t)((M + 15) / 16), M, splits, sps)
                             : nullptr;
-        return ternix_hip::launch_skinny_wave(dA, dWt, dC, M, K, N, 16, 2, splits, sps, partials, st, os, 0,
-                                              ternix_hip::ActQuant{}, 1, cnt);
+        return TX_LAUNCH(c, ternix_hip::launch_skinny_wave(dA, dWt, dC, M, K, N, 16, 2, splits, sps, partials, st, os, 0,
+                                              ternix_hip::ActQuant{}, 1, cnt));
     }
-    return run_gemm(dA, dWt, dC, M, K, N, st, os, 1);
+    return run_gemm(dA, dWt, dC, M, K, N, c, os, 1);
 }
 
 enum class Path { Auto, Skinny, Gemm, Naive };
 
+int dispatch_ctx(Path path, const int8_t* dA, const uint8_t* dB, int32_t* dC, int64_t M64, int64_t K64,
+                 int64_t N64, Ctx& c);
+
 int dispatch(Path path, const int8_t* dA, const uint8_t* dB, int32_t* dC, int64_t M64, int64_t K64, int64_t N64,
              void* stream) {
+    Ctx c;
+    c.st = static_cast<hipStream_t>(stream);
+    return dispatch_ctx(path, dA, dB, dC, M64, K64, N64, c);
+}
+
+int dispatch_ctx(Path path, const int8_t* dA, const uint8_t* dB, int32_t* dC, int64_t M64, int64_t K64,
+                 int64_t N64, Ctx& c) {
     bool trivial = false;
     hipError_t e = validate(dA, dB, dC, M64, K64, N64, &trivial);
     if (e != hipSuccess) return (int)e;
     if (path == Path::Skinny && M64 > kSkinnyMaxM) return (int)hipErrorInvalidValue;
     if (trivial) return (int)hipSuccess;
     const int M = (int)M64, K = (int)K64, N = (int)N64;
-    hipStream_t st = static_cast<hipStream_t>(stream);
-    static const int auto_skinny_max = [] {
-        const char* e = std::getenv("TERNIX_SKINNY_MAX_M");  // experiments only
-        return e ? std::atoi(e) : kSkinnyMaxM;
-    }();
-    if (path == Path::Auto) return (int)run_auto(dA, dB, dC, M, K, N, st, ternix_hip::OutScale{}, auto_skinny_max);
+    if (path == Path::Auto) return (int)run_auto(dA, dB, dC, M, K, N, c, ternix_hip::OutScale{}, kSkinnyMaxM);
     switch (path) {
-        case Path::Skinny: e = run_skinny(dA, dB, dC, M, K, N, st); break;
-        case Path::Gemm: e = run_gemm(dA, dB, dC, M, K, N, st); break;
-        default: e = ternix_hip::launch_naive(dA, dB, dC, M, K, N, st); break;
+        case Path::Skinny: e = run_skinny(dA, dB, dC, M, K, N, c); break;
+        case Path::Gemm: e = run_gemm(dA, dB, dC, M, K, N, c); break;
+        default:
+            c.note("naive_kernel");
+            e = TX_LAUNCH(c, ternix_hip::launch_naive(dA, dB, dC, M, K, N, c.st));
+            break;
     }
     return (int)e;
+}
+
+// Dry run of the automatic path for operands at the given addresses (only their alignment matters;
+// nothing is dereferenced or launched).
+Ctx plan_auto(int64_t M, int64_t K, int64_t N, uintptr_t a_addr, uintptr_t b_addr) {
+    Ctx c;
+    c.dry = true;
+    std::snprintf(c.desc, sizeof(c.desc), "none");
+    const int s = dispatch_ctx(Path::Auto, reinterpret_cast<const int8_t*>(a_addr),
+                               reinterpret_cast<const uint8_t*>(b_addr), reinterpret_cast<int32_t*>(uintptr_t(1) << 20),
+                               M, K, N, c);
+    if (s != 0) std::snprintf(c.desc, sizeof(c.desc), "rejected");
+    return c;
 }
 
 }  // namespace
@@ -574,6 +685,57 @@ extern "C" {
 int ternix_hip_mul_mat_ternary(const int8_t* dA, const uint8_t* dB, int32_t* dC, int64_t M, int64_t K, int64_t N,
                                void* stream) {
     return dispatch(Path::Auto, dA, dB, dC, M, K, N, stream);
+}
+
+size_t ternix_hip_mul_mat_ternary_workspace_size(int64_t M, int64_t K, int64_t N) {
+    // For 16-byte aligned A and W (what hipMalloc returns).
+    return plan_auto(M, K, N, uintptr_t(1) << 20, uintptr_t(1) << 24).need;
+}
+
+size_t ternix_hip_mul_mat_ternary_workspace_size_for(const int8_t* dA, const uint8_t* dB, int64_t M, int64_t K,
+                                                     int64_t N) {
+    return plan_auto(M, K, N, reinterpret_cast<uintptr_t>(dA), reinterpret_cast<uintptr_t>(dB)).need;
+}
+
+int ternix_hip_mul_mat_ternary_ws(const int8_t* dA, const uint8_t* dB, int32_t* dC, int64_t M, int64_t K, int64_t N,
+                                  void* dWorkspace, size_t workspace_bytes, void* stream) {
+    if (workspace_bytes > 0 && (dWorkspace == nullptr || reinterpret_cast<uintptr_t>(dWorkspace) % 256 != 0))
+        return (int)hipErrorInvalidValue;
+    Ctx c;
+    c.st = static_cast<hipStream_t>(stream);
+    c.use_caller = true;
+    c.caller = static_cast<char*>(dWorkspace);
+    c.caller_bytes = dWorkspace ? workspace_bytes : 0;
+    return dispatch_ctx(Path::Auto, dA, dB, dC, M, K, N, c);
+}
+
+int ternix_hip_plan_describe(const int8_t* dA, const uint8_t* dB, int64_t M, int64_t K, int64_t N, char* buf,
+                             size_t len) {
+    if (buf == nullptr || len == 0) return (int)hipErrorInvalidValue;
+    const Ctx c = plan_auto(M, K, N, reinterpret_cast<uintptr_t>(dA), reinterpret_cast<uintptr_t>(dB));
+    std::snprintf(buf, len, "%s", c.desc);
+    return std::strcmp(c.desc, "rejected") == 0 ? (int)hipErrorInvalidValue : (int)hipSuccess;
+}
+
+int ternix_hip_release_stream(void* stream) {
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    Workspace w;
+    {
+        std::lock_guard<std::mutex> lock(g_ws_mutex);
+        auto it = g_ws.find({dev, st});
+        if (it == g_ws.end()) return (int)hipSuccess;
+        w = std::move(it->second);
+        g_ws.erase(it);
+    }
+    // Work already queued on the stream may still use the buffers.
+    e = hipStreamSynchronize(st);
+    if (w.ptr) (void)hipFree(w.ptr);
+    for (void* p : w.retired) (void)hipFree(p);
+    if (w.counters) (void)hipFree(w.counters);
+    return (int)e;
 }
 
 int ternix_hip_mul_mat_ternary_gemv(const int8_t* dA, const uint8_t* dB, int32_t* dC, int64_t M, int64_t K,
@@ -613,9 +775,9 @@ int ternix_hip_mul_mat_ternary_host(const int8_t* A, const uint8_t* B_packed, in
     uint8_t* dB = nullptr;
     int32_t* dC = nullptr;
     // hipMalloc of 0 bytes returns a null pointer; keep the pointers non-null for validation.
-    if ((e = hipMalloc(reinterpret_cast<void**>(&dA), a_bytes ? a_bytes : 16)) != hipSuccess) goto done;
-    if ((e = hipMalloc(reinterpret_cast<void**>(&dB), b_bytes ? b_bytes : 16)) != hipSuccess) goto done;
-    if ((e = hipMalloc(reinterpret_cast<void**>(&dC), c_bytes)) != hipSuccess) goto done;
+    if ((e = lib_malloc(reinterpret_cast<void**>(&dA), a_bytes ? a_bytes : 16)) != hipSuccess) goto done;
+    if ((e = lib_malloc(reinterpret_cast<void**>(&dB), b_bytes ? b_bytes : 16)) != hipSuccess) goto done;
+    if ((e = lib_malloc(reinterpret_cast<void**>(&dC), c_bytes)) != hipSuccess) goto done;
     if (a_bytes && (e = hipMemcpy(dA, A, a_bytes, hipMemcpyHostToDevice)) != hipSuccess) goto done;
     if (b_bytes && (e = hipMemcpy(dB, B_packed, b_bytes, hipMemcpyHostToDevice)) != hipSuccess) goto done;
     {
@@ -656,7 +818,7 @@ int ternix_hip_mul_mat_ternary_dequant(const int8_t* dA, const uint8_t* dB, floa
     // The int32 C never exists in memory on the fused paths; where one is needed (atomic split-K, K
     // chunks) it is kept in dY itself (same size) and converted in place.
     int32_t* c_alias = reinterpret_cast<int32_t*>(dY);
-    e = run_auto(dA, dB, c_alias, m, k, n, st, os, kSkinnyMaxM);
+    e = run_auto(dA, dB, c_alias, m, k, n, ctx_of(st), os, kSkinnyMaxM);
     return (int)e;
 }
 
@@ -677,7 +839,7 @@ int ternix_hip_mul_mat_ternary_swiglu(const int8_t* dA, const uint8_t* dB, float
     os.rs = dRowScale;
     os.ws = w_scale;
     os.swiglu = 1;
-    e = run_auto(dA, dB, dScratch, m, k, n, st, os, kSkinnyMaxM);
+    e = run_auto(dA, dB, dScratch, m, k, n, ctx_of(st), os, kSkinnyMaxM);
     return (int)e;
 }
 
@@ -781,9 +943,9 @@ int ternix_hip_ffn_forward(float* dY, const float* dX, const float* dNormWeight,
         const SkinnyPlan p1 = plan_skinny(m, hd, 2 * f), p2 = plan_skinny(m, f, hd);
         if (ternix_hip::skinny_short_ok(dWgu, m, hd, 2 * f, p1.sps, p1.splits) &&
             ternix_hip::skinny_short_ok(dWd, m, f, hd, p2.sps, p2.splits)) {
-            hipError_t e = run_skinny(nullptr, dWgu, scratch, m, hd, 2 * f, st, os1, aq1);
+            hipError_t e = run_skinny(nullptr, dWgu, scratch, m, hd, 2 * f, ctx_of(st), os1, aq1);
             if (e != hipSuccess) return (int)e;
-            return (int)run_skinny(nullptr, dWd, reinterpret_cast<int32_t*>(dY), m, f, hd, st, os2, aq2);
+            return (int)run_skinny(nullptr, dWd, reinterpret_cast<int32_t*>(dY), m, f, hd, ctx_of(st), os2, aq2);
         }
     }
     int s = ternix_hip_rms_norm_quantize(q1, rs1, dX, dNormWeight, M, H, eps, stream);
@@ -838,7 +1000,7 @@ int ternix_hip_ffn_forward_tile64(float* dY, const float* dX, const float* dNorm
     } else {
         const int s = ternix_hip_rms_norm_quantize(q1, rs1, dX, dNormWeight, M, H, eps, stream);
         if (s != 0) return s;
-        e = run_tile64(q1, dWguT, scratch, m, hd, 2 * f, st, os1);
+        e = run_tile64(q1, dWguT, scratch, m, hd, 2 * f, ctx_of(st), os1);
     }
     if (e != hipSuccess) return (int)e;
     e = ternix_hip::launch_quantize_rows(h, q2, rs2, m, f, st);
@@ -847,7 +1009,7 @@ int ternix_hip_ffn_forward_tile64(float* dY, const float* dX, const float* dNorm
     os2.Y = dY;
     os2.rs = rs2;
     os2.ws = ws_d;
-    return (int)run_tile64(q2, dWdT, reinterpret_cast<int32_t*>(dY), m, f, hd, st, os2);
+    return (int)run_tile64(q2, dWdT, reinterpret_cast<int32_t*>(dY), m, f, hd, ctx_of(st), os2);
 }
 
 int ternix_hip_quantize_activations(const float* dX, int8_t* dQ, float* dRowScale, int64_t M, int64_t K,
@@ -895,7 +1057,7 @@ int ternix_hip_mul_mat_ternary_tile64(const int8_t* dA, const uint8_t* dWt, int3
         reinterpret_cast<uintptr_t>(dA) % 16 != 0 || reinterpret_cast<uintptr_t>(dWt) % 16 != 0)
         return (int)hipErrorInvalidValue;
     if (trivial) return (int)hipSuccess;
-    return (int)run_tile64(dA, dWt, dC, (int)M, (int)K, (int)N, static_cast<hipStream_t>(stream));
+    return (int)run_tile64(dA, dWt, dC, (int)M, (int)K, (int)N, ctx_of(static_cast<hipStream_t>(stream)));
 }
 
 int ternix_hip_mul_mat_ternary_tile64_dequant(const int8_t* dA, const uint8_t* dWt, float* dY, int64_t M, int64_t K,
@@ -914,7 +1076,37 @@ int ternix_hip_mul_mat_ternary_tile64_dequant(const int8_t* dA, const uint8_t* d
     os.ws = w_scale;
     // As in ternix_hip_mul_mat_ternary_dequant: an int32 C, where a path needs one, lives in dY.
     return (int)run_tile64(dA, dWt, reinterpret_cast<int32_t*>(dY), (int)M, (int)K, (int)N,
-                           static_cast<hipStream_t>(stream), os);
+                           ctx_of(static_cast<hipStream_t>(stream)), os);
+}
+
+int ternix_hip_debug_set(const char* key, int v0, int v1, int v2, int v3) {
+    static const struct {
+        const char* name;
+        ternix_hip::DebugKey key;
+    } names[] = {
+        {"wave_last", ternix_hip::DBG_WAVE_LAST},     {"skinny_wave", ternix_hip::DBG_SKINNY_WAVE},
+        {"wave_sw", ternix_hip::DBG_WAVE_SW},         {"skinny_dma", ternix_hip::DBG_SKINNY_DMA},
+        {"skinny_short", ternix_hip::DBG_SKINNY_SHORT}, {"ragged_pad", ternix_hip::DBG_RAGGED_PAD},
+        {"gemm_narrow", ternix_hip::DBG_GEMM_NARROW}, {"gemm_generic", ternix_hip::DBG_GEMM_GENERIC},
+        {"gemm_splits", ternix_hip::DBG_GEMM_SPLITS}, {"gemm_bm", ternix_hip::DBG_GEMM_BM},
+        {"deep", ternix_hip::DBG_DEEP},             {"sk_order", ternix_hip::DBG_SK_ORDER},
+    };
+    if (key == nullptr) return (int)hipErrorInvalidValue;
+    for (const auto& n : names) {
+        if (std::strcmp(n.name, key) != 0) continue;
+        const int v[4] = {v0, v1, v2, v3};
+        for (int i = 0; i < 4; ++i)
+            ternix_hip::g_debug[n.key][i].store(v[i] < 0 ? 0 : v[i] + 1, std::memory_order_relaxed);
+        return (int)hipSuccess;
+    }
+    return (int)hipErrorInvalidValue;
+}
+
+long long ternix_hip_debug_alloc_count(void) { return g_alloc_count.load(std::memory_order_relaxed); }
+
+void ternix_hip_debug_reset(void) {
+    for (auto& k : ternix_hip::g_debug)
+        for (auto& v : k) v.store(0, std::memory_order_relaxed);
 }
 
 const char* ternix_hip_error_string(int status) {
@@ -922,6 +1114,15 @@ const char* ternix_hip_error_string(int status) {
     return s ? s : "unknown error";
 }
 
-int ternix_hip_version(void) { return 100; }
+int ternix_hip_version(void) { return 200; }
+
+int ternix_hip_device_count(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    return n;
+}
 
 }  // extern "C"

@@ -1,27 +1,57 @@
 """The kernels the automatic dispatch only falls back to (register-staged skinny kernels, generic
-kernels for ragged shapes, 256-column GEMM tiles for small M) stay bit-exact: each switch set runs
-tests/fallback_paths_run.py in one child process (the library reads its switches once per process)."""
-import os
-import subprocess
-import sys
-
+kernels for ragged shapes, 256-column GEMM tiles for small M, the reduce launch instead of in-launch
+split sums, the generic GEMM) stay bit-exact.  Each switch set is applied in-process through the
+library's explicit test hook, ternix_hip_debug_set (the library never reads the environment)."""
+import numpy as np
 import pytest
 
-ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+import ternixengine_amd as tx
+from ternixengine_amd import hip_runtime as hr
+
+SHAPES = [(1, 2560, 2560), (1, 6912, 2560), (4, 4096, 1024), (16, 2048, 4096), (16, 8192, 1024), (24, 4096, 512),
+          (32, 2560, 1024), (48, 1024, 2048), (64, 4096, 1024), (129, 1001, 516), (1, 1000, 3076), (17, 4093, 1028),
+          (256, 2048, 1024)]
+
 SWITCHES = [
-    {"TERNIX_SKINNY_WAVE": "0"},                                                     # DMA-staged GEMVs
-    {"TERNIX_WAVE_SW": "16"},                                                        # 16-byte wave strips
-    {"TERNIX_SKINNY_WAVE": "0", "TERNIX_SKINNY_DMA": "0"},                           # short / fast kernels
-    {"TERNIX_SKINNY_WAVE": "0", "TERNIX_SKINNY_DMA": "0", "TERNIX_SKINNY_SHORT": "0"},  # fast kernel only
-    {"TERNIX_RAGGED_PAD": "0"},                                                      # generic ragged kernels
-    {"TERNIX_GEMM_NARROW": "0"},                                                     # 256-column small-M GEMM
+    {"skinny_wave": 0},                                    # DMA-staged GEMVs
+    {"wave_sw": 16},                                       # 16-byte wave strips
+    {"skinny_wave": 0, "skinny_dma": 0},                   # short / fast kernels
+    {"skinny_wave": 0, "skinny_dma": 0, "skinny_short": 0},  # fast kernel only
+    {"ragged_pad": 0},                                     # generic ragged kernels
+    {"gemm_narrow": 0},                                    # 256-column small-M GEMM
+    {"wave_last": 0},                                      # reduce launch instead of in-launch sums
+    {"gemm_generic": 1},                                   # register-staged generic GEMM
+    {"sk_order": 1},                                       # release/acquire form of the in-launch sums
 ]
 
 
+@pytest.fixture
+def switches(request):
+    lib = tx._load()
+    lib.ternix_hip_debug_reset()
+    for k, v in request.param.items():
+        assert lib.ternix_hip_debug_set(k.encode(), v, -1, -1, -1) == 0, k
+    yield request.param
+    lib.ternix_hip_debug_reset()
+
+
+def test_debug_set_rejects_unknown_key():
+    lib = tx._load()
+    assert lib.ternix_hip_debug_set(b"no_such_switch", 1, -1, -1, -1) == 1
+    assert lib.ternix_hip_debug_set(None, 1, -1, -1, -1) == 1
+
+
 @pytest.mark.gpu
-@pytest.mark.parametrize("env", SWITCHES, ids=lambda e: ",".join(f"{k}={v}" for k, v in e.items()))
-def test_fallback_kernels_bit_exact(env):
-    r = subprocess.run([sys.executable, os.path.join(ROOT, "tests", "fallback_paths_run.py")],
-                       env={**os.environ, **env}, capture_output=True, text=True, timeout=240)
-    print(r.stdout[-3000:])
-    assert r.returncode == 0, r.stdout[-3000:] + r.stderr[-2000:]
+@pytest.mark.parametrize("switches", SWITCHES, ids=lambda e: ",".join(f"{k}={v}" for k, v in e.items()),
+                         indirect=True)
+def test_fallback_kernels_bit_exact(switches, oracle):
+    rng = np.random.default_rng(5)
+    for m, k, n in SHAPES:
+        a = rng.integers(-128, 128, size=(m, k), dtype=np.int8)
+        wp = rng.integers(0, 256, size=(k, n // 4), dtype=np.uint8)
+        da, db, dc = hr.DeviceBuffer.from_array(a), hr.DeviceBuffer.from_array(wp), hr.DeviceBuffer(4 * m * n)
+        dc.upload(np.full(m * n, -7, np.int32))
+        print(f"M={m} K={k} N={n} {switches}", flush=True)
+        assert tx.mul_mat_ternary(da.value, db.value, dc.value, m, k, n) == 0
+        hr.synchronize()
+        assert (dc.download(np.int32, (m, n)) == oracle.mm("scalar_mt", a, wp, n)).all(), (m, k, n)

@@ -189,7 +189,7 @@ def test_host_wrapper_and_python_api(oracle, golden):
     a = rng.integers(-128, 128, size=(128, 256), dtype=np.int8)
     w = rng.integers(-1, 2, size=(256, 192), dtype=np.int8)
     assert (tx.ternary_matmul(a, tx.pack_ternary(w), "hip_tiled") == a.astype(np.int32) @ w.astype(np.int32)).all()
-    with pytest.raises(ValueError):
+    with pytest.raises(RuntimeError, match="HIP error"):
         tx.ternary_matmul(a[:65], tx.pack_ternary(w), "hip_tiled")
 
 

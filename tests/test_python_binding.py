@@ -4,8 +4,8 @@ implementations in place of the CPU and CUDA ones.
 
 The reference checks every CPU impl at (1,8,8), (5,33,24), (64,256,128) and the CUDA impls at
 (128,256,192); here every HIP impl runs all four shapes (the `hip_tiled` impl keeps the reference
-tiled kernel's M,N,K % 64 contract, so shapes outside it must raise ValueError, which is what the
-reference's `cuda_tiled` returns as cudaErrorInvalidValue)."""
+tiled kernel's M,N,K % 64 contract, so shapes outside it must raise RuntimeError("HIP error: ..."),
+which is how the reference binding reports cuda_tiled's cudaErrorInvalidValue, :62-65)."""
 import numpy as np
 import pytest
 
@@ -45,12 +45,8 @@ def test_hip_kernels_match_numpy(impl, shape):
     m, k, n = shape
     a, w = make(*shape, seed=sum(shape))
     packed = ternix.pack_ternary(w)
-    if impl == "hip_tiled" and (m % 64 or k % 64 or n % 64):
-        with pytest.raises(ValueError):
-            ternix.ternary_matmul(a, packed, impl)
-        return
-    if impl == "hip_gemv" and m > 32:
-        with pytest.raises(ValueError):
+    if (impl == "hip_tiled" and (m % 64 or k % 64 or n % 64)) or (impl == "hip_gemv" and m > 32):
+        with pytest.raises(RuntimeError, match="HIP error"):
             ternix.ternary_matmul(a, packed, impl)
         return
     got = ternix.ternary_matmul(a, packed, impl)
