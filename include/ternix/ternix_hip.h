@@ -117,6 +117,21 @@ int ternix_hip_mul_mat_ternary_ws(const int8_t* dA, const uint8_t* dB, int32_t* 
                                   int64_t M, int64_t K, int64_t N,
                                   void* dWorkspace, size_t workspace_bytes, void* stream);
 
+/* ternix_hip_mul_mat_ternary that allocates nothing: its scratch is a fixed device
+ * array of ternix_hip_noalloc_scratch_bytes() (32 MiB) inside the library, one per
+ * GPU, held until the process ends.  Same results and status contract as
+ * ternix_hip_mul_mat_ternary; hipErrorOutOfMemory (2), before any work, when the
+ * shape needs more scratch than that (ternix_hip_mul_mat_ternary_workspace_size).
+ * Every call on one GPU shares that GPU's array and nothing in it carries over
+ * between calls: calls that overlap in time on one GPU (two streams, two host
+ * threads) race and must be serialised by the caller.
+ * No reference counterpart: for callers that cannot allocate device memory
+ * (code under hipGraph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). */
+int ternix_hip_mul_mat_ternary_noalloc(const int8_t* dA, const uint8_t* dB, int32_t* dC,
+                                       int64_t M, int64_t K, int64_t N, void* stream);
+size_t ternix_hip_noalloc_scratch_bytes(void);
+
 /* Frees the library-owned workspace of (current device, stream) after synchronising
  * the stream.  The caller guarantees that no hipGraph captured on that stream with
  * library calls runs again afterwards (it would reference the freed buffers).  The next

@@ -51,6 +51,10 @@ def load():
     lib.ternix_hip_mul_mat_ternary_ws.argtypes = [i8p, i8p, i8p, i64, i64, i64, ctypes.c_void_p, ctypes.c_size_t,
                                                   ctypes.c_void_p]
     lib.ternix_hip_mul_mat_ternary_ws.restype = ctypes.c_int
+    lib.ternix_hip_mul_mat_ternary_noalloc.argtypes = [i8p, i8p, i8p, i64, i64, i64, ctypes.c_void_p]
+    lib.ternix_hip_mul_mat_ternary_noalloc.restype = ctypes.c_int
+    lib.ternix_hip_noalloc_scratch_bytes.argtypes = []
+    lib.ternix_hip_noalloc_scratch_bytes.restype = ctypes.c_size_t
     lib.ternix_hip_release_stream.argtypes = [ctypes.c_void_p]
     lib.ternix_hip_release_stream.restype = ctypes.c_int
     lib.ternix_hip_plan_describe.argtypes = [i8p, i8p, i64, i64, i64, ctypes.c_char_p, ctypes.c_size_t]
