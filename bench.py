@@ -52,15 +52,47 @@ def parse():
     return ap.parse_args()
 
 
-def profiled_traffic():
-    """HBM bytes per GEMV call from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary, or None."""
+def profiled_traffic(key):
+    """HBM bytes per call from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary (key
+    'gemv_cfg2' or 'gemm_cfg4'), with the commit and kernel plan the counters were taken on, or None.
+    The counters cannot be read inside this process; the figure is as current as that summary."""
     path = os.path.join(ROOT, "profiles", "hbm_traffic_fetch_write.md")
     try:
         text = open(path).read()
-        block = text.split("```json", 1)[1].split("```", 1)[0]
-        return int(json.loads(block)["gemv_cfg2_traffic_bytes_per_call"])
-    except (OSError, IndexError, KeyError, ValueError):
+        block = json.loads(text.split("```json", 1)[1].split("```", 1)[0])
+        return {"bytes": int(block[key]["traffic_bytes_per_call"]), "source": "profiles/hbm_traffic_fetch_write.md",
+                "measured_at_commit": block.get("commit"), "plan": block[key].get("plan")}
+    except (OSError, IndexError, KeyError, ValueError, TypeError):
         return None
+
+
+def plan_of(lib, prob):
+    """The kernel(s) the library's automatic path launches for this problem (its own description)."""
+    buf = ctypes.create_string_buffer(192)
+    c = prob.case
+    lib.ternix_hip_plan_describe(prob.dA.value, prob.dW[0].value, c.M, c.K, c.N, buf, len(buf))
+    return buf.value.decode()
+
+
+def read_floor_us(lib, nbytes, copies, stream, steps):
+    """Time of a bare streaming read of `nbytes` (ternix_hip_debug_stream_read), rotating over `copies`
+    buffers of exactly that size (as the matmul's weights rotate) and timed with the same graph method:
+    the least any kernel that reads those bytes from HBM takes here, launch and dispatch included."""
+    from ternixengine_amd import hip_runtime as hr
+    nbytes = nbytes // 16 * 16
+    bufs = [hr.DeviceBuffer(nbytes) for _ in range(copies)]
+    flag = hr.DeviceBuffer(16)
+
+    def step(i):
+        b = bufs[i % len(bufs)]
+        if nbytes > b.nbytes:  # the read must stay inside the buffer
+            raise ValueError("read floor buffer too small")
+        st = lib.ternix_hip_debug_stream_read(b.value, nbytes, flag.value, stream.handle)
+        if st != 0:
+            raise RuntimeError(f"stream read failed: {st}")
+
+    prewarm(step, 0.2, stream)
+    return time_launches(step, steps, 5, stream) / steps * 1e3
 
 
 def calibrate_copy():
@@ -176,6 +208,8 @@ def bench_gemv_pair(args, stream, lib):
     # hot-cache variant (same weights every step) for reference only
     ms_hot = time_launches(lambda i: (launch(fn, pu, 0, stream), launch(fn, pd, 0, stream)), args.steps,
                            args.warmup, stream)
+    # bare-read floor of one GEMV's bytes, over the same weight pools (alternating up / down buffers)
+    floor = read_floor_us(lib, bytes_step // 2, 2 * copies, stream, 2 * args.steps)
     return {
         "ms_per_step": ms / args.steps,
         "bytes_per_step": bytes_step,
@@ -186,6 +220,8 @@ def bench_gemv_pair(args, stream, lib):
         "single_launch_median_us": per_launch,
         "pool_copies": copies,
         "pool_bytes": copies * pair_w,
+        "read_floor_us": floor,
+        "plan": {"up": plan_of(lib, pu), "down": plan_of(lib, pd)},
         "verified": ok,
     }
 
@@ -200,8 +236,10 @@ def bench_big_m1(args, stream, lib):
     steps = max(10, args.steps // 4)
     prewarm(lambda i: launch(fn, p, i % copies, stream), args.prewarm_s, stream)
     ms = time_launches(lambda i: launch(fn, p, i % copies, stream), steps, max(2, args.warmup // 4), stream)
+    floor = read_floor_us(lib, case.bytes_algorithmic, copies, stream, steps)
     return {"shape": [case.M, case.K, case.N], "launch_us": ms / steps * 1e3,
-            "gbs": case.bytes_algorithmic / (ms / steps * 1e-3) / 1e9, "verified": verify(p), "pool_copies": copies}
+            "gbs": case.bytes_algorithmic / (ms / steps * 1e-3) / 1e9, "verified": verify(p), "pool_copies": copies,
+            "read_floor_us": floor, "plan": plan_of(lib, p)}
 
 
 def bench_gemm(args, stream, lib):
@@ -216,7 +254,7 @@ def bench_gemm(args, stream, lib):
         per = ms / args.gemm_steps
         tops = case.ops / (per * 1e-3) / 1e12
         out.append({"shape": [case.M, case.K, case.N], "us": per * 1e3, "tops": tops,
-                    "frac": tops / INT8_PEAK_TOPS, "verified": verify(p)})
+                    "frac": tops / INT8_PEAK_TOPS, "verified": verify(p), "plan": plan_of(lib, p)})
         tot_ops += case.ops
         tot_ms += per
         del p
@@ -359,11 +397,86 @@ def bench_ffn(args, stream, lib):
             "tile64_us_per_block": ms_t / args.steps * 1e3, "tile64_equal": same}
 
 
+def _cpu_kernels():
+    """The reference's CPU kernels (oracle/_ref, compiled from its sources) or, without them, the
+    oracle's plain-C restatement: (avx2_blocked, scalar, kind)."""
+    vp, sz = ctypes.c_void_p, ctypes.c_size_t
+    ref_so = os.path.join(ROOT, "oracle", "_ref", "libternix_ref.so")
+    if os.path.exists(ref_so):
+        L = ctypes.CDLL(ref_so)
+        fns, kind = (L.ref_mm_avx2_blocked, L.ref_mm_scalar), "reference"
+    else:
+        L = ctypes.CDLL(os.path.join(ROOT, "oracle", "liboracle.so"))
+        fns, kind = (L.oracle_mm_avx2_blocked, L.oracle_mm_scalar), "port"
+    for f in fns:
+        f.argtypes = [vp, vp, vp, sz, sz, sz]
+    return fns[0], fns[1], kind
+
+
+def cpu_config(case, a, wp, budget_s=0.3, threads=None):
+    """The reference CPU kernel on one configuration, on this host: mul_mat_ternary_avx2_blocked (the
+    scalar kernel where N % 8 != 0, outside the AVX2 contract), 1 thread and all threads (up to 16, the
+    GPU box's CPU share).  Large M is timed on a sample of rows (a multiple of 4, so the blocked kernel
+    runs as on the full matrix) and scaled to M; every row costs the same.  Threads split rows when
+    there are at least 4 per thread, else re-strided column slices of W (N_t % 8 == 0).  GIL released in
+    the foreign calls."""
+    import threading
+    vp = ctypes.c_void_p
+    blocked, scalar, kind = _cpu_kernels()
+    avx = case.N % 8 == 0
+    fn, kname = (blocked, "avx2_blocked") if avx else (scalar, "scalar")
+    rate = 14e9 if avx else 3e9  # rough single-thread ops/s, only to size the row sample
+    row_s = 2.0 * case.K * case.N / rate
+    m_s = case.M if case.M < 8 else max(4, min(case.M, int(budget_s / max(row_s, 1e-9)) // 4 * 4))
+    a_s = np.ascontiguousarray(a[:m_s])
+    out = np.empty((m_s, case.N), np.int32)
+
+    def call(aa, ww, oo, m, n):
+        fn(aa.ctypes.data_as(vp), ww.ctypes.data_as(vp), oo.ctypes.data_as(vp), m, case.K, n)
+
+    ts, t_end = [], time.perf_counter() + budget_s
+    while not ts or (time.perf_counter() < t_end and len(ts) < 50):
+        t0 = time.perf_counter()
+        call(a_s, wp, out, m_s, case.N)
+        ts.append(time.perf_counter() - t0)
+    t1 = statistics.median(ts) * case.M / m_s
+    T = threads or max(1, min(16, os.cpu_count() or 1))
+    jobs = []
+    if m_s >= 4 * T:
+        per = -(-m_s // T // 4) * 4
+        for i in range(T):
+            r0, r1 = i * per, min(m_s, (i + 1) * per)
+            if r1 > r0:
+                jobs.append((np.ascontiguousarray(a_s[r0:r1]), wp, np.empty((r1 - r0, case.N), np.int32), r1 - r0,
+                             case.N))
+    else:
+        step = 8 if avx else 4
+        per = -(-case.N // T // step) * step
+        for i in range(T):
+            n0, n1 = i * per, min(case.N, (i + 1) * per)
+            if n1 > n0:
+                jobs.append((a_s, np.ascontiguousarray(wp[:, n0 // 4:n1 // 4]), np.empty((m_s, n1 - n0), np.int32),
+                             m_s, n1 - n0))
+    reps = max(1, int(budget_s / max(t1 * m_s / case.M * 2 / len(jobs), 1e-6)))
+    ths = [threading.Thread(target=lambda j=j: [call(*j) for _ in range(reps)]) for j in jobs]
+    t0 = time.perf_counter()
+    for th in ths:
+        th.start()
+    for th in ths:
+        th.join()
+    tall = (time.perf_counter() - t0) / reps * case.M / m_s
+    return {"kernel": kname, "kind": kind, "us_1t": round(t1 * 1e6, 1), "us_all": round(tall * 1e6, 1),
+            "cores": len(jobs), "sample_rows": m_s,
+            "gbs_1t": round(case.bytes_algorithmic / t1 / 1e9, 3), "gops_1t": round(case.ops / t1 / 1e9, 2),
+            "gops_all": round(case.ops / tall / 1e9, 2)}
+
+
 def bench_configs(args, stream, lib):
     """Every BASELINE configuration through ternix_hip_mul_mat_ternary (automatic kernel choice),
     outputs checked against the committed digests: time per call, effective GB/s (M*K + K*N/4 + 4*M*N)
     and TOPS (2*M*N*K).  Weights rotate over >= 512 MiB of distinct copies (cold, as in a model's
-    layer sequence)."""
+    layer sequence).  Beside each, the reference CPU kernel on the same inputs on this host
+    (cpu_config: 1 thread and all threads)."""
     from ternixengine_amd import configs
     fn = lib.ternix_hip_mul_mat_ternary
     out = []
@@ -375,9 +488,13 @@ def bench_configs(args, stream, lib):
         prewarm(lambda i: launch(fn, p, i % copies, stream), 0.1, stream)
         ms = time_launches(lambda i: launch(fn, p, i % copies, stream), steps, 3, stream)
         us = ms / steps * 1e3
-        out.append({"name": name, "shape": [case.M, case.K, case.N], "us": round(us, 2),
-                    "gbs": round(case.bytes_algorithmic / (us * 1e-6) / 1e9, 1),
-                    "tops": round(case.ops / (us * 1e-6) / 1e12, 1), "verified": verify(p)})
+        entry = {"name": name, "shape": [case.M, case.K, case.N], "us": round(us, 2),
+                 "gbs": round(case.bytes_algorithmic / (us * 1e-6) / 1e9, 1),
+                 "tops": round(case.ops / (us * 1e-6) / 1e12, 1), "verified": verify(p), "plan": plan_of(lib, p)}
+        if not args.no_cpu:
+            entry["cpu"] = cpu_config(case, p.a, p.wp)
+            entry["gpu_vs_cpu_1t"] = round(entry["cpu"]["us_1t"] / us, 1)
+        out.append(entry)
         del p
     return out
 
@@ -579,21 +696,31 @@ def main():
                    "parallelism": "single GPU"},
     }
     if g:
+        tr = profiled_traffic("gemv_cfg2")
         line["roofline"] = {"bound": "hbm", "achieved": round(g["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                            "frac": round(g["gbs"] / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(),
+                            "frac": round(g["gbs"] / HBM_PEAK_GBS, 4), "traffic": tr["bytes"] if tr else None,
+                            "traffic_source": tr,
                             "algorithmic_bytes": g["bytes_per_step"] // 2,
-                            "kernel": "skinny_wave_kernel<32,2> (up: 4 K splits, down: 8, each summed inside the launch); one launch per ternix_hip_mul_mat_ternary call, M=1",
-                            "avg_launch_us": round(g["launch_us"], 3)}
+                            "kernel": f"up: {g['plan']['up']}; down: {g['plan']['down']}",
+                            "avg_launch_us": round(g["launch_us"], 3),
+                            "read_floor_us": round(g["read_floor_us"], 3),
+                            "frac_of_read_floor": round(g["read_floor_us"] / g["launch_us"], 4)}
         line["gemv_detail"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in g.items()}
     if "bigm1" in res:
         b = res["bigm1"]
         line["gemv_big_m1"] = {"shape": b["shape"], "gbs": round(b["gbs"], 1), "frac": round(b["gbs"] / HBM_PEAK_GBS, 4),
-                               "launch_us": round(b["launch_us"], 3), "verified": b["verified"]}
+                               "launch_us": round(b["launch_us"], 3), "verified": b["verified"], "plan": b["plan"],
+                               "read_floor_us": round(b["read_floor_us"], 3),
+                               "frac_of_read_floor": round(b["read_floor_us"] / b["launch_us"], 4)}
     if "gemm" in res:
         gm = res["gemm"]
+        tg = profiled_traffic("gemm_cfg4")
         line["roofline_gemm"] = {"bound": "mfma", "achieved": round(gm["tops"], 1), "peak": INT8_PEAK_TOPS,
-                                 "unit": "TFLOP/s", "frac": round(gm["frac"], 4), "traffic": None,
-                                 "kernel": "gemm_pipe_kernel / gemm_fast_kernel (cfg4, M=2048, int8 ops)"}
+                                 "unit": "TOPS", "op_type": "int8 multiply-accumulate, 2 ops each",
+                                 "frac": round(gm["frac"], 4), "traffic": tg["bytes"] if tg else None,
+                                 "traffic_source": tg,
+                                 "kernel": "; ".join(f"{s['shape'][1]}x{s['shape'][2]}: {s['plan']}"
+                                                     for s in gm["shapes"])}
         line["gemm_m2048"] = {"tops": round(gm["tops"], 1), "peak": INT8_PEAK_TOPS, "unit": "TOPS",
                               "frac": round(gm["frac"], 4),
                               "shapes": [{k: (round(v, 3) if isinstance(v, float) else v) for k, v in s.items()}

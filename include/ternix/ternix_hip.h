@@ -189,14 +189,21 @@ int ternix_hip_device_count(void);
  *   "gemm_narrow" v0    0 / 1: 64 x 64 GEMM tiles for M <= 64 off / forced
  *   "gemm_generic" v0   1: the generic GEMM for every GEMM call
  *   "gemm_splits" v0    GEMM split-K count forced
- *   "gemm_bm" v0        128 / 256: GEMM tile height forced
+ *   "gemm_bm" v0        64 / 128 / 256: GEMM tile height forced
  *   "deep" v0..3        0: no whole-K deep GEMV; else force (strip bytes, waves
  *                       per workgroup, ring slots, splits)
+ *   "sk_order" v0       1: release/acquire form of the in-launch split sums
+ *   "m1_atomic" v0      0: M = 1 GEMVs without the zero-fill + int32-atomic split plan
  * Returns 0, or 1 (hipErrorInvalidValue) for an unknown key.  Switches are
  * process-wide; a call running concurrently sees the old or the new value.
  * No reference counterpart (test hook of this library). */
 int ternix_hip_debug_set(const char* key, int v0, int v1, int v2, int v3);
 void ternix_hip_debug_reset(void);
+/* Measurement hook: one launch that only streams `bytes` (rounded down to a multiple
+ * of 16) from dSrc (16-byte aligned); dFlag (one int) is written only in a case that
+ * does not occur in practice.  Benchmarks time it as the bare HBM read floor of a
+ * matmul that reads the same number of bytes. */
+int ternix_hip_debug_stream_read(const void* dSrc, size_t bytes, int* dFlag, void* stream);
 /* Number of device allocations the library has made in this process (workspace
  * buffers, split counters, the host wrapper's temporaries); a test hook. */
 long long ternix_hip_debug_alloc_count(void);

@@ -42,6 +42,8 @@ def load():
     lib.ternix_hip_debug_set.restype = ctypes.c_int
     lib.ternix_hip_debug_reset.argtypes = []
     lib.ternix_hip_debug_reset.restype = None
+    lib.ternix_hip_debug_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p]
+    lib.ternix_hip_debug_stream_read.restype = ctypes.c_int
     lib.ternix_hip_debug_alloc_count.argtypes = []
     lib.ternix_hip_debug_alloc_count.restype = ctypes.c_longlong
     lib.ternix_hip_mul_mat_ternary_workspace_size.argtypes = [i64, i64, i64]

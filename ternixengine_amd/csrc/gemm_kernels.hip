@@ -441,7 +441,7 @@ struct PipeFrag {
     uint64_t lo[GT], hi[GT];
 };
 
-template <int BM, int WGN, int NS, int BK, int NWV, int BNB, bool TILED>
+template <int BM, int WGN, int NS, int BK, int NWV, int BNB, bool TILED, int GM = 4>
 __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2)))
 void gemm_pipe_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ B, int32_t* __restrict__ C, int M,
                       int K, int N, int tiles_n, int k_begin, int k_end, int accumulate, int vec_store,
@@ -487,7 +487,6 @@ void gemm_pipe_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ 
     int tm, tn;
     {
         const int t = xcd_linear(blockIdx.x, gridDim.x);
-        constexpr int GM = 4;
         const int first_m = (t / (GM * tiles_n)) * GM;
         const int gm = min(tiles_m - first_m, GM);
         const int local = t % (GM * tiles_n);
@@ -702,8 +701,9 @@ bool gemm_narrow_ok(int M, int K, int N, int k_len, int splits, int k_split) {
     return gemm_narrow_wanted(M, K, N) && k_len % 256 == 0 && (splits == 1 || k_split % 256 == 0);
 }
 
-hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int k_begin, int k_end,
-                       int accumulate, hipStream_t st, const OutScale& os, int splits, int k_split, int tiled) {
+// Which GEMM kernel a launch_gemm call runs (the single place the choice is made).
+GemmChoice gemm_choice(const int8_t* A, const uint8_t* B, int M, int K, int N, int k_begin, int k_end, int splits,
+                       int k_split, int tiled) {
     const int NB = N >> 2;
     const bool force_generic = debug_get(DBG_GEMM_GENERIC) == 1;  // tests
     if (splits < 1) splits = 1;
@@ -714,81 +714,93 @@ hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int
                       (size_t)GF_BK * (size_t)NB < ((size_t)1 << 32) &&
                       (tiled || !force_generic);
     // The tile-64 layout is read by the LDS-DMA GEMMs only (whole 128-row stages, at most 4 GiB of W).
-    if (tiled && (!fast || (size_t)K * (size_t)NB >= ((size_t)1 << 32))) return hipErrorInvalidValue;
-    if (fast) {
-        const int vs = ((uintptr_t)(os.Y ? (const void*)os.Y : (const void*)C) % 16) == 0;
-        const int tiles_n = NB / GF_BNB;
-        const int bm_env = debug_get(DBG_GEMM_BM);
-        // Measured on MI355X (cfg4 shapes): 256-row tiles only when they still give >= 1.5 tiles per
-        // CU, else 128-row tiles; 8 waves as 2 (M) x 4 (N); 128-deep stages.
-        const int cus = device_cu_count();
-        int bm = (splits == 1 && (long)((M + 255) / 256) * tiles_n * 2 >= 3L * cus) ? 256 : 128;
-        if (bm_env > 0) bm = bm_env == 128 ? 128 : 256;
-        const dim3 grid(((M + bm - 1) / bm) * tiles_n, splits);
-        // 128-row tiles run the software-pipelined kernel (measured faster on MI355X); 256-row tiles
-        // keep gemm_fast_kernel, whose wave tile leaves no registers for a second fragment set.
-        const int pipe = bm == 128 ? 1 : 0;
-        constexpr int small_m_max = 64;
-        if (M <= small_m_max && gemm_narrow_ok(M, K, N, k_end - k_begin, splits, k_split)) {
-            // 64 x 64 output tiles (16 bytes of every weight row): enough workgroups without a K
-            // split where the 256-column tiles would need one; one m-tile per wave, 256-deep stages.
-            const dim3 gridn((unsigned)(((M + 63) / 64) * (NB / 16)), splits);
-            if (tiled)
-                hipLaunchKernelGGL((gemm_pipe_kernel<64, 1, 3, 256, 4, 16, true>), gridn, dim3(256), 0, st, A, B, C, M,
-                                   K, N, NB / 16, k_begin, k_end, accumulate, vs, k_split, os);
-            else
-                hipLaunchKernelGGL((gemm_pipe_kernel<64, 1, 3, 256, 4, 16, false>), gridn, dim3(256), 0, st, A, B, C,
-                                   M, K, N, NB / 16, k_begin, k_end, accumulate, vs, k_split, os);
-            return hipGetLastError();
-        }
-        // One round of 128-row tiles with a short k-range (cfg4 4096^2): two co-resident workgroups
-        // of 64-row tiles per CU instead, whose barriers and final stores overlap each other's work
-        // (measured on MI355X: 29.5 -> 27.9 us; with long K or several rounds the 128-row tiles win).
-        const long tiles128 = (long)((M + 127) / 128) * tiles_n;
-        const bool short_round = splits == 1 && bm == 128 && bm_env <= 0 && tiles128 <= cus &&
-                                 2 * tiles128 >= cus && (k_end - k_begin) <= 4096;
-        if (M <= small_m_max || short_round) {
-            // Small M (64 rows or fewer): four-wave workgroups on 64-row tiles, so no MFMA row or A
-            // byte is spent on padding rows; the caller splits K to fill the chip.
-            const dim3 grid64((unsigned)(((M + 63) / 64) * tiles_n), splits);
-            if (tiled)
-                hipLaunchKernelGGL((gemm_pipe_kernel<64, 4, 3, 128, 4, 64, true>), grid64, dim3(256), 0, st, A, B, C,
-                                   M, K, N, tiles_n, k_begin, k_end, accumulate, vs, k_split, os);
-            else
-                hipLaunchKernelGGL((gemm_pipe_kernel<64, 4, 3, 128, 4, 64, false>), grid64, dim3(256), 0, st, A, B, C,
-                                   M, K, N, tiles_n, k_begin, k_end, accumulate, vs, k_split, os);
-            return hipGetLastError();
-        }
-        if (pipe) {
-#define TX_GP_LAUNCH(BM_, WGN_, NS_, BK_)                                                                          \
-    do {                                                                                                           \
-        if (tiled)                                                                                                 \
-            hipLaunchKernelGGL((gemm_pipe_kernel<BM_, WGN_, NS_, BK_, 8, GF_BNB, true>), grid, dim3(GF_THREADS), 0, \
-                               st, A, B, C, M, K, N, tiles_n, k_begin, k_end, accumulate, vs, k_split, os);      \
-        else                                                                                                       \
-            hipLaunchKernelGGL((gemm_pipe_kernel<BM_, WGN_, NS_, BK_, 8, GF_BNB, false>), grid, dim3(GF_THREADS), 0, \
-                               st, A, B, C, M, K, N, tiles_n, k_begin, k_end, accumulate, vs, k_split, os);      \
-    } while (0)
-            TX_GP_LAUNCH(128, 4, 3, 128);
-#undef TX_GP_LAUNCH
-            return hipGetLastError();
-        }
-#define TX_GF_LAUNCH(BM_, WGN_, NS_, BK_)                                                                         \
-    do {                                                                                                          \
-        if (tiled)                                                                                                \
-            hipLaunchKernelGGL((gemm_fast_kernel<BM_, WGN_, NS_, BK_, true>), grid, dim3(GF_THREADS), 0, st, A, B, \
-                               C, M, K, N, tiles_n, k_begin, k_end, accumulate, vs, k_split, os);               \
-        else                                                                                                      \
-            hipLaunchKernelGGL((gemm_fast_kernel<BM_, WGN_, NS_, BK_, false>), grid, dim3(GF_THREADS), 0, st, A,  \
-                               B, C, M, K, N, tiles_n, k_begin, k_end, accumulate, vs, k_split, os);            \
-    } while (0)
-        TX_GF_LAUNCH(256, 4, 3, 128);
-#undef TX_GF_LAUNCH
-        return hipGetLastError();
+    if (tiled && (!fast || (size_t)K * (size_t)NB >= ((size_t)1 << 32))) return GemmChoice::Invalid;
+    if (!fast) return GemmChoice::Generic;
+    const int tiles_n = NB / GF_BNB;
+    const int bm_env = debug_get(DBG_GEMM_BM);
+    // Measured on MI355X (cfg4 shapes): 256-row tiles only when they still give >= 1.5 tiles per
+    // CU, else 128-row tiles; 8 waves as 2 (M) x 4 (N); 128-deep stages.
+    const int cus = device_cu_count();
+    int bm = (splits == 1 && (long)((M + 255) / 256) * tiles_n * 2 >= 3L * cus) ? 256 : 128;
+    if (bm_env > 0) bm = bm_env == 128 ? 128 : (bm_env == 64 ? 64 : 256);  // tests and measurements
+    constexpr int small_m_max = 64;
+    // 64 x 64 output tiles (16 bytes of every weight row): enough workgroups without a K split where
+    // the 256-column tiles would need one; one m-tile per wave, 256-deep stages.
+    if (M <= small_m_max && gemm_narrow_ok(M, K, N, k_end - k_begin, splits, k_split)) return GemmChoice::Narrow64;
+    // One round of 128-row tiles with a short k-range (cfg4 4096^2): two co-resident workgroups of
+    // 64-row tiles per CU instead, whose barriers and final stores overlap each other's work
+    // (measured on MI355X: 29.5 -> 27.9 us; with long K or several rounds the 128-row tiles win).
+    // Small M (64 rows or fewer): the same four-wave workgroups on 64-row tiles, so no MFMA row or A
+    // byte is spent on padding rows; the caller splits K to fill the chip.
+    const long tiles128 = (long)((M + 127) / 128) * tiles_n;
+    const bool short_round = splits == 1 && bm == 128 && bm_env <= 0 && tiles128 <= cus && 2 * tiles128 >= cus &&
+                             (k_end - k_begin) <= 4096;
+    if (M <= small_m_max || short_round || bm == 64) return GemmChoice::Pipe64;
+    // 128-row tiles run the software-pipelined kernel (measured faster on MI355X); 256-row tiles
+    // keep gemm_fast_kernel, whose wave tile leaves no registers for a second fragment set.
+    return bm == 128 ? GemmChoice::Pipe128 : GemmChoice::Fast256;
+}
+
+const char* gemm_choice_name(GemmChoice c) {
+    switch (c) {
+        case GemmChoice::Narrow64: return "gemm_pipe_kernel<64 rows x 64 cols, 4 waves>";
+        case GemmChoice::Pipe64: return "gemm_pipe_kernel<64 rows x 256 cols, 4 waves>";
+        case GemmChoice::Pipe128: return "gemm_pipe_kernel<128 rows x 256 cols, 8 waves>";
+        case GemmChoice::Fast256: return "gemm_fast_kernel<256 rows x 256 cols, 8 waves>";
+        case GemmChoice::Generic: return "gemm_kernel<128 rows x 256 cols, register-staged>";
+        default: return "invalid";
     }
-    const bool aw = (NB % 4 == 0) && ((uintptr_t)B % 4 == 0);
-    const bool aa = (K % 16 == 0) && ((uintptr_t)A % 16 == 0);
-    return launch_gemm_t<128, 64>(A, B, C, M, K, N, aw, aa, k_begin, k_end, accumulate, st, os, splits, k_split);
+}
+
+hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int k_begin, int k_end,
+                       int accumulate, hipStream_t st, const OutScale& os, int splits, int k_split, int tiled) {
+    const int NB = N >> 2;
+    if (splits < 1) splits = 1;
+    const GemmChoice choice = gemm_choice(A, B, M, K, N, k_begin, k_end, splits, k_split, tiled);
+    if (choice == GemmChoice::Invalid) return hipErrorInvalidValue;
+    if (choice == GemmChoice::Generic) {
+        const bool aw = (NB % 4 == 0) && ((uintptr_t)B % 4 == 0);
+        const bool aa = (K % 16 == 0) && ((uintptr_t)A % 16 == 0);
+        return launch_gemm_t<128, 64>(A, B, C, M, K, N, aw, aa, k_begin, k_end, accumulate, st, os, splits, k_split);
+    }
+    const int vs = ((uintptr_t)(os.Y ? (const void*)os.Y : (const void*)C) % 16) == 0;
+    const int tiles_n = NB / GF_BNB;
+    if (choice == GemmChoice::Narrow64) {
+        const dim3 gridn((unsigned)(((M + 63) / 64) * (NB / 16)), splits);
+        if (tiled)
+            hipLaunchKernelGGL((gemm_pipe_kernel<64, 1, 3, 256, 4, 16, true>), gridn, dim3(256), 0, st, A, B, C, M, K,
+                               N, NB / 16, k_begin, k_end, accumulate, vs, k_split, os);
+        else
+            hipLaunchKernelGGL((gemm_pipe_kernel<64, 1, 3, 256, 4, 16, false>), gridn, dim3(256), 0, st, A, B, C, M,
+                               K, N, NB / 16, k_begin, k_end, accumulate, vs, k_split, os);
+    } else if (choice == GemmChoice::Pipe64) {
+        // Tiles are visited in groups of 8 row tiles per column band (512 rows, as 4 groups of 128-row
+        // tiles): measured on MI355X with cold weights, 2048x4096x4096 28.4 -> 27.0 us against groups of 4.
+        const dim3 grid64((unsigned)(((M + 63) / 64) * tiles_n), splits);
+        if (tiled)
+            hipLaunchKernelGGL((gemm_pipe_kernel<64, 4, 3, 128, 4, 64, true, 8>), grid64, dim3(256), 0, st, A, B, C,
+                               M, K, N, tiles_n, k_begin, k_end, accumulate, vs, k_split, os);
+        else
+            hipLaunchKernelGGL((gemm_pipe_kernel<64, 4, 3, 128, 4, 64, false, 8>), grid64, dim3(256), 0, st, A, B, C,
+                               M, K, N, tiles_n, k_begin, k_end, accumulate, vs, k_split, os);
+    } else if (choice == GemmChoice::Pipe128) {
+        const dim3 grid(((M + 127) / 128) * tiles_n, splits);
+        if (tiled)
+            hipLaunchKernelGGL((gemm_pipe_kernel<128, 4, 3, 128, 8, GF_BNB, true>), grid, dim3(GF_THREADS), 0, st, A,
+                               B, C, M, K, N, tiles_n, k_begin, k_end, accumulate, vs, k_split, os);
+        else
+            hipLaunchKernelGGL((gemm_pipe_kernel<128, 4, 3, 128, 8, GF_BNB, false>), grid, dim3(GF_THREADS), 0, st, A,
+                               B, C, M, K, N, tiles_n, k_begin, k_end, accumulate, vs, k_split, os);
+    } else {
+        const dim3 grid(((M + 255) / 256) * tiles_n, splits);
+        if (tiled)
+            hipLaunchKernelGGL((gemm_fast_kernel<256, 4, 3, 128, true>), grid, dim3(GF_THREADS), 0, st, A, B, C, M, K,
+                               N, tiles_n, k_begin, k_end, accumulate, vs, k_split, os);
+        else
+            hipLaunchKernelGGL((gemm_fast_kernel<256, 4, 3, 128, false>), grid, dim3(GF_THREADS), 0, st, A, B, C, M,
+                               K, N, tiles_n, k_begin, k_end, accumulate, vs, k_split, os);
+    }
+    return hipGetLastError();
 }
 
 }  // namespace ternix_hip

@@ -36,14 +36,17 @@ enum DebugKey : int {
     DBG_GEMM_NARROW,     // [0] 0 / 1: 64 x 64 GEMM tiles for M <= 64 off / forced
     DBG_GEMM_GENERIC,    // [0] == 1: the generic (register-staged) GEMM for every GEMM call
     DBG_GEMM_SPLITS,     // [0] GEMM split-K count forced
-    DBG_GEMM_BM,         // [0] 128 / 256: GEMM tile height forced
+    DBG_GEMM_BM,         // [0] 64 / 128 / 256: GEMM tile height forced
     DBG_DEEP,            // [0] == 0: no whole-K deep GEMV; else (sw, nw, nsw, splits) forced
     DBG_SK_ORDER,        // [0] 1: release/acquire (agent scope) for the in-launch split sums
+    DBG_M1_ATOMIC,       // [0] 0: no zero-fill + atomic split plan for M = 1 GEMVs
     DBG_COUNT
 };
 int debug_get(DebugKey key, int idx = 0);
 
 hipError_t launch_zero(int32_t* C, size_t n, hipStream_t st);
+// Bare streaming read of `bytes` (rounded down to 16) at p (16-byte aligned): the HBM floor reference.
+hipError_t launch_stream_read(const void* p, size_t bytes, int* out, hipStream_t st);
 // LDS bytes the skinny fast kernel uses for one workgroup's activation slice (the rows of one
 // m-group x steps_per_split * 64 bytes, each row padded by 16 bytes); the fast kernel runs only up
 // to kSkinnyALdsMax, so planners keep steps_per_split small enough for it.
@@ -103,6 +106,11 @@ hipError_t launch_skinny_wave(const int8_t* A, const uint8_t* B, int32_t* C, int
 // True when launch_gemm runs this M <= 64 shape on 64 x 64 tiles (K % 256 == 0, N/4 % 16 == 0, at
 // most one tile per CU); split-K k-ranges must then be multiples of 256.
 bool gemm_narrow_wanted(int M, int K, int N);
+// The GEMM kernel launch_gemm runs for these arguments (Invalid: it would return hipErrorInvalidValue).
+enum class GemmChoice { Invalid, Narrow64, Pipe64, Pipe128, Fast256, Generic };
+GemmChoice gemm_choice(const int8_t* A, const uint8_t* B, int M, int K, int N, int k_begin, int k_end, int splits,
+                       int k_split, int tiled);
+const char* gemm_choice_name(GemmChoice c);
 // LDS-tiled MFMA GEMM over k-rows [k_begin, k_end); accumulate != 0 adds into C instead of storing.
 // With os.Y set the tile epilogue writes the dequantised floats instead (accumulate must be 0).
 // splits > 1: split-K over gridDim.y, each workgroup row of the grid covering k_split k-rows (a

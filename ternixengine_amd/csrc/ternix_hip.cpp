@@ -109,15 +109,17 @@ int last_max_splits() {
 // they exist, when `need` exceeds the slots or for more than last_max_splits() splits: the caller
 // then uses the reduce launch.
 constexpr size_t kCounterSlots = size_t(1) << 16;
-int* arrival_counters(hipStream_t st, size_t need, int M, int splits, int sps) {
-    // Up to 4 rows with long k-ranges per split (>= 8 steps) also sum up to 8 splits inside the
-    // launch: their workgroups finish far apart, so the arrivals hardly queue (cold cfg3 M=4 down:
-    // 8 splits 9.8 us against 11.5 for the DMA-staged kernel and its reduce launch; 12 splits of
-    // cfg2 down 8.6 us against 7.8 with 8; 16 splits of tile-64 cfg3 M=4 down 12.2 against 9.3 us
-    // with the reduce launch).
+// Up to 4 rows with long k-ranges per split (>= 8 steps) also sum up to 8 splits inside the
+// launch: their workgroups finish far apart, so the arrivals hardly queue (cold cfg3 M=4 down:
+// 8 splits 9.8 us against 11.5 for the DMA-staged kernel and its reduce launch; 12 splits of
+// cfg2 down 8.6 us against 7.8 with 8; 16 splits of tile-64 cfg3 M=4 down 12.2 against 9.3 us
+// with the reduce launch).
+bool counters_wanted(size_t need, int M, int splits, int sps) {
     const int lim = last_max_splits();
-    if (lim <= 0 || (splits > lim && !(M <= 4 && sps >= 8 && splits <= 8)) || need > kCounterSlots)
-        return nullptr;
+    return !(lim <= 0 || (splits > lim && !(M <= 4 && sps >= 8 && splits <= 8)) || need > kCounterSlots);
+}
+int* arrival_counters(hipStream_t st, size_t need, int M, int splits, int sps) {
+    if (!counters_wanted(need, M, splits, sps)) return nullptr;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return nullptr;
     std::lock_guard<std::mutex> lock(g_ws_mutex);
@@ -144,15 +146,17 @@ int* arrival_counters(hipStream_t st, size_t need, int M, int splits, int sps) {
 //     ternix_hip_mul_mat_ternary_noalloc): a request larger than the buffer gets nullptr (the planners
 //     then take a path that needs less), and the in-launch split sum is not used (its counters must be
 //     zero between calls, which only library-owned memory guarantees);
-//   * dry run (ternix_hip_mul_mat_ternary_workspace_size, ternix_hip_plan_describe): the caller-owned
-//     rules with an unbounded buffer; requests are recorded, nothing is launched, and the chosen
-//     kernel is described in `desc`.
+//   * dry run: requests are recorded, nothing is launched, and the chosen kernels are described in
+//     `desc`; under the caller-owned rules with an unbounded buffer for
+//     ternix_hip_mul_mat_ternary_workspace_size, under the library-owned ones (counters granted when
+//     they would be, nothing allocated) for ternix_hip_plan_describe.
 struct Ctx {
     hipStream_t st = nullptr;
     char* caller = nullptr;
     size_t caller_bytes = 0;
     bool use_caller = false;
     bool dry = false;
+    bool dry_library = false;  // dry run under the library-owned rules (plan description)
     size_t need = 0;
     char desc[192] = {0};
 
@@ -166,7 +170,10 @@ struct Ctx {
         return workspace(st, bytes);
     }
     int* counters(size_t slots, int M, int splits, int sps) {
-        if (dry || use_caller) return nullptr;
+        if (dry)  // never dereferenced: nothing launches
+            return dry_library && counters_wanted(slots, M, splits, sps) ? reinterpret_cast<int*>(uintptr_t(4096))
+                                                                        : nullptr;
+        if (use_caller) return nullptr;
         return arrival_counters(st, slots, M, splits, sps);
     }
     void note(const char* fmt, ...) __attribute__((format(printf, 2, 3))) {
@@ -361,6 +368,32 @@ hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
                                                       partials, st, os));
         }
     }
+    // M = 1 with an int32 output: the K splits add into C with int32 atomics after one fill kernel has
+    // zeroed it (exact, order-free), instead of summing them inside the launch through a same-address
+    // arrival counter or in a reduce launch.  Measured on MI355X with cold weights (graph timing): cfg1
+    // 5.80 -> 5.08 us (16-byte strips, 6 splits), cfg2 up 6.70 -> 6.36 (32-byte, 4), cfg2 down 7.48 ->
+    // 6.44 (32-byte, 10); at M = 4 and 16 the other plans stay faster (cfg3 M=4 up 9.3 vs 10.2), and
+    // for wide matrices (cfg5 big, 224 32-byte strips) the DMA-staged kernel is (15.7 vs 24+ us).
+    if (!generic && M == 1 && aq.mode == 0 && os.Y == nullptr && dC != nullptr && wave_kernel_enabled() &&
+        ternix_hip::debug_get(ternix_hip::DBG_SKINNY_WAVE) < 0 && ternix_hip::debug_get(ternix_hip::DBG_M1_ATOMIC) != 0) {
+        const int NB = N / 4, nsteps = K / 64, cus = cu_count();
+        int sw = 0, sp = 0;
+        if (K <= 4096 && NB <= 1024 && NB % 16 == 0) {
+            sw = 16;
+            sp = std::max(1, std::min(6, cus / (NB / 16)));
+        } else if (NB % 32 == 0 && (long)(NB / 32) * 4 * 50 <= (long)cus * 53) {
+            sw = 32;
+            sp = std::min(cus / (NB / 32), std::max(1, nsteps / 4));
+        }
+        if (sw > 0 && sp > 1 && ternix_hip::skinny_wave_ok(dA, dB, M, K, N, sw)) {
+            const int sps = (nsteps + sp - 1) / sp, splits = (nsteps + sps - 1) / sps;
+            if (splits > 1 && sps * 64 <= ternix_hip::kMaxKPerAccumulator) {
+                c.note("zero_kernel + skinny_wave_kernel sw=%d nsw=2 splits=%d (splits added with int32 atomics)", sw,
+                       splits);
+                return TX_LAUNCH(c, ternix_hip::launch_skinny_wave(dA, dB, dC, M, K, N, sw, 2, splits, sps, nullptr, st));
+            }
+        }
+    }
     // Wave-pipelined kernel (32-byte strips, 16-byte with fused quantisation; 2 ring slots per wave),
     // measured on MI355X (16-byte strips) against the DMA-staged kernel: faster for K <= 4096 (cfg1
     // 6.26 -> 5.64 us, cfg2 up 6.94 -> 6.29, cfg3 M=4 up 11.62 -> 10.41, M=16 up 14.27 -> 11.45) and
@@ -481,14 +514,16 @@ hipError_t run_gemm(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int
             int32_t* partials = (splits > 1 && need <= kWorkspaceMax) ? static_cast<int32_t*>(c.get(need))
                                                                        : nullptr;
             if (partials) {
-                c.note("gemm (tile by launch_gemm) splits=%d + splitk_reduce_kernel", splits);
+                c.note("%s splits=%d + splitk_reduce_kernel",
+                       ternix_hip::gemm_choice_name(ternix_hip::gemm_choice(dA, dB, M, K, N, 0, K, splits, k_split, tiled)),
+                       splits);
                 hipError_t e = TX_LAUNCH(c, ternix_hip::launch_gemm(dA, dB, partials, M, K, N, 0, K, 0, st, ternix_hip::OutScale{},
                                                        splits, k_split, tiled));
                 if (e != hipSuccess) return e;
                 return TX_LAUNCH(c, ternix_hip::launch_splitk_reduce(partials, dC, M, N, splits, os, st));
             }
         }
-        c.note("gemm (tile by launch_gemm)");
+        c.note("%s", ternix_hip::gemm_choice_name(ternix_hip::gemm_choice(dA, dB, M, K, N, 0, K, 1, 0, tiled)));
         return TX_LAUNCH(c, ternix_hip::launch_gemm(dA, dB, dC, M, K, N, 0, K, 0, st, os, 1, 0, tiled));
     }
     if (dC == nullptr) return hipErrorInvalidValue;  // scaled call without int scratch
@@ -667,9 +702,10 @@ int dispatch_ctx(Path path, const int8_t* dA, const uint8_t* dB, int32_t* dC, in
 
 // Dry run of the automatic path for operands at the given addresses (only their alignment matters;
 // nothing is dereferenced or launched).
-Ctx plan_auto(int64_t M, int64_t K, int64_t N, uintptr_t a_addr, uintptr_t b_addr) {
+Ctx plan_auto(int64_t M, int64_t K, int64_t N, uintptr_t a_addr, uintptr_t b_addr, bool library = false) {
     Ctx c;
     c.dry = true;
+    c.dry_library = library;
     std::snprintf(c.desc, sizeof(c.desc), "none");
     const int s = dispatch_ctx(Path::Auto, reinterpret_cast<const int8_t*>(a_addr),
                                reinterpret_cast<const uint8_t*>(b_addr), reinterpret_cast<int32_t*>(uintptr_t(1) << 20),
@@ -712,7 +748,7 @@ int ternix_hip_mul_mat_ternary_ws(const int8_t* dA, const uint8_t* dB, int32_t* 
 int ternix_hip_plan_describe(const int8_t* dA, const uint8_t* dB, int64_t M, int64_t K, int64_t N, char* buf,
                              size_t len) {
     if (buf == nullptr || len == 0) return (int)hipErrorInvalidValue;
-    const Ctx c = plan_auto(M, K, N, reinterpret_cast<uintptr_t>(dA), reinterpret_cast<uintptr_t>(dB));
+    const Ctx c = plan_auto(M, K, N, reinterpret_cast<uintptr_t>(dA), reinterpret_cast<uintptr_t>(dB), true);
     std::snprintf(buf, len, "%s", c.desc);
     return std::strcmp(c.desc, "rejected") == 0 ? (int)hipErrorInvalidValue : (int)hipSuccess;
 }
@@ -1090,6 +1126,7 @@ int ternix_hip_debug_set(const char* key, int v0, int v1, int v2, int v3) {
         {"gemm_narrow", ternix_hip::DBG_GEMM_NARROW}, {"gemm_generic", ternix_hip::DBG_GEMM_GENERIC},
         {"gemm_splits", ternix_hip::DBG_GEMM_SPLITS}, {"gemm_bm", ternix_hip::DBG_GEMM_BM},
         {"deep", ternix_hip::DBG_DEEP},             {"sk_order", ternix_hip::DBG_SK_ORDER},
+        {"m1_atomic", ternix_hip::DBG_M1_ATOMIC},
     };
     if (key == nullptr) return (int)hipErrorInvalidValue;
     for (const auto& n : names) {
@@ -1100,6 +1137,13 @@ int ternix_hip_debug_set(const char* key, int v0, int v1, int v2, int v3) {
         return (int)hipSuccess;
     }
     return (int)hipErrorInvalidValue;
+}
+
+int ternix_hip_debug_stream_read(const void* dSrc, size_t bytes, int* dFlag, void* stream) {
+    if (bytes / 16 == 0) return (int)hipSuccess;
+    if (dSrc == nullptr || dFlag == nullptr || reinterpret_cast<uintptr_t>(dSrc) % 16 != 0)
+        return (int)hipErrorInvalidValue;
+    return (int)ternix_hip::launch_stream_read(dSrc, bytes, dFlag, static_cast<hipStream_t>(stream));
 }
 
 long long ternix_hip_debug_alloc_count(void) { return g_alloc_count.load(std::memory_order_relaxed); }

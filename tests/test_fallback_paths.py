@@ -22,6 +22,8 @@ SWITCHES = [
     {"wave_last": 0},                                      # reduce launch instead of in-launch sums
     {"gemm_generic": 1},                                   # register-staged generic GEMM
     {"sk_order": 1},                                       # release/acquire form of the in-launch sums
+    {"m1_atomic": 0},                                      # M = 1 without the zero-fill + atomic plan
+    {"m1_atomic": 0, "sk_order": 1},                       # ... and its in-launch sums in release/acquire form
 ]
 
 

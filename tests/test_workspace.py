@@ -12,7 +12,8 @@ from ternixengine_amd import hip_runtime as hr
 
 # (M, K, N): one shape per planner branch of ternix_hip_mul_mat_ternary
 BRANCH_SHAPES = [
-    (1, 2560, 6912),     # wave GEMV, K split (in-launch sum with library workspace, reduce with caller's)
+    (1, 2560, 6912),     # M = 1: zero fill + wave GEMV whose splits add with atomics (no workspace)
+    (4, 2560, 6912),     # wave GEMV, K split (in-launch sum with library workspace, reduce with caller's)
     (1, 8192, 28672),    # DMA-staged GEMV with split + reduce
     (1, 2560, 2560),     # wave GEMV, small N
     (16, 11008, 4096),   # wave GEMV, many splits + reduce
@@ -37,7 +38,8 @@ def test_workspace_size_and_plan_host():
     lib = tx._load()
     sizes = {s: lib.ternix_hip_mul_mat_ternary_workspace_size(*s) for s in BRANCH_SHAPES}
     assert sizes[(512, 1024, 1024)] == 0
-    assert sizes[(1, 2560, 6912)] >= 2 * 6912 * 4          # split partials of the wave GEMV
+    assert sizes[(1, 2560, 6912)] == 0                      # M = 1: splits add into C with atomics
+    assert sizes[(4, 2560, 6912)] >= 2 * 4 * 6912 * 4      # split partials of the wave GEMV
     assert sizes[(64, 11008, 4096)] >= 2 * 64 * 4096 * 4    # GEMM split partials
     assert sizes[(1, 1000, 3076)] >= 1024 * (3076 // 4)     # padded copy of W
     assert lib.ternix_hip_mul_mat_ternary_workspace_size(1, 64, 6) == 0     # rejected (N % 4)
