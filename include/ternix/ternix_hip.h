@@ -21,18 +21,28 @@
  * NULL for the default stream).  The caller owns A, B and C; C is fully
  * overwritten (never accumulated into).  Shapes are int64; N must be a
  * multiple of 4; M, K or N may be 0.
- * Workspace: the skinny path (small M) splits K over workgroups; the partial
- * sums go through a device workspace that the library allocates per (device,
- * stream) the first time a shape needs it (at most 256 MiB, kept until the
- * process ends) and that a second, small kernel adds into C.  No allocation
- * happens while the stream is being captured into a hipGraph: a call that
- * would need one then zeroes C and accumulates the partial sums with int32
- * atomics instead (exact, order-independent).  Warm the shapes up eagerly
- * before capturing to keep the faster path in the graph; such a graph uses
- * the capturing stream's workspace, so it must not run concurrently with
- * other small-M work issued on that stream.  Workspace buffers are never
- * freed before the process ends (an outgrown one is kept for the graphs and
- * queued work that still reference it).
+ * Workspace.  Some plans need device scratch besides A, B and C:
+ *   - split-K partial sums [splits][M][N] int32 of the small-M GEMVs (M = 2..32,
+ *     and M = 1 on wide matrices) and of GEMMs whose output tiles alone cannot fill
+ *     the chip (mid-size M against K > 4096);
+ *   - padded copies of W (K' x N'/4) and A (M x K') for ragged shapes (K % 64,
+ *     N/4 % 64) and misaligned operands, at any M;
+ *   - 64 K int32 arrival counters of the GEMVs that add a few K splits inside one
+ *     launch (zero between calls).
+ * M = 1 GEMVs on all but wide matrices need none: C is zeroed by a fill kernel and
+ * the K splits add into it with int32 atomics.  By default the library owns this
+ * scratch per (device, stream): allocated the first time a shape needs more than
+ * the current size (at most 256 MiB unless one call needs more), kept until the
+ * process ends or ternix_hip_release_stream, outgrown buffers retired but not
+ * freed.  No allocation happens while the stream is being captured into a hipGraph:
+ * a call that would need one then takes a plan that needs none (GEMV splits zero C
+ * and add with atomics, ragged shapes run the generic kernels), with identical
+ * results.  A graph captured with library calls on a stream uses that stream's
+ * buffers, so it must not run concurrently with any other library work issued on
+ * that stream (every call on one stream is ordered, so ordinary use is safe).
+ * Callers that must not allocate on the call pass their own workspace
+ * (ternix_hip_mul_mat_ternary_ws, sized by ..._workspace_size) or use
+ * ternix_hip_mul_mat_ternary_noalloc.
  * Calls are thread-safe; calls that share an output buffer race as any two
  * kernels writing one buffer do.
  *
