@@ -727,17 +727,14 @@ GemmChoice gemm_choice(const int8_t* A, const uint8_t* B, int M, int K, int N, i
     // 64 x 64 output tiles (16 bytes of every weight row): enough workgroups without a K split where
     // the 256-column tiles would need one; one m-tile per wave, 256-deep stages.
     if (M <= small_m_max && gemm_narrow_ok(M, K, N, k_end - k_begin, splits, k_split)) return GemmChoice::Narrow64;
-    // One round of 128-row tiles with a short k-range (cfg4 4096^2): two co-resident workgroups of
-    // 64-row tiles per CU instead, whose barriers and final stores overlap each other's work
-    // (measured on MI355X: 29.5 -> 27.9 us; with long K or several rounds the 128-row tiles win).
-    // Small M (64 rows or fewer): the same four-wave workgroups on 64-row tiles, so no MFMA row or A
-    // byte is spent on padding rows; the caller splits K to fill the chip.
-    const long tiles128 = (long)((M + 127) / 128) * tiles_n;
-    const bool short_round = splits == 1 && bm == 128 && bm_env <= 0 && tiles128 <= cus && 2 * tiles128 >= cus &&
-                             (k_end - k_begin) <= 4096;
-    if (M <= small_m_max || short_round || bm == 64) return GemmChoice::Pipe64;
-    // 128-row tiles run the software-pipelined kernel (measured faster on MI355X); 256-row tiles
-    // keep gemm_fast_kernel, whose wave tile leaves no registers for a second fragment set.
+    // Without a K split, 64-row tiles in workgroups of four waves (two co-resident per CU, whose
+    // barriers and final stores overlap each other's work) instead of 128-row tiles of eight waves:
+    // measured on MI355X, cold weights, 2048x4096x4096 29.1 -> 27.6 us, 1024x4096x4096 25.4 -> 20.3,
+    // 512x4096x4096 25.1 -> 19.5, 768x4096x11008 52.2 -> 46.1, 1536x4096x11008 81.2 -> 71.7,
+    // 2048x14336x4096 90.6 -> 90.4 (one round: equal).  With a K split the 128-row tiles stay
+    // (256x16384x4096: 31.8 against 35.5 us).  Small M (64 rows or fewer): the same four-wave
+    // workgroups, so no MFMA row or A byte is spent on padding rows; the caller splits K to fill the chip.
+    if (M <= small_m_max || bm == 64 || (splits == 1 && bm == 128 && bm_env <= 0)) return GemmChoice::Pipe64;
     return bm == 128 ? GemmChoice::Pipe128 : GemmChoice::Fast256;
 }
 

@@ -10,7 +10,7 @@ from ternixengine_amd import hip_runtime as hr
 
 SHAPES = [(1, 2560, 2560), (1, 6912, 2560), (4, 4096, 1024), (16, 2048, 4096), (16, 8192, 1024), (24, 4096, 512),
           (32, 2560, 1024), (48, 1024, 2048), (64, 4096, 1024), (129, 1001, 516), (1, 1000, 3076), (17, 4093, 1028),
-          (256, 2048, 1024)]
+          (256, 2048, 1024), (320, 1024, 2048)]
 
 SWITCHES = [
     {"skinny_wave": 0},                                    # DMA-staged GEMVs
@@ -24,6 +24,8 @@ SWITCHES = [
     {"sk_order": 1},                                       # release/acquire form of the in-launch sums
     {"m1_atomic": 0},                                      # M = 1 without the zero-fill + atomic plan
     {"m1_atomic": 0, "sk_order": 1},                       # ... and its in-launch sums in release/acquire form
+    {"gemm_bm": 128},                                      # 128-row GEMM tiles of eight waves
+    {"gemm_bm": 256},                                      # 256-row GEMM tiles
 ]
 
 
