@@ -28,9 +28,14 @@
  *   - padded copies of W (K' x N'/4) and A (M x K') for ragged shapes (K % 64,
  *     N/4 % 64) and misaligned operands, at any M;
  *   - 64 K int32 arrival counters of the GEMVs that add a few K splits inside one
- *     launch (zero between calls).
- * M = 1 GEMVs on all but wide matrices need none: C is zeroed by a fill kernel and
- * the K splits add into it with int32 atomics.  By default the library owns this
+ *     launch (zero between calls), and in the same 512 KiB buffer 16 K pairs of
+ *     64-bit per-strip tickets of the M = 1 GEMVs below (advanced by every call,
+ *     never reset).
+ * M = 1 GEMVs on all but wide matrices need no workspace: the K splits add into C
+ * with int32 atomics; with the library's tickets each strip's first split zeroes
+ * its outputs inside the same launch, else (caller-owned workspace, the allocation-
+ * free entry point, or capture before the tickets exist) a fill kernel zeroes C
+ * first.  By default the library owns this
  * scratch per (device, stream): allocated the first time a shape needs more than
  * the current size (at most 256 MiB unless one call needs more), kept until the
  * process ends or ternix_hip_release_stream, outgrown buffers retired but not
@@ -204,6 +209,7 @@ int ternix_hip_device_count(void);
  *                       per workgroup, ring slots, splits)
  *   "sk_order" v0       1: release/acquire form of the in-launch split sums
  *   "m1_atomic" v0      0: M = 1 GEMVs without the zero-fill + int32-atomic split plan
+ *   "self_zero" v0      0: that plan zeroes C with a fill kernel, not inside the launch
  * Returns 0, or 1 (hipErrorInvalidValue) for an unknown key.  Switches are
  * process-wide; a call running concurrently sees the old or the new value.
  * No reference counterpart (test hook of this library). */

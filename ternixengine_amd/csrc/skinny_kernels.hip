@@ -50,7 +50,19 @@ constexpr int kRowRegs = 32;  // fused activation quantisation: row elements per
 // split to arrive sums all partials of the tile (agent-scope loads) and writes C, then resets the
 // counter.  No L2 writeback or invalidate is needed because only those coherent accesses touch the
 // exchanged data, and no second launch is needed.
-enum SkinnyMode { SK_STORE = 0, SK_ATOMIC = 1, SK_PARTIAL = 2, SK_LAST = 3 };
+// SK_ATOMZ (skinny_wave_kernel only, one m-group): SK_ATOMIC without the fill launch.  Each strip
+// has a 64-bit ticket counter and a 64-bit "zeroed" word that persist across calls.  Every split
+// takes a ticket at its start (a returning add, issued after its first weight loads); each call
+// uses one block of 64 ticket values per strip (the split holding the block's last ticket adds the
+// rest of the block), so the first ticket of a call is a multiple of 64 and names the call.  The
+// split that draws it zeroes the strip's outputs with coherent agent-scope stores, waits for them,
+// and writes the call's number + 1 to the zeroed word; every other split checks that word before
+// its atomics (it reads it with its last weight loads) and, if it is not there yet, waits:
+// the split it waits for has already taken its ticket, so it is running and waits for nothing.
+enum SkinnyMode { SK_STORE = 0, SK_ATOMIC = 1, SK_PARTIAL = 2, SK_LAST = 3, SK_ATOMZ = 4 };
+// Bound of the SK_ATOMZ wait (each try is one memory round trip, so about a second): only a guard
+// that every wave exits.
+constexpr int kZeroSpinLimit = 1 << 20;
 
 struct SkinnyArgs {
     const int8_t* A;
@@ -76,6 +88,7 @@ struct SkinnyArgs {
     int tiled;            // skinny_wave_kernel: W in the tile-64 layout (kernel_common.h)
     int* cnt;             // SK_LAST: arrival counters, one per (m-group, strip), zero between calls
     int order;            // SK_LAST: 1 = C++ release/acquire at agent scope, 0 = coherent accesses only
+    unsigned long long* tick;  // SK_ATOMZ: per strip {ticket counter, zeroed word}, persistent
 };
 
 // One k-step of MFMA work for one 16-row x 4-byte-column block: raw[r] is the dword of row r.
@@ -946,8 +959,43 @@ void skinny_wave_kernel(SkinnyArgs args) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[g][j] = v4i{0, 0, 0, 0};
 
+    // SK_ATOMZ: ticket (wave 0; the other waves never touch C), requested before the first weight
+    // loads and waited for after them (the vmcnt wait below counts them), so that waiting for it
+    // does not wait for them.  Written as one instruction so that the compiler neither rewrites the
+    // single-lane atomic nor places its own wait for the result right after it.
+    unsigned long long call1 = 0;  // this call's number + 1, as the zeroer writes it
+    bool zeroer = false;
+    unsigned long long* tk = args.tick + 2 * (size_t)cx;
+    unsigned long long old = 0;
+    const bool ticket = AQ == 0 && args.mode == SK_ATOMZ && wave == 0;
+    if (ticket && lane == 0)
+        __asm__ volatile("global_atomic_add_x2 %0, %1, %2, off sc0" : "=v"(old) : "v"(tk), "v"(1ull) : "memory");
 #pragma unroll
     for (int p = 0; p < NSW - 1; ++p) issue(p, p, a_ring[p]);
+    if (ticket) {
+        TX_VMCNT((NSW - 1) * (NL + 1));  // the ticket has returned (the weight loads may not have)
+        __asm__ volatile("" : "+v"(old));
+        old = ((unsigned long long)(uint32_t)__builtin_amdgcn_readfirstlane((int)(old >> 32)) << 32) |
+              (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)old);
+        const int rank = (int)(old & 63);
+        call1 = (old >> 6) + 1;
+        zeroer = rank == 0;
+        if (rank == args.splits - 1 && args.splits < 64 && lane == 0)
+            __hip_atomic_fetch_add(tk, (unsigned long long)(64 - args.splits), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (zeroer) {
+            // rows m0 .. m0 + a_rows - 1, columns 4 * bc0 .. 4 * (bc0 + SW) - 1: 8 bytes per lane
+            for (int r = 0; r < a_rows; ++r) {
+                if (lane < SW * 2) {
+                    unsigned long long* z =
+                        reinterpret_cast<unsigned long long*>(args.C + (size_t)(m0 + r) * (size_t)args.N + 4 * bc0) + lane;
+                    __hip_atomic_store(z, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+            __builtin_amdgcn_s_waitcnt(0);  // the zeroes are stored, coherent at agent scope
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            if (lane == 0) __hip_atomic_store(tk + 1, call1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
     if constexpr (AQ != 0) {
         __shared__ float red[4];
         for (int r = 0; r < a_rows; ++r) {  // uniform: every thread takes part in the reductions
@@ -982,12 +1030,17 @@ void skinny_wave_kernel(SkinnyArgs args) {
         __syncthreads();  // qbuf and rscale complete
     }
     constexpr int VPS = NL + (AQ ? 0 : 1);  // vector memory operations per step and wave
+    // SK_ATOMZ: the zeroed word, read in the last iteration beside that iteration's (padding) loads,
+    // whose wait after the loop then covers it
+    unsigned long long zw = 0;
     for (int it0 = 0; it0 < iters; it0 += NSW) {
 #pragma unroll
         for (int p = 0; p < NSW; ++p) {
             const int it = it0 + p;
             issue(it + NSW - 1, (p + NSW - 1) % NSW, a_ring[(p + NSW - 1) % NSW]);
             TX_VMCNT((NSW - 1) * VPS);       // step `it` (DMAs and activation load) has landed
+            if (ticket && !zeroer && it == iters - 1 && lane == 0)
+                zw = __hip_atomic_load(tk + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (wave + 4 * it < nst) {       // wave-uniform
                 const uint32_t base = lds_u32(ring + p * SLOT);
                 uint64_t lo[G], hi[G];
@@ -1126,6 +1179,14 @@ void skinny_wave_kernel(SkinnyArgs args) {
         if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;
     }
+    if (AQ == 0 && args.mode == SK_ATOMZ && !zeroer) {  // wave 0: wait until the strip is zeroed
+        if (lane == 0)
+            for (int n = 0; zw != call1 && n < kZeroSpinLimit; ++n) {
+                __builtin_amdgcn_s_sleep(1);
+                zw = __hip_atomic_load(args.tick + 2 * (size_t)cx + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        __builtin_amdgcn_wave_barrier();
+    }
     if (LOW_M && kb != 0) return;
     int32_t* out_base = args.mode == SK_PARTIAL ? args.P + (size_t)sy * (size_t)M * (size_t)args.N : args.C;
     const bool vec = args.mode == SK_PARTIAL || args.vec_store;
@@ -1146,7 +1207,7 @@ void skinny_wave_kernel(SkinnyArgs args) {
                 continue;
             }
             int32_t* out = out_base + (size_t)row * (size_t)NO + 4 * bcol;
-            if (args.mode == SK_ATOMIC) {
+            if (args.mode == SK_ATOMIC || args.mode == SK_ATOMZ) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
                     if (v[j] != 0) atomicAdd(out + j, v[j]);
@@ -1377,7 +1438,7 @@ bool skinny_wave_ok(const int8_t* A, const uint8_t* B, int M, int K, int N, int 
 
 hipError_t launch_skinny_wave(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int sw, int nsw,
                               int splits, int steps_per_split, int32_t* partials, hipStream_t st, const OutScale& os,
-                              int n_out, const ActQuant& aq, int tiled, int* counters) {
+                              int n_out, const ActQuant& aq, int tiled, int* counters, unsigned long long* tickets) {
     if (tiled && (sw != 16 || n_out > 0)) return hipErrorInvalidValue;
     if (!skinny_wave_ok(A, B, M, K, N, sw) || nsw < 2 || nsw > 4 || steps_per_split < 1) return hipErrorInvalidValue;
     // Fused activation quantisation: one launch over whole rows (K <= 4096), 16-byte strips, 2 slots.
@@ -1389,6 +1450,10 @@ hipError_t launch_skinny_wave(const int8_t* A, const uint8_t* B, int32_t* C, int
     if (mode == SK_PARTIAL && counters && n_out == 0 && aq.mode == 0) mode = SK_LAST;
     if (n_out > 0 && (mode == SK_ATOMIC || n_out > N || n_out % 4 != 0)) return hipErrorInvalidValue;
     if (mode == SK_ATOMIC && C == nullptr) return hipErrorInvalidValue;
+    // Self-zeroing atomics: one m-group, C rows 8-byte aligned, at most 64 splits.
+    if (mode == SK_ATOMIC && tickets && M <= 16 && aq.mode == 0 && splits <= 64 && (uintptr_t)C % 8 == 0 &&
+        N % 2 == 0)
+        mode = SK_ATOMZ;
     if (mode == SK_ATOMIC) {
         const hipError_t e = launch_zero(C, (size_t)M * (size_t)N, st);
         if (e != hipSuccess) return e;
@@ -1398,6 +1463,7 @@ hipError_t launch_skinny_wave(const int8_t* A, const uint8_t* B, int32_t* C, int
     SkinnyArgs a{A, B, C, partials, M, K, N, steps_per_split, splits, mode, vec_store, 1, 1,
                  (mode == SK_STORE || mode == SK_LAST) ? os : OutScale{}};
     a.cnt = counters;
+    a.tick = tickets;
     a.order = debug_get(DBG_SK_ORDER) == 1;
     a.n_out = n_out;
     a.tiled = tiled;
@@ -1432,7 +1498,7 @@ hipError_t launch_skinny_wave(const int8_t* A, const uint8_t* B, int32_t* C, int
 #undef TX_SW_LAUNCH
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    if (mode == SK_ATOMIC && scaled) return launch_dequant(C, os, M, N, st);
+    if ((mode == SK_ATOMIC || mode == SK_ATOMZ) && scaled) return launch_dequant(C, os, M, N, st);
     if (mode != SK_PARTIAL) return e;
     return n_out > 0 ? launch_splitk_reduce(partials, C, M, n_out, splits, os, st, N)
                      : launch_splitk_reduce(partials, C, M, N, splits, os, st);

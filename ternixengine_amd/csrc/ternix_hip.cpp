@@ -118,8 +118,11 @@ bool counters_wanted(size_t need, int M, int splits, int sps) {
     const int lim = last_max_splits();
     return !(lim <= 0 || (splits > lim && !(M <= 4 && sps >= 8 && splits <= 8)) || need > kCounterSlots);
 }
-int* arrival_counters(hipStream_t st, size_t need, int M, int splits, int sps) {
-    if (!counters_wanted(need, M, splits, sps)) return nullptr;
+// Self-zeroing atomic GEMV tickets (skinny_kernels.hip, SK_ATOMZ): two 64-bit words per strip after
+// the arrival counters in the same zero-initialised buffer; they advance with every call and are
+// never reset.
+constexpr size_t kTicketStrips = size_t(1) << 14;
+int* counter_buffer(hipStream_t st) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return nullptr;
     std::lock_guard<std::mutex> lock(g_ws_mutex);
@@ -128,15 +131,24 @@ int* arrival_counters(hipStream_t st, size_t need, int M, int splits, int sps) {
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
     void* p = nullptr;
-    if (lib_malloc(&p, kCounterSlots * sizeof(int)) != hipSuccess) return nullptr;
+    constexpr size_t words = kCounterSlots + 4 * kTicketStrips;
+    if (lib_malloc(&p, words * sizeof(int)) != hipSuccess) return nullptr;
     // A fill kernel, not hipMemsetAsync (never inside capture here anyway: checked above).
-    if (ternix_hip::launch_zero(static_cast<int32_t*>(p), kCounterSlots, st) != hipSuccess) {
+    if (ternix_hip::launch_zero(static_cast<int32_t*>(p), words, st) != hipSuccess) {
         (void)hipGetLastError();
         (void)hipFree(p);
         return nullptr;
     }
     w.counters = static_cast<int*>(p);
     return w.counters;
+}
+int* arrival_counters(hipStream_t st, size_t need, int M, int splits, int sps) {
+    return counters_wanted(need, M, splits, sps) ? counter_buffer(st) : nullptr;
+}
+unsigned long long* zero_tickets(hipStream_t st, size_t strips) {
+    if (strips > kTicketStrips) return nullptr;
+    int* b = counter_buffer(st);
+    return b ? reinterpret_cast<unsigned long long*>(b + kCounterSlots) : nullptr;
 }
 
 // Execution context of one call: the stream, where split-K partials and padded copies live, and a
@@ -175,6 +187,14 @@ struct Ctx {
                                                                         : nullptr;
         if (use_caller) return nullptr;
         return arrival_counters(st, slots, M, splits, sps);
+    }
+    // Tickets of the self-zeroing atomic GEMV, under the same ownership rules as the counters.
+    unsigned long long* tickets(size_t strips) {
+        if (dry)  // never dereferenced: nothing launches
+            return dry_library && strips <= kTicketStrips ? reinterpret_cast<unsigned long long*>(uintptr_t(4096))
+                                                          : nullptr;
+        if (use_caller) return nullptr;
+        return zero_tickets(st, strips);
     }
     void note(const char* fmt, ...) __attribute__((format(printf, 2, 3))) {
         if (!dry) return;
@@ -374,6 +394,9 @@ hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
     // 5.80 -> 5.08 us (16-byte strips, 6 splits), cfg2 up 6.70 -> 6.36 (32-byte, 4), cfg2 down 7.48 ->
     // 6.44 (32-byte, 10); at M = 4 and 16 the other plans stay faster (cfg3 M=4 up 9.3 vs 10.2), and
     // for wide matrices (cfg5 big, 224 32-byte strips) the DMA-staged kernel is (15.7 vs 24+ us).
+    // With the library's tickets the fill launch goes too: each strip's first split zeroes its
+    // outputs inside the launch (skinny_kernels.hip, SK_ATOMZ); measured on MI355X, cold weights,
+    // graph timing of the cfg2 up + down pair: 6.75 -> 5.57 us per GEMV.
     if (!generic && M == 1 && aq.mode == 0 && os.Y == nullptr && dC != nullptr && wave_kernel_enabled() &&
         ternix_hip::debug_get(ternix_hip::DBG_SKINNY_WAVE) < 0 && ternix_hip::debug_get(ternix_hip::DBG_M1_ATOMIC) != 0) {
         const int NB = N / 4, nsteps = K / 64, cus = cu_count();
@@ -388,9 +411,18 @@ hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
         if (sw > 0 && sp > 1 && ternix_hip::skinny_wave_ok(dA, dB, M, K, N, sw)) {
             const int sps = (nsteps + sp - 1) / sp, splits = (nsteps + sps - 1) / sps;
             if (splits > 1 && sps * 64 <= ternix_hip::kMaxKPerAccumulator) {
-                c.note("zero_kernel + skinny_wave_kernel sw=%d nsw=2 splits=%d (splits added with int32 atomics)", sw,
-                       splits);
-                return TX_LAUNCH(c, ternix_hip::launch_skinny_wave(dA, dB, dC, M, K, N, sw, 2, splits, sps, nullptr, st));
+                unsigned long long* tk = ternix_hip::debug_get(ternix_hip::DBG_SELF_ZERO) != 0 && splits <= 64
+                                             ? c.tickets((size_t)(NB / sw))
+                                             : nullptr;
+                if (tk)
+                    c.note("skinny_wave_kernel sw=%d nsw=2 splits=%d (splits added with int32 atomics into C zeroed "
+                           "by each strip's first split)", sw, splits);
+                else
+                    c.note("zero_kernel + skinny_wave_kernel sw=%d nsw=2 splits=%d (splits added with int32 atomics)",
+                           sw, splits);
+                return TX_LAUNCH(c, ternix_hip::launch_skinny_wave(dA, dB, dC, M, K, N, sw, 2, splits, sps, nullptr, st,
+                                                                   ternix_hip::OutScale{}, 0, ternix_hip::ActQuant{},
+                                                                   0, nullptr, tk));
             }
         }
     }
@@ -1126,7 +1158,7 @@ int ternix_hip_debug_set(const char* key, int v0, int v1, int v2, int v3) {
         {"gemm_narrow", ternix_hip::DBG_GEMM_NARROW}, {"gemm_generic", ternix_hip::DBG_GEMM_GENERIC},
         {"gemm_splits", ternix_hip::DBG_GEMM_SPLITS}, {"gemm_bm", ternix_hip::DBG_GEMM_BM},
         {"deep", ternix_hip::DBG_DEEP},             {"sk_order", ternix_hip::DBG_SK_ORDER},
-        {"m1_atomic", ternix_hip::DBG_M1_ATOMIC},
+        {"m1_atomic", ternix_hip::DBG_M1_ATOMIC},     {"self_zero", ternix_hip::DBG_SELF_ZERO},
     };
     if (key == nullptr) return (int)hipErrorInvalidValue;
     for (const auto& n : names) {

@@ -24,6 +24,7 @@ SWITCHES = [
     {"sk_order": 1},                                       # release/acquire form of the in-launch sums
     {"m1_atomic": 0},                                      # M = 1 without the zero-fill + atomic plan
     {"m1_atomic": 0, "sk_order": 1},                       # ... and its in-launch sums in release/acquire form
+    {"self_zero": 0},                                      # M = 1 atomic plan with the fill launch
     {"gemm_bm": 128},                                      # 128-row GEMM tiles of eight waves
     {"gemm_bm": 256},                                      # 256-row GEMM tiles
 ]

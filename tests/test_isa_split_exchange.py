@@ -34,9 +34,11 @@ def wave_kernels(tmp_path_factory):
 
 
 def _relaxed_exchange(lines):
-    """Index of the relaxed arrival atomic (a returning global_atomic_add not preceded by buffer_wbl2)."""
+    """Index of the relaxed arrival atomic (a returning 32-bit global_atomic_add not preceded by
+    buffer_wbl2; the 64-bit ticket add of the self-zeroing mode is another exchange)."""
     for i, l in enumerate(lines):
-        if "global_atomic_add" in l and " sc0" in l and not any("buffer_wbl2" in x for x in lines[max(0, i - 4):i]):
+        if re.search(r"global_atomic_add\s", l) and " sc0" in l and \
+                not any("buffer_wbl2" in x for x in lines[max(0, i - 4):i]):
             return i
     return None
 
@@ -54,8 +56,36 @@ def test_wave_kernels_use_coherent_exchange(wave_kernels):
         between = lines[stores[-1] + 1:i]
         assert any(re.search(r"s_waitcnt vmcnt\(0\)", l) for l in between), \
             f"{name}: the arrival atomic is not preceded by a full vmcnt wait after the sc1 stores"
-        loads = [j for j, l in enumerate(lines) if re.search(r"global_load_dwordx2\b.*\bsc1\b", l)]
-        assert loads and min(loads) > i, f"{name}: last-arriver loads are not sc1 loads after the atomic"
+        # (sc1 loads before the atomic belong to the self-zeroing mode: its zeroed-word reads)
+        loads = [j for j, l in enumerate(lines) if j > i and re.search(r"global_load_dwordx2\b.*\bsc1\b", l)]
+        assert loads, f"{name}: last-arriver loads are not sc1 loads after the atomic"
         after = lines[i + 1:min(loads)]
         assert any(re.search(r"s_waitcnt vmcnt\(0\)", l) for l in after), \
             f"{name}: the last-arriver loads are issued before the counter value returned"
+
+
+def test_self_zeroing_atomics_order(wave_kernels):
+    """SK_ATOMZ (the M = 1 plan without a fill launch): the strip's first split zeroes its outputs
+    with coherent stores (global_store_dwordx2 ... sc1), waits for every store (vmcnt(0)), and only
+    then stores the zeroed word (sc1); the other splits read the zeroed word with a coherent load
+    and wait for it before their first int32 atomic add into C."""
+    names = [n for n in wave_kernels if re.search(r"skinny_wave_kernelILi(16|32)ELi\dELb1ELi0E", n)]
+    assert names
+    for name in names:
+        lines = wave_kernels[name]
+        ticket = [i for i, l in enumerate(lines) if "global_atomic_add_x2" in l and " sc0" in l]
+        assert ticket, f"{name}: no returning 64-bit ticket add"
+        t = ticket[0]
+        zstores = [i for i, l in enumerate(lines) if i > t and re.search(r"global_store_dwordx2\b.*\bsc1\b", l)]
+        assert len(zstores) >= 2, f"{name}: zero stores and zeroed-word store are not coherent 8-byte stores"
+        flag = zstores[-1]
+        zeros = zstores[:-1]
+        between = lines[zeros[-1] + 1:flag]
+        assert any(re.search(r"s_waitcnt vmcnt\(0\)", l) for l in between), \
+            f"{name}: the zeroed word is stored before the zero stores completed"
+        adds = [i for i, l in enumerate(lines) if re.search(r"global_atomic_add\b(?!_x2)", l) and " sc0" not in l]
+        assert adds, f"{name}: no int32 atomic adds"
+        zloads = [i for i, l in enumerate(lines) if re.search(r"global_load_dwordx2\b.*offset:8 sc1", l)]
+        assert zloads and min(zloads) < min(adds), f"{name}: the zeroed word is not read before the atomics"
+        assert any(re.search(r"s_waitcnt vmcnt\(0\)", l) for l in lines[min(zloads) + 1:min(adds)]), \
+            f"{name}: the atomics may be issued before the zeroed word returned"

@@ -1,0 +1,109 @@
+"""The M = 1 split-K GEMV whose splits add into C with int32 atomics, C being zeroed inside the same
+launch by each strip's first split (per-strip ticket counters and "zeroed" words that persist across
+calls, one block of 64 tickets per call): bit-exact for calls of different shapes and split counts
+that share the strips' tickets, issued back to back without synchronisation, replayed from a
+hipGraph with eager calls in between, and on two streams at once."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import ternixengine_amd as tx
+from ternixengine_amd import hip_runtime as hr
+
+GARBAGE = -123456789
+# (K, N): 16-byte strips with 6 splits, 32-byte strips with 4 and 10 splits, a 1024-wide strip count
+SHAPES = [(2560, 2560), (2560, 6912), (6912, 2560), (4096, 4096), (1024, 2048)]
+
+
+def log(msg):
+    print(msg, flush=True)
+
+
+def _plan(lib, k, n):
+    buf = ctypes.create_string_buffer(192)
+    assert lib.ternix_hip_plan_describe(1 << 20, 1 << 24, 1, k, n, buf, len(buf)) == 0
+    return buf.value.decode()
+
+
+def test_plan_names_self_zeroing():
+    lib = tx._load()
+    lib.ternix_hip_debug_reset()
+    for k, n in SHAPES[:3]:
+        assert "zeroed by each strip's first split" in _plan(lib, k, n), (k, n)
+    assert lib.ternix_hip_debug_set(b"self_zero", 0, -1, -1, -1) == 0
+    try:
+        assert _plan(lib, 2560, 6912).startswith("zero_kernel + ")
+    finally:
+        lib.ternix_hip_debug_reset()
+
+
+def _problems(oracle, seed):
+    rng = np.random.default_rng(seed)
+    out = []
+    for k, n in SHAPES:
+        a = rng.integers(-128, 128, size=(1, k), dtype=np.int8)
+        wp = rng.integers(0, 256, size=(k, n // 4), dtype=np.uint8)
+        expect = oracle.mm("scalar_mt", a, wp, n)
+        out.append((k, n, hr.DeviceBuffer.from_array(a), hr.DeviceBuffer.from_array(wp), hr.DeviceBuffer(4 * n),
+                    expect))
+    return out
+
+
+def _issue(probs, s):
+    for k, n, da, db, dc, _ in probs:
+        assert tx.mul_mat_ternary(da.value, db.value, dc.value, 1, k, n, stream=s.handle) == 0
+
+
+def _check(probs, tag):
+    for k, n, _, _, dc, expect in probs:
+        assert (dc.download(np.int32, (1, n)) == expect).all(), (tag, k, n)
+
+
+def _reset(probs):
+    for _, n, _, _, dc, _ in probs:
+        dc.upload(np.full(n, GARBAGE, np.int32))
+
+
+@pytest.mark.gpu
+def test_self_zero_interleaved_and_graph(oracle):
+    s = hr.Stream()
+    probs = _problems(oracle, 41)
+    log("[self-zero] one call each")
+    _reset(probs)
+    _issue(probs, s)
+    s.synchronize()
+    _check(probs, "first")
+    log("[self-zero] 300 interleaved rounds without synchronisation")
+    _reset(probs)
+    for _ in range(300):
+        _issue(probs, s)
+    s.synchronize()
+    _check(probs, "interleaved")
+    log("[self-zero] graph replays with eager calls between")
+    g = hr.Graph(s, lambda: [_issue(probs, s) for _ in range(3)])
+    for rep in range(5):
+        _reset(probs)
+        g.launch()
+        s.synchronize()
+        _check(probs, f"replay {rep}")
+        _reset(probs)
+        _issue(probs, s)
+        s.synchronize()
+        _check(probs, f"eager after replay {rep}")
+
+
+@pytest.mark.gpu
+def test_self_zero_two_streams(oracle):
+    s1, s2 = hr.Stream(), hr.Stream()
+    p1, p2 = _problems(oracle, 42), _problems(oracle, 43)
+    _reset(p1)
+    _reset(p2)
+    log("[self-zero] two streams, 100 rounds each")
+    for _ in range(100):
+        _issue(p1, s1)
+        _issue(p2, s2)
+    s1.synchronize()
+    s2.synchronize()
+    _check(p1, "stream 1")
+    _check(p2, "stream 2")
