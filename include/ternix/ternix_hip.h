@@ -209,7 +209,8 @@ int ternix_hip_device_count(void);
  *                       per workgroup, ring slots, splits)
  *   "sk_order" v0       1: release/acquire form of the in-launch split sums
  *   "m1_atomic" v0      0: M = 1 GEMVs without the zero-fill + int32-atomic split plan
- *   "self_zero" v0      0: that plan zeroes C with a fill kernel, not inside the launch
+ *   "self_zero" v0      0: M = 1 GEMVs never zero C inside the launch (the wave plan
+ *                       zeroes it with a fill kernel, wide ones use the reduce launch)
  * Returns 0, or 1 (hipErrorInvalidValue) for an unknown key.  Switches are
  * process-wide; a call running concurrently sees the old or the new value.
  * No reference counterpart (test hook of this library). */

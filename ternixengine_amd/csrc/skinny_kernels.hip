@@ -670,6 +670,44 @@ void skinny_dma_kernel(SkinnyArgs args) {
             if constexpr (AQ == 2) gv[j] = k < K ? args.G[k] : 0.0f;
         }
     };
+    // SK_ATOMZ (as in skinny_wave_kernel): wave 0 takes the strip's ticket before any DMA; the
+    // first loop wait of wave 0 (for a step issued after it) covers its return.
+    const bool ticket = AQ == 0 && args.mode == SK_ATOMZ && wave == 0;
+    unsigned long long* tk = args.tick + 2 * (size_t)cx;
+    unsigned long long old = 0, call1 = 0, zw = 0;
+    bool zeroer = false;
+    __shared__ int s_zero_ok;
+    if (ticket && lane == 0)
+        __asm__ volatile("global_atomic_add_x2 %0, %1, %2, off sc0" : "=v"(old) : "v"(tk), "v"(1ull) : "memory");
+    // After the first wait: learn the ticket; the strip's first split zeroes its 4 KB of C per row
+    // (wave 0, coherent stores; they complete before the tail's full wait, which publishes them).
+    auto take_ticket = [&]() {
+        __asm__ volatile("" : "+v"(old));
+        old = ((unsigned long long)(uint32_t)__builtin_amdgcn_readfirstlane((int)(old >> 32)) << 32) |
+              (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)old);
+        const int rank = (int)(old & 63);
+        call1 = (old >> 6) + 1;
+        zeroer = rank == 0;
+        if (rank == args.splits - 1 && args.splits < 64 && lane == 0)
+            __hip_atomic_fetch_add(tk, (unsigned long long)(64 - args.splits), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (zeroer)
+            for (int r = 0; r < a_rows; ++r) {
+                unsigned long long* z =
+                    reinterpret_cast<unsigned long long*>(args.C + (size_t)(m0 + r) * (size_t)args.N + 4 * bc0);
+                const int n8 = min(SD_BNB, NB - bc0) * 2;  // 8-byte units of this strip's outputs
+                for (int u = lane; u < n8; u += 64)
+                    __hip_atomic_store(z + u, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+    };
+    // In the tail (after a full wait of every wave and a barrier): the zeroer publishes, the others
+    // request the zeroed word.
+    auto tail_ticket = [&]() {
+        if (zeroer) {
+            if (lane == 0) __hip_atomic_store(tk + 1, call1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else if (lane == 0) {
+            zw = __hip_atomic_load(tk + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    };
     if constexpr (AQ != 0) {
         load_row(0);  // before the weight DMAs, so waiting for it does not wait for them
     } else {
@@ -784,16 +822,34 @@ void skinny_dma_kernel(SkinnyArgs args) {
         TX_VMCNT((NS - 2) * SD_NL);
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
+        if (ticket && it == 0) take_ticket();
         issue(it + NS - 1, (it + NS - 1) % NS);
         step(it, it % NS);
         __builtin_amdgcn_sched_barrier(0);
     }
+    const int tail0 = it;
     for (; it < nst; ++it) {
         TX_VMCNT(0);
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
+        if (ticket) {
+            if (it == 0) take_ticket();
+            if (it == tail0) {
+                if (it == 0) TX_VMCNT(0);  // a zeroer that took the ticket just now: its stores are complete
+                tail_ticket();
+            }
+        }
         step(it, it % NS);
         __builtin_amdgcn_sched_barrier(0);
+    }
+    if (AQ == 0 && args.mode == SK_ATOMZ) {
+        // every wave's atomics wait until the strip is zeroed (wave 0 checks, the barrier spreads it)
+        if (wave == 0 && !zeroer && lane == 0)
+            for (int n = 0; zw != call1 && n < kZeroSpinLimit; ++n) {
+                __builtin_amdgcn_s_sleep(1);
+                zw = __hip_atomic_load(tk + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        __syncthreads();
     }
 
     // Epilogue: lane (q, kb) holds rows 4kb+i of byte-columns bc0 + 16(4 wave + g) + q.
@@ -814,7 +870,7 @@ void skinny_dma_kernel(SkinnyArgs args) {
                 continue;
             }
             int32_t* out = out_base + (size_t)row * (size_t)args.N + 4 * bcol;
-            if (args.mode == SK_ATOMIC) {
+            if (args.mode == SK_ATOMIC || args.mode == SK_ATOMZ) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
                     if (v[j] != 0) atomicAdd(out + j, v[j]);
@@ -1362,12 +1418,16 @@ bool skinny_short_ok(const uint8_t* B, int M, int K, int N, int steps_per_split,
 
 hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int tb, int kw,
                          int splits, int steps_per_split, int32_t* partials, hipStream_t st, const OutScale& os,
-                         const ActQuant& aq, int dma_ns, int n_out) {
+                         const ActQuant& aq, int dma_ns, int n_out, unsigned long long* tickets) {
     const int NB = N >> 2;
-    const int mode = splits <= 1 ? SK_STORE : (partials ? SK_PARTIAL : SK_ATOMIC);
+    int mode = splits <= 1 ? SK_STORE : (partials ? SK_PARTIAL : SK_ATOMIC);
     if (n_out > 0 && (mode != SK_PARTIAL || n_out > N || n_out % 4 != 0)) return hipErrorInvalidValue;
     if (mode == SK_ATOMIC && C == nullptr) return hipErrorInvalidValue;  // scaled call without int scratch
     if (aq.mode != 0 && !skinny_short_ok(B, M, K, N, steps_per_split, splits)) return hipErrorInvalidValue;
+    // Self-zeroing atomics: DMA-staged kernel, one m-group, C rows 8-byte aligned, at most 64 splits.
+    if (mode == SK_ATOMIC && tickets && dma_ns > 0 && aq.mode == 0 && M <= 16 && splits <= 64 &&
+        (uintptr_t)C % 8 == 0 && N % 2 == 0)
+        mode = SK_ATOMZ;
     if (mode == SK_ATOMIC) {
         const hipError_t e = launch_zero(C, (size_t)M * (size_t)N, st);
         if (e != hipSuccess) return e;
@@ -1378,6 +1438,7 @@ hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, i
     const int aa = (K % 16 == 0) && ((uintptr_t)A % 16 == 0);
     SkinnyArgs a{A, B, C, partials, M, K, N, steps_per_split, splits, mode, vec_store, aw, aa,
                  mode == SK_STORE ? os : OutScale{}};
+    a.tick = tickets;
     const int mt = M <= 16 ? 1 : 2;
     const int mgroups = (M + 16 * mt - 1) / (16 * mt);
     hipError_t e;
@@ -1419,7 +1480,7 @@ hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, i
         else e = launch_generic<1, false>(a, grid, st);
     }
     if (e != hipSuccess) return e;
-    if (mode == SK_ATOMIC && scaled) return launch_dequant(C, os, M, N, st);  // C: alias of os.Y or scratch
+    if ((mode == SK_ATOMIC || mode == SK_ATOMZ) && scaled) return launch_dequant(C, os, M, N, st);  // C: alias of os.Y or scratch
     if (mode != SK_PARTIAL) return e;
     const size_t n4 = (size_t)M * (size_t)N / 4;
     const int n_c = n_out > 0 ? n_out : N;

@@ -40,7 +40,7 @@ enum DebugKey : int {
     DBG_DEEP,            // [0] == 0: no whole-K deep GEMV; else (sw, nw, nsw, splits) forced
     DBG_SK_ORDER,        // [0] 1: release/acquire (agent scope) for the in-launch split sums
     DBG_M1_ATOMIC,       // [0] 0: no zero-fill + atomic split plan for M = 1 GEMVs
-    DBG_SELF_ZERO,       // [0] 0: the M = 1 atomic plan zeroes C with a fill launch (no tickets)
+    DBG_SELF_ZERO,       // [0] 0: no in-launch zeroing of C for M = 1 (fill launch or reduce launch instead)
     DBG_COUNT
 };
 int debug_get(DebugKey key, int idx = 0);
@@ -87,7 +87,9 @@ bool skinny_dma_aq_ok(int aq_mode, int K, int splits);
 hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int tb, int kw,
                          int splits, int steps_per_split, int32_t* partials, hipStream_t st,
                          const OutScale& os = OutScale{}, const ActQuant& aq = ActQuant{}, int dma_ns = 0,
-                         int n_out = 0);
+                         int n_out = 0, unsigned long long* tickets = nullptr);
+// (tickets, with the DMA-staged kernel and no partials: the splits add into C with int32 atomics,
+// each strip's first split zeroing its outputs inside the launch instead of a fill launch.)
 // (n_out > 0: a padded problem -- N is the padded column count of A x W, and C / os.Y has n_out <= N
 // columns; only with a split-K workspace, whose reduce drops the padding.)
 // Compute units of the current device (cached per device).

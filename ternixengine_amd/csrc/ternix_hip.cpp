@@ -502,6 +502,19 @@ hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
     // back to the standalone quantisation launch when this returns hipErrorInvalidValue.
     if (aq.mode != 0 && p.dma == 0 && !ternix_hip::skinny_short_ok(dB, M, K, N, p.sps, p.splits))
         return hipErrorInvalidValue;
+    // DMA-staged kernel at M = 1 into C: the splits add with int32 atomics into C zeroed by each
+    // strip's first split instead of going through partial sums and the reduce launch (measured on
+    // MI355X, cold weights, cfg5 big 1x8192x28672: 15.67 -> 15.0 us; 9 splits stay the best count,
+    // 12 to 32 splits 17.8-26.2 us).
+    if (p.dma && M == 1 && p.splits > 1 && p.splits <= 64 && aq.mode == 0 && os.Y == nullptr && dC != nullptr &&
+        ternix_hip::debug_get(ternix_hip::DBG_SELF_ZERO) != 0) {
+        if (unsigned long long* tk = c.tickets((size_t)((N / 4 + 255) / 256))) {
+            c.note("skinny_dma_kernel splits=%d (splits added with int32 atomics into C zeroed by each strip's first "
+                   "split)", p.splits);
+            return TX_LAUNCH(c, ternix_hip::launch_skinny(dA, dB, dC, M, K, N, p.tb, p.kw, p.splits, p.sps, nullptr, st,
+                                                          os, aq, p.dma, 0, tk));
+        }
+    }
     int32_t* partials = nullptr;
     if (p.splits > 1) {
         const size_t need = (size_t)p.splits * (size_t)M * (size_t)N * sizeof(int32_t);
@@ -687,6 +700,17 @@ hipError_t run_tile64(const int8_t* dA, const uint8_t* dWt, int32_t* dC, int M, 
         const int sps = (nsteps + sp - 1) / sp;
         const int splits = (nsteps + sps - 1) / sps;
         if (sps * 64 > ternix_hip::kMaxKPerAccumulator) return hipErrorInvalidValue;
+        // M = 1 into C: the splits add with int32 atomics into C zeroed by each strip's first split
+        // (as on the row-major layout).
+        if (M == 1 && splits > 1 && splits <= 64 && os.Y == nullptr && dC != nullptr &&
+            ternix_hip::debug_get(ternix_hip::DBG_SELF_ZERO) != 0 && ternix_hip::debug_get(ternix_hip::DBG_M1_ATOMIC) != 0) {
+            if (unsigned long long* tk = c.tickets((size_t)(N / 4 / 16))) {
+                c.note("skinny_wave_kernel (tile-64) sw=16 nsw=2 splits=%d (splits added with int32 atomics into C "
+                       "zeroed by each strip's first split)", splits);
+                return TX_LAUNCH(c, ternix_hip::launch_skinny_wave(dA, dWt, dC, M, K, N, 16, 2, splits, sps, nullptr, st,
+                                                                   os, 0, ternix_hip::ActQuant{}, 1, nullptr, tk));
+            }
+        }
         int32_t* partials = nullptr;
         if (splits > 1) {
             const size_t need = (size_t)splits * (size_t)M * (size_t)N * sizeof(int32_t);

@@ -38,30 +38,35 @@ def test_plan_names_self_zeroing():
         lib.ternix_hip_debug_reset()
 
 
+# tile-64 weights: K > 4096 takes the split wave kernel (the shorter K the whole-K kernel)
+TILE64_SHAPES = [(6912, 2560), (8192, 1024)]
+
+
 def _problems(oracle, seed):
     rng = np.random.default_rng(seed)
     out = []
-    for k, n in SHAPES:
+    for (k, n), path in [(s, "auto") for s in SHAPES] + [(s, "tile64") for s in TILE64_SHAPES]:
         a = rng.integers(-128, 128, size=(1, k), dtype=np.int8)
         wp = rng.integers(0, 256, size=(k, n // 4), dtype=np.uint8)
         expect = oracle.mm("scalar_mt", a, wp, n)
-        out.append((k, n, hr.DeviceBuffer.from_array(a), hr.DeviceBuffer.from_array(wp), hr.DeviceBuffer(4 * n),
-                    expect))
+        w_dev = tx.interleave_tile64(wp) if path == "tile64" else wp
+        out.append((k, n, path, hr.DeviceBuffer.from_array(a), hr.DeviceBuffer.from_array(w_dev),
+                    hr.DeviceBuffer(4 * n), expect))
     return out
 
 
 def _issue(probs, s):
-    for k, n, da, db, dc, _ in probs:
-        assert tx.mul_mat_ternary(da.value, db.value, dc.value, 1, k, n, stream=s.handle) == 0
+    for k, n, path, da, db, dc, _ in probs:
+        assert tx.mul_mat_ternary(da.value, db.value, dc.value, 1, k, n, stream=s.handle, path=path) == 0
 
 
 def _check(probs, tag):
-    for k, n, _, _, dc, expect in probs:
-        assert (dc.download(np.int32, (1, n)) == expect).all(), (tag, k, n)
+    for k, n, path, _, _, dc, expect in probs:
+        assert (dc.download(np.int32, (1, n)) == expect).all(), (tag, k, n, path)
 
 
 def _reset(probs):
-    for _, n, _, _, dc, _ in probs:
+    for _, n, _, _, _, dc, _ in probs:
         dc.upload(np.full(n, GARBAGE, np.int32))
 
 
@@ -107,3 +112,36 @@ def test_self_zero_two_streams(oracle):
     s2.synchronize()
     _check(p1, "stream 1")
     _check(p2, "stream 2")
+
+
+@pytest.mark.gpu
+def test_self_zero_dma_kernel(oracle):
+    """The DMA-staged kernel's form of the same plan (wide M = 1 GEMVs): repeated calls of two
+    shapes sharing the strips' tickets, then the reduce plan (self_zero off) on the same buffers."""
+    lib = tx._load()
+    lib.ternix_hip_debug_reset()
+    assert lib.ternix_hip_debug_set(b"self_zero", 2, -1, -1, -1) == 0
+    try:
+        s = hr.Stream()
+        rng = np.random.default_rng(44)
+        probs = []
+        for k, n in [(8192, 28672), (4096, 16384)]:
+            assert "skinny_dma_kernel" in _plan(lib, k, n) and "zeroed" in _plan(lib, k, n), _plan(lib, k, n)
+            a = rng.integers(-128, 128, size=(1, k), dtype=np.int8)
+            wp = rng.integers(0, 256, size=(k, n // 4), dtype=np.uint8)
+            probs.append((k, n, "auto", hr.DeviceBuffer.from_array(a), hr.DeviceBuffer.from_array(wp),
+                          hr.DeviceBuffer(4 * n), oracle.mm("scalar_mt", a, wp, n)))
+        log("[self-zero dma] 50 interleaved rounds")
+        _reset(probs)
+        for _ in range(50):
+            _issue(probs, s)
+        s.synchronize()
+        _check(probs, "dma interleaved")
+        assert lib.ternix_hip_debug_set(b"self_zero", 0, -1, -1, -1) == 0
+        assert "splitk_reduce_kernel" in _plan(lib, 8192, 28672)
+        _reset(probs)
+        _issue(probs, s)
+        s.synchronize()
+        _check(probs, "reduce plan after")
+    finally:
+        lib.ternix_hip_debug_reset()
