@@ -6,6 +6,8 @@
 #include <stdint.h>
 #include <stdlib.h>
 
+#include <algorithm>
+
 #include "kernel_common.h"
 #include "ternary_kernels.h"
 
@@ -445,7 +447,7 @@ template <int BM, int WGN, int NS, int BK, int NWV, int BNB, bool TILED, int GM 
 __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2)))
 void gemm_pipe_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ B, int32_t* __restrict__ C, int M,
                       int K, int N, int tiles_n, int k_begin, int k_end, int accumulate, int vec_store,
-                      int k_split, OutScale os) {
+                      int k_split, OutScale os, int group_m) {
     if (gridDim.y > 1) {  // split-K: this workgroup's k-range, partial tile in slab blockIdx.y
         k_begin += (int)blockIdx.y * k_split;
         k_end = min(k_end, k_begin + k_split);
@@ -487,9 +489,10 @@ void gemm_pipe_kernel(const int8_t* __restrict__ A, const uint8_t* __restrict__ 
     int tm, tn;
     {
         const int t = xcd_linear(blockIdx.x, gridDim.x);
-        const int first_m = (t / (GM * tiles_n)) * GM;
-        const int gm = min(tiles_m - first_m, GM);
-        const int local = t % (GM * tiles_n);
+        const int G_M = group_m > 0 ? group_m : GM;  // row tiles per group of the tile order
+        const int first_m = (t / (G_M * tiles_n)) * G_M;
+        const int gm = min(tiles_m - first_m, G_M);
+        const int local = t % (G_M * tiles_n);
         tm = first_m + local % gm;
         tn = local / gm;
     }
@@ -762,32 +765,33 @@ hipError_t launch_gemm(const int8_t* A, const uint8_t* B, int32_t* C, int M, int
     }
     const int vs = ((uintptr_t)(os.Y ? (const void*)os.Y : (const void*)C) % 16) == 0;
     const int tiles_n = NB / GF_BNB;
+    const int gm_env = std::max(0, debug_get(DBG_GEMM_GM));  // tests and measurements: tile-order group
     if (choice == GemmChoice::Narrow64) {
         const dim3 gridn((unsigned)(((M + 63) / 64) * (NB / 16)), splits);
         if (tiled)
             hipLaunchKernelGGL((gemm_pipe_kernel<64, 1, 3, 256, 4, 16, true>), gridn, dim3(256), 0, st, A, B, C, M, K,
-                               N, NB / 16, k_begin, k_end, accumulate, vs, k_split, os);
+                               N, NB / 16, k_begin, k_end, accumulate, vs, k_split, os, gm_env);
         else
             hipLaunchKernelGGL((gemm_pipe_kernel<64, 1, 3, 256, 4, 16, false>), gridn, dim3(256), 0, st, A, B, C, M,
-                               K, N, NB / 16, k_begin, k_end, accumulate, vs, k_split, os);
+                               K, N, NB / 16, k_begin, k_end, accumulate, vs, k_split, os, gm_env);
     } else if (choice == GemmChoice::Pipe64) {
         // Tiles are visited in groups of 8 row tiles per column band (512 rows, as 4 groups of 128-row
         // tiles): measured on MI355X with cold weights, 2048x4096x4096 28.4 -> 27.0 us against groups of 4.
         const dim3 grid64((unsigned)(((M + 63) / 64) * tiles_n), splits);
         if (tiled)
             hipLaunchKernelGGL((gemm_pipe_kernel<64, 4, 3, 128, 4, 64, true, 8>), grid64, dim3(256), 0, st, A, B, C,
-                               M, K, N, tiles_n, k_begin, k_end, accumulate, vs, k_split, os);
+                               M, K, N, tiles_n, k_begin, k_end, accumulate, vs, k_split, os, gm_env);
         else
             hipLaunchKernelGGL((gemm_pipe_kernel<64, 4, 3, 128, 4, 64, false, 8>), grid64, dim3(256), 0, st, A, B, C,
-                               M, K, N, tiles_n, k_begin, k_end, accumulate, vs, k_split, os);
+                               M, K, N, tiles_n, k_begin, k_end, accumulate, vs, k_split, os, gm_env);
     } else if (choice == GemmChoice::Pipe128) {
         const dim3 grid(((M + 127) / 128) * tiles_n, splits);
         if (tiled)
             hipLaunchKernelGGL((gemm_pipe_kernel<128, 4, 3, 128, 8, GF_BNB, true>), grid, dim3(GF_THREADS), 0, st, A,
-                               B, C, M, K, N, tiles_n, k_begin, k_end, accumulate, vs, k_split, os);
+                               B, C, M, K, N, tiles_n, k_begin, k_end, accumulate, vs, k_split, os, gm_env);
         else
             hipLaunchKernelGGL((gemm_pipe_kernel<128, 4, 3, 128, 8, GF_BNB, false>), grid, dim3(GF_THREADS), 0, st, A,
-                               B, C, M, K, N, tiles_n, k_begin, k_end, accumulate, vs, k_split, os);
+                               B, C, M, K, N, tiles_n, k_begin, k_end, accumulate, vs, k_split, os, gm_env);
     } else {
         const dim3 grid(((M + 255) / 256) * tiles_n, splits);
         if (tiled)

@@ -1243,6 +1243,32 @@ void skinny_wave_kernel(SkinnyArgs args) {
             }
         __builtin_amdgcn_wave_barrier();
     }
+    if (LOW_M && AQ == 0 && (args.mode == SK_ATOMIC || args.mode == SK_ATOMZ)) {
+        // Few rows: wave 0 lays each row's 4 * SW outputs out in LDS in column order (lane q of
+        // group g holds columns 4 (16 g + q) + j), then every lane adds one column per instruction:
+        // 64 consecutive int32 per atomic instruction, no per-element branch.  The LDS area is the
+        // reduction buffer this wave alone has just read.
+        int32_t* row_lds = reinterpret_cast<int32_t*>(lds);
+        const int rows = min(4, M - m0);
+        for (int i = 0; i < rows; ++i) {
+            if (kb == 0) {
+#pragma unroll
+                for (int g = 0; g < G; ++g)
+                    *reinterpret_cast<v4i*>(row_lds + (16 * g + q) * 4) =
+                        v4i{acc[g][0][i] >> 6, acc[g][1][i] >> 6, acc[g][2][i] >> 6, acc[g][3][i] >> 6};
+            }
+            __builtin_amdgcn_wave_barrier();
+            int32_t vals[G];
+#pragma unroll
+            for (int u = 0; u < G; ++u) vals[u] = row_lds[64 * u + lane];
+            int32_t* out = args.C + (size_t)(m0 + i) * (size_t)args.N + 4 * bc0;
+#pragma unroll
+            for (int u = 0; u < G; ++u) atomicAdd(out + 64 * u + lane, vals[u]);
+            __builtin_amdgcn_wave_barrier();  // the reads are issued before the next row's writes
+            TX_LGKMCNT0();
+        }
+        return;
+    }
     if (LOW_M && kb != 0) return;
     int32_t* out_base = args.mode == SK_PARTIAL ? args.P + (size_t)sy * (size_t)M * (size_t)args.N : args.C;
     const bool vec = args.mode == SK_PARTIAL || args.vec_store;

@@ -40,6 +40,7 @@ enum DebugKey : int {
     DBG_DEEP,            // [0] == 0: no whole-K deep GEMV; else (sw, nw, nsw, splits) forced
     DBG_SK_ORDER,        // [0] 1: release/acquire (agent scope) for the in-launch split sums
     DBG_M1_ATOMIC,       // [0] 0: no zero-fill + atomic split plan for M = 1 GEMVs
+    DBG_GEMM_GM,         // [0] > 0: row tiles per group in the tile order of the 64/128-row GEMM kernels
     DBG_SELF_ZERO,       // [0] 0: no in-launch zeroing of C for M = 1 (fill launch or reduce launch instead)
     DBG_COUNT
 };
