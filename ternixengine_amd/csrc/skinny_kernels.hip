@@ -853,6 +853,34 @@ void skinny_dma_kernel(SkinnyArgs args) {
     }
 
     // Epilogue: lane (q, kb) holds rows 4kb+i of byte-columns bc0 + 16(4 wave + g) + q.
+    if (LOW_M && AQ == 0 && args.mode == SK_ATOMZ) {
+        // Few rows into C with atomics: each wave lays its row's 256 outputs out in column order in
+        // its own 1 KB of the (now idle) stage buffer, then adds one column per lane per instruction
+        // (64 consecutive int32 per atomic instruction, no per-element branch).  The barrier above
+        // ended every wave's reads of the stage buffers.
+        int32_t* row_lds = reinterpret_cast<int32_t*>(sW0) + wave * 256;
+        const int rows = min(4, M - m0);
+        const int col0 = bc0 + wave * 64;  // this wave's first byte-column
+        for (int i = 0; i < rows; ++i) {
+            if (kb == 0) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g)
+                    *reinterpret_cast<v4i*>(row_lds + (16 * g + q) * 4) =
+                        v4i{acc[g][0][i] >> 6, acc[g][1][i] >> 6, acc[g][2][i] >> 6, acc[g][3][i] >> 6};
+            }
+            __builtin_amdgcn_wave_barrier();
+            int32_t vals[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) vals[u] = row_lds[64 * u + lane];
+            int32_t* out = args.C + (size_t)(m0 + i) * (size_t)args.N + 4 * col0;
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                if (col0 + 16 * u + lane / 4 < NB) atomicAdd(out + 64 * u + lane, vals[u]);
+            __builtin_amdgcn_wave_barrier();
+            TX_LGKMCNT0();
+        }
+        return;
+    }
     if (LOW_M && kb != 0) return;
     int32_t* out_base = args.mode == SK_PARTIAL ? args.P + (size_t)sy * (size_t)M * (size_t)args.N : args.C;
     const bool vec = args.mode == SK_PARTIAL || args.vec_store;
