@@ -396,17 +396,23 @@ hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
     // for wide matrices (cfg5 big, 224 32-byte strips) the DMA-staged kernel is (15.7 vs 24+ us).
     // With the library's tickets the fill launch goes too: each strip's first split zeroes its
     // outputs inside the launch (skinny_kernels.hip, SK_ATOMZ); measured on MI355X, cold weights,
-    // graph timing of the cfg2 up + down pair: 6.75 -> 5.57 us per GEMV.
-    if (!generic && M == 1 && aq.mode == 0 && os.Y == nullptr && dC != nullptr && wave_kernel_enabled() &&
+    // graph timing of the cfg2 up + down pair: 6.75 -> 5.57 us per GEMV (5.25 with the coalesced
+    // atomic epilogue).  With tickets the plan also serves 2..4 rows (32-byte strips, as many splits
+    // as fit in one round of workgroups with 6 % slack): cfg3 M=4 up 9.45 -> 8.05 us (3 splits),
+    // M=4 down 9.76 -> 8.47 (8 splits); without tickets those rows keep the plans below.
+    if (!generic && M <= 4 && aq.mode == 0 && os.Y == nullptr && dC != nullptr && wave_kernel_enabled() &&
         ternix_hip::debug_get(ternix_hip::DBG_SKINNY_WAVE) < 0 && ternix_hip::debug_get(ternix_hip::DBG_M1_ATOMIC) != 0) {
         const int NB = N / 4, nsteps = K / 64, cus = cu_count();
         int sw = 0, sp = 0;
-        if (K <= 4096 && NB <= 1024 && NB % 16 == 0) {
+        if (M == 1 && K <= 4096 && NB <= 1024 && NB % 16 == 0) {
             sw = 16;
             sp = std::max(1, std::min(6, cus / (NB / 16)));
-        } else if (NB % 32 == 0 && (long)(NB / 32) * 4 * 50 <= (long)cus * 53) {
+        } else if (M == 1 && NB % 32 == 0 && (long)(NB / 32) * 4 * 50 <= (long)cus * 53) {
             sw = 32;
             sp = std::min(cus / (NB / 32), std::max(1, nsteps / 4));
+        } else if (M > 1 && NB % 32 == 0) {
+            sw = 32;
+            sp = (int)std::min<long>((long)cus * 53 / 50 / (NB / 32), std::max(1, nsteps / 4));
         }
         if (sw > 0 && sp > 1 && ternix_hip::skinny_wave_ok(dA, dB, M, K, N, sw)) {
             const int sps = (nsteps + sp - 1) / sp, splits = (nsteps + sps - 1) / sps;
@@ -417,12 +423,13 @@ hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
                 if (tk)
                     c.note("skinny_wave_kernel sw=%d nsw=2 splits=%d (splits added with int32 atomics into C zeroed "
                            "by each strip's first split)", sw, splits);
-                else
+                else if (M == 1)
                     c.note("zero_kernel + skinny_wave_kernel sw=%d nsw=2 splits=%d (splits added with int32 atomics)",
                            sw, splits);
-                return TX_LAUNCH(c, ternix_hip::launch_skinny_wave(dA, dB, dC, M, K, N, sw, 2, splits, sps, nullptr, st,
-                                                                   ternix_hip::OutScale{}, 0, ternix_hip::ActQuant{},
-                                                                   0, nullptr, tk));
+                if (tk || M == 1)
+                    return TX_LAUNCH(c, ternix_hip::launch_skinny_wave(dA, dB, dC, M, K, N, sw, 2, splits, sps, nullptr,
+                                                                       st, ternix_hip::OutScale{}, 0,
+                                                                       ternix_hip::ActQuant{}, 0, nullptr, tk));
             }
         }
     }
@@ -502,11 +509,11 @@ hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
     // back to the standalone quantisation launch when this returns hipErrorInvalidValue.
     if (aq.mode != 0 && p.dma == 0 && !ternix_hip::skinny_short_ok(dB, M, K, N, p.sps, p.splits))
         return hipErrorInvalidValue;
-    // DMA-staged kernel at M = 1 into C: the splits add with int32 atomics into C zeroed by each
+    // DMA-staged kernel at M <= 4 into C: the splits add with int32 atomics into C zeroed by each
     // strip's first split instead of going through partial sums and the reduce launch (measured on
-    // MI355X, cold weights, cfg5 big 1x8192x28672: 15.67 -> 15.0 us; 9 splits stay the best count,
-    // 12 to 32 splits 17.8-26.2 us).
-    if (p.dma && M == 1 && p.splits > 1 && p.splits <= 64 && aq.mode == 0 && os.Y == nullptr && dC != nullptr &&
+    // MI355X, cold weights, cfg5 big 1x8192x28672: 15.67 -> 13.5 us with the coalesced atomic
+    // epilogue; 9 splits stay the best count, 11 to 18 splits 16.2-18.0 us).
+    if (p.dma && M <= 4 && p.splits > 1 && p.splits <= 64 && aq.mode == 0 && os.Y == nullptr && dC != nullptr &&
         ternix_hip::debug_get(ternix_hip::DBG_SELF_ZERO) != 0) {
         if (unsigned long long* tk = c.tickets((size_t)((N / 4 + 255) / 256))) {
             c.note("skinny_dma_kernel splits=%d (splits added with int32 atomics into C zeroed by each strip's first "

@@ -115,6 +115,40 @@ def test_self_zero_two_streams(oracle):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("m", [2, 3, 4])
+def test_self_zero_few_rows(oracle, m):
+    """2..4 rows take the same plans (wave kernel with 32-byte strips, DMA kernel on wide matrices):
+    interleaved calls of three shapes, every row bit-exact."""
+    lib = tx._load()
+    lib.ternix_hip_debug_reset()
+    s = hr.Stream()
+    rng = np.random.default_rng(50 + m)
+    probs = []
+    for k, n in [(4096, 11008), (11008, 4096), (8192, 28672)]:
+        plan = _plan_m(lib, m, k, n)
+        assert "zeroed by each strip's first split" in plan, plan
+        a = rng.integers(-128, 128, size=(m, k), dtype=np.int8)
+        wp = rng.integers(0, 256, size=(k, n // 4), dtype=np.uint8)
+        probs.append((m, k, n, hr.DeviceBuffer.from_array(a), hr.DeviceBuffer.from_array(wp),
+                      hr.DeviceBuffer(4 * m * n), oracle.mm("scalar_mt", a, wp, n)))
+    for _, _, n, _, _, dc, _ in probs:
+        dc.upload(np.full(m * n, GARBAGE, np.int32))
+    log(f"[self-zero M={m}] 30 interleaved rounds")
+    for _ in range(30):
+        for mm, k, n, da, db, dc, _ in probs:
+            assert tx.mul_mat_ternary(da.value, db.value, dc.value, mm, k, n, stream=s.handle) == 0
+    s.synchronize()
+    for mm, k, n, _, _, dc, expect in probs:
+        assert (dc.download(np.int32, (mm, n)) == expect).all(), (mm, k, n)
+
+
+def _plan_m(lib, m, k, n):
+    buf = ctypes.create_string_buffer(192)
+    assert lib.ternix_hip_plan_describe(1 << 20, 1 << 24, m, k, n, buf, len(buf)) == 0
+    return buf.value.decode()
+
+
+@pytest.mark.gpu
 def test_self_zero_dma_kernel(oracle):
     """The DMA-staged kernel's form of the same plan (wide M = 1 GEMVs): repeated calls of two
     shapes sharing the strips' tickets, then the reduce plan (self_zero off) on the same buffers."""
