@@ -181,6 +181,11 @@ __device__ __forceinline__ void lds_dma16(const void* gsrc, void* lds) {
     __builtin_amdgcn_global_load_lds(gsrc, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
 }
 
+// The same with a non-temporal load (streamed past the caches: weight streams far larger than L2).
+__device__ __forceinline__ void lds_dma16_nt(const void* gsrc, void* lds) {
+    __builtin_amdgcn_global_load_lds(gsrc, (__attribute__((address_space(3))) void*)lds, 16, 0, 2);
+}
+
 // Transposing 8-byte LDS read (ds_read_b64_tr_b8: within each 16-lane group, result lane j byte i
 // is byte j % 8 of the 8 bytes addressed by lane 2i + j/8).  Issued as inline assembly: the compiler then neither
 // waits for the LDS DMA in flight into other stage buffers before it (it cannot tell they do not

@@ -89,6 +89,7 @@ struct SkinnyArgs {
     int* cnt;             // SK_LAST: arrival counters, one per (m-group, strip), zero between calls
     int order;            // SK_LAST: 1 = C++ release/acquire at agent scope, 0 = coherent accesses only
     unsigned long long* tick;  // SK_ATOMZ: per strip {ticket counter, zeroed word}, persistent
+    int nt;               // DMA-staged / wave-pipelined kernels: non-temporal weight loads
 };
 
 // One k-step of MFMA work for one 16-row x 4-byte-column block: raw[r] is the dword of row r.
@@ -730,8 +731,13 @@ void skinny_dma_kernel(SkinnyArgs args) {
     auto issue = [&](int st, int buf) {
         const uint8_t* wbase = B + (size_t)(s_begin + st) * 64 * (size_t)NB;
         uint8_t* wdst = stage_w(buf);
+        if (args.nt) {
 #pragma unroll
-        for (int p = 0; p < SD_NL; ++p) lds_dma16(wbase + w_off[p], wdst + (p * 4 + wave) * 1024);
+            for (int p = 0; p < SD_NL; ++p) lds_dma16_nt(wbase + w_off[p], wdst + (p * 4 + wave) * 1024);
+        } else {
+#pragma unroll
+            for (int p = 0; p < SD_NL; ++p) lds_dma16(wbase + w_off[p], wdst + (p * 4 + wave) * 1024);
+        }
     };
     uint32_t w_lane[4];
 #pragma unroll
@@ -1002,8 +1008,13 @@ void skinny_wave_kernel(SkinnyArgs args) {
             lds_dma16(B + ((size_t)cx * (size_t)(K >> 6) + (size_t)s) * 1024 + lane * 16, dst);
         } else {
             const uint8_t* wbase = B + (size_t)s * 64 * (size_t)NB;
+            if (args.nt) {
 #pragma unroll
-            for (int p = 0; p < NL; ++p) lds_dma16(wbase + w_off[p], dst + p * 1024);
+                for (int p = 0; p < NL; ++p) lds_dma16_nt(wbase + w_off[p], dst + p * 1024);
+            } else {
+#pragma unroll
+                for (int p = 0; p < NL; ++p) lds_dma16(wbase + w_off[p], dst + p * 1024);
+            }
         }
         if constexpr (AQ == 0) a_dst = *reinterpret_cast<const v4i*>(a_row + (size_t)s * 64);
     };
@@ -1493,6 +1504,10 @@ hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, i
     SkinnyArgs a{A, B, C, partials, M, K, N, steps_per_split, splits, mode, vec_store, aw, aa,
                  mode == SK_STORE ? os : OutScale{}};
     a.tick = tickets;
+    // Non-temporal weight loads for the DMA-staged kernel on matrices larger than the L2s together
+    // (measured on MI355X, cold weights, cfg5 big 1x8192x28672: 13.35 -> 12.61 us; on the small
+    // decode matrices, whose lines neighbouring strips share through L2, plain loads are faster).
+    a.nt = debug_get(DBG_NT, 0) >= 0 ? debug_get(DBG_NT, 0) == 1 : (size_t)K * (size_t)NB >= (size_t(32) << 20);
     const int mt = M <= 16 ? 1 : 2;
     const int mgroups = (M + 16 * mt - 1) / (16 * mt);
     hipError_t e;
@@ -1579,6 +1594,7 @@ hipError_t launch_skinny_wave(const int8_t* A, const uint8_t* B, int32_t* C, int
                  (mode == SK_STORE || mode == SK_LAST) ? os : OutScale{}};
     a.cnt = counters;
     a.tick = tickets;
+    a.nt = debug_get(DBG_NT, 1) == 1;  // plain loads unless forced (slower here on every decode shape measured)
     a.order = debug_get(DBG_SK_ORDER) == 1;
     a.n_out = n_out;
     a.tiled = tiled;

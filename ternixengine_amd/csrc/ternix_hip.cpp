@@ -256,6 +256,8 @@ SkinnyPlan plan_skinny_dma(int M, int K, int N, int ns) {
     splits = std::min<long>(splits, nsteps);
     int sps = (int)((nsteps + splits - 1) / splits);
     while (col_wgs * ((nsteps + sps - 1) / sps) > std::max(cus, col_wgs)) ++sps;  // no second wave
+    const int forced = ternix_hip::debug_get(ternix_hip::DBG_SKINNY_DMA, 1);  // split count (tuning)
+    if (forced > 0) sps = (nsteps + std::min(forced, nsteps) - 1) / std::min(forced, nsteps);
     SkinnyPlan p{1, 1, (nsteps + sps - 1) / sps, sps, ns};
     if (p.sps > 16 || p.sps > ternix_hip::kMaxKPerAccumulator / 64) p.dma = 0;
     return p;
@@ -1190,7 +1192,7 @@ int ternix_hip_debug_set(const char* key, int v0, int v1, int v2, int v3) {
         {"gemm_splits", ternix_hip::DBG_GEMM_SPLITS}, {"gemm_bm", ternix_hip::DBG_GEMM_BM},
         {"deep", ternix_hip::DBG_DEEP},             {"sk_order", ternix_hip::DBG_SK_ORDER},
         {"m1_atomic", ternix_hip::DBG_M1_ATOMIC},     {"self_zero", ternix_hip::DBG_SELF_ZERO},
-        {"gemm_gm", ternix_hip::DBG_GEMM_GM},
+        {"gemm_gm", ternix_hip::DBG_GEMM_GM},         {"nt", ternix_hip::DBG_NT},
     };
     if (key == nullptr) return (int)hipErrorInvalidValue;
     for (const auto& n : names) {

@@ -27,6 +27,9 @@ SWITCHES = [
     {"self_zero": 0},                                      # M = 1 atomic plan with the fill launch
     {"gemm_bm": 128},                                      # 128-row GEMM tiles of eight waves
     {"gemm_bm": 256},                                      # 256-row GEMM tiles
+    {"nt": (1, 1)},                                        # non-temporal weight loads in both GEMV kernels
+    {"skinny_wave": 0, "nt": (1, 1)},                      # ... in the DMA-staged GEMVs on every shape
+    {"skinny_wave": 0, "skinny_dma": (3, 12)},             # DMA-staged GEMVs with a forced split count
 ]
 
 
@@ -35,7 +38,9 @@ def switches(request):
     lib = tx._load()
     lib.ternix_hip_debug_reset()
     for k, v in request.param.items():
-        assert lib.ternix_hip_debug_set(k.encode(), v, -1, -1, -1) == 0, k
+        v = tuple(v) if isinstance(v, tuple) else (v,)
+        v = v + (-1,) * (4 - len(v))
+        assert lib.ternix_hip_debug_set(k.encode(), *v) == 0, k
     yield request.param
     lib.ternix_hip_debug_reset()
 
