@@ -708,7 +708,9 @@ def main():
         line["gemv_detail"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in g.items()}
     if "bigm1" in res:
         b = res["bigm1"]
+        tb = profiled_traffic("gemv_cfg5_big")
         line["gemv_big_m1"] = {"shape": b["shape"], "gbs": round(b["gbs"], 1), "frac": round(b["gbs"] / HBM_PEAK_GBS, 4),
+                               "traffic": tb["bytes"] if tb else None, "traffic_source": tb,
                                "launch_us": round(b["launch_us"], 3), "verified": b["verified"], "plan": b["plan"],
                                "read_floor_us": round(b["read_floor_us"], 3),
                                "frac_of_read_floor": round(b["read_floor_us"] / b["launch_us"], 4)}

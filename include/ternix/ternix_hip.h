@@ -198,19 +198,23 @@ int ternix_hip_device_count(void);
  *   "skinny_wave" v0..2 0: no wave-pipelined GEMV; else force (strip bytes,
  *                       ring slots, splits)
  *   "wave_sw" v0        16: 16-byte wave strips on row-major weights
- *   "skinny_dma" v0     0: no DMA-staged GEMV; 2..4: its stage count
+ *   "skinny_dma" v0,v1  v0 0: no DMA-staged GEMV; 2..4: its stage count; v1: its
+ *                       split count forced
  *   "skinny_short" v0   0: no register-staged short GEMV
  *   "ragged_pad" v0     0: ragged shapes run the generic kernels, not a padded copy
  *   "gemm_narrow" v0    0 / 1: 64 x 64 GEMM tiles for M <= 64 off / forced
  *   "gemm_generic" v0   1: the generic GEMM for every GEMM call
  *   "gemm_splits" v0    GEMM split-K count forced
  *   "gemm_bm" v0        64 / 128 / 256: GEMM tile height forced
+ *   "gemm_gm" v0        row tiles per group in the tile order of the 64/128-row GEMMs
  *   "deep" v0..3        0: no whole-K deep GEMV; else force (strip bytes, waves
  *                       per workgroup, ring slots, splits)
  *   "sk_order" v0       1: release/acquire form of the in-launch split sums
  *   "m1_atomic" v0      0: M = 1 GEMVs without the zero-fill + int32-atomic split plan
  *   "self_zero" v0      0: M = 1 GEMVs never zero C inside the launch (the wave plan
  *                       zeroes it with a fill kernel, wide ones use the reduce launch)
+ *   "nt" v0,v1          1 / 0: non-temporal weight loads on / off in the DMA-staged
+ *                       (v0) and the wave-pipelined (v1) GEMVs
  * Returns 0, or 1 (hipErrorInvalidValue) for an unknown key.  Switches are
  * process-wide; a call running concurrently sees the old or the new value.
  * No reference counterpart (test hook of this library). */
