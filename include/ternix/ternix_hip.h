@@ -197,7 +197,8 @@ int ternix_hip_device_count(void);
  *   "wave_last" v0      most K splits summed inside one wave-GEMV launch (0: none)
  *   "skinny_wave" v0..2 0: no wave-pipelined GEMV; else force (strip bytes,
  *                       ring slots, splits)
- *   "wave_sw" v0        16: 16-byte wave strips on row-major weights
+ *   "wave_sw" v0,v1     v0 16: 16-byte wave strips on row-major weights; with v1 > 1 the
+ *                       strip width (16 / 32) and split count of the atomic split plan
  *   "skinny_dma" v0,v1  v0 0: no DMA-staged GEMV; 2..4: its stage count; v1: its
  *                       split count forced
  *   "skinny_short" v0   0: no register-staged short GEMV
@@ -210,7 +211,8 @@ int ternix_hip_device_count(void);
  *   "deep" v0..3        0: no whole-K deep GEMV; else force (strip bytes, waves
  *                       per workgroup, ring slots, splits)
  *   "sk_order" v0       1: release/acquire form of the in-launch split sums
- *   "m1_atomic" v0      0: M = 1 GEMVs without the zero-fill + int32-atomic split plan
+ *   "m1_atomic" v0,v1   v0 0: M = 1 GEMVs without the zero-fill + int32-atomic split plan;
+ *                       v1: largest M (<= 16) of the self-zeroing atomic split plan
  *   "self_zero" v0      0: M = 1 GEMVs never zero C inside the launch (the wave plan
  *                       zeroes it with a fill kernel, wide ones use the reduce launch)
  *   "nt" v0,v1          1 / 0: non-temporal weight loads on / off in the DMA-staged

@@ -1308,6 +1308,31 @@ void skinny_wave_kernel(SkinnyArgs args) {
         }
         return;
     }
+    if (!LOW_M && AQ == 0 && args.mode == SK_ATOMZ) {
+        // Up to 16 rows: wave 0 lays every row's 4 * SW outputs out in LDS in column order (row r at
+        // r * 4 * SW; lane (q, kb) holds rows 4 kb + i), then adds one column per lane per instruction,
+        // row by row: 64 consecutive int32 per atomic instruction.  The LDS area is the reduction
+        // buffer this wave alone has just read.
+        int32_t* row_lds = reinterpret_cast<int32_t*>(lds);
+        const int rows = min(16, M - m0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = 4 * kb + i;
+            if (r < rows) {
+#pragma unroll
+                for (int g = 0; g < G; ++g)
+                    *reinterpret_cast<v4i*>(row_lds + r * 4 * SW + (16 * g + q) * 4) =
+                        v4i{acc[g][0][i] >> 6, acc[g][1][i] >> 6, acc[g][2][i] >> 6, acc[g][3][i] >> 6};
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+        for (int r = 0; r < rows; ++r) {
+            int32_t* out = args.C + (size_t)(m0 + r) * (size_t)args.N + 4 * bc0;
+#pragma unroll
+            for (int u = 0; u < G; ++u) atomicAdd(out + 64 * u + lane, row_lds[r * 4 * SW + 64 * u + lane]);
+        }
+        return;
+    }
     if (LOW_M && kb != 0) return;
     int32_t* out_base = args.mode == SK_PARTIAL ? args.P + (size_t)sy * (size_t)M * (size_t)args.N : args.C;
     const bool vec = args.mode == SK_PARTIAL || args.vec_store;

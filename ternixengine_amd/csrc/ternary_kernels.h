@@ -29,7 +29,8 @@ struct OutScale {
 enum DebugKey : int {
     DBG_WAVE_LAST = 0,   // [0] largest split count summed inside the wave GEMV launch (0: never)
     DBG_SKINNY_WAVE,     // [0] == 0: no wave-pipelined GEMV; else (sw, nsw, splits) forced
-    DBG_WAVE_SW,         // [0] strip width of the wave-pipelined GEMV on row-major weights (16 / 32)
+    DBG_WAVE_SW,         // [0] strip width of the wave-pipelined GEMV on row-major weights (16 / 32);
+                         //     with [1] > 1 also the atomic split plan's strip width and split count
     DBG_SKINNY_DMA,      // [0] == 0: no DMA-staged GEMV; 2..4: its stage count; [1] > 0: its split count
     DBG_SKINNY_SHORT,    // [0] == 0: no register-staged short GEMV
     DBG_RAGGED_PAD,      // [0] == 0: ragged shapes run the generic kernels instead of a padded copy
@@ -39,7 +40,8 @@ enum DebugKey : int {
     DBG_GEMM_BM,         // [0] 64 / 128 / 256: GEMM tile height forced
     DBG_DEEP,            // [0] == 0: no whole-K deep GEMV; else (sw, nw, nsw, splits) forced
     DBG_SK_ORDER,        // [0] 1: release/acquire (agent scope) for the in-launch split sums
-    DBG_M1_ATOMIC,       // [0] 0: no zero-fill + atomic split plan for M = 1 GEMVs
+    DBG_M1_ATOMIC,       // [0] 0: no zero-fill + atomic split plan for M = 1 GEMVs; [1] largest M of the
+                         //     self-zeroing atomic plan (default 16)
     DBG_GEMM_GM,         // [0] > 0: row tiles per group in the tile order of the 64/128-row GEMM kernels
     DBG_SELF_ZERO,       // [0] 0: no in-launch zeroing of C for M = 1 (fill launch or reduce launch instead)
     DBG_NT,              // [0] DMA-staged GEMV, [1] wave-pipelined GEMV: 1 non-temporal weight loads, 0 plain

@@ -399,10 +399,17 @@ hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
     // With the library's tickets the fill launch goes too: each strip's first split zeroes its
     // outputs inside the launch (skinny_kernels.hip, SK_ATOMZ); measured on MI355X, cold weights,
     // graph timing of the cfg2 up + down pair: 6.75 -> 5.57 us per GEMV (5.25 with the coalesced
-    // atomic epilogue).  With tickets the plan also serves 2..4 rows (32-byte strips, as many splits
+    // atomic epilogue).  With tickets the plan also serves 2..16 rows (32-byte strips, as many splits
     // as fit in one round of workgroups with 6 % slack): cfg3 M=4 up 9.45 -> 8.05 us (3 splits),
     // M=4 down 9.76 -> 8.47 (8 splits); without tickets those rows keep the plans below.
-    if (!generic && M <= 4 && aq.mode == 0 && os.Y == nullptr && dC != nullptr && wave_kernel_enabled() &&
+    // Up to 16 rows (one m-group) with tickets: 5..16 rows add their splits with the coalesced 16-row
+    // atomic epilogue (skinny_kernels.hip), measured on MI355X with cold weights against the in-launch
+    // sums / reduce launch they replaced (same strips and splits): 1.11-1.59x on 28 decode shapes
+    // (M 5, 8, 12, 16 x K,N in {4096x11008, 11008x4096, 2560x6912, 6912x2560, 4096x4096, 4096x14336,
+    // 14336x4096}); cfg3 M=16 up 12.39 -> 9.20 us, down 12.38 -> 9.51 us.  The DBG_M1_ATOMIC switch
+    // [1] lowers the row limit (tests and measurements).
+    const int atomic_max_m = ternix_hip::debug_get(ternix_hip::DBG_M1_ATOMIC, 1) > 0 ? ternix_hip::debug_get(ternix_hip::DBG_M1_ATOMIC, 1) : 16;
+    if (!generic && M <= std::min(16, atomic_max_m) && aq.mode == 0 && os.Y == nullptr && dC != nullptr && wave_kernel_enabled() &&
         ternix_hip::debug_get(ternix_hip::DBG_SKINNY_WAVE) < 0 && ternix_hip::debug_get(ternix_hip::DBG_M1_ATOMIC) != 0) {
         const int NB = N / 4, nsteps = K / 64, cus = cu_count();
         int sw = 0, sp = 0;
@@ -415,6 +422,11 @@ hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
         } else if (M > 1 && NB % 32 == 0) {
             sw = 32;
             sp = (int)std::min<long>((long)cus * 53 / 50 / (NB / 32), std::max(1, nsteps / 4));
+        }
+        const int fsw = ternix_hip::debug_get(ternix_hip::DBG_WAVE_SW, 0), fsp = ternix_hip::debug_get(ternix_hip::DBG_WAVE_SW, 1);
+        if ((fsw == 16 || fsw == 32) && fsp > 1 && NB % fsw == 0) {  // forced split plan (tests and tuning)
+            sw = fsw;
+            sp = std::min(fsp, nsteps);
         }
         if (sw > 0 && sp > 1 && ternix_hip::skinny_wave_ok(dA, dB, M, K, N, sw)) {
             const int sps = (nsteps + sp - 1) / sp, splits = (nsteps + sps - 1) / sps;

@@ -142,6 +142,40 @@ def test_self_zero_few_rows(oracle, m):
         assert (dc.download(np.int32, (mm, n)) == expect).all(), (mm, k, n)
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("m", [5, 8, 16])
+def test_self_zero_up_to_16_rows(oracle, m):
+    """5..16 rows take the same plan with the 16-row coalesced atomic epilogue: interleaved calls of
+    three shapes on one stream, then the same calls with the plan limited to 4 rows (in-launch sums
+    and the reduce launch) on the same output buffers, every row bit-exact."""
+    lib = tx._load()
+    lib.ternix_hip_debug_reset()
+    s = hr.Stream()
+    rng = np.random.default_rng(60 + m)
+    probs = []
+    for k, n in [(4096, 11008), (11008, 4096), (2560, 6912)]:
+        plan = _plan_m(lib, m, k, n)
+        assert "zeroed by each strip's first split" in plan, plan
+        a = rng.integers(-128, 128, size=(m, k), dtype=np.int8)
+        wp = rng.integers(0, 256, size=(k, n // 4), dtype=np.uint8)
+        probs.append((m, k, n, hr.DeviceBuffer.from_array(a), hr.DeviceBuffer.from_array(wp),
+                      hr.DeviceBuffer(4 * m * n), oracle.mm("scalar_mt", a, wp, n)))
+    try:
+        for limit in (-1, 4):
+            assert lib.ternix_hip_debug_set(b"m1_atomic", -1, limit, -1, -1) == 0
+            for _, _, n, _, _, dc, _ in probs:
+                dc.upload(np.full(m * n, GARBAGE, np.int32))
+            log(f"[self-zero M={m} row limit {limit}] 30 interleaved rounds")
+            for _ in range(30):
+                for mm, k, n, da, db, dc, _ in probs:
+                    assert tx.mul_mat_ternary(da.value, db.value, dc.value, mm, k, n, stream=s.handle) == 0
+            s.synchronize()
+            for mm, k, n, _, _, dc, expect in probs:
+                assert (dc.download(np.int32, (mm, n)) == expect).all(), (mm, k, n, limit)
+    finally:
+        lib.ternix_hip_debug_reset()
+
+
 def _plan_m(lib, m, k, n):
     buf = ctypes.create_string_buffer(192)
     assert lib.ternix_hip_plan_describe(1 << 20, 1 << 24, m, k, n, buf, len(buf)) == 0
