@@ -721,9 +721,12 @@ hipError_t run_tile64(const int8_t* dA, const uint8_t* dWt, int32_t* dC, int M, 
         const int sps = (nsteps + sp - 1) / sp;
         const int splits = (nsteps + sps - 1) / sps;
         if (sps * 64 > ternix_hip::kMaxKPerAccumulator) return hipErrorInvalidValue;
-        // M = 1 into C: the splits add with int32 atomics into C zeroed by each strip's first split
-        // (as on the row-major layout).
-        if (M == 1 && splits > 1 && splits <= 64 && os.Y == nullptr && dC != nullptr &&
+        // Up to 16 rows into C: the splits add with int32 atomics into C zeroed by each strip's first
+        // split (as on the row-major layout).  Measured on MI355X, cold weights, against the reduce
+        // launch: cfg3 M=4 down 9.46 -> 6.72 us, M=16 down 10.70 -> 7.57 us (the K <= 4096 shapes run
+        // the whole-K kernel above).  The DBG_M1_ATOMIC switch [2] lowers the row limit.
+        const int t64_atomic_max_m = ternix_hip::debug_get(ternix_hip::DBG_M1_ATOMIC, 2) > 0 ? ternix_hip::debug_get(ternix_hip::DBG_M1_ATOMIC, 2) : 16;
+        if (M <= std::min(16, t64_atomic_max_m) && splits > 1 && splits <= 64 && os.Y == nullptr && dC != nullptr &&
             ternix_hip::debug_get(ternix_hip::DBG_SELF_ZERO) != 0 && ternix_hip::debug_get(ternix_hip::DBG_M1_ATOMIC) != 0) {
             if (unsigned long long* tk = c.tickets((size_t)(N / 4 / 16))) {
                 c.note("skinny_wave_kernel (tile-64) sw=16 nsw=2 splits=%d (splits added with int32 atomics into C "

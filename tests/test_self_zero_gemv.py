@@ -176,6 +176,38 @@ def test_self_zero_up_to_16_rows(oracle, m):
         lib.ternix_hip_debug_reset()
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("m", [4, 16])
+def test_self_zero_tile64_rows(oracle, m):
+    """Tile-64 weights with K > 4096 take the atomic plan for up to 16 rows too: interleaved calls of
+    two shapes, bit-exact, then the reduce plan (row limit 1) on the same buffers."""
+    lib = tx._load()
+    lib.ternix_hip_debug_reset()
+    s = hr.Stream()
+    rng = np.random.default_rng(70 + m)
+    probs = []
+    for k, n in [(11008, 4096), (6912, 2560)]:
+        a = rng.integers(-128, 128, size=(m, k), dtype=np.int8)
+        wp = rng.integers(0, 256, size=(k, n // 4), dtype=np.uint8)
+        probs.append((m, k, n, hr.DeviceBuffer.from_array(a), hr.DeviceBuffer.from_array(tx.interleave_tile64(wp)),
+                      hr.DeviceBuffer(4 * m * n), oracle.mm("scalar_mt", a, wp, n)))
+    try:
+        for limit in (-1, 1):
+            assert lib.ternix_hip_debug_set(b"m1_atomic", -1, -1, limit, -1) == 0
+            for _, _, n, _, _, dc, _ in probs:
+                dc.upload(np.full(m * n, GARBAGE, np.int32))
+            log(f"[self-zero tile-64 M={m} row limit {limit}] 30 interleaved rounds")
+            for _ in range(30):
+                for mm, k, n, da, db, dc, _ in probs:
+                    assert tx.mul_mat_ternary(da.value, db.value, dc.value, mm, k, n, stream=s.handle,
+                                              path="tile64") == 0
+            s.synchronize()
+            for mm, k, n, _, _, dc, expect in probs:
+                assert (dc.download(np.int32, (mm, n)) == expect).all(), (mm, k, n, limit)
+    finally:
+        lib.ternix_hip_debug_reset()
+
+
 def _plan_m(lib, m, k, n):
     buf = ctypes.create_string_buffer(192)
     assert lib.ternix_hip_plan_describe(1 << 20, 1 << 24, m, k, n, buf, len(buf)) == 0
