@@ -212,8 +212,8 @@ int ternix_hip_device_count(void);
  *                       per workgroup, ring slots, splits)
  *   "sk_order" v0       1: release/acquire form of the in-launch split sums
  *   "m1_atomic" v0..2   v0 0: M = 1 GEMVs without the zero-fill + int32-atomic split plan;
- *                       v1 / v2: largest M (<= 16) of the self-zeroing atomic split plan
- *                       on row-major / tile-64 weights
+ *                       v1 / v2: largest M of the self-zeroing atomic split plan on
+ *                       row-major (<= 64) / tile-64 (<= 16) weights
  *   "self_zero" v0      0: M = 1 GEMVs never zero C inside the launch (the wave plan
  *                       zeroes it with a fill kernel, wide ones use the reduce launch)
  *   "nt" v0,v1          1 / 0: non-temporal weight loads on / off in the DMA-staged

@@ -1060,7 +1060,8 @@ void skinny_wave_kernel(SkinnyArgs args) {
     // single-lane atomic nor places its own wait for the result right after it.
     unsigned long long call1 = 0;  // this call's number + 1, as the zeroer writes it
     bool zeroer = false;
-    unsigned long long* tk = args.tick + 2 * (size_t)cx;
+    // one ticket pair per (m-group, strip)
+    unsigned long long* tk = args.tick + 2 * ((size_t)blockIdx.z * (size_t)n_strips + (size_t)cx);
     unsigned long long old = 0;
     const bool ticket = AQ == 0 && args.mode == SK_ATOMZ && wave == 0;
     if (ticket && lane == 0)
@@ -1278,7 +1279,7 @@ void skinny_wave_kernel(SkinnyArgs args) {
         if (lane == 0)
             for (int n = 0; zw != call1 && n < kZeroSpinLimit; ++n) {
                 __builtin_amdgcn_s_sleep(1);
-                zw = __hip_atomic_load(args.tick + 2 * (size_t)cx + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                zw = __hip_atomic_load(tk + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         __builtin_amdgcn_wave_barrier();
     }
@@ -1587,7 +1588,7 @@ hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, i
 
 bool skinny_wave_ok(const int8_t* A, const uint8_t* B, int M, int K, int N, int sw) {
     const int NB = N >> 2;
-    return M <= 32 && (sw == 16 || sw == 32) && K % 64 == 0 && NB % sw == 0 && (uintptr_t)B % 16 == 0 &&
+    return M <= 64 && (sw == 16 || sw == 32) && K % 64 == 0 && NB % sw == 0 && (uintptr_t)B % 16 == 0 &&
            (uintptr_t)A % 16 == 0 && NB < (1 << 26);
 }
 
@@ -1605,8 +1606,9 @@ hipError_t launch_skinny_wave(const int8_t* A, const uint8_t* B, int32_t* C, int
     if (mode == SK_PARTIAL && counters && n_out == 0 && aq.mode == 0) mode = SK_LAST;
     if (n_out > 0 && (mode == SK_ATOMIC || n_out > N || n_out % 4 != 0)) return hipErrorInvalidValue;
     if (mode == SK_ATOMIC && C == nullptr) return hipErrorInvalidValue;
-    // Self-zeroing atomics: one m-group, C rows 8-byte aligned, at most 64 splits.
-    if (mode == SK_ATOMIC && tickets && M <= 16 && aq.mode == 0 && splits <= 64 && (uintptr_t)C % 8 == 0 &&
+    // Self-zeroing atomics: up to four m-groups (tickets for m-groups x strips), C rows 8-byte aligned,
+    // at most 64 splits.
+    if (mode == SK_ATOMIC && tickets && M <= 64 && aq.mode == 0 && splits <= 64 && (uintptr_t)C % 8 == 0 &&
         N % 2 == 0)
         mode = SK_ATOMZ;
     if (mode == SK_ATOMIC) {

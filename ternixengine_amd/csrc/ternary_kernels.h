@@ -41,7 +41,7 @@ enum DebugKey : int {
     DBG_DEEP,            // [0] == 0: no whole-K deep GEMV; else (sw, nw, nsw, splits) forced
     DBG_SK_ORDER,        // [0] 1: release/acquire (agent scope) for the in-launch split sums
     DBG_M1_ATOMIC,       // [0] 0: no zero-fill + atomic split plan for M = 1 GEMVs; [1] / [2] largest M of
-                         //     the self-zeroing atomic plan on row-major / tile-64 weights (default 16)
+                         //     the self-zeroing atomic plan on row-major / tile-64 weights (default 64 / 16)
     DBG_GEMM_GM,         // [0] > 0: row tiles per group in the tile order of the 64/128-row GEMM kernels
     DBG_SELF_ZERO,       // [0] 0: no in-launch zeroing of C for M = 1 (fill launch or reduce launch instead)
     DBG_NT,              // [0] DMA-staged GEMV, [1] wave-pipelined GEMV: 1 non-temporal weight loads, 0 plain

@@ -368,6 +368,56 @@ DeepPlan plan_deep(const int8_t* dA, const uint8_t* dB, int M, int K, int N, boo
     return DeepPlan{16, 16, 4, 1, nsteps};
 }
 
+// The self-zeroing atomic split plan of the wave-pipelined GEMV (the measurements are with its call
+// in run_skinny): true when it takes the call (*e then holds the launch status).  Int32 output, aligned
+// operands (skinny_wave_ok), one ticket pair per (m-group, strip).
+bool run_atomic_wave(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int K, int N, Ctx& c, hipError_t* e) {
+    const hipStream_t st = c.st;
+    (void)st;
+    const int atomic_max_m = ternix_hip::debug_get(ternix_hip::DBG_M1_ATOMIC, 1) > 0 ? ternix_hip::debug_get(ternix_hip::DBG_M1_ATOMIC, 1) : 64;
+    if (!(M <= std::min(64, atomic_max_m) && dC != nullptr && wave_kernel_enabled() &&
+          ternix_hip::debug_get(ternix_hip::DBG_SKINNY_WAVE) < 0 && ternix_hip::debug_get(ternix_hip::DBG_M1_ATOMIC) != 0))
+        return false;
+    const int NB = N / 4, nsteps = K / 64, cus = cu_count(), mgroups = (M + 15) / 16;
+    int sw = 0, sp = 0;
+    if (M == 1 && K <= 4096 && NB <= 1024 && NB % 16 == 0) {
+        sw = 16;
+        sp = std::max(1, std::min(6, cus / (NB / 16)));
+    } else if (M == 1 && NB % 32 == 0 && (long)(NB / 32) * 4 * 50 <= (long)cus * 53) {
+        sw = 32;
+        sp = std::min(cus / (NB / 32), std::max(1, nsteps / 4));
+    } else if (M > 1 && NB % 32 == 0) {
+        sw = 32;
+        sp = (int)std::min<long>((long)cus * 53 / 50 / ((long)(NB / 32) * mgroups), std::max(1, nsteps / 4));
+    }
+    const int fsw = ternix_hip::debug_get(ternix_hip::DBG_WAVE_SW, 0), fsp = ternix_hip::debug_get(ternix_hip::DBG_WAVE_SW, 1);
+    if ((fsw == 16 || fsw == 32) && fsp > 1 && NB % fsw == 0) {  // forced split plan (tests and tuning)
+        sw = fsw;
+        sp = std::min(fsp, nsteps);
+    }
+    if (!(sw > 0 && sp > 1 && ternix_hip::skinny_wave_ok(dA, dB, M, K, N, sw))) return false;
+    const int sps = (nsteps + sp - 1) / sp, splits = (nsteps + sps - 1) / sps;
+    if (!(splits > 1 && sps * 64 <= ternix_hip::kMaxKPerAccumulator)) return false;
+    // 33..64 rows (several m-groups) only with short k-ranges per split: against the narrow-tile GEMM,
+    // measured on MI355X (cold): 64x4096x4096 14.1 -> 10.6 us (32 steps per split), 64x6912x2560 11.1
+    // -> 10.4 (36), but 64x11008x4096 15.6 -> 21.5 (86) and 64x14336x4096 17.9 -> 26.4 (112).  Up to
+    // 32 rows it wins wherever it splits K (24 and 32 rows: 1.11-1.42x against the in-launch sums and
+    // the reduce launch on five decode shapes).
+    if (M > 32 && sps > 40 && fsp <= 1) return false;
+    unsigned long long* tk = ternix_hip::debug_get(ternix_hip::DBG_SELF_ZERO) != 0 && splits <= 64
+                                 ? c.tickets((size_t)(NB / sw) * (size_t)mgroups)
+                                 : nullptr;
+    if (tk)
+        c.note("skinny_wave_kernel sw=%d nsw=2 splits=%d (splits added with int32 atomics into C zeroed "
+               "by each strip's first split)", sw, splits);
+    else if (M == 1)
+        c.note("zero_kernel + skinny_wave_kernel sw=%d nsw=2 splits=%d (splits added with int32 atomics)", sw, splits);
+    if (!(tk || M == 1)) return false;
+    *e = TX_LAUNCH(c, ternix_hip::launch_skinny_wave(dA, dB, dC, M, K, N, sw, 2, splits, sps, nullptr, st,
+                                                     ternix_hip::OutScale{}, 0, ternix_hip::ActQuant{}, 0, nullptr, tk));
+    return true;
+}
+
 hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int K, int N, Ctx& c,
                       const ternix_hip::OutScale& os = ternix_hip::OutScale{},
                       const ternix_hip::ActQuant& aq = ternix_hip::ActQuant{}) {
@@ -408,44 +458,9 @@ hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
     // (M 5, 8, 12, 16 x K,N in {4096x11008, 11008x4096, 2560x6912, 6912x2560, 4096x4096, 4096x14336,
     // 14336x4096}); cfg3 M=16 up 12.39 -> 9.20 us, down 12.38 -> 9.51 us.  The DBG_M1_ATOMIC switch
     // [1] lowers the row limit (tests and measurements).
-    const int atomic_max_m = ternix_hip::debug_get(ternix_hip::DBG_M1_ATOMIC, 1) > 0 ? ternix_hip::debug_get(ternix_hip::DBG_M1_ATOMIC, 1) : 16;
-    if (!generic && M <= std::min(16, atomic_max_m) && aq.mode == 0 && os.Y == nullptr && dC != nullptr && wave_kernel_enabled() &&
-        ternix_hip::debug_get(ternix_hip::DBG_SKINNY_WAVE) < 0 && ternix_hip::debug_get(ternix_hip::DBG_M1_ATOMIC) != 0) {
-        const int NB = N / 4, nsteps = K / 64, cus = cu_count();
-        int sw = 0, sp = 0;
-        if (M == 1 && K <= 4096 && NB <= 1024 && NB % 16 == 0) {
-            sw = 16;
-            sp = std::max(1, std::min(6, cus / (NB / 16)));
-        } else if (M == 1 && NB % 32 == 0 && (long)(NB / 32) * 4 * 50 <= (long)cus * 53) {
-            sw = 32;
-            sp = std::min(cus / (NB / 32), std::max(1, nsteps / 4));
-        } else if (M > 1 && NB % 32 == 0) {
-            sw = 32;
-            sp = (int)std::min<long>((long)cus * 53 / 50 / (NB / 32), std::max(1, nsteps / 4));
-        }
-        const int fsw = ternix_hip::debug_get(ternix_hip::DBG_WAVE_SW, 0), fsp = ternix_hip::debug_get(ternix_hip::DBG_WAVE_SW, 1);
-        if ((fsw == 16 || fsw == 32) && fsp > 1 && NB % fsw == 0) {  // forced split plan (tests and tuning)
-            sw = fsw;
-            sp = std::min(fsp, nsteps);
-        }
-        if (sw > 0 && sp > 1 && ternix_hip::skinny_wave_ok(dA, dB, M, K, N, sw)) {
-            const int sps = (nsteps + sp - 1) / sp, splits = (nsteps + sps - 1) / sps;
-            if (splits > 1 && sps * 64 <= ternix_hip::kMaxKPerAccumulator) {
-                unsigned long long* tk = ternix_hip::debug_get(ternix_hip::DBG_SELF_ZERO) != 0 && splits <= 64
-                                             ? c.tickets((size_t)(NB / sw))
-                                             : nullptr;
-                if (tk)
-                    c.note("skinny_wave_kernel sw=%d nsw=2 splits=%d (splits added with int32 atomics into C zeroed "
-                           "by each strip's first split)", sw, splits);
-                else if (M == 1)
-                    c.note("zero_kernel + skinny_wave_kernel sw=%d nsw=2 splits=%d (splits added with int32 atomics)",
-                           sw, splits);
-                if (tk || M == 1)
-                    return TX_LAUNCH(c, ternix_hip::launch_skinny_wave(dA, dB, dC, M, K, N, sw, 2, splits, sps, nullptr,
-                                                                       st, ternix_hip::OutScale{}, 0,
-                                                                       ternix_hip::ActQuant{}, 0, nullptr, tk));
-            }
-        }
+    {
+        hipError_t e = hipSuccess;
+        if (!generic && aq.mode == 0 && os.Y == nullptr && run_atomic_wave(dA, dB, dC, M, K, N, c, &e)) return e;
     }
     // Wave-pipelined kernel (32-byte strips, 16-byte with fused quantisation; 2 ring slots per wave),
     // measured on MI355X (16-byte strips) against the DMA-staged kernel: faster for K <= 4096 (cfg1
@@ -689,6 +704,10 @@ hipError_t run_auto(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int
     if (!pad_off && needs_padding(dA, dB, K, N, M <= skinny_max)) {
         const hipError_t e = run_padded(dA, dB, dC, M, K, N, c, os, M <= skinny_max);
         if (e != hipErrorNotSupported) return e;
+    }
+    if (M > skinny_max && M <= 64 && os.Y == nullptr && K % 64 == 0) {  // 33..64 rows: the atomic wave plan if it applies
+        hipError_t e = hipSuccess;
+        if (run_atomic_wave(dA, dB, dC, M, K, N, c, &e)) return e;
     }
     return M <= skinny_max ? run_skinny(dA, dB, dC, M, K, N, c, os) : run_gemm(dA, dB, dC, M, K, N, c, os);
 }

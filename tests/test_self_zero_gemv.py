@@ -177,6 +177,40 @@ def test_self_zero_up_to_16_rows(oracle, m):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("m", [17, 24, 32, 64])
+def test_self_zero_several_m_groups(oracle, m):
+    """Above 16 rows the plan runs one 16-row m-group per workgroup row of the grid, with one ticket
+    pair per (m-group, strip): interleaved calls of two shapes with several m-groups, bit-exact, then
+    the same calls with the plan limited to 16 rows on the same output buffers."""
+    lib = tx._load()
+    lib.ternix_hip_debug_reset()
+    s = hr.Stream()
+    rng = np.random.default_rng(80 + m)
+    probs = []
+    for k, n in [(4096, 4096), (6912, 2560)]:
+        plan = _plan_m(lib, m, k, n)
+        assert "zeroed by each strip's first split" in plan, (m, k, n, plan)
+        a = rng.integers(-128, 128, size=(m, k), dtype=np.int8)
+        wp = rng.integers(0, 256, size=(k, n // 4), dtype=np.uint8)
+        probs.append((m, k, n, hr.DeviceBuffer.from_array(a), hr.DeviceBuffer.from_array(wp),
+                      hr.DeviceBuffer(4 * m * n), oracle.mm("scalar_mt", a, wp, n)))
+    try:
+        for limit in (-1, 16):
+            assert lib.ternix_hip_debug_set(b"m1_atomic", -1, limit, -1, -1) == 0
+            for _, _, n, _, _, dc, _ in probs:
+                dc.upload(np.full(m * n, GARBAGE, np.int32))
+            log(f"[self-zero M={m} row limit {limit}] 30 interleaved rounds")
+            for _ in range(30):
+                for mm, k, n, da, db, dc, _ in probs:
+                    assert tx.mul_mat_ternary(da.value, db.value, dc.value, mm, k, n, stream=s.handle) == 0
+            s.synchronize()
+            for mm, k, n, _, _, dc, expect in probs:
+                assert (dc.download(np.int32, (mm, n)) == expect).all(), (mm, k, n, limit)
+    finally:
+        lib.ternix_hip_debug_reset()
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("m", [4, 16])
 def test_self_zero_tile64_rows(oracle, m):
     """Tile-64 weights with K > 4096 take the atomic plan for up to 16 rows too: interleaved calls of
