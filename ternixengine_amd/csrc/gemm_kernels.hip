@@ -690,7 +690,7 @@ hipError_t launch_gemm_t(const int8_t* A, const uint8_t* B, int32_t* C, int M, i
 
 // Narrow 64 x 64 tiles for M <= 64 when they alone fill at most one workgroup per CU (measured on
 // MI355X: cfg3 M=64 up 18.0 -> 13.4 us with no K split, 4096^2 at M=64 16.2 -> 9.9 us; with more
-// tiles than CUs, e.g. N = 28672, the 256-column tiles are faster).  TERNIX_GEMM_NARROW=0 / 1 turns
+// tiles than CUs, e.g. N = 28672, the 256-column tiles are faster).  The gemm_narrow debug switch (0 / 1) turns
 // the choice off / on regardless (experiments).
 bool gemm_narrow_wanted(int M, int K, int N) {
     const int env = debug_get(DBG_GEMM_NARROW);
