@@ -218,6 +218,9 @@ int ternix_hip_device_count(void);
  *                       zeroes it with a fill kernel, wide ones use the reduce launch)
  *   "nt" v0,v1          1 / 0: non-temporal weight loads on / off in the DMA-staged
  *                       (v0) and the wave-pipelined (v1) GEMVs
+ *   "wave_ticket" v0    1 / 0: the wave-pipelined GEMV's self-zeroing splits wait
+ *                       for their ticket in the first k-step / right after the
+ *                       first weight loads (default: 1 for k-ranges of >= 9 steps)
  * Returns 0, or 1 (hipErrorInvalidValue) for an unknown key.  Switches are
  * process-wide; a call running concurrently sees the old or the new value.
  * No reference counterpart (test hook of this library). */

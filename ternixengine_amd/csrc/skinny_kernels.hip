@@ -90,6 +90,7 @@ struct SkinnyArgs {
     int order;            // SK_LAST: 1 = C++ release/acquire at agent scope, 0 = coherent accesses only
     unsigned long long* tick;  // SK_ATOMZ: per strip {ticket counter, zeroed word}, persistent
     int nt;               // DMA-staged / wave-pipelined kernels: non-temporal weight loads
+    int defer_ticket;     // skinny_wave_kernel, SK_ATOMZ: wave 0 waits for its ticket with its first step
 };
 
 // One k-step of MFMA work for one 16-row x 4-byte-column block: raw[r] is the dword of row r.
@@ -1068,8 +1069,10 @@ void skinny_wave_kernel(SkinnyArgs args) {
         __asm__ volatile("global_atomic_add_x2 %0, %1, %2, off sc0" : "=v"(old) : "v"(tk), "v"(1ull) : "memory");
 #pragma unroll
     for (int p = 0; p < NSW - 1; ++p) issue(p, p, a_ring[p]);
-    if (ticket) {
-        TX_VMCNT((NSW - 1) * (NL + 1));  // the ticket has returned (the weight loads may not have)
+    // The ticket is learnt either right after the prologue (its own wait) or, with defer_ticket, in
+    // the first loop step, whose wait covers it (it is older than step 0), so that wave 0 issues one
+    // more weight step before it waits for the atomic's round trip.
+    auto take_ticket = [&]() {
         __asm__ volatile("" : "+v"(old));
         old = ((unsigned long long)(uint32_t)__builtin_amdgcn_readfirstlane((int)(old >> 32)) << 32) |
               (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)old);
@@ -1091,6 +1094,10 @@ void skinny_wave_kernel(SkinnyArgs args) {
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
             if (lane == 0) __hip_atomic_store(tk + 1, call1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
+    };
+    if (ticket && !args.defer_ticket) {
+        TX_VMCNT((NSW - 1) * (NL + 1));  // the ticket has returned (the weight loads may not have)
+        take_ticket();
     }
     if constexpr (AQ != 0) {
         __shared__ float red[4];
@@ -1135,6 +1142,7 @@ void skinny_wave_kernel(SkinnyArgs args) {
             const int it = it0 + p;
             issue(it + NSW - 1, (p + NSW - 1) % NSW, a_ring[(p + NSW - 1) % NSW]);
             TX_VMCNT((NSW - 1) * VPS);       // step `it` (DMAs and activation load) has landed
+            if (ticket && args.defer_ticket && it == 0) take_ticket();  // the older ticket has too
             if (ticket && !zeroer && it == iters - 1 && lane == 0)
                 zw = __hip_atomic_load(tk + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (wave + 4 * it < nst) {       // wave-uniform
@@ -1621,6 +1629,11 @@ hipError_t launch_skinny_wave(const int8_t* A, const uint8_t* B, int32_t* C, int
                  (mode == SK_STORE || mode == SK_LAST) ? os : OutScale{}};
     a.cnt = counters;
     a.tick = tickets;
+    // Deferred ticket wait for k-ranges of 9 or more steps (measured on MI355X, cold weights, us:
+    // cfg2 up 5.58 -> 5.42, down 5.75 -> 5.67, 4x11008x4096 8.70 -> 8.44, 16x11008x4096 9.55 -> 9.26);
+    // with shorter ones the zeroing split's publish, which then also waits for the extra step, is
+    // on the critical path (1x2560x2560, 7 steps: 3.93 -> 4.31).
+    a.defer_ticket = debug_get(DBG_WAVE_TICKET) >= 0 ? debug_get(DBG_WAVE_TICKET) == 1 : steps_per_split >= 9;
     a.nt = debug_get(DBG_NT, 1) == 1;  // plain loads unless forced (slower here on every decode shape measured)
     a.order = debug_get(DBG_SK_ORDER) == 1;
     a.n_out = n_out;

@@ -45,6 +45,7 @@ enum DebugKey : int {
     DBG_GEMM_GM,         // [0] > 0: row tiles per group in the tile order of the 64/128-row GEMM kernels
     DBG_SELF_ZERO,       // [0] 0: no in-launch zeroing of C for M = 1 (fill launch or reduce launch instead)
     DBG_NT,              // [0] DMA-staged GEMV, [1] wave-pipelined GEMV: 1 non-temporal weight loads, 0 plain
+    DBG_WAVE_TICKET,     // [0] 1 / 0: wave-pipelined GEMV waits for its split ticket in the first step / before it
     DBG_COUNT
 };
 int debug_get(DebugKey key, int idx = 0);

@@ -1226,7 +1226,7 @@ int ternix_hip_debug_set(const char* key, int v0, int v1, int v2, int v3) {
         {"gemm_splits", ternix_hip::DBG_GEMM_SPLITS}, {"gemm_bm", ternix_hip::DBG_GEMM_BM},
         {"deep", ternix_hip::DBG_DEEP},             {"sk_order", ternix_hip::DBG_SK_ORDER},
         {"m1_atomic", ternix_hip::DBG_M1_ATOMIC},     {"self_zero", ternix_hip::DBG_SELF_ZERO},
-        {"gemm_gm", ternix_hip::DBG_GEMM_GM},         {"nt", ternix_hip::DBG_NT},
+        {"gemm_gm", ternix_hip::DBG_GEMM_GM},         {"nt", ternix_hip::DBG_NT}, {"wave_ticket", ternix_hip::DBG_WAVE_TICKET},
     };
     if (key == nullptr) return (int)hipErrorInvalidValue;
     for (const auto& n : names) {

@@ -30,6 +30,8 @@ SWITCHES = [
     {"nt": (1, 1)},                                        # non-temporal weight loads in both GEMV kernels
     {"skinny_wave": 0, "nt": (1, 1)},                      # ... in the DMA-staged GEMVs on every shape
     {"skinny_wave": 0, "skinny_dma": (3, 12)},             # DMA-staged GEMVs with a forced split count
+    {"wave_ticket": 1},                                    # split ticket waited in the first k-step everywhere
+    {"wave_ticket": 0},                                    # ... and right after the prologue everywhere
 ]
 
 
