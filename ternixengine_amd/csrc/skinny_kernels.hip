@@ -932,8 +932,9 @@ void skinny_dma_kernel(SkinnyArgs args) {
 // splits are summed inside the launch (SK_LAST), so a decode GEMV is one launch.
 //   * SW = 32: chunk c of row r at position c ^ ((r / 16) % 2) (the two 16-lane groups of a
 //     transposing read use different banks); SW = 16: row r at position r ^ (8 ((r / 16) % 2)).
-// Loads are issued for the same number of steps on every wave (clamped addresses past the range, no
-// MFMAs for them), so the vmcnt waits are static.
+// Each wave issues its own steps only (the prologue's NSW-1 steps always, clamped past the range, no
+// MFMAs for those); each wait names the number of steps issued after the one it waits for, one
+// literal count per branch.
 // ------------------------------------------------------------------------------------------------
 template <int SW, int NSW, bool LOW_M, int AQ = 0>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
@@ -980,7 +981,7 @@ void skinny_wave_kernel(SkinnyArgs args) {
     const int m0 = blockIdx.z * 16;
     const int s_begin = sy * args.steps_per_split;
     const int nst = min(K >> 6, s_begin + args.steps_per_split) - s_begin;  // >= 1
-    const int iters = ((nst + 3) / 4 + NSW - 1) / NSW * NSW;                  // per wave, padded
+    const int nreal = nst > wave ? (nst - wave + 3) / 4 : 0;                  // this wave's k-steps
     uint8_t* ring = lds + wave * NSW * SLOT;
 
     // DMA lane mapping: instruction p, lane l -> LDS byte 1024 p + 16 l of the slot.
@@ -1133,19 +1134,26 @@ void skinny_wave_kernel(SkinnyArgs args) {
         __syncthreads();  // qbuf and rscale complete
     }
     constexpr int VPS = NL + (AQ ? 0 : 1);  // vector memory operations per step and wave
-    // SK_ATOMZ: the zeroed word, read in the last iteration beside that iteration's (padding) loads,
-    // whose wait after the loop then covers it
+    // SK_ATOMZ: the zeroed word, read in wave 0's last step (wave 0 has the most steps); the full wait
+    // after the loop covers it
     unsigned long long zw = 0;
-    for (int it0 = 0; it0 < iters; it0 += NSW) {
+    // Only the wave's own steps are issued (the prologue's NSW-1 always, clamped): each iteration
+    // waits for its step with a count of the steps issued after it, a literal in each branch.
+    for (int it0 = 0; it0 < nreal; it0 += NSW) {
 #pragma unroll
         for (int p = 0; p < NSW; ++p) {
             const int it = it0 + p;
-            issue(it + NSW - 1, (p + NSW - 1) % NSW, a_ring[(p + NSW - 1) % NSW]);
-            TX_VMCNT((NSW - 1) * VPS);       // step `it` (DMAs and activation load) has landed
+            if (it >= nreal) break;  // wave-uniform
+            if (it + NSW - 1 < nreal) issue(it + NSW - 1, (p + NSW - 1) % NSW, a_ring[(p + NSW - 1) % NSW]);
+            const int later = max(NSW - 1, min(nreal, it + NSW)) - it - 1;  // steps issued after `it`
+            if (later >= NSW - 1) TX_VMCNT((NSW - 1) * VPS);  // step `it` (DMAs, activation load) has landed
+            else if (later == 2) TX_VMCNT(2 * VPS);
+            else if (later == 1) TX_VMCNT(VPS);
+            else TX_VMCNT(0);
             if (ticket && args.defer_ticket && it == 0) take_ticket();  // the older ticket has too
-            if (ticket && !zeroer && it == iters - 1 && lane == 0)
+            if (ticket && !zeroer && it == nreal - 1 && lane == 0)
                 zw = __hip_atomic_load(tk + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (wave + 4 * it < nst) {       // wave-uniform
+            {
                 const uint32_t base = lds_u32(ring + p * SLOT);
                 uint64_t lo[G], hi[G];
 #pragma unroll
@@ -1181,7 +1189,7 @@ void skinny_wave_kernel(SkinnyArgs args) {
             __builtin_amdgcn_sched_barrier(0);
         }
     }
-    TX_VMCNT(0);  // the padding loads into the ring have landed before the ring is reused
+    TX_VMCNT(0);  // every DMA into the ring (and the zeroed word) has landed before the ring is reused
 
     // Sum the four waves: waves 1-3 put, wave 0 adds and stores.
     __syncthreads();
