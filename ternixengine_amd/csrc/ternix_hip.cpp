@@ -720,7 +720,14 @@ hipError_t run_tile64(const int8_t* dA, const uint8_t* dWt, int32_t* dC, int M, 
                       const ternix_hip::OutScale& os = ternix_hip::OutScale{}) {
     const hipStream_t st = c.st;
     (void)st;
-    if (M <= 16) {
+    // The self-zeroing atomic plan below applies to int32 output up to 16 rows; where it does, it is
+    // faster than the whole-K kernel (cold, one box, us: cfg1 4.80 -> 3.64, cfg2 up 5.10 -> 4.49, 4x4096x11008
+    // 6.46 -> 6.32, 16x4096x11008 7.69 -> 7.31), which keeps the dequantising calls.
+    const int t64_atomic_max_m = ternix_hip::debug_get(ternix_hip::DBG_M1_ATOMIC, 2) > 0 ? ternix_hip::debug_get(ternix_hip::DBG_M1_ATOMIC, 2) : 16;
+    const bool t64_atomic = M <= std::min(16, t64_atomic_max_m) && os.Y == nullptr && dC != nullptr &&
+                            ternix_hip::debug_get(ternix_hip::DBG_SELF_ZERO) != 0 &&
+                            ternix_hip::debug_get(ternix_hip::DBG_M1_ATOMIC) != 0;
+    if (M <= 16 && !(t64_atomic && ternix_hip::debug_get(ternix_hip::DBG_DEEP) < 0)) {
         const DeepPlan dp = plan_deep(dA, dWt, M, K, N, true);
         if (dp.sw > 0) {
             int32_t* partials =
@@ -735,6 +742,9 @@ hipError_t run_tile64(const int8_t* dA, const uint8_t* dWt, int32_t* dC, int M, 
     if (M <= 32) {
         const int nsteps = K / 64;
         int sp = wave_splits(M, K, N);
+        // Atomic plan with few strips and long K: at least 12 k-steps per split (cold, one box, us:
+        // cfg2 down 40 strips 16 -> 9 splits 5.75 -> 4.90; 4x11008x4096 64 strips 16 -> 14 splits).
+        if (t64_atomic && N / 4 / 16 <= 64 && nsteps >= 96) sp = std::min(sp, std::max(1, nsteps / 12));
         if (ternix_hip::debug_get(ternix_hip::DBG_SKINNY_WAVE) > 0 && ternix_hip::debug_get(ternix_hip::DBG_SKINNY_WAVE, 2) >= 1)
             sp = ternix_hip::debug_get(ternix_hip::DBG_SKINNY_WAVE, 2);
         const int sps = (nsteps + sp - 1) / sp;
@@ -742,11 +752,9 @@ hipError_t run_tile64(const int8_t* dA, const uint8_t* dWt, int32_t* dC, int M, 
         if (sps * 64 > ternix_hip::kMaxKPerAccumulator) return hipErrorInvalidValue;
         // Up to 16 rows into C: the splits add with int32 atomics into C zeroed by each strip's first
         // split (as on the row-major layout).  Measured on MI355X, cold weights, against the reduce
-        // launch: cfg3 M=4 down 9.46 -> 6.72 us, M=16 down 10.70 -> 7.57 us (the K <= 4096 shapes run
-        // the whole-K kernel above).  The DBG_M1_ATOMIC switch [2] lowers the row limit.
-        const int t64_atomic_max_m = ternix_hip::debug_get(ternix_hip::DBG_M1_ATOMIC, 2) > 0 ? ternix_hip::debug_get(ternix_hip::DBG_M1_ATOMIC, 2) : 16;
-        if (M <= std::min(16, t64_atomic_max_m) && splits > 1 && splits <= 64 && os.Y == nullptr && dC != nullptr &&
-            ternix_hip::debug_get(ternix_hip::DBG_SELF_ZERO) != 0 && ternix_hip::debug_get(ternix_hip::DBG_M1_ATOMIC) != 0) {
+        // launch: cfg3 M=4 down 9.46 -> 6.72 us, M=16 down 10.70 -> 7.57 us.  The DBG_M1_ATOMIC switch
+        // [2] lowers the row limit.
+        if (t64_atomic && splits > 1 && splits <= 64) {
             if (unsigned long long* tk = c.tickets((size_t)(N / 4 / 16))) {
                 c.note("skinny_wave_kernel (tile-64) sw=16 nsw=2 splits=%d (splits added with int32 atomics into C "
                        "zeroed by each strip's first split)", splits);
