@@ -1062,6 +1062,8 @@ void skinny_wave_kernel(SkinnyArgs args) {
     // single-lane atomic nor places its own wait for the result right after it.
     unsigned long long call1 = 0;  // this call's number + 1, as the zeroer writes it
     bool zeroer = false;
+    // Atomic modes: C has CN columns at pitch CN (a padded problem's real columns when n_out > 0)
+    const int CN = args.n_out > 0 ? args.n_out : args.N;
     // one ticket pair per (m-group, strip)
     unsigned long long* tk = args.tick + 2 * ((size_t)blockIdx.z * (size_t)n_strips + (size_t)cx);
     unsigned long long old = 0;
@@ -1085,9 +1087,9 @@ void skinny_wave_kernel(SkinnyArgs args) {
         if (zeroer) {
             // rows m0 .. m0 + a_rows - 1, columns 4 * bc0 .. 4 * (bc0 + SW) - 1: 8 bytes per lane
             for (int r = 0; r < a_rows; ++r) {
-                if (lane < SW * 2) {
+                if (lane < SW * 2 && 4 * bc0 + 2 * lane < CN) {
                     unsigned long long* z =
-                        reinterpret_cast<unsigned long long*>(args.C + (size_t)(m0 + r) * (size_t)args.N + 4 * bc0) + lane;
+                        reinterpret_cast<unsigned long long*>(args.C + (size_t)(m0 + r) * (size_t)CN + 4 * bc0) + lane;
                     __hip_atomic_store(z, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 }
             }
@@ -1317,9 +1319,10 @@ void skinny_wave_kernel(SkinnyArgs args) {
             int32_t vals[G];
 #pragma unroll
             for (int u = 0; u < G; ++u) vals[u] = row_lds[64 * u + lane];
-            int32_t* out = args.C + (size_t)(m0 + i) * (size_t)args.N + 4 * bc0;
+            int32_t* out = args.C + (size_t)(m0 + i) * (size_t)CN + 4 * bc0;
 #pragma unroll
-            for (int u = 0; u < G; ++u) atomicAdd(out + 64 * u + lane, vals[u]);
+            for (int u = 0; u < G; ++u)
+                if (4 * bc0 + 64 * u + lane < CN) atomicAdd(out + 64 * u + lane, vals[u]);
             __builtin_amdgcn_wave_barrier();  // the reads are issued before the next row's writes
             TX_LGKMCNT0();
         }
@@ -1344,9 +1347,10 @@ void skinny_wave_kernel(SkinnyArgs args) {
         }
         __builtin_amdgcn_wave_barrier();
         for (int r = 0; r < rows; ++r) {
-            int32_t* out = args.C + (size_t)(m0 + r) * (size_t)args.N + 4 * bc0;
+            int32_t* out = args.C + (size_t)(m0 + r) * (size_t)CN + 4 * bc0;
 #pragma unroll
-            for (int u = 0; u < G; ++u) atomicAdd(out + 64 * u + lane, row_lds[r * 4 * SW + 64 * u + lane]);
+            for (int u = 0; u < G; ++u)
+                if (4 * bc0 + 64 * u + lane < CN) atomicAdd(out + 64 * u + lane, row_lds[r * 4 * SW + 64 * u + lane]);
         }
         return;
     }
@@ -1620,13 +1624,13 @@ hipError_t launch_skinny_wave(const int8_t* A, const uint8_t* B, int32_t* C, int
     const int NB = N >> 2;
     int mode = splits <= 1 ? SK_STORE : (partials ? SK_PARTIAL : SK_ATOMIC);
     if (mode == SK_PARTIAL && counters && n_out == 0 && aq.mode == 0) mode = SK_LAST;
-    if (n_out > 0 && (mode == SK_ATOMIC || n_out > N || n_out % 4 != 0)) return hipErrorInvalidValue;
     if (mode == SK_ATOMIC && C == nullptr) return hipErrorInvalidValue;
     // Self-zeroing atomics: up to four m-groups (tickets for m-groups x strips), C rows 8-byte aligned,
-    // at most 64 splits.
+    // at most 64 splits; C may hold only the n_out real columns of a padded problem.
     if (mode == SK_ATOMIC && tickets && M <= 64 && aq.mode == 0 && splits <= 64 && (uintptr_t)C % 8 == 0 &&
         N % 2 == 0)
         mode = SK_ATOMZ;
+    if (n_out > 0 && (mode == SK_ATOMIC || n_out > N || n_out % 4 != 0)) return hipErrorInvalidValue;
     if (mode == SK_ATOMIC) {
         const hipError_t e = launch_zero(C, (size_t)M * (size_t)N, st);
         if (e != hipSuccess) return e;

@@ -371,7 +371,9 @@ DeepPlan plan_deep(const int8_t* dA, const uint8_t* dB, int M, int K, int N, boo
 // The self-zeroing atomic split plan of the wave-pipelined GEMV (the measurements are with its call
 // in run_skinny): true when it takes the call (*e then holds the launch status).  Int32 output, aligned
 // operands (skinny_wave_ok), one ticket pair per (m-group, strip).
-bool run_atomic_wave(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int K, int N, Ctx& c, hipError_t* e) {
+// n_out > 0: a padded problem (K, N the padded sizes) whose C holds its n_out real columns.
+bool run_atomic_wave(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int K, int N, Ctx& c, hipError_t* e,
+                     int n_out = 0, const char* prefix = "") {
     const hipStream_t st = c.st;
     (void)st;
     const int atomic_max_m = ternix_hip::debug_get(ternix_hip::DBG_M1_ATOMIC, 1) > 0 ? ternix_hip::debug_get(ternix_hip::DBG_M1_ATOMIC, 1) : 64;
@@ -408,13 +410,13 @@ bool run_atomic_wave(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, in
                                  ? c.tickets((size_t)(NB / sw) * (size_t)mgroups)
                                  : nullptr;
     if (tk)
-        c.note("skinny_wave_kernel sw=%d nsw=2 splits=%d (splits added with int32 atomics into C zeroed "
-               "by each strip's first split)", sw, splits);
-    else if (M == 1)
+        c.note("%sskinny_wave_kernel sw=%d nsw=2 splits=%d (splits added with int32 atomics into C zeroed "
+               "by each strip's first split)", prefix, sw, splits);
+    else if (M == 1 && n_out == 0)
         c.note("zero_kernel + skinny_wave_kernel sw=%d nsw=2 splits=%d (splits added with int32 atomics)", sw, splits);
-    if (!(tk || M == 1)) return false;
+    if (!(tk || (M == 1 && n_out == 0))) return false;
     *e = TX_LAUNCH(c, ternix_hip::launch_skinny_wave(dA, dB, dC, M, K, N, sw, 2, splits, sps, nullptr, st,
-                                                     ternix_hip::OutScale{}, 0, ternix_hip::ActQuant{}, 0, nullptr, tk));
+                                                     ternix_hip::OutScale{}, n_out, ternix_hip::ActQuant{}, 0, nullptr, tk));
     return true;
 }
 
@@ -675,6 +677,12 @@ hipError_t run_padded(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
                                                reinterpret_cast<const uint8_t*>(dA), reinterpret_cast<uint8_t*>(Ap),
                                                M, M, K, K, (int)Kp, st));
     if (e != hipSuccess) return e;
+    // int32 output up to 32 rows: the self-zeroing atomic split plan on the padded copies, writing the
+    // N real columns (measured on MI355X, cold weights, us, against the whole-K store kernel:
+    // 1x1000x3076 7.0 -> 6.6, 17x4093x1028 12.6 -> 10.1, both including the pad launch)
+    if (skinny && os.Y == nullptr && dC != nullptr && N % 4 == 0 &&
+        run_atomic_wave(Ap, Wp, dC, M, (int)Kp, (int)Np, c, &e, N, "pad_rows_kernel + "))
+        return e;
     if (wave)
         return TX_LAUNCH(c, ternix_hip::launch_skinny_wave(Ap, Wp, dC, M, (int)Kp, (int)Np, 16, 2, 1, (int)(Kp / 64), nullptr, st,
                                               os, N));
