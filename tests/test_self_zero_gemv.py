@@ -279,3 +279,30 @@ def test_self_zero_dma_kernel(oracle):
         _check(probs, "reduce plan after")
     finally:
         lib.ternix_hip_debug_reset()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("m,k,n", [(1, 1000, 3076), (3, 2000, 1036), (17, 4093, 1028), (32, 1000, 516)])
+def test_self_zero_padded_real_columns(oracle, m, k, n):
+    """Ragged shapes run the atomic plan on padded copies and write only the N real columns of C at
+    pitch N: a guard region after C keeps its values, and C is bit-exact over repeated calls, two
+    of them back to back without synchronisation."""
+    lib = tx._load()
+    lib.ternix_hip_debug_reset()
+    plan = _plan_m(lib, m, k, n)
+    assert plan.startswith("pad_rows_kernel + skinny_wave_kernel") and "zeroed by each strip's first split" in plan, plan
+    rng = np.random.default_rng(1000 + m)
+    a = rng.integers(-128, 128, size=(m, k), dtype=np.int8)
+    wp = rng.integers(0, 256, size=(k, n // 4), dtype=np.uint8)
+    expect = oracle.mm("scalar_mt", a, wp, n)
+    guard = 4096
+    da, db = hr.DeviceBuffer.from_array(a), hr.DeviceBuffer.from_array(wp)
+    dc = hr.DeviceBuffer(4 * (m * n + guard))
+    dc.upload(np.full(m * n + guard, GARBAGE, np.int32))
+    log(f"[self-zero padded] M={m} K={k} N={n}")
+    for _ in range(3):
+        assert tx.mul_mat_ternary(da.value, db.value, dc.value, m, k, n) == 0
+    hr.synchronize()
+    got = dc.download(np.int32, (m * n + guard,))
+    assert (got[: m * n].reshape(m, n) == expect).all(), (m, k, n)
+    assert (got[m * n:] == GARBAGE).all(), (m, k, n)
