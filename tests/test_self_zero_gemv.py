@@ -306,3 +306,24 @@ def test_self_zero_padded_real_columns(oracle, m, k, n):
     got = dc.download(np.int32, (m * n + guard,))
     assert (got[: m * n].reshape(m, n) == expect).all(), (m, k, n)
     assert (got[m * n:] == GARBAGE).all(), (m, k, n)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("m,k,n", [(1, 192, 4096), (1, 128, 16384), (3, 192, 8192), (1, 320, 2048), (16, 192, 4096)])
+def test_self_zero_short_k_ranges(oracle, m, k, n):
+    """Splits of one to three k-steps, so some of a workgroup's four waves own no step at all (each
+    wave issues only its own steps): bit-exact over repeated calls."""
+    lib = tx._load()
+    lib.ternix_hip_debug_reset()
+    plan = _plan_m(lib, m, k, n)
+    rng = np.random.default_rng(2000 + k + m)
+    a = rng.integers(-128, 128, size=(m, k), dtype=np.int8)
+    wp = rng.integers(0, 256, size=(k, n // 4), dtype=np.uint8)
+    expect = oracle.mm("scalar_mt", a, wp, n)
+    da, db, dc = hr.DeviceBuffer.from_array(a), hr.DeviceBuffer.from_array(wp), hr.DeviceBuffer(4 * m * n)
+    dc.upload(np.full(m * n, GARBAGE, np.int32))
+    log(f"[short k-ranges] M={m} K={k} N={n}: {plan}")
+    for _ in range(3):
+        assert tx.mul_mat_ternary(da.value, db.value, dc.value, m, k, n) == 0
+    hr.synchronize()
+    assert (dc.download(np.int32, (m, n)) == expect).all(), (m, k, n, plan)
