@@ -936,10 +936,14 @@ void skinny_dma_kernel(SkinnyArgs args) {
 // MFMAs for those); each wait names the number of steps issued after the one it waits for, one
 // literal count per branch.
 // ------------------------------------------------------------------------------------------------
-template <int SW, int NSW, bool LOW_M, int AQ = 0>
+template <int SW, int NSW, bool LOW_M, int AQ = 0, bool CW = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 void skinny_wave_kernel(SkinnyArgs args) {
     static_assert(SW == 16 || SW == 32, "16- or 32-byte strips");
+    // CW (column waves, self-zeroing atomics at M <= 4 only): the workgroup owns a 4 * SW-byte strip
+    // and wave w its w-th SW-byte part over every k-step of the range, so the four parts of each
+    // weight line reach one CU together; each wave adds its own outputs (no cross-wave sum).
+    static_assert(!CW || (AQ == 0 && LOW_M), "column waves: int32 atomics, M <= 4");
     constexpr int QK = 4096;                   // AQ: whole rows of K <= QK quantised into LDS
     constexpr int G = SW / 16;                 // 16-byte column groups per strip
     constexpr int SLOT = 64 * SW;              // bytes per ring slot (one k-step)
@@ -963,7 +967,18 @@ void skinny_wave_kernel(SkinnyArgs args) {
     constexpr int SPL = 128 / SW;  // strips per 128-byte line
     const int n_strips = NB / SW, lines = (n_strips + SPL - 1) / SPL;
     int cx, sy;
-    if (args.line_units) {
+    const int n_cw = (NB + 4 * SW - 1) / (4 * SW);  // CW: 4*SW-byte strips (the last may be partial)
+    int c4 = 0;
+    bool part_ok = true;  // CW: this wave's part lies inside the matrix
+    if (CW) {
+        const int total = n_cw * args.splits;
+        if ((int)blockIdx.x >= total) return;
+        const int lin = xcd_linear(blockIdx.x, total);
+        c4 = lin % n_cw;
+        sy = lin / n_cw;
+        part_ok = c4 * 4 + wave < n_strips;
+        cx = min(c4 * 4 + wave, n_strips - 1);  // a part past the last column re-reads the last one
+    } else if (args.line_units) {
         const int b = blockIdx.x, t = b >> 3;
         const int u = (b & 7) + 8 * (t / SPL);  // unit: (split, line group)
         sy = u / lines;
@@ -981,7 +996,7 @@ void skinny_wave_kernel(SkinnyArgs args) {
     const int m0 = blockIdx.z * 16;
     const int s_begin = sy * args.steps_per_split;
     const int nst = min(K >> 6, s_begin + args.steps_per_split) - s_begin;  // >= 1
-    const int nreal = nst > wave ? (nst - wave + 3) / 4 : 0;                  // this wave's k-steps
+    const int nreal = CW ? nst : (nst > wave ? (nst - wave + 3) / 4 : 0);    // this wave's k-steps
     uint8_t* ring = lds + wave * NSW * SLOT;
 
     // DMA lane mapping: instruction p, lane l -> LDS byte 1024 p + 16 l of the slot.
@@ -1004,7 +1019,7 @@ void skinny_wave_kernel(SkinnyArgs args) {
     const int s_last = s_begin + nst - 1;
     v4i a_ring[NSW];
     auto issue = [&](int it, int slot_c, v4i& a_dst) {
-        const int s = min(s_begin + wave + 4 * it, s_last);
+        const int s = CW ? min(s_begin + it, s_last) : min(s_begin + wave + 4 * it, s_last);
         uint8_t* dst = ring + slot_c * SLOT;
         if (SW == 16 && args.tiled) {  // one contiguous 1 KB block, already in LDS order
             lds_dma16(B + ((size_t)cx * (size_t)(K >> 6) + (size_t)s) * 1024 + lane * 16, dst);
@@ -1065,7 +1080,8 @@ void skinny_wave_kernel(SkinnyArgs args) {
     // Atomic modes: C has CN columns at pitch CN (a padded problem's real columns when n_out > 0)
     const int CN = args.n_out > 0 ? args.n_out : args.N;
     // one ticket pair per (m-group, strip)
-    unsigned long long* tk = args.tick + 2 * ((size_t)blockIdx.z * (size_t)n_strips + (size_t)cx);
+    unsigned long long* tk = CW ? args.tick + 2 * ((size_t)blockIdx.z * (size_t)n_cw + (size_t)c4)
+                                : args.tick + 2 * ((size_t)blockIdx.z * (size_t)n_strips + (size_t)cx);
     unsigned long long old = 0;
     const bool ticket = AQ == 0 && args.mode == SK_ATOMZ && wave == 0;
     if (ticket && lane == 0)
@@ -1085,12 +1101,16 @@ void skinny_wave_kernel(SkinnyArgs args) {
         if (rank == args.splits - 1 && args.splits < 64 && lane == 0)
             __hip_atomic_fetch_add(tk, (unsigned long long)(64 - args.splits), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (zeroer) {
-            // rows m0 .. m0 + a_rows - 1, columns 4 * bc0 .. 4 * (bc0 + SW) - 1: 8 bytes per lane
+            // rows m0 .. m0 + a_rows - 1, the strip's columns (4 * SW, or 16 * SW with CW): 8 bytes a lane
+            constexpr int ZB = CW ? 4 * SW : SW;  // strip bytes per row
+            const int zb0 = CW ? c4 * 4 * SW : bc0;
             for (int r = 0; r < a_rows; ++r) {
-                if (lane < SW * 2 && 4 * bc0 + 2 * lane < CN) {
-                    unsigned long long* z =
-                        reinterpret_cast<unsigned long long*>(args.C + (size_t)(m0 + r) * (size_t)CN + 4 * bc0) + lane;
-                    __hip_atomic_store(z, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                for (int u = lane; u < ZB * 2; u += 64) {
+                    if (4 * zb0 + 2 * u < CN) {
+                        unsigned long long* z =
+                            reinterpret_cast<unsigned long long*>(args.C + (size_t)(m0 + r) * (size_t)CN + 4 * zb0) + u;
+                        __hip_atomic_store(z, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    }
                 }
             }
             __builtin_amdgcn_s_waitcnt(0);  // the zeroes are stored, coherent at agent scope
@@ -1193,6 +1213,39 @@ void skinny_wave_kernel(SkinnyArgs args) {
     }
     TX_VMCNT(0);  // every DMA into the ring (and the zeroed word) has landed before the ring is reused
 
+    if constexpr (CW) {
+        // Column waves: wave 0 waits until the strip is zeroed, the barrier spreads it, then each wave
+        // adds its own part's outputs (row by row, 64 consecutive int32 per atomic instruction) from
+        // its own 512 bytes of LDS (the ring is idle: every wave's DMAs have landed).
+        if (!zeroer && wave == 0 && lane == 0)
+            for (int n = 0; zw != call1 && n < kZeroSpinLimit; ++n) {
+                __builtin_amdgcn_s_sleep(1);
+                zw = __hip_atomic_load(tk + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        __syncthreads();
+        if (!part_ok) return;
+        int32_t* row_lds = reinterpret_cast<int32_t*>(lds) + wave * 4 * SW;
+        const int rows = min(4, M - m0);
+        for (int i = 0; i < rows; ++i) {
+            if (kb == 0) {
+#pragma unroll
+                for (int g = 0; g < G; ++g)
+                    *reinterpret_cast<v4i*>(row_lds + (16 * g + q) * 4) =
+                        v4i{acc[g][0][i] >> 6, acc[g][1][i] >> 6, acc[g][2][i] >> 6, acc[g][3][i] >> 6};
+            }
+            __builtin_amdgcn_wave_barrier();
+            int32_t vals[G];
+#pragma unroll
+            for (int u = 0; u < G; ++u) vals[u] = row_lds[64 * u + lane];
+            int32_t* out = args.C + (size_t)(m0 + i) * (size_t)CN + 4 * bc0;
+#pragma unroll
+            for (int u = 0; u < G; ++u)
+                if (4 * bc0 + 64 * u + lane < CN) atomicAdd(out + 64 * u + lane, vals[u]);
+            __builtin_amdgcn_wave_barrier();
+            TX_LGKMCNT0();
+        }
+        return;
+    }
     // Sum the four waves: waves 1-3 put, wave 0 adds and stores.
     __syncthreads();
     if (wave > 0) {
@@ -1614,7 +1667,7 @@ bool skinny_wave_ok(const int8_t* A, const uint8_t* B, int M, int K, int N, int 
 
 hipError_t launch_skinny_wave(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int sw, int nsw,
                               int splits, int steps_per_split, int32_t* partials, hipStream_t st, const OutScale& os,
-                              int n_out, const ActQuant& aq, int tiled, int* counters, unsigned long long* tickets) {
+                              int n_out, const ActQuant& aq, int tiled, int* counters, unsigned long long* tickets, int column_waves) {
     if (tiled && (sw != 16 || n_out > 0)) return hipErrorInvalidValue;
     if (!skinny_wave_ok(A, B, M, K, N, sw) || nsw < 2 || nsw > 4 || steps_per_split < 1) return hipErrorInvalidValue;
     // Fused activation quantisation: one launch over whole rows (K <= 4096), 16-byte strips, 2 slots.
@@ -1662,6 +1715,13 @@ hipError_t launch_skinny_wave(const int8_t* A, const uint8_t* B, int32_t* C, int
     const unsigned gx = a.line_units ? (unsigned)(8 * spl * ((units + 7) / 8)) : (unsigned)((NB / sw) * splits);
     const dim3 grid(gx, 1, (M + 15) / 16), block(256);
     const bool low = M <= 4;
+    if (column_waves) {  // 128-byte strips, wave w on 32-byte part w (skinny_wave_kernel's CW form)
+        if (!(mode == SK_ATOMZ && low && sw == 32 && nsw == 2 && aq.mode == 0 && !tiled)) return hipErrorInvalidValue;
+        a.line_units = 0;
+        const dim3 gcw((unsigned)(((NB + 127) / 128) * splits), 1, 1);
+        hipLaunchKernelGGL((skinny_wave_kernel<32, 2, true, 0, true>), gcw, block, 0, st, a);
+        return hipGetLastError();
+    }
 #define TX_SW_LAUNCH(SW_, NSW_)                                                              \
     do {                                                                                      \
         if (low) hipLaunchKernelGGL((skinny_wave_kernel<SW_, NSW_, true>), grid, block, 0, st, a);  \

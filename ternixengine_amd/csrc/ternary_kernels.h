@@ -106,7 +106,8 @@ bool skinny_wave_ok(const int8_t* A, const uint8_t* B, int M, int K, int N, int 
 hipError_t launch_skinny_wave(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int sw, int nsw,
                               int splits, int steps_per_split, int32_t* partials, hipStream_t st,
                               const OutScale& os = OutScale{}, int n_out = 0, const ActQuant& aq = ActQuant{},
-                              int tiled = 0, int* counters = nullptr, unsigned long long* tickets = nullptr);
+                              int tiled = 0, int* counters = nullptr, unsigned long long* tickets = nullptr,
+                              int column_waves = 0);
 // (tiled != 0: W is in the tile-64 layout of launch_interleave_weights, sw must be 16.
 // n_out > 0: a padded problem -- C / os.Y has n_out <= N columns; not with the atomic mode.
 // aq set: the activations are quantised in the kernel from aq.X (splits == 1, K <= 4096, sw 16,

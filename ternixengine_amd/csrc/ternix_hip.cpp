@@ -398,7 +398,7 @@ bool run_atomic_wave(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, in
         sp = std::min(fsp, nsteps);
     }
     if (!(sw > 0 && sp > 1 && ternix_hip::skinny_wave_ok(dA, dB, M, K, N, sw))) return false;
-    const int sps = (nsteps + sp - 1) / sp, splits = (nsteps + sps - 1) / sps;
+    int sps = (nsteps + sp - 1) / sp, splits = (nsteps + sps - 1) / sps;
     if (!(splits > 1 && sps * 64 <= ternix_hip::kMaxKPerAccumulator)) return false;
     // 33..64 rows (several m-groups) only with short k-ranges per split: against the narrow-tile GEMM,
     // measured on MI355X (cold): 64x4096x4096 14.1 -> 10.6 us (32 steps per split), 64x6912x2560 11.1
@@ -406,17 +406,45 @@ bool run_atomic_wave(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, in
     // 32 rows it wins wherever it splits K (24 and 32 rows: 1.11-1.42x against the in-launch sums and
     // the reduce launch on five decode shapes).
     if (M > 32 && sps > 40 && fsp <= 1) return false;
+    // Column waves (M <= 4, 32-byte parts): a workgroup owns a 128-byte strip and each wave one
+    // 32-byte part over the workgroup's whole k-range, so the four parts of each weight line reach one
+    // CU together.  More K splits for the same workgroups (more atomic adds per output), so only where
+    // one round of workgroups (>= 3/4 of the CUs, none doubled) takes <= 32 splits.  Measured on
+    // MI355X, cold weights (us, current plan -> column waves): 4x4096x11008 8.08 -> 7.47,
+    // 4x11008x4096 8.4 -> 8.13, 4x4096x14336 9.85 -> 8.78, 1x14336x4096 9.0 -> 8.36, cfg2 up 5.35 ->
+    // 5.27; cfg2 down (5 strips: 36 splits for 180 workgroups) 5.64 -> 5.93 stays.
+    int cw = 0, cw_sps = 0;
+    const int fcw = ternix_hip::debug_get(ternix_hip::DBG_WAVE_SW, 2);  // 1 / 0: force on / off (tests)
+    if (M <= 4 && sw == 32 && n_out == 0 && fcw != 0 && fsp <= 1) {
+        const long n_cw = (NB + 127) / 128;
+        long best = 0;
+        for (int q = 1; q * 64 <= ternix_hip::kMaxKPerAccumulator && q <= nsteps; ++q) {
+            const long sc = (nsteps + q - 1) / q;
+            if (sc >= 2 && sc <= 32 && n_cw * sc <= cus && n_cw * sc > best) {
+                best = n_cw * sc;
+                cw_sps = q;
+            }
+        }
+        if (best > 0 && (best * 4 >= (long)cus * 3 || fcw == 1)) cw = 1;
+    } else if (M <= 4 && sw == 32 && n_out == 0 && fcw == 1 && fsp > 1) {
+        cw = 1;  // forced split count with column waves (tuning)
+    }
+    if (cw && cw_sps > 0) {
+        sps = cw_sps;
+        splits = (nsteps + sps - 1) / sps;
+    }
     unsigned long long* tk = ternix_hip::debug_get(ternix_hip::DBG_SELF_ZERO) != 0 && splits <= 64
-                                 ? c.tickets((size_t)(NB / sw) * (size_t)mgroups)
+                                 ? c.tickets(cw ? (size_t)((NB + 127) / 128) : (size_t)(NB / sw) * (size_t)mgroups)
                                  : nullptr;
+    if (cw && !tk) return false;
     if (tk)
-        c.note("%sskinny_wave_kernel sw=%d nsw=2 splits=%d (splits added with int32 atomics into C zeroed "
-               "by each strip's first split)", prefix, sw, splits);
+        c.note("%sskinny_wave_kernel sw=%d nsw=2 splits=%d%s (splits added with int32 atomics into C zeroed "
+               "by each strip's first split)", prefix, sw, splits, cw ? " column waves" : "");
     else if (M == 1 && n_out == 0)
         c.note("zero_kernel + skinny_wave_kernel sw=%d nsw=2 splits=%d (splits added with int32 atomics)", sw, splits);
     if (!(tk || (M == 1 && n_out == 0))) return false;
     *e = TX_LAUNCH(c, ternix_hip::launch_skinny_wave(dA, dB, dC, M, K, N, sw, 2, splits, sps, nullptr, st,
-                                                     ternix_hip::OutScale{}, n_out, ternix_hip::ActQuant{}, 0, nullptr, tk));
+                                                     ternix_hip::OutScale{}, n_out, ternix_hip::ActQuant{}, 0, nullptr, tk, cw));
     return true;
 }
 

@@ -32,6 +32,8 @@ SWITCHES = [
     {"skinny_wave": 0, "skinny_dma": (3, 12)},             # DMA-staged GEMVs with a forced split count
     {"wave_ticket": 1},                                    # split ticket waited in the first k-step everywhere
     {"wave_ticket": 0},                                    # ... and right after the prologue everywhere
+    {"wave_sw": (-1, -1, 0)},                              # no column waves in the M <= 4 atomic plan
+    {"wave_sw": (-1, -1, 1)},                              # column waves wherever the plan allows them
 ]
 
 
