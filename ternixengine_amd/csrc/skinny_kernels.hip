@@ -674,7 +674,7 @@ void skinny_dma_kernel(SkinnyArgs args) {
     };
     // SK_ATOMZ (as in skinny_wave_kernel): wave 0 takes the strip's ticket before any DMA; the
     // first loop wait of wave 0 (for a step issued after it) covers its return.
-    const bool ticket = AQ == 0 && args.mode == SK_ATOMZ && wave == 0;
+    const bool ticket = args.mode == SK_ATOMZ && wave == 0;
     unsigned long long* tk = args.tick + 2 * (size_t)cx;
     unsigned long long old = 0, call1 = 0, zw = 0;
     bool zeroer = false;
@@ -849,7 +849,7 @@ void skinny_dma_kernel(SkinnyArgs args) {
         step(it, it % NS);
         __builtin_amdgcn_sched_barrier(0);
     }
-    if (AQ == 0 && args.mode == SK_ATOMZ) {
+    if (args.mode == SK_ATOMZ) {
         // every wave's atomics wait until the strip is zeroed (wave 0 checks, the barrier spreads it)
         if (wave == 0 && !zeroer && lane == 0)
             for (int n = 0; zw != call1 && n < kZeroSpinLimit; ++n) {
@@ -860,7 +860,7 @@ void skinny_dma_kernel(SkinnyArgs args) {
     }
 
     // Epilogue: lane (q, kb) holds rows 4kb+i of byte-columns bc0 + 16(4 wave + g) + q.
-    if (LOW_M && AQ == 0 && args.mode == SK_ATOMZ) {
+    if (LOW_M && args.mode == SK_ATOMZ) {
         // Few rows into C with atomics: each wave lays its row's 256 outputs out in column order in
         // its own 1 KB of the (now idle) stage buffer, then adds one column per lane per instruction
         // (64 consecutive int32 per atomic instruction, no per-element branch).  The barrier above
@@ -1588,8 +1588,9 @@ hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, i
     if (n_out > 0 && (mode != SK_PARTIAL || n_out > N || n_out % 4 != 0)) return hipErrorInvalidValue;
     if (mode == SK_ATOMIC && C == nullptr) return hipErrorInvalidValue;  // scaled call without int scratch
     if (aq.mode != 0 && !skinny_short_ok(B, M, K, N, steps_per_split, splits)) return hipErrorInvalidValue;
-    // Self-zeroing atomics: DMA-staged kernel, one m-group, C rows 8-byte aligned, at most 64 splits.
-    if (mode == SK_ATOMIC && tickets && dma_ns > 0 && aq.mode == 0 && M <= 16 && splits <= 64 &&
+    // Self-zeroing atomics: DMA-staged kernel (also with fused activation quantisation), one m-group,
+    // C rows 8-byte aligned, at most 64 splits.
+    if (mode == SK_ATOMIC && tickets && dma_ns > 0 && M <= 16 && splits <= 64 &&
         (uintptr_t)C % 8 == 0 && N % 2 == 0)
         mode = SK_ATOMZ;
     if (mode == SK_ATOMIC) {
