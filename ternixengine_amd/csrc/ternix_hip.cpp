@@ -429,6 +429,7 @@ bool run_atomic_wave(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, in
     } else if (M <= 4 && sw == 32 && n_out == 0 && fcw == 1 && fsp > 1) {
         cw = 1;  // forced split count with column waves (tuning)
     }
+    const int sps0 = sps, splits0 = splits;  // the plan without column waves
     if (cw && cw_sps > 0) {
         sps = cw_sps;
         splits = (nsteps + sps - 1) / sps;
@@ -436,7 +437,13 @@ bool run_atomic_wave(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, in
     unsigned long long* tk = ternix_hip::debug_get(ternix_hip::DBG_SELF_ZERO) != 0 && splits <= 64
                                  ? c.tickets(cw ? (size_t)((NB + 127) / 128) : (size_t)(NB / sw) * (size_t)mgroups)
                                  : nullptr;
-    if (cw && !tk) return false;
+    if (cw && !tk) {  // column waves need the tickets: the plan without them (zero fill at M = 1)
+        cw = 0;
+        sps = sps0;
+        splits = splits0;
+        if (ternix_hip::debug_get(ternix_hip::DBG_SELF_ZERO) != 0 && splits <= 64)
+            tk = c.tickets((size_t)(NB / sw) * (size_t)mgroups);
+    }
     if (tk)
         c.note("%sskinny_wave_kernel sw=%d nsw=2 splits=%d%s (splits added with int32 atomics into C zeroed "
                "by each strip's first split)", prefix, sw, splits, cw ? " column waves" : "");

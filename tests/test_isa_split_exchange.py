@@ -44,8 +44,9 @@ def _relaxed_exchange(lines):
 
 
 def test_wave_kernels_use_coherent_exchange(wave_kernels):
-    # instantiations without fused quantisation take part in the in-launch split sum
-    names = [n for n in wave_kernels if re.search(r"skinny_wave_kernelILi(16|32)ELi\dELb[01]ELi0E", n)]
+    # instantiations without fused quantisation take part in the in-launch split sum (the column-wave
+    # form, last template argument true, only adds with atomics)
+    names = [n for n in wave_kernels if re.search(r"skinny_wave_kernelILi(16|32)ELi\dELb[01]ELi0ELb0E", n)]
     assert names, "no wave-kernel instantiation found in the assembly"
     for name in names:
         lines = wave_kernels[name]
