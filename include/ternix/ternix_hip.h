@@ -197,8 +197,9 @@ int ternix_hip_device_count(void);
  *   "wave_last" v0      most K splits summed inside one wave-GEMV launch (0: none)
  *   "skinny_wave" v0..2 0: no wave-pipelined GEMV; else force (strip bytes,
  *                       ring slots, splits)
- *   "wave_sw" v0,v1     v0 16: 16-byte wave strips on row-major weights; with v1 > 1 the
- *                       strip width (16 / 32) and split count of the atomic split plan
+ *   "wave_sw" v0..v2    v0 16: 16-byte wave strips on row-major weights; with v1 > 1 the
+ *                       strip width (16 / 32) and split count of the atomic split plan;
+ *                       v2 1 / 0: column waves (M <= 4) on / off in that plan
  *   "skinny_dma" v0,v1  v0 0: no DMA-staged GEMV; 2..4: its stage count; v1: its
  *                       split count forced
  *   "skinny_short" v0   0: no register-staged short GEMV

@@ -30,7 +30,8 @@ enum DebugKey : int {
     DBG_WAVE_LAST = 0,   // [0] largest split count summed inside the wave GEMV launch (0: never)
     DBG_SKINNY_WAVE,     // [0] == 0: no wave-pipelined GEMV; else (sw, nsw, splits) forced
     DBG_WAVE_SW,         // [0] strip width of the wave-pipelined GEMV on row-major weights (16 / 32);
-                         //     with [1] > 1 also the atomic split plan's strip width and split count
+                         //     with [1] > 1 also the atomic split plan's strip width and split count;
+                         //     [2] 1 / 0: column waves (M <= 4) forced on / off in that plan
     DBG_SKINNY_DMA,      // [0] == 0: no DMA-staged GEMV; 2..4: its stage count; [1] > 0: its split count
     DBG_SKINNY_SHORT,    // [0] == 0: no register-staged short GEMV
     DBG_RAGGED_PAD,      // [0] == 0: ragged shapes run the generic kernels instead of a padded copy
