@@ -327,3 +327,20 @@ def test_self_zero_short_k_ranges(oracle, m, k, n):
         assert tx.mul_mat_ternary(da.value, db.value, dc.value, m, k, n) == 0
     hr.synchronize()
     assert (dc.download(np.int32, (m, n)) == expect).all(), (m, k, n, plan)
+
+
+def test_plan_column_waves():
+    """The M <= 4 atomic plan takes column waves where one round of workgroups needs at most 32
+    splits (cfg3 M=4, cfg2 up), not for cfg2 down (5 strips), cfg1 (16-byte strips) or M = 16, and
+    the switch forces them off."""
+    lib = tx._load()
+    lib.ternix_hip_debug_reset()
+    for m, k, n in [(4, 4096, 11008), (4, 11008, 4096), (1, 2560, 6912)]:
+        assert "column waves" in _plan_m(lib, m, k, n), (m, k, n)
+    for m, k, n in [(1, 6912, 2560), (1, 2560, 2560), (16, 4096, 11008)]:
+        assert "column waves" not in _plan_m(lib, m, k, n), (m, k, n)
+    assert lib.ternix_hip_debug_set(b"wave_sw", -1, -1, 0, -1) == 0
+    try:
+        assert "column waves" not in _plan_m(lib, 4, 4096, 11008)
+    finally:
+        lib.ternix_hip_debug_reset()
