@@ -678,7 +678,6 @@ void skinny_dma_kernel(SkinnyArgs args) {
     unsigned long long* tk = args.tick + 2 * (size_t)cx;
     unsigned long long old = 0, call1 = 0, zw = 0;
     bool zeroer = false;
-    __shared__ int s_zero_ok;
     if (ticket && lane == 0)
         __asm__ volatile("global_atomic_add_x2 %0, %1, %2, off sc0" : "=v"(old) : "v"(tk), "v"(1ull) : "memory");
     // After the first wait: learn the ticket; the strip's first split zeroes its 4 KB of C per row
