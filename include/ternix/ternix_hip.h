@@ -232,6 +232,15 @@ void ternix_hip_debug_reset(void);
  * does not occur in practice.  Benchmarks time it as the bare HBM read floor of a
  * matmul that reads the same number of bytes. */
 int ternix_hip_debug_stream_read(const void* dSrc, size_t bytes, int* dFlag, void* stream);
+/* Device fault word of the current GPU: the kernels' bounded in-launch waits never
+ * hang, and a wave whose wait gives up records it here instead (the call that hit
+ * it still returned hipSuccess, and its output is not trustworthy).  This
+ * synchronises the device, stores the recorded TERNIX_FAULT_* bits in *bits (0 when
+ * none) and clears them.  Returns 0, hipErrorInvalidValue for a null pointer, or
+ * the runtime's error.  No reference counterpart (the reference's kernels have no
+ * in-launch waits, cuda_kernels.cu:42-122). */
+#define TERNIX_FAULT_ZERO_WAIT 1u /* a K split's wait for its strip's zeroed outputs gave up */
+int ternix_hip_take_faults(unsigned int* bits);
 /* Number of device allocations the library has made in this process (workspace
  * buffers, split counters, the host wrapper's temporaries); a test hook. */
 long long ternix_hip_debug_alloc_count(void);

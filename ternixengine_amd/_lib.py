@@ -46,6 +46,8 @@ def load():
     lib.ternix_hip_debug_stream_read.restype = ctypes.c_int
     lib.ternix_hip_debug_alloc_count.argtypes = []
     lib.ternix_hip_debug_alloc_count.restype = ctypes.c_longlong
+    lib.ternix_hip_take_faults.argtypes = [ctypes.c_void_p]
+    lib.ternix_hip_take_faults.restype = ctypes.c_int
     lib.ternix_hip_mul_mat_ternary_workspace_size.argtypes = [i64, i64, i64]
     lib.ternix_hip_mul_mat_ternary_workspace_size.restype = ctypes.c_size_t
     lib.ternix_hip_mul_mat_ternary_workspace_size_for.argtypes = [i8p, i8p, i64, i64, i64]

@@ -64,6 +64,30 @@ enum SkinnyMode { SK_STORE = 0, SK_ATOMIC = 1, SK_PARTIAL = 2, SK_LAST = 3, SK_A
 // that every wave exits.
 constexpr int kZeroSpinLimit = 1 << 20;
 
+}  // namespace
+
+// Device fault word of this library on each GPU: a wave whose bounded wait gives up ORs its bit in
+// (kFaultZeroWait: the zeroed word of an SK_ATOMZ strip never arrived, so that split added into
+// outputs that may not have been zeroed and the call's result is not trustworthy).  Read and cleared
+// by take_faults (ternix_hip_take_faults); nothing else writes it.
+__device__ unsigned int g_tx_fault_word;
+
+namespace {
+
+__device__ __forceinline__ void note_fault(unsigned bit) {
+    __hip_atomic_fetch_or(&g_tx_fault_word, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The SK_ATOMZ wait of a non-zeroing split (one lane): re-read the strip's zeroed word until it holds
+// this call's number, at most kZeroSpinLimit times; on giving up, record kFaultZeroWait.
+__device__ __forceinline__ void wait_zeroed(unsigned long long* tk, unsigned long long zw, unsigned long long call1) {
+    for (int n = 0; zw != call1 && n < kZeroSpinLimit; ++n) {
+        __builtin_amdgcn_s_sleep(1);
+        zw = __hip_atomic_load(tk + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (zw != call1) note_fault(kFaultZeroWait);
+}
+
 struct SkinnyArgs {
     const int8_t* A;
     const uint8_t* B;
@@ -851,10 +875,7 @@ void skinny_dma_kernel(SkinnyArgs args) {
     if (args.mode == SK_ATOMZ) {
         // every wave's atomics wait until the strip is zeroed (wave 0 checks, the barrier spreads it)
         if (wave == 0 && !zeroer && lane == 0)
-            for (int n = 0; zw != call1 && n < kZeroSpinLimit; ++n) {
-                __builtin_amdgcn_s_sleep(1);
-                zw = __hip_atomic_load(tk + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
+            wait_zeroed(tk, zw, call1);
         __syncthreads();
     }
 
@@ -1217,10 +1238,7 @@ void skinny_wave_kernel(SkinnyArgs args) {
         // adds its own part's outputs (row by row, 64 consecutive int32 per atomic instruction) from
         // its own 512 bytes of LDS (the ring is idle: every wave's DMAs have landed).
         if (!zeroer && wave == 0 && lane == 0)
-            for (int n = 0; zw != call1 && n < kZeroSpinLimit; ++n) {
-                __builtin_amdgcn_s_sleep(1);
-                zw = __hip_atomic_load(tk + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
+            wait_zeroed(tk, zw, call1);
         __syncthreads();
         if (!part_ok) return;
         int32_t* row_lds = reinterpret_cast<int32_t*>(lds) + wave * 4 * SW;
@@ -1347,10 +1365,7 @@ void skinny_wave_kernel(SkinnyArgs args) {
     }
     if (AQ == 0 && args.mode == SK_ATOMZ && !zeroer) {  // wave 0: wait until the strip is zeroed
         if (lane == 0)
-            for (int n = 0; zw != call1 && n < kZeroSpinLimit; ++n) {
-                __builtin_amdgcn_s_sleep(1);
-                zw = __hip_atomic_load(tk + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
+            wait_zeroed(tk, zw, call1);
         __builtin_amdgcn_wave_barrier();
     }
     if (LOW_M && AQ == 0 && (args.mode == SK_ATOMIC || args.mode == SK_ATOMZ)) {
@@ -1745,6 +1760,21 @@ hipError_t launch_skinny_wave(const int8_t* A, const uint8_t* B, int32_t* C, int
     if (mode != SK_PARTIAL) return e;
     return n_out > 0 ? launch_splitk_reduce(partials, C, M, n_out, splits, os, st, N)
                      : launch_splitk_reduce(partials, C, M, N, splits, os, st);
+}
+
+hipError_t take_faults(unsigned* bits) {
+    *bits = 0;
+    hipError_t e = hipDeviceSynchronize();
+    if (e != hipSuccess) return e;
+    unsigned v = 0;
+    e = hipMemcpyFromSymbol(&v, HIP_SYMBOL(g_tx_fault_word), sizeof(v), 0, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return e;
+    if (v != 0) {
+        const unsigned zero = 0;
+        e = hipMemcpyToSymbol(HIP_SYMBOL(g_tx_fault_word), &zero, sizeof(zero), 0, hipMemcpyHostToDevice);
+    }
+    *bits = v;
+    return e;
 }
 
 hipError_t launch_splitk_reduce(const int32_t* P, int32_t* C, int M, int N, int splits, const OutScale& os,

@@ -52,6 +52,10 @@ enum DebugKey : int {
 int debug_get(DebugKey key, int idx = 0);
 
 hipError_t launch_zero(int32_t* C, size_t n, hipStream_t st);
+// Bits of the device fault word (skinny_kernels.hip); the same values as TERNIX_FAULT_* in ternix_hip.h.
+constexpr unsigned kFaultZeroWait = 1u;  // a bounded wait for a strip's zeroed word gave up
+// Synchronises the current device, returns the fault word's bits in *bits and clears them.
+hipError_t take_faults(unsigned* bits);
 // Bare streaming read of `bytes` (rounded down to 16) at p (16-byte aligned): the HBM floor reference.
 hipError_t launch_stream_read(const void* p, size_t bytes, int* out, hipStream_t st);
 // LDS bytes the skinny fast kernel uses for one workgroup's activation slice (the rows of one

@@ -16,6 +16,7 @@
 #include <cstdarg>
 #include <map>
 #include <mutex>
+#include <thread>
 #include <utility>
 #include <vector>
 
@@ -56,7 +57,25 @@ struct Workspace {
     int* counters = nullptr;  // arrival counters of the single-launch split-K GEMV (zero between calls)
 };
 std::mutex g_ws_mutex;
-std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
+// Key of a stream's buffers: (device, stream handle, thread).  hipStreamPerThread is one handle that
+// names a different real stream in every host thread, so calls from two threads through it may run
+// concurrently and must not share counters or tickets: for that handle the key also holds the
+// calling thread.  Every other handle names one stream, whichever thread uses it (the null stream
+// included: work on it runs in submission order), and the thread part is left empty.
+struct WsKey {
+    int dev;
+    hipStream_t st;
+    std::thread::id thread;
+    bool operator<(const WsKey& o) const {
+        if (dev != o.dev) return dev < o.dev;
+        if (st != o.st) return std::less<hipStream_t>()(st, o.st);
+        return thread < o.thread;
+    }
+};
+WsKey ws_key(int dev, hipStream_t st) {
+    return WsKey{dev, st, st == hipStreamPerThread ? std::this_thread::get_id() : std::thread::id()};
+}
+std::map<WsKey, Workspace> g_ws;
 std::atomic<long long> g_alloc_count{0};  // device allocations made by the library (a test hook)
 
 // Every device allocation of the library goes through here.  A failed hipMalloc leaves its error in
@@ -76,7 +95,7 @@ void* workspace(hipStream_t st, size_t bytes) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return nullptr;
     std::lock_guard<std::mutex> lock(g_ws_mutex);
-    Workspace& w = g_ws[{dev, st}];
+    Workspace& w = g_ws[ws_key(dev, st)];
     if (w.bytes >= bytes) return w.ptr;
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
@@ -126,7 +145,7 @@ int* counter_buffer(hipStream_t st) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return nullptr;
     std::lock_guard<std::mutex> lock(g_ws_mutex);
-    Workspace& w = g_ws[{dev, st}];
+    Workspace& w = g_ws[ws_key(dev, st)];
     if (w.counters) return w.counters;
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
@@ -914,7 +933,7 @@ int ternix_hip_release_stream(void* stream) {
     Workspace w;
     {
         std::lock_guard<std::mutex> lock(g_ws_mutex);
-        auto it = g_ws.find({dev, st});
+        auto it = g_ws.find(ws_key(dev, st));
         if (it == g_ws.end()) return (int)hipSuccess;
         w = std::move(it->second);
         g_ws.erase(it);
@@ -1301,6 +1320,11 @@ int ternix_hip_debug_stream_read(const void* dSrc, size_t bytes, int* dFlag, voi
 }
 
 long long ternix_hip_debug_alloc_count(void) { return g_alloc_count.load(std::memory_order_relaxed); }
+
+int ternix_hip_take_faults(unsigned int* bits) {
+    if (bits == nullptr) return (int)hipErrorInvalidValue;
+    return (int)ternix_hip::take_faults(bits);
+}
 
 void ternix_hip_debug_reset(void) {
     for (auto& k : ternix_hip::g_debug)

@@ -20,6 +20,20 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU")
 
 
+@pytest.fixture(autouse=True)
+def _no_device_faults(request):
+    """Every GPU test ends with the library's device fault word clear: no bounded in-launch wait of
+    the kernels gave up during the test (such a wait does not fail the call, it records a bit)."""
+    yield
+    if request.node.get_closest_marker("gpu") is None:
+        return
+    from ternixengine_amd import _lib
+    bits = ctypes.c_uint(0)
+    st = _lib.load().ternix_hip_take_faults(ctypes.byref(bits))
+    assert st == 0, f"ternix_hip_take_faults failed: {st}"
+    assert bits.value == 0, f"device fault word 0x{bits.value:x} after {request.node.nodeid}"
+
+
 def _oracle_lib():
     so = os.path.join(ROOT, "oracle", "liboracle.so")
     if not os.path.exists(so):
