@@ -1772,8 +1772,11 @@ hipError_t take_faults(unsigned* bits) {
     if (v != 0) {
         const unsigned zero = 0;
         e = hipMemcpyToSymbol(HIP_SYMBOL(g_tx_fault_word), &zero, sizeof(zero), 0, hipMemcpyHostToDevice);
+        if (e != hipSuccess) return e;
     }
-    *bits = v;
+    unsigned w = 0;
+    e = take_line_faults(&w);
+    *bits = v | w;
     return e;
 }
 

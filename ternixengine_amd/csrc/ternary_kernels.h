@@ -47,6 +47,7 @@ enum DebugKey : int {
     DBG_SELF_ZERO,       // [0] 0: no in-launch zeroing of C for M = 1 (fill launch or reduce launch instead)
     DBG_NT,              // [0] DMA-staged GEMV, [1] wave-pipelined GEMV: 1 non-temporal weight loads, 0 plain
     DBG_WAVE_TICKET,     // [0] 1 / 0: wave-pipelined GEMV waits for its split ticket in the first step / before it
+    DBG_LINE,            // [0] 0: no whole-line GEMV; > 0: its k-steps per workgroup forced; [1] its data waves (4 / 8)
     DBG_COUNT
 };
 int debug_get(DebugKey key, int idx = 0);
@@ -56,6 +57,14 @@ hipError_t launch_zero(int32_t* C, size_t n, hipStream_t st);
 constexpr unsigned kFaultZeroWait = 1u;  // a bounded wait for a strip's zeroed word gave up
 // Synchronises the current device, returns the fault word's bits in *bits and clears them.
 hipError_t take_faults(unsigned* bits);
+// Whole-line decode GEMV (line_gemv.hip): M <= 4, K % 64 == 0, N/4 % 16 == 0, 16-byte aligned A and W;
+// S k-steps per workgroup, NW data waves (4 or 8); K splits added with int32 atomics into C zeroed by
+// each strip's split 0 (tickets: two 64-bit words per 128-byte strip, persistent).
+bool line_gemv_ok(const int8_t* A, const uint8_t* B, int M, int K, int N);
+int line_gemv_splits(int K, int S);
+hipError_t launch_line_gemv(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int S, int NW,
+                            unsigned long long* tk, int tk_stride, hipStream_t st);
+hipError_t take_line_faults(unsigned* bits);
 // Bare streaming read of `bytes` (rounded down to 16) at p (16-byte aligned): the HBM floor reference.
 hipError_t launch_stream_read(const void* p, size_t bytes, int* out, hipStream_t st);
 // LDS bytes the skinny fast kernel uses for one workgroup's activation slice (the rows of one

@@ -474,6 +474,45 @@ bool run_atomic_wave(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, in
     return true;
 }
 
+// The whole-line GEMV (line_gemv.hip): true when it takes the call (*e then holds the launch status).
+// M <= 4, int32 output into a 16-byte aligned C, the library's tickets (one pair per 128-byte strip, one
+// 256-byte line apart so that the strips' ticket atomics do not queue on one line: measured on MI355X,
+// cfg2 up 8.2 -> 5.1 us with two k-steps per workgroup).  Plan: the fewest k-steps per workgroup
+// (2, 3, 4, 6 or 8) whose grid stays within about one workgroup per CU (<= 250 workgroups) with at most
+// 64 splits per strip; none for wide matrices that would need more (the DMA-staged and wave kernels
+// keep those).  The DBG_LINE switch turns it off (0) or forces the k-steps [0] and data waves [1].
+bool run_line_gemv(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int K, int N, Ctx& c, hipError_t* e) {
+    const int fs = ternix_hip::debug_get(ternix_hip::DBG_LINE, 0), fw = ternix_hip::debug_get(ternix_hip::DBG_LINE, 1);
+    if (fs == 0) return false;
+    if (!(dC != nullptr && reinterpret_cast<uintptr_t>(dC) % 16 == 0 && ternix_hip::line_gemv_ok(dA, dB, M, K, N)))
+        return false;
+    const int strips = (N / 4 + 127) / 128;
+    int S = 0;
+    if (fs > 0) {
+        S = fs;
+    } else {
+        const long cap = std::max(1L, (long)cu_count() * 250 / 256);
+        for (int cand : {2, 3, 4, 6, 8}) {
+            const long sp = ternix_hip::line_gemv_splits(K, cand);
+            if (sp <= 64 && (long)strips * sp <= cap) {
+                S = cand;
+                break;
+            }
+        }
+        if (S == 0) return false;
+    }
+    const int NW = fw == 4 ? 4 : 8;
+    const int splits = ternix_hip::line_gemv_splits(K, S);
+    if (splits > 64) return false;
+    const int stride = strips * 32 <= (int)kTicketStrips * 2 ? 32 : 2;  // one 256-byte line per strip when they fit
+    unsigned long long* tk = c.tickets((size_t)strips * (size_t)stride / 2);
+    if (!tk) return false;
+    c.note("line_gemv_kernel S=%d waves=%d+1 splits=%d (splits added with int32 atomics into C zeroed by each "
+           "strip's split 0)", S, NW, splits);
+    *e = TX_LAUNCH(c, ternix_hip::launch_line_gemv(dA, dB, dC, M, K, N, S, NW, tk, stride, c.st));
+    return true;
+}
+
 hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int K, int N, Ctx& c,
                       const ternix_hip::OutScale& os = ternix_hip::OutScale{},
                       const ternix_hip::ActQuant& aq = ternix_hip::ActQuant{}) {
@@ -516,6 +555,7 @@ hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
     // [1] lowers the row limit (tests and measurements).
     {
         hipError_t e = hipSuccess;
+        if (!generic && aq.mode == 0 && os.Y == nullptr && run_line_gemv(dA, dB, dC, M, K, N, c, &e)) return e;
         if (!generic && aq.mode == 0 && os.Y == nullptr && run_atomic_wave(dA, dB, dC, M, K, N, c, &e)) return e;
     }
     // Wave-pipelined kernel (32-byte strips, 16-byte with fused quantisation; 2 ring slots per wave),
@@ -1300,6 +1340,7 @@ int ternix_hip_debug_set(const char* key, int v0, int v1, int v2, int v3) {
         {"deep", ternix_hip::DBG_DEEP},             {"sk_order", ternix_hip::DBG_SK_ORDER},
         {"m1_atomic", ternix_hip::DBG_M1_ATOMIC},     {"self_zero", ternix_hip::DBG_SELF_ZERO},
         {"gemm_gm", ternix_hip::DBG_GEMM_GM},         {"nt", ternix_hip::DBG_NT}, {"wave_ticket", ternix_hip::DBG_WAVE_TICKET},
+        {"line", ternix_hip::DBG_LINE},
     };
     if (key == nullptr) return (int)hipErrorInvalidValue;
     for (const auto& n : names) {

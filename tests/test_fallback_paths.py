@@ -1,6 +1,7 @@
 """The kernels the automatic dispatch only falls back to (register-staged skinny kernels, generic
 kernels for ragged shapes, 256-column GEMM tiles for small M, the reduce launch instead of in-launch
-split sums, the generic GEMM) stay bit-exact.  Each switch set is applied in-process through the
+split sums, the generic GEMM, the self-zeroing wave kernel that the whole-line GEMV replaces for most
+M <= 4 shapes) stay bit-exact.  Each switch set is applied in-process through the
 library's explicit test hook, ternix_hip_debug_set (the library never reads the environment)."""
 import numpy as np
 import pytest
@@ -34,6 +35,8 @@ SWITCHES = [
     {"wave_ticket": 0},                                    # ... and right after the prologue everywhere
     {"wave_sw": (-1, -1, 0)},                              # no column waves in the M <= 4 atomic plan
     {"wave_sw": (-1, -1, 1)},                              # column waves wherever the plan allows them
+    {"line": (2, 4)},                                      # whole-line GEMV, 2 k-steps, 4 data waves, M <= 4
+    {"line": (4, 8)},                                      # whole-line GEMV, 4 k-steps, 8 data waves
 ]
 
 
@@ -41,6 +44,8 @@ SWITCHES = [
 def switches(request):
     lib = tx._load()
     lib.ternix_hip_debug_reset()
+    if "line" not in request.param:  # the switched kernels, not the whole-line GEMV that precedes them
+        assert lib.ternix_hip_debug_set(b"line", 0, -1, -1, -1) == 0
     for k, v in request.param.items():
         v = tuple(v) if isinstance(v, tuple) else (v,)
         v = v + (-1,) * (4 - len(v))

@@ -1,0 +1,130 @@
+"""The whole-line decode GEMV (line_gemv.hip): 128-byte weight strips over a few k-steps per
+workgroup, all staged at once, K splits added with int32 atomics into C that each strip's split 0
+zeroes inside the launch.  Bit-exact against the CPU oracle (the reference's scalar decode, code 10
+included) for every k-step count and wave form, 1 to 4 rows, a partial last strip, a partial last
+split, calls that share the strips' tickets with the other self-zeroing GEMV issued back to back,
+and graph replays with eager calls between."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import ternixengine_amd as tx
+from ternixengine_amd import hip_runtime as hr
+
+GARBAGE = -123456789
+# (M, K, N): whole strips, a partial last strip (N/4 = 1728 = 13.5 x 128), one k-step, ragged split counts
+SHAPES = [(1, 2560, 2560), (1, 2560, 6912), (1, 6912, 2560), (2, 4096, 4096), (3, 192, 1024), (4, 4160, 1536),
+          (1, 64, 512), (4, 11008, 4096)]
+FORMS = [(1, 8), (2, 8), (3, 8), (4, 8), (6, 8), (8, 8), (2, 4), (4, 4)]
+
+
+def log(msg):
+    print(msg, flush=True)
+
+
+def _plan(lib, m, k, n):
+    buf = ctypes.create_string_buffer(192)
+    assert lib.ternix_hip_plan_describe(1 << 20, 1 << 24, m, k, n, buf, len(buf)) == 0
+    return buf.value.decode()
+
+
+def test_plan_names_line_kernel_when_forced():
+    lib = tx._load()
+    try:
+        assert lib.ternix_hip_debug_set(b"line", 2, 8, -1, -1) == 0
+        assert _plan(lib, 1, 2560, 6912).startswith("line_gemv_kernel S=2 waves=8+1 splits=20")
+        assert not _plan(lib, 5, 2560, 6912).startswith("line_gemv_kernel")  # M <= 4 only
+        assert not _plan(lib, 1, 2560, 6900).startswith("line_gemv_kernel")  # N/4 % 16 != 0
+        assert lib.ternix_hip_debug_set(b"line", 1, 8, -1, -1) == 0
+        assert not _plan(lib, 1, 8192, 4096).startswith("line_gemv_kernel")  # 128 splits > 64
+    finally:
+        lib.ternix_hip_debug_reset()
+
+
+def _problem(oracle, rng, m, k, n):
+    a = rng.integers(-128, 128, size=(m, k), dtype=np.int8)
+    wp = rng.integers(0, 256, size=(k, n // 4), dtype=np.uint8)
+    return (m, k, n, hr.DeviceBuffer.from_array(a), hr.DeviceBuffer.from_array(wp), hr.DeviceBuffer(4 * m * n),
+            oracle.mm("scalar_mt", a, wp, n))
+
+
+def _run(p, stream=None):
+    m, k, n, da, db, dc, _ = p
+    kw = {} if stream is None else {"stream": stream.handle}
+    assert tx.mul_mat_ternary(da.value, db.value, dc.value, m, k, n, **kw) == 0
+
+
+def _check(p, tag):
+    m, k, n, _, _, dc, expect = p
+    got = dc.download(np.int32, (m, n))
+    assert (got == expect).all(), (tag, m, k, n, int((got != expect).sum()))
+
+
+def _reset(p):
+    m, _, n, _, _, dc, _ = p
+    dc.upload(np.full(m * n, GARBAGE, np.int32))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("form", FORMS, ids=[f"S{s}_W{w}" for s, w in FORMS])
+def test_line_gemv_matches_oracle(oracle, form):
+    lib = tx._load()
+    rng = np.random.default_rng(7 + form[0] * 10 + form[1])
+    probs = [_problem(oracle, rng, *sh) for sh in SHAPES]
+    try:
+        assert lib.ternix_hip_debug_set(b"line", form[0], form[1], -1, -1) == 0
+        for p in probs:
+            if (p[1] // 64 + form[0] - 1) // form[0] > 64:
+                continue  # more than 64 splits: another plan
+            log(f"[line] S={form[0]} W={form[1]} M={p[0]} K={p[1]} N={p[2]}")
+            _reset(p)
+            _run(p)
+            hr.synchronize()
+            _check(p, "first")
+            _run(p)  # second call on the same tickets and outputs
+            hr.synchronize()
+            _check(p, "second")
+    finally:
+        lib.ternix_hip_debug_reset()
+
+
+@pytest.mark.gpu
+def test_line_gemv_interleaved_with_wave_kernel_and_graph(oracle):
+    """Line-kernel calls and the wave kernel's self-zeroing calls share ticket words on one stream."""
+    lib = tx._load()
+    rng = np.random.default_rng(99)
+    probs = [_problem(oracle, rng, *sh) for sh in [(1, 2560, 6912), (1, 6912, 2560), (4, 4096, 4096)]]
+    s = hr.Stream()
+
+    def issue_all():
+        for i, p in enumerate(probs):
+            lib.ternix_hip_debug_set(b"line", 2 if i != 1 else 4, 8, -1, -1)
+            _run(p, s)
+            lib.ternix_hip_debug_reset()  # the wave kernel's plan for the same shape and strips
+            _run(p, s)
+
+    try:
+        log("[line] 200 interleaved rounds without synchronisation")
+        for p in probs:
+            _reset(p)
+        for _ in range(200):
+            issue_all()
+        s.synchronize()
+        for p in probs:
+            _check(p, "interleaved")
+        log("[line] graph replays with eager calls between")
+        g = hr.Graph(s, lambda: [issue_all() for _ in range(2)])
+        for rep in range(4):
+            for p in probs:
+                _reset(p)
+            g.launch()
+            s.synchronize()
+            for p in probs:
+                _check(p, f"replay {rep}")
+            issue_all()
+            s.synchronize()
+            for p in probs:
+                _check(p, f"eager after replay {rep}")
+    finally:
+        lib.ternix_hip_debug_reset()

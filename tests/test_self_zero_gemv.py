@@ -16,6 +16,21 @@ GARBAGE = -123456789
 SHAPES = [(2560, 2560), (2560, 6912), (6912, 2560), (4096, 4096), (1024, 2048)]
 
 
+def _debug_reset(lib):
+    """Every switch off, and the whole-line GEMV (which takes most M <= 4 shapes first) off too: these
+    tests cover the wave-pipelined and DMA-staged kernels' self-zeroing plans."""
+    lib.ternix_hip_debug_reset()
+    assert lib.ternix_hip_debug_set(b"line", 0, -1, -1, -1) == 0
+
+
+@pytest.fixture(autouse=True)
+def _no_line_kernel():
+    lib = tx._load()
+    _debug_reset(lib)
+    yield
+    lib.ternix_hip_debug_reset()
+
+
 def log(msg):
     print(msg, flush=True)
 
@@ -28,14 +43,14 @@ def _plan(lib, k, n):
 
 def test_plan_names_self_zeroing():
     lib = tx._load()
-    lib.ternix_hip_debug_reset()
+    _debug_reset(lib)
     for k, n in SHAPES[:3]:
         assert "zeroed by each strip's first split" in _plan(lib, k, n), (k, n)
     assert lib.ternix_hip_debug_set(b"self_zero", 0, -1, -1, -1) == 0
     try:
         assert _plan(lib, 2560, 6912).startswith("zero_kernel + ")
     finally:
-        lib.ternix_hip_debug_reset()
+        _debug_reset(lib)
 
 
 # tile-64 weights: K > 4096 takes the split wave kernel (the shorter K the whole-K kernel)
@@ -120,7 +135,7 @@ def test_self_zero_few_rows(oracle, m):
     """2..4 rows take the same plans (wave kernel with 32-byte strips, DMA kernel on wide matrices):
     interleaved calls of three shapes, every row bit-exact."""
     lib = tx._load()
-    lib.ternix_hip_debug_reset()
+    _debug_reset(lib)
     s = hr.Stream()
     rng = np.random.default_rng(50 + m)
     probs = []
@@ -149,7 +164,7 @@ def test_self_zero_up_to_16_rows(oracle, m):
     three shapes on one stream, then the same calls with the plan limited to 4 rows (in-launch sums
     and the reduce launch) on the same output buffers, every row bit-exact."""
     lib = tx._load()
-    lib.ternix_hip_debug_reset()
+    _debug_reset(lib)
     s = hr.Stream()
     rng = np.random.default_rng(60 + m)
     probs = []
@@ -173,7 +188,7 @@ def test_self_zero_up_to_16_rows(oracle, m):
             for mm, k, n, _, _, dc, expect in probs:
                 assert (dc.download(np.int32, (mm, n)) == expect).all(), (mm, k, n, limit)
     finally:
-        lib.ternix_hip_debug_reset()
+        _debug_reset(lib)
 
 
 @pytest.mark.gpu
@@ -183,7 +198,7 @@ def test_self_zero_several_m_groups(oracle, m):
     pair per (m-group, strip): interleaved calls of two shapes with several m-groups, bit-exact, then
     the same calls with the plan limited to 16 rows on the same output buffers."""
     lib = tx._load()
-    lib.ternix_hip_debug_reset()
+    _debug_reset(lib)
     s = hr.Stream()
     rng = np.random.default_rng(80 + m)
     probs = []
@@ -207,7 +222,7 @@ def test_self_zero_several_m_groups(oracle, m):
             for mm, k, n, _, _, dc, expect in probs:
                 assert (dc.download(np.int32, (mm, n)) == expect).all(), (mm, k, n, limit)
     finally:
-        lib.ternix_hip_debug_reset()
+        _debug_reset(lib)
 
 
 @pytest.mark.gpu
@@ -216,7 +231,7 @@ def test_self_zero_tile64_rows(oracle, m):
     """Tile-64 weights with K > 4096 take the atomic plan for up to 16 rows too: interleaved calls of
     two shapes, bit-exact, then the reduce plan (row limit 1) on the same buffers."""
     lib = tx._load()
-    lib.ternix_hip_debug_reset()
+    _debug_reset(lib)
     s = hr.Stream()
     rng = np.random.default_rng(70 + m)
     probs = []
@@ -239,7 +254,7 @@ def test_self_zero_tile64_rows(oracle, m):
             for mm, k, n, _, _, dc, expect in probs:
                 assert (dc.download(np.int32, (mm, n)) == expect).all(), (mm, k, n, limit)
     finally:
-        lib.ternix_hip_debug_reset()
+        _debug_reset(lib)
 
 
 def _plan_m(lib, m, k, n):
@@ -253,7 +268,7 @@ def test_self_zero_dma_kernel(oracle):
     """The DMA-staged kernel's form of the same plan (wide M = 1 GEMVs): repeated calls of two
     shapes sharing the strips' tickets, then the reduce plan (self_zero off) on the same buffers."""
     lib = tx._load()
-    lib.ternix_hip_debug_reset()
+    _debug_reset(lib)
     assert lib.ternix_hip_debug_set(b"self_zero", 2, -1, -1, -1) == 0
     try:
         s = hr.Stream()
@@ -278,7 +293,7 @@ def test_self_zero_dma_kernel(oracle):
         s.synchronize()
         _check(probs, "reduce plan after")
     finally:
-        lib.ternix_hip_debug_reset()
+        _debug_reset(lib)
 
 
 @pytest.mark.gpu
@@ -288,7 +303,7 @@ def test_self_zero_padded_real_columns(oracle, m, k, n):
     pitch N: a guard region after C keeps its values, and C is bit-exact over repeated calls, two
     of them back to back without synchronisation."""
     lib = tx._load()
-    lib.ternix_hip_debug_reset()
+    _debug_reset(lib)
     plan = _plan_m(lib, m, k, n)
     assert plan.startswith("pad_rows_kernel + skinny_wave_kernel") and "zeroed by each strip's first split" in plan, plan
     rng = np.random.default_rng(1000 + m)
@@ -314,7 +329,7 @@ def test_self_zero_short_k_ranges(oracle, m, k, n):
     """Splits of one to three k-steps, so some of a workgroup's four waves own no step at all (each
     wave issues only its own steps): bit-exact over repeated calls."""
     lib = tx._load()
-    lib.ternix_hip_debug_reset()
+    _debug_reset(lib)
     plan = _plan_m(lib, m, k, n)
     rng = np.random.default_rng(2000 + k + m)
     a = rng.integers(-128, 128, size=(m, k), dtype=np.int8)
@@ -334,7 +349,7 @@ def test_plan_column_waves():
     splits (cfg3 M=4, cfg2 up), not for cfg2 down (5 strips), cfg1 (16-byte strips) or M = 16, and
     the switch forces them off."""
     lib = tx._load()
-    lib.ternix_hip_debug_reset()
+    _debug_reset(lib)
     for m, k, n in [(4, 4096, 11008), (4, 11008, 4096), (1, 2560, 6912)]:
         assert "column waves" in _plan_m(lib, m, k, n), (m, k, n)
     for m, k, n in [(1, 6912, 2560), (1, 2560, 2560), (16, 4096, 11008)]:
@@ -343,4 +358,4 @@ def test_plan_column_waves():
     try:
         assert "column waves" not in _plan_m(lib, 4, 4096, 11008)
     finally:
-        lib.ternix_hip_debug_reset()
+        _debug_reset(lib)

@@ -47,7 +47,7 @@ def test_workspace_size_and_plan_host():
     for s in BRANCH_SHAPES[:-1]:
         st, d = describe(lib, *s)
         assert st == 0 and d and d not in ("none", "rejected"), (s, d)
-    assert "skinny_wave_kernel" in describe(lib, 1, 2560, 6912)[1]
+    assert describe(lib, 1, 2560, 6912)[1].startswith("line_gemv_kernel")
     assert "pad_rows_kernel" in describe(lib, 1, 2560, 6912, (1 << 20) + 1)[1]  # misaligned A: padded
     assert describe(lib, 1, 64, 6)[0] == 1
     buf = ctypes.create_string_buffer(8)
