@@ -113,6 +113,7 @@ struct SkinnyArgs {
     int* cnt;             // SK_LAST: arrival counters, one per (m-group, strip), zero between calls
     int order;            // SK_LAST: 1 = C++ release/acquire at agent scope, 0 = coherent accesses only
     unsigned long long* tick;  // SK_ATOMZ: per strip {ticket counter, zeroed word}, persistent
+    int tk_stride;             // SK_ATOMZ: 64-bit words between consecutive strips' pairs (ticket_stride)
     int nt;               // DMA-staged / wave-pipelined kernels: non-temporal weight loads
     int defer_ticket;     // skinny_wave_kernel, SK_ATOMZ: wave 0 waits for its ticket with its first step
 };
@@ -699,7 +700,7 @@ void skinny_dma_kernel(SkinnyArgs args) {
     // SK_ATOMZ (as in skinny_wave_kernel): wave 0 takes the strip's ticket before any DMA; the
     // first loop wait of wave 0 (for a step issued after it) covers its return.
     const bool ticket = args.mode == SK_ATOMZ && wave == 0;
-    unsigned long long* tk = args.tick + 2 * (size_t)cx;
+    unsigned long long* tk = args.tick + (size_t)args.tk_stride * (size_t)cx;
     unsigned long long old = 0, call1 = 0, zw = 0;
     bool zeroer = false;
     if (ticket && lane == 0)
@@ -1100,8 +1101,8 @@ void skinny_wave_kernel(SkinnyArgs args) {
     // Atomic modes: C has CN columns at pitch CN (a padded problem's real columns when n_out > 0)
     const int CN = args.n_out > 0 ? args.n_out : args.N;
     // one ticket pair per (m-group, strip)
-    unsigned long long* tk = CW ? args.tick + 2 * ((size_t)blockIdx.z * (size_t)n_cw + (size_t)c4)
-                                : args.tick + 2 * ((size_t)blockIdx.z * (size_t)n_strips + (size_t)cx);
+    unsigned long long* tk = CW ? args.tick + (size_t)args.tk_stride * ((size_t)blockIdx.z * (size_t)n_cw + (size_t)c4)
+                                : args.tick + (size_t)args.tk_stride * ((size_t)blockIdx.z * (size_t)n_strips + (size_t)cx);
     unsigned long long old = 0;
     const bool ticket = AQ == 0 && args.mode == SK_ATOMZ && wave == 0;
     if (ticket && lane == 0)
@@ -1631,6 +1632,7 @@ hipError_t launch_skinny(const int8_t* A, const uint8_t* B, int32_t* C, int M, i
         return hipErrorInvalidValue;
     if (dma_ns != 0) {
         const dim3 grid((NB + SD_BNB - 1) / SD_BNB, splits, mgroups);
+        a.tk_stride = ticket_stride(grid.x);
         a.X = aq.X;
         a.G = aq.G;
         a.eps = aq.eps;
@@ -1730,6 +1732,7 @@ hipError_t launch_skinny_wave(const int8_t* A, const uint8_t* B, int32_t* C, int
     const unsigned gx = a.line_units ? (unsigned)(8 * spl * ((units + 7) / 8)) : (unsigned)((NB / sw) * splits);
     const dim3 grid(gx, 1, (M + 15) / 16), block(256);
     const bool low = M <= 4;
+    a.tk_stride = ticket_stride(column_waves ? (size_t)((NB + 127) / 128) : (size_t)(NB / sw) * (size_t)((M + 15) / 16));
     if (column_waves) {  // 128-byte strips, wave w on 32-byte part w (skinny_wave_kernel's CW form)
         if (!(mode == SK_ATOMZ && low && sw == 32 && nsw == 2 && aq.mode == 0 && !tiled)) return hipErrorInvalidValue;
         a.line_units = 0;

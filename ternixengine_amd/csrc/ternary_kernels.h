@@ -53,6 +53,13 @@ enum DebugKey : int {
 int debug_get(DebugKey key, int idx = 0);
 
 hipError_t launch_zero(int32_t* C, size_t n, hipStream_t st);
+// Ticket words of the self-zeroing GEMVs: a strip's {T, Z} pair sits tk_stride 64-bit words after the
+// previous strip's, one 256-byte line apart when there are at most kTicketSpreadMax strips, so that
+// different strips' ticket atomics never queue on one line (measured on MI355X, whole-line GEMV, cfg2
+// up: 8.2 -> 5.1 us).  ticket_units: 16-byte units of the library's ticket region the strips need.
+constexpr size_t kTicketSpreadMax = 1024;
+inline int ticket_stride(size_t strips) { return strips <= kTicketSpreadMax ? 32 : 2; }
+inline size_t ticket_units(size_t strips) { return strips * (size_t)ticket_stride(strips) / 2; }
 // Bits of the device fault word (skinny_kernels.hip); the same values as TERNIX_FAULT_* in ternix_hip.h.
 constexpr unsigned kFaultZeroWait = 1u;  // a bounded wait for a strip's zeroed word gave up
 // Synchronises the current device, returns the fault word's bits in *bits and clears them.

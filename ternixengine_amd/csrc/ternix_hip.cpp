@@ -454,14 +454,14 @@ bool run_atomic_wave(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, in
         splits = (nsteps + sps - 1) / sps;
     }
     unsigned long long* tk = ternix_hip::debug_get(ternix_hip::DBG_SELF_ZERO) != 0 && splits <= 64
-                                 ? c.tickets(cw ? (size_t)((NB + 127) / 128) : (size_t)(NB / sw) * (size_t)mgroups)
+                                 ? c.tickets(ternix_hip::ticket_units(cw ? (size_t)((NB + 127) / 128) : (size_t)(NB / sw) * (size_t)mgroups))
                                  : nullptr;
     if (cw && !tk) {  // column waves need the tickets: the plan without them (zero fill at M = 1)
         cw = 0;
         sps = sps0;
         splits = splits0;
         if (ternix_hip::debug_get(ternix_hip::DBG_SELF_ZERO) != 0 && splits <= 64)
-            tk = c.tickets((size_t)(NB / sw) * (size_t)mgroups);
+            tk = c.tickets(ternix_hip::ticket_units((size_t)(NB / sw) * (size_t)mgroups));
     }
     if (tk)
         c.note("%sskinny_wave_kernel sw=%d nsw=2 splits=%d%s (splits added with int32 atomics into C zeroed "
@@ -475,9 +475,8 @@ bool run_atomic_wave(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, in
 }
 
 // The whole-line GEMV (line_gemv.hip): true when it takes the call (*e then holds the launch status).
-// M <= 4, int32 output into a 16-byte aligned C, the library's tickets (one pair per 128-byte strip, one
-// 256-byte line apart so that the strips' ticket atomics do not queue on one line: measured on MI355X,
-// cfg2 up 8.2 -> 5.1 us with two k-steps per workgroup).  Plan: the fewest k-steps per workgroup
+// M <= 4, int32 output into a 16-byte aligned C, the library's tickets (one pair per 128-byte strip,
+// spread as ticket_stride says).  Plan: the fewest k-steps per workgroup
 // (2, 3, 4, 6 or 8) whose grid stays within about one workgroup per CU (<= 250 workgroups) with at most
 // 64 splits per strip; none for wide matrices that would need more (the DMA-staged and wave kernels
 // keep those).  The DBG_LINE switch turns it off (0) or forces the k-steps [0] and data waves [1].
@@ -504,8 +503,8 @@ bool run_line_gemv(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int 
     const int NW = fw == 4 ? 4 : 8;
     const int splits = ternix_hip::line_gemv_splits(K, S);
     if (splits > 64) return false;
-    const int stride = strips * 32 <= (int)kTicketStrips * 2 ? 32 : 2;  // one 256-byte line per strip when they fit
-    unsigned long long* tk = c.tickets((size_t)strips * (size_t)stride / 2);
+    const int stride = ternix_hip::ticket_stride((size_t)strips);
+    unsigned long long* tk = c.tickets(ternix_hip::ticket_units((size_t)strips));
     if (!tk) return false;
     c.note("line_gemv_kernel S=%d waves=%d+1 splits=%d (splits added with int32 atomics into C zeroed by each "
            "strip's split 0)", S, NW, splits);
@@ -643,7 +642,7 @@ hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
     // the reduce launch: the decode FFN block's down GEMV, 21.33 -> 20.96 us per block (bit-equal).
     if (p.dma && M <= 4 && p.splits > 1 && p.splits <= 64 && dC != nullptr &&
         ternix_hip::debug_get(ternix_hip::DBG_SELF_ZERO) != 0) {
-        if (unsigned long long* tk = c.tickets((size_t)((N / 4 + 255) / 256))) {
+        if (unsigned long long* tk = c.tickets(ternix_hip::ticket_units((size_t)((N / 4 + 255) / 256)))) {
             c.note("skinny_dma_kernel splits=%d (splits added with int32 atomics into C zeroed by each strip's first "
                    "split)%s", p.splits, os.Y ? " + dequant_kernel" : "");
             return TX_LAUNCH(c, ternix_hip::launch_skinny(dA, dB, dC, M, K, N, p.tb, p.kw, p.splits, p.sps, nullptr, st,
@@ -860,7 +859,7 @@ hipError_t run_tile64(const int8_t* dA, const uint8_t* dWt, int32_t* dC, int M, 
         // launch: cfg3 M=4 down 9.46 -> 6.72 us, M=16 down 10.70 -> 7.57 us.  The DBG_M1_ATOMIC switch
         // [2] lowers the row limit.
         if (t64_atomic && splits > 1 && splits <= 64) {
-            if (unsigned long long* tk = c.tickets((size_t)(N / 4 / 16))) {
+            if (unsigned long long* tk = c.tickets(ternix_hip::ticket_units((size_t)(N / 4 / 16)))) {
                 c.note("skinny_wave_kernel (tile-64) sw=16 nsw=2 splits=%d (splits added with int32 atomics into C "
                        "zeroed by each strip's first split)", splits);
                 return TX_LAUNCH(c, ternix_hip::launch_skinny_wave(dA, dWt, dC, M, K, N, 16, 2, splits, sps, nullptr, st,
