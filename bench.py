@@ -10,7 +10,9 @@ the kernels run on, bracketing exactly `--steps` steps after `--warmup` untimed 
 Also reported on the same line: the prefill GEMM of configuration 4 (M=2048; ops = 2*M*N*K, against
 the int8 dense MFMA peak; `roofline_gemm`), the large-M=1 GEMV of configuration 5 (K=8192, N=28672),
 the device weight packer, the quantised layer boundary (activation quantisation, dequantising
-matmuls), the decode feed-forward block, and the reference's own CPU kernel
+matmuls), the decode feed-forward block, every configuration with its roofline bound and fraction
+(`all_configs`), the reference's own GPU benchmark shapes n^3 timed with its method beside its
+published figures (`reference_benchmark_shapes`), and the reference's own CPU kernel
 (mul_mat_ternary_avx2_blocked, compiled from the reference sources into oracle/_ref, or the plain-C
 restatement in oracle/ when that is absent) timed on this host on a bounded sample of the same
 workload.  Every GPU measurement is preceded by about --prewarm-s seconds of untimed load (clock ramp).
@@ -44,7 +46,8 @@ def parse():
                     help="untimed sustained load before each GPU measurement (clock ramp)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["all", "gemv", "gemm", "bigm1", "pack", "layer", "ffn", "configs", "tile64"],
+    ap.add_argument("--only", choices=["all", "gemv", "gemm", "bigm1", "pack", "layer", "ffn", "configs", "tile64",
+                                       "refshapes"],
                     default="all")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run 4 device-to-device copies of 256 MiB (the runtime's copy kernel), the "
@@ -466,10 +469,79 @@ def cpu_config(case, a, wp, budget_s=0.3, threads=None):
     for th in ths:
         th.join()
     tall = (time.perf_counter() - t0) / reps * case.M / m_s
-    return {"kernel": kname, "kind": kind, "us_1t": round(t1 * 1e6, 1), "us_all": round(tall * 1e6, 1),
-            "cores": len(jobs), "sample_rows": m_s,
+    # Rates are measured on the sample; whole-matrix times are measured when the sample is every row,
+    # else scaled from the sample (rows all cost the same) and named *_extrapolated.
+    sfx = "" if m_s == case.M else "_extrapolated"
+    return {"kernel": kname, "kind": kind, "rows_timed": m_s, "rows": case.M,
+            "us_1t" + sfx: round(t1 * 1e6, 1), "us_all" + sfx: round(tall * 1e6, 1), "cores": len(jobs),
             "gbs_1t": round(case.bytes_algorithmic / t1 / 1e9, 3), "gops_1t": round(case.ops / t1 / 1e9, 2),
-            "gops_all": round(case.ops / tall / 1e9, 2)}
+            "gops_all": round(case.ops / tall / 1e9, 2), "us_1t_total": t1 * 1e6}
+
+
+RIDGE_OPS_PER_BYTE = INT8_PEAK_TOPS * 1e12 / (HBM_PEAK_GBS * 1e9)  # 625: int8 peak / HBM peak
+
+
+def roofline_fields(case, us):
+    """The bound of one configuration (HBM when its arithmetic intensity, 2*M*N*K ops over the
+    algorithmic bytes, is below the ridge of int8 peak over HBM peak, else MFMA) and the fraction of
+    that peak the call reaches."""
+    ai = case.ops / case.bytes_algorithmic
+    if ai < RIDGE_OPS_PER_BYTE:
+        gbs = case.bytes_algorithmic / (us * 1e-6) / 1e9
+        return {"bound": "hbm", "ops_per_byte": round(ai, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    tops = case.ops / (us * 1e-6) / 1e12
+    return {"bound": "mfma", "ops_per_byte": round(ai, 1), "frac": round(tops / INT8_PEAK_TOPS, 4)}
+
+
+# The reference's published GPU figures for its own benchmark (README.md:178-181, RTX 5060 Laptop GPU):
+# tiled (cp.async) kernel median ms per launch at n^3.
+REFERENCE_TILED_MS = {512: 0.066, 1024: 0.341, 2048: 2.657, 4096: 21.28}
+
+
+def median_launch_ms(launch, warmup, iters, stream):
+    """The reference benchmark's method (benchmarks/bench_cuda.cu:16-34): `warmup` launches, then
+    `iters` launches each bracketed by its own pair of events and synchronised; the median."""
+    from ternixengine_amd import hip_runtime as hr
+    for _ in range(warmup):
+        launch()
+    stream.synchronize()
+    ts = []
+    for _ in range(iters):
+        e0, e1 = hr.Event(), hr.Event()
+        e0.record(stream)
+        launch()
+        e1.record(stream)
+        e1.synchronize()
+        ts.append(e0.elapsed_ms(e1))
+    return statistics.median(ts)
+
+
+def bench_reference_shapes(args, stream, lib):
+    """The reference's own GPU benchmark, n^3 for n in {512, 1024, 2048, 4096} (bench_cuda.cu:45-79),
+    with its method: data resident, per-launch median of 11 naive / 31 tiled launches after 3 / 5
+    warm-up launches, effective TOPS = 2 n^3 / time.  Run through the drop-in replacements of its two
+    entry points (ternix_hip_mul_mat_ternary_naive / _tiled) and the automatic path, each output
+    checked against the reference digest; beside them the reference's published tiled time."""
+    from ternixengine_amd import configs
+    out = []
+    for n in (512, 1024, 2048, 4096):
+        case = configs.CASES[f"refbench_n{n}"]
+        p = Problem(case, 1)
+        row = {"n": n, "published_tiled_ms": REFERENCE_TILED_MS[n]}
+        for key, fname, warm, iters in (("naive", "ternix_hip_mul_mat_ternary_naive", 3, 11),
+                                        ("tiled", "ternix_hip_mul_mat_ternary_tiled", 5, 31),
+                                        ("auto", "ternix_hip_mul_mat_ternary", 5, 31)):
+            fn = getattr(lib, fname)
+            p.dC.upload(np.full(case.M * case.N, -7, np.int32))
+            ms = median_launch_ms(lambda: launch(fn, p, 0, stream), warm, iters, stream)
+            row[f"{key}_ms"] = round(ms, 4)
+            row[f"{key}_tops"] = round(case.ops / (ms * 1e-3) / 1e12, 1)
+            row[f"{key}_verified"] = verify(p)
+        row["tiled_frac_int8_peak"] = round(row["tiled_tops"] / INT8_PEAK_TOPS, 4)
+        row["speedup_vs_published_tiled"] = round(REFERENCE_TILED_MS[n] / row["tiled_ms"], 1)
+        out.append(row)
+        del p
+    return out
 
 
 def bench_configs(args, stream, lib):
@@ -482,6 +554,8 @@ def bench_configs(args, stream, lib):
     fn = lib.ternix_hip_mul_mat_ternary
     out = []
     for name, case in configs.CASES.items():
+        if case.config == 0:  # the reference's own benchmark shapes: bench_reference_shapes
+            continue
         w = case.K * case.N // 4
         copies = min(64, max(2, -(-POOL_MIN_BYTES // w)))
         p = Problem(case, copies)
@@ -492,9 +566,14 @@ def bench_configs(args, stream, lib):
         entry = {"name": name, "shape": [case.M, case.K, case.N], "us": round(us, 2),
                  "gbs": round(case.bytes_algorithmic / (us * 1e-6) / 1e9, 1),
                  "tops": round(case.ops / (us * 1e-6) / 1e12, 1), "verified": verify(p), "plan": plan_of(lib, p)}
+        entry.update(roofline_fields(case, us))
+        if entry["bound"] == "hbm":
+            floor = read_floor_us(lib, case.bytes_algorithmic, copies, stream, steps)
+            entry["read_floor_us"] = round(floor, 3)
+            entry["frac_of_read_floor"] = round(floor / us, 4)
         if not args.no_cpu:
             entry["cpu"] = cpu_config(case, p.a, p.wp)
-            entry["gpu_vs_cpu_1t"] = round(entry["cpu"]["us_1t"] / us, 1)
+            entry["gpu_vs_cpu_1t"] = round(entry["cpu"].pop("us_1t_total") / us, 1)
         out.append(entry)
         del p
     return out
@@ -676,6 +755,8 @@ def main():
         res["configs"] = bench_configs(args, stream, lib)
     if args.only in ("all", "tile64"):
         res["tile64"] = bench_tile64(args, stream, lib)
+    if args.only in ("all", "refshapes"):
+        res["refshapes"] = bench_reference_shapes(args, stream, lib)
     g = res.get("gemv")
     line = {
         "metric": METRIC,
@@ -740,6 +821,8 @@ def main():
         line["all_configs"] = res["configs"]
     if "tile64" in res:
         line["tile64_layout"] = res["tile64"]
+    if "refshapes" in res:
+        line["reference_benchmark_shapes"] = res["refshapes"]
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
         line["cpu_baseline"]["value"] = round(line["cpu_baseline"]["value"], 3)

@@ -59,6 +59,10 @@ def _cases():
     add("cfg5_big_m1", 5, 1, 8192, 28672, "uniform", third, third)
     add("cfg5_big_m4096", 5, 4096, 8192, 28672, "uniform", third, third)
     add("cfg5_worst", 5, 256, 16384, 4096, "const-128", 1.0, 0.0)
+    # The reference's own GPU benchmark (benchmarks/bench_cuda.cu:45-50): square n^3 problems, A uniform
+    # int8, W uniform over {-1, 0, +1}; its published figures are for these shapes (README.md:178-181).
+    for n in (512, 1024, 2048, 4096):
+        add(f"refbench_n{n}", 0, n, n, n, "uniform", third, third)
     return out
 
 

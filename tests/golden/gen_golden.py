@@ -13,7 +13,7 @@ ctypes on inputs from the library's deterministic generators (include/ternix/syn
                       (ternixengine_amd/configs.py), C computed by the reference avx2_blocked kernel
                       (scalar where N % 8 != 0, the AVX2 precondition), multi-threaded over row blocks.
 
-Run from the repository root:  python tests/golden/gen_golden.py [--skip-digests]
+Run from the repository root:  python tests/golden/gen_golden.py [--skip-digests] [--only name,...]
 """
 import argparse
 import ctypes
@@ -119,9 +119,11 @@ def sha(arr):
     return hashlib.sha256(np.ascontiguousarray(arr).tobytes()).hexdigest()
 
 
-def digests(ref, threads):
+def digests(ref, threads, only=None):
     res = {}
     for name, case in configs.CASES.items():
+        if only and name not in only:
+            continue
         t0 = time.time()
         a = configs.gen_a(case)
         wp = configs.gen_w_packed(case)
@@ -144,12 +146,21 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--skip-digests", action="store_true")
     ap.add_argument("--threads", type=int, default=os.cpu_count() or 1)
+    ap.add_argument("--only", default="", help="comma-separated case names: (re)compute just these digests "
+                                               "and keep the others already in config_digests.json")
     args = ap.parse_args()
     ref = load_ref()
-    np.savez_compressed(os.path.join(HERE, "small_cases.npz"), **small_cases(ref))
+    only = [x for x in args.only.split(",") if x]
+    if not only:
+        np.savez_compressed(os.path.join(HERE, "small_cases.npz"), **small_cases(ref))
     if not args.skip_digests:
-        d = digests(ref, args.threads)
-        with open(os.path.join(HERE, "config_digests.json"), "w") as f:
+        path = os.path.join(HERE, "config_digests.json")
+        d = {}
+        if only and os.path.exists(path):
+            with open(path) as f:
+                d = json.load(f)["cases"]
+        d.update(digests(ref, args.threads, only))
+        with open(path, "w") as f:
             json.dump({"generator": "ternixengine_amd.configs (seed 0)", "cases": d}, f, indent=1, sort_keys=True)
 
 
