@@ -212,7 +212,8 @@ def test_config_against_oracle(oracle, digests, name):
         assert hashlib.sha256(got.tobytes()).hexdigest() == digests[name]["sha256_C"]
 
 
-FULL_CASES = ["cfg4_4096x4096", "cfg4_4096x14336", "cfg4_14336x4096", "cfg5_big_m4096", "cfg5_worst"]
+FULL_CASES = ["cfg4_4096x4096", "cfg4_4096x14336", "cfg4_14336x4096", "cfg5_big_m4096", "cfg5_worst",
+              "refbench_n512", "refbench_n1024", "refbench_n2048", "refbench_n4096"]
 
 
 @pytest.mark.parametrize("name", FULL_CASES)
@@ -223,7 +224,9 @@ def test_config_full_size_digest(digests, name):
     d = digests[name]
     assert hashlib.sha256(a.tobytes()).hexdigest() == d["sha256_A"]
     assert hashlib.sha256(wp.tobytes()).hexdigest() == d["sha256_Wp"]
-    for path in ("auto", "gemm"):
+    # the reference's own benchmark shapes also through the drop-ins of its two CUDA entry points
+    paths = ("auto", "gemm", "tiled", "naive") if name.startswith("refbench") and case.M <= 2048 else ("auto", "gemm")
+    for path in paths:
         log(f"[{path}] {name} M={case.M} K={case.K} N={case.N}")
         got = run(path, a, wp, case.N)
         assert [int(x) for x in got.ravel()[:8]] == d["C_first8"], (path, name)
