@@ -351,8 +351,8 @@ def bench_layer(args, stream, lib):
 def bench_ffn(args, stream, lib):
     """Decode feed-forward block of the cfg2 model shape (hidden 2560, intermediate 6912, M=1):
     RMSNorm+quantise, gate/up GEMV (2560 x 13824) with SwiGLU fused, requantise, down GEMV
-    (6912 x 2560) dequantised -- three launches per block at M=1 (the two GEMVs with their activation
-    quantisation fused, and the down projection's split sum), weights rotating over >= 512 MiB."""
+    (6912 x 2560) dequantised -- two launches per block at M=1 (the two whole-line GEMVs with their
+    activation quantisation, dequantisation and SwiGLU fused), weights rotating over >= 512 MiB."""
     from ternixengine_amd import hip_runtime as hr
     m, h, f = 1, 2560, 6912
     rng = np.random.default_rng(0)

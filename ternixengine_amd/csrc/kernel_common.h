@@ -207,6 +207,16 @@ __device__ __forceinline__ uint64_t lds_read_tr8_asm(uint32_t addr) {
     __asm__ volatile("ds_read_b64_tr_b8 %0, %1" : "=v"(v) : "v"(addr));
     return v;
 }
+__device__ __forceinline__ uint32_t lds_read_b32_asm(uint32_t addr) {
+    uint32_t v;
+    __asm__ volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"(addr));
+    return v;
+}
+// LDS byte store as inline assembly (no compiler-placed wait for LDS DMA in flight); the caller waits
+// with lgkmcnt before anything reads it.
+__device__ __forceinline__ void lds_write_b8_asm(uint32_t addr, uint32_t v) {
+    __asm__ volatile("ds_write_b8 %0, %1" : : "v"(addr), "v"(v) : "memory");
+}
 __device__ __forceinline__ uint32_t lds_u32(const void* p) {
     return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
 }

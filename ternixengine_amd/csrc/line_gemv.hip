@@ -31,11 +31,26 @@
 // there.  The waited-for split was dispatched first (lower workgroup id, in-order dispatch), so it
 // runs while any other split of its strip waits.  The wait is still bounded; a wave that gives up
 // records kFaultZeroWait in the library's fault word (ternix_hip_take_faults) and adds anyway.
+//
+// Fused forms (the decode feed-forward block's GEMVs, and dequantising calls):
+//   * AQ = 1 / 2: the int8 activations are made inside the kernel from fp32 rows X (absmax
+//     quantisation; AQ = 2 RMS-normalises with weight G first), with the loops and rounding of
+//     row_stats.h, so they are bit-identical to quantize_rows_kernel / rmsnorm_kernel.  Every
+//     workgroup DMAs the rows (and G) into LDS ahead of its weights, computes the row statistics
+//     itself and quantises just the 16 activations each lane feeds the MFMA.
+//   * EPI: a float output Y = C * (row scale * weight scale), optionally with the SwiGLU of
+//     interleaved (gate, up) column pairs.  The splits add into the int32 buffer C as above; each
+//     split then counts itself on the strip's arrival word (the third word of its ticket line: every
+//     call adds exactly 64 -- split 0 adds 64 - splits at its start, every split 1 once its atomics have
+//     completed), and the split that brings it to 63 mod 64 reads the strip's complete sums back with
+//     coherent loads and writes Y.  One launch, no dequantisation launch.
 
 #include <hip/hip_runtime.h>
+#include <math.h>
 #include <stdint.h>
 
 #include "kernel_common.h"
+#include "row_stats.h"
 #include "ternary_kernels.h"
 
 namespace ternix_hip {
@@ -47,27 +62,65 @@ __device__ unsigned int g_line_fault_word;
 namespace {
 
 constexpr int kLineSpinLimit = 1 << 20;  // tries of the zeroed-word wait (about a second)
+constexpr int kLineQK = 8192;            // fused quantisation: M x K <= kLineQK fp32 activations (in LDS)
 
 struct LineArgs {
     const int8_t* A;
     const uint8_t* B;
-    int32_t* C;
+    int32_t* C;                    // int32 sums (the output, or with EPI the int32 buffer of the sums)
     int M, K, N;
     int strips;                    // ceil(N/4 / 128)
     int splits;                    // workgroups per strip (<= 64)
-    unsigned long long* tk;        // per strip {T, Z}
-    int tk_stride;                 // 64-bit words between consecutive strips' {T, Z}
+    unsigned long long* tk;        // per strip {T, Z, arrivals}
+    int tk_stride;                 // 64-bit words between consecutive strips' words
+    const float* X;                // AQ: fp32 rows (M x K)
+    const float* G;                // AQ == 2: RMSNorm weight (K)
+    float eps;
+    float* rs_out;                 // AQ: row scales (M), written by workgroup 0
+    OutScale os;                   // EPI: float output
+    int vec_y;                     // EPI: Y 16-byte aligned
 };
-
 
 __device__ __forceinline__ int line_swz(int r) { return ((r >> 1) & 3) ^ (((r >> 4) & 1) << 2); }
 
-template <int S, int NW>
+// row_block_sum / row_block_max of row_stats.h for a workgroup of more than four waves: the same
+// butterfly and the same combine of waves 0-3 (threads 0-255 hold the row; the other waves pass 0 and
+// only keep the barrier count), with plain barriers: no memory fence, so no wave waits here for its
+// weight loads in flight.
+__device__ __forceinline__ float line_block_sum(float v, float* red) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+    __builtin_amdgcn_s_barrier();  // red may still be read from a previous call
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    TX_LGKMCNT0();
+    __builtin_amdgcn_s_barrier();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+__device__ __forceinline__ float line_block_max(float v, float* red) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+    __builtin_amdgcn_s_barrier();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    TX_LGKMCNT0();
+    __builtin_amdgcn_s_barrier();
+    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+template <int S, int NW, int AQ, bool EPI>
 __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args) {
     static_assert(NW == 4 || NW == 8, "4 or 8 data waves");
+    static_assert(AQ == 0 || EPI, "fused quantisation comes with the float output");
     constexpr int GW = 8 / NW;  // 16-byte column groups per data wave
     constexpr int STEP = 8192;  // bytes per k-step of the strip (64 rows x 128 bytes)
+    constexpr int QR = AQ ? kLineQK / 256 : 1;
     __shared__ __attribute__((aligned(16))) uint8_t lds[S * STEP];
+    __shared__ __attribute__((aligned(16))) float xl[AQ ? kLineQK + 256 : 4];      // rows of X (+ DMA tail)
+    __shared__ __attribute__((aligned(16))) float gl[AQ == 2 ? kLineQK + 256 : 4];  // G
+    __shared__ __attribute__((aligned(16))) int8_t qbuf[AQ ? 4 * S * 64 : 16];  // AQ: the unit's int8 rows
+    __shared__ float red[16];
+    __shared__ float rscale[4];
+    __shared__ int last_flag;
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -81,6 +134,42 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
     const bool zeroer = split == 0;
     unsigned long long* tk = args.tk + (size_t)args.tk_stride * (size_t)s;
 
+    // AQ: the M rows of X (and G) go global -> LDS ahead of the weights, 1 KB per wave instruction,
+    // chunk c by data wave c % NW (the last chunk's lanes past the end re-read valid bytes into the
+    // padding), so that waiting for them leaves the weight DMAs in flight.
+    if constexpr (AQ != 0) {
+        if (wave < NW) {
+            const int nx = (M * K * 4 + 1023) >> 10, ng = AQ == 2 ? (K * 4 + 1023) >> 10 : 0;
+            const uint8_t* xb = reinterpret_cast<const uint8_t*>(args.X);
+            const uint8_t* gb = reinterpret_cast<const uint8_t*>(args.G);
+            for (int c = wave; c < nx + ng; c += NW) {
+                if (c < nx) {
+                    const int off = min(c * 1024 + lane * 16, M * K * 4 - 16);
+                    lds_dma16(xb + off, reinterpret_cast<uint8_t*>(xl) + c * 1024);
+                } else {
+                    const int off = min((c - nx) * 1024 + lane * 16, K * 4 - 16);
+                    lds_dma16(gb + off, reinterpret_cast<uint8_t*>(gl) + (c - nx) * 1024);
+                }
+            }
+        }
+    }
+
+    auto issue_weights = [&]() {
+        const int r_in = lane >> 3, pos = lane & 7;
+#pragma unroll
+        for (int i = 0; i < (S * 8 + NW - 1) / NW; ++i) {
+            const int p = wave + NW * i;
+            if (p < S * 8) {  // compile-time per (i, wave-uniform p): all waves issue ceil(8S / NW) or fewer
+                const int step = min(p >> 3, nst - 1), r = (p & 7) * 8 + r_in;
+                int c = pos ^ line_swz(r);
+                if (bc0 + 16 * c >= NB) c = 0;  // past the last column (a partial last strip): a valid chunk, unused
+                const uint8_t* src = args.B + ((size_t)(s0 + step) * 64 + (size_t)r) * (size_t)NB + (size_t)(bc0 + 16 * c);
+                lds_dma16(src, lds + (p >> 3) * STEP + (p & 7) * 1024);
+            }
+        }
+    };
+
+    unsigned long long old = 0, saved_exec;
     if (wave == NW) {
         // Protocol wave.  Split 0 first issues the zeroing stores (they need no ticket).
         if (zeroer) {
@@ -89,45 +178,126 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
                 unsigned long long* z = reinterpret_cast<unsigned long long*>(args.C + (size_t)r * (size_t)N + 4 * bc0);
                 for (int u = lane; u < n8; u += 64) __hip_atomic_store(z + u, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
-        }
-        if (zeroer) {
-            // Split 0: T += 64 - (splits - 1) (no return needed), barrier (1), wait until the zeroing
-            // stores have completed, then Z += 1.  One statement, lane 0 alone enabled for the two
-            // atomics, so that barrier (1) is reached at once and is one instruction of a uniform path.
-            const unsigned long long inc = (unsigned long long)(64 - (args.splits - 1)), one = 1;
-            unsigned long long saved_exec;
+            // T += 64 - (splits - 1) (no return needed); with EPI also arrivals += 64 - splits.  Lane 0
+            // alone enabled; nothing waited for here.
+            const unsigned long long inc = (unsigned long long)(64 - (args.splits - 1));
+            if constexpr (EPI) {
+                const unsigned long long inc_a = (unsigned long long)(64 - args.splits);
+                __asm__ volatile(
+                    "s_mov_b64 %0, exec\n\t"
+                    "s_mov_b64 exec, 1\n\t"
+                    "global_atomic_add_x2 %1, %2, off\n\t"
+                    "global_atomic_add_x2 %3, %4, off\n\t"
+                    "s_mov_b64 exec, %0"
+                    : "=&s"(saved_exec)
+                    : "v"(tk), "v"(inc), "v"(tk + 2), "v"(inc_a)
+                    : "memory");
+            } else {
+                __asm__ volatile(
+                    "s_mov_b64 %0, exec\n\t"
+                    "s_mov_b64 exec, 1\n\t"
+                    "global_atomic_add_x2 %1, %2, off\n\t"
+                    "s_mov_b64 exec, %0"
+                    : "=&s"(saved_exec)
+                    : "v"(tk), "v"(inc)
+                    : "memory");
+            }
+        } else {
+            // The returning T += 1 (its value / 64 + 1 names this call), lane 0 alone enabled, not
+            // waited for here: `old` is only read after the wait below, which names it.
             __asm__ volatile(
+                "s_mov_b64 %1, exec\n\t"
+                "s_mov_b64 exec, 1\n\t"
+                "global_atomic_add_x2 %0, %2, %3, off sc0\n\t"
+                "s_mov_b64 exec, %1"
+                : "=&v"(old), "=&s"(saved_exec)
+                : "v"(tk), "v"(1ull)
+                : "memory");
+        }
+    } else {
+        // Data waves.  DMA instruction p (k-step p / 8, rows 8 (p % 8) .. +7) is issued by wave p % NW;
+        // lane l fills 16-byte position l % 8 of row 8 (p % 8) + l / 8.  Steps past the unit's last
+        // re-read its last step into their own (unused) stage slot, so every wave issues the same number
+        // of DMAs on every path.
+        issue_weights();
+    }
+
+    // AQ: the row statistics of every row.  Waves 0-3 hold the row (thread t: k = t + 256 j, in
+    // increasing j, the order of row_stats.h) and do the arithmetic; every wave takes part in the
+    // reductions' barriers.  LDS is read with inline-assembly reads, eight per thread and wait: a
+    // compiler-placed LDS read would first wait for every LDS DMA in flight, the weights included.
+    float r_inv[4] = {1.0f, 1.0f, 1.0f, 1.0f}, r_sc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (AQ != 0) {
+        if (wave < NW) TX_VMCNT((S * 8 + NW - 1) / NW);  // this wave's row chunks have landed (its weights may not)
+        __builtin_amdgcn_s_barrier();                      // ... every wave's
+        __builtin_amdgcn_sched_barrier(0);
+        // visit(f): f(x, g) for this thread's elements of row r, in increasing k (waves 0-3 only)
+        auto visit = [&](int r, auto&& f) {
+            if (wave >= 4) return;
+            const uint32_t xa = lds_u32(xl + r * K), ga = lds_u32(gl);
+            for (int k0 = 0; k0 < K; k0 += 2048) {
+                uint32_t xb[8], gb[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const int k = min(k0 + tid + 256 * u, K - 1);  // clamped: only used when in the row
+                    xb[u] = lds_read_b32_asm(xa + 4 * k);
+                    gb[u] = AQ == 2 ? lds_read_b32_asm(ga + 4 * k) : 0u;
+                }
+                TX_LGKMCNT0();
+#pragma unroll
+                for (int u = 0; u < 8; ++u) __asm__ volatile("" : "+v"(xb[u]), "+v"(gb[u]));
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    if (k0 + tid + 256 * u < K) f(__uint_as_float(xb[u]), __uint_as_float(gb[u]));
+            }
+        };
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            if (r >= M) break;  // workgroup-uniform
+            float inv = 1.0f;
+            if constexpr (AQ == 2) {
+                float ss = 0.0f;
+                visit(r, [&](float x, float) { ss = fmaf(x, x, ss); });
+                ss = line_block_sum(ss, red);
+                inv = 1.0f / sqrtf(ss / (float)K + args.eps);
+            }
+            float amax = 0.0f;
+            visit(r, [&](float x, float g) { amax = fmaxf(amax, fabsf(AQ == 2 ? x * inv * g : x)); });
+            const float am = fmaxf(line_block_max(amax, red), 1e-5f);
+            if (tid == 0) {
+                rscale[r] = am / 127.0f;
+                if (blockIdx.x == 0) args.rs_out[r] = am / 127.0f;
+            }
+            r_inv[r] = inv;
+            r_sc[r] = 127.0f / am;
+        }
+    }
+
+    if (wave == NW) {
+        __builtin_amdgcn_s_barrier();  // (1) the data waves' weights have landed
+        if (zeroer) {
+            // wait until the zeroing stores have completed, then Z += 1 (lane 0 alone enabled)
+            const unsigned long long one = 1;
+            __asm__ volatile(
+                "s_waitcnt vmcnt(0)\n\t"
                 "s_mov_b64 %0, exec\n\t"
                 "s_mov_b64 exec, 1\n\t"
                 "global_atomic_add_x2 %1, %2, off\n\t"
-                "s_mov_b64 exec, %0\n\t"
-                "s_barrier\n\t"
-                "s_waitcnt vmcnt(0)\n\t"
-                "s_mov_b64 exec, 1\n\t"
-                "global_atomic_add_x2 %3, %4, off\n\t"
                 "s_mov_b64 exec, %0"
                 : "=&s"(saved_exec)
-                : "v"(tk), "v"(inc), "v"(tk + 1), "v"(one)
+                : "v"(tk + 1), "v"(one)
                 : "memory");
         } else {
-            // Every other split: the returning T += 1 (its value / 64 + 1 names this call), barrier (1)
-            // (this workgroup's weights have landed, so split 0 has long started its zeroing), then the
-            // coherent (sc1) load of Z and the wait for both.  One statement, lane 0 alone enabled for
-            // the memory operations: nothing reads `old` or `zw`, or reuses their registers, while they
-            // are in flight.
-            unsigned long long old, zw, saved_exec;
+            // the coherent (sc1) load of Z, lane 0 alone enabled, then the wait for it and the ticket
+            unsigned long long zw;
             __asm__ volatile(
                 "s_mov_b64 %2, exec\n\t"
                 "s_mov_b64 exec, 1\n\t"
-                "global_atomic_add_x2 %0, %3, %4, off sc0\n\t"
-                "s_mov_b64 exec, %2\n\t"
-                "s_barrier\n\t"
-                "s_mov_b64 exec, 1\n\t"
-                "global_load_dwordx2 %1, %5, off sc1\n\t"
+                "global_load_dwordx2 %0, %3, off sc1\n\t"
                 "s_mov_b64 exec, %2\n\t"
                 "s_waitcnt vmcnt(0)"
-                : "=&v"(old), "=&v"(zw), "=&s"(saved_exec)
-                : "v"(tk), "v"(1ull), "v"(tk + 1)
+                : "=&v"(zw), "+v"(old), "=&s"(saved_exec)
+                : "v"(tk + 1)
                 : "memory");
             // lane 0's values (the other lanes' registers were not written)
             const unsigned long long old0 =
@@ -150,35 +320,57 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
         return;
     }
 
-    // Data waves.  DMA instruction p (k-step p / 8, rows 8 (p % 8) .. +7) is issued by wave p % NW;
-    // lane l fills 16-byte position l % 8 of row 8 (p % 8) + l / 8.
-    {
-        const int r_in = lane >> 3, pos = lane & 7;
+    // Activation fragments: lane (q, kb) feeds row q, activations 16 kb .. 16 kb + 15 of each k-step.
+    const int q = lane & 15, kb = lane >> 4;
+    v4i a[S];
 #pragma unroll
-        for (int i = 0; i < (S * 8 + NW - 1) / NW; ++i) {
-            const int p = wave + NW * i;
-            if (p < nst * 8) {
-                const int step = p >> 3, r = (p & 7) * 8 + r_in;
-                int c = pos ^ line_swz(r);
-                if (bc0 + 16 * c >= NB) c = 0;  // past the last column (a partial last strip): a valid chunk, unused
-                const uint8_t* src = args.B + ((size_t)(s0 + step) * 64 + (size_t)r) * (size_t)NB + (size_t)(bc0 + 16 * c);
-                lds_dma16(src, lds + step * STEP + (p & 7) * 1024);
+    for (int st = 0; st < S; ++st) a[st] = v4i{0, 0, 0, 0};
+    if constexpr (AQ == 0) {
+        const int8_t* arow = args.A + (size_t)min(q, M - 1) * (size_t)K + (size_t)s0 * 64 + kb * 16;
+#pragma unroll
+        for (int st = 0; st < S; ++st)
+            if (st < nst && q < M) a[st] = *reinterpret_cast<const v4i*>(arow + st * 64);
+    } else {
+        // Quantised once per workgroup: the M x 64 nst activations of the unit, one per data-wave
+        // thread and pass, q = clamp(rint(v * s)), v = x (* inv * g), into LDS as int8 rows; each lane
+        // then reads its 16-byte fragment after the barrier below.
+        const uint32_t xa = lds_u32(xl), ga = lds_u32(gl), qa = lds_u32(qbuf);
+        const int per_row = nst * 64, total = M * per_row;
+        for (int e0 = 0; e0 < total; e0 += NW * 64 * 4) {
+            uint32_t xb[4], gb[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int e = min(e0 + tid + NW * 64 * u, total - 1);
+                const int r = e / per_row, k = s0 * 64 + e % per_row;
+                xb[u] = lds_read_b32_asm(xa + 4 * (r * K + k));
+                gb[u] = AQ == 2 ? lds_read_b32_asm(ga + 4 * k) : 0u;
+            }
+            TX_LGKMCNT0();
+#pragma unroll
+            for (int u = 0; u < 4; ++u) __asm__ volatile("" : "+v"(xb[u]), "+v"(gb[u]));
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int e = e0 + tid + NW * 64 * u;
+                if (e < total) {
+                    const int r = e / per_row, kk = e % per_row;
+                    const float inv = r == 0 ? r_inv[0] : (r == 1 ? r_inv[1] : (r == 2 ? r_inv[2] : r_inv[3]));
+                    const float sc = r == 0 ? r_sc[0] : (r == 1 ? r_sc[1] : (r == 2 ? r_sc[2] : r_sc[3]));
+                    const float xv = __uint_as_float(xb[u]);
+                    const float v = AQ == 2 ? xv * inv * __uint_as_float(gb[u]) : xv;
+                    lds_write_b8_asm(qa + (uint32_t)(r * (S * 64) + kk), (uint32_t)quantize_value(v, sc) & 0xFFu);
+                }
             }
         }
     }
-    const int q = lane & 15, kb = lane >> 4;
-    v4i a[S];
-    {
-        const int8_t* arow = args.A + (size_t)min(q, M - 1) * (size_t)K + (size_t)s0 * 64 + kb * 16;
-#pragma unroll
-        for (int st = 0; st < S; ++st) {
-            a[st] = v4i{0, 0, 0, 0};
-            if (st < nst && q < M) a[st] = *reinterpret_cast<const v4i*>(arow + st * 64);
-        }
-    }
+    TX_LGKMCNT0();  // AQ: the int8 rows are in LDS
     TX_VMCNT(0);
     __builtin_amdgcn_s_barrier();  // (1) every data wave's weights are in LDS
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (AQ != 0) {
+#pragma unroll
+        for (int st = 0; st < S; ++st)
+            if (st < nst && q < M) a[st] = *reinterpret_cast<const v4i*>(qbuf + q * (S * 64) + st * 64 + kb * 16);
+    }
 
     v4i acc[GW][4];
 #pragma unroll
@@ -252,6 +444,33 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
             __hip_atomic_fetch_add(out + (size_t)i * (size_t)N, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
+    if constexpr (EPI) {
+        // Count this split once its atomics have completed; the split that brings the strip's
+        // arrival word to 63 mod 64 has every split's sums and writes the float output.
+        TX_VMCNT(0);
+        __builtin_amdgcn_s_barrier();  // (3) every data wave's atomics have completed (the protocol wave has left)
+        if (tid == 0) {
+            const unsigned long long a_old =
+                __hip_atomic_fetch_add(tk + 2, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            last_flag = (a_old & 63) == 63;
+        }
+        __syncthreads();  // (4)
+        if (!last_flag) return;
+        // The strip's sums, read with coherent loads (they bypass this XCD's L2, which may hold none of
+        // the other splits' additions), four consecutive columns per lane, every row.
+        const int ncol = min(512, N - 4 * bc0);
+        for (int idx = tid; idx < M * 128; idx += NW * 64) {
+            const int r = idx >> 7, c4 = (idx & 127) * 4;
+            if (c4 >= ncol) continue;
+            const unsigned long long* src =
+                reinterpret_cast<const unsigned long long*>(args.C + (size_t)r * (size_t)N + 4 * bc0 + c4);
+            const unsigned long long u0 = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const unsigned long long u1 = __hip_atomic_load(src + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const v4i v = {(int)(uint32_t)u0, (int)(uint32_t)(u0 >> 32), (int)(uint32_t)u1, (int)(uint32_t)(u1 >> 32)};
+            const float f = (AQ != 0 ? rscale[r] : args.os.rs[r]) * args.os.ws;
+            store_scaled_f(args.os, f, r, N, 4 * bc0 + c4, v, args.vec_y);
+        }
+    }
 }
 
 }  // namespace
@@ -264,9 +483,18 @@ bool line_gemv_ok(const int8_t* A, const uint8_t* B, int M, int K, int N) {
 
 int line_gemv_splits(int K, int S) { return ((K / 64) + S - 1) / S; }
 
+
 hipError_t launch_line_gemv(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int S, int NW,
-                            unsigned long long* tk, int tk_stride, hipStream_t st) {
-    if (!line_gemv_ok(A, B, M, K, N) || tk == nullptr) return hipErrorInvalidValue;
+                            unsigned long long* tk, int tk_stride, hipStream_t st, const OutScale& os,
+                            const ActQuant& aq) {
+    if (!line_gemv_ok(A, B, M, K, N) || tk == nullptr || C == nullptr) return hipErrorInvalidValue;
+    const bool epi = os.Y != nullptr;
+    if (aq.mode != 0 && (!epi || (size_t)M * (size_t)K > (size_t)kLineQK || aq.X == nullptr || aq.rs_out == nullptr ||
+                         (aq.mode == 2 && aq.G == nullptr) || (uintptr_t)aq.X % 16 != 0 ||
+                         (aq.mode == 2 && (uintptr_t)aq.G % 16 != 0)))
+        return hipErrorInvalidValue;
+    if (epi && (tk_stride < 4 || (aq.mode == 0 && os.rs == nullptr) || (os.swiglu && N % 8 != 0)))
+        return hipErrorInvalidValue;
     LineArgs a;
     a.A = A;
     a.B = B;
@@ -278,24 +506,39 @@ hipError_t launch_line_gemv(const int8_t* A, const uint8_t* B, int32_t* C, int M
     a.splits = line_gemv_splits(K, S);
     a.tk = tk;
     a.tk_stride = tk_stride;
+    a.X = aq.X;
+    a.G = aq.G;
+    a.eps = aq.eps;
+    a.rs_out = aq.rs_out;
+    a.os = os;
+    a.vec_y = epi && (uintptr_t)os.Y % 16 == 0;
+
     if (a.splits > 64 || (size_t)S * 64 > (size_t)kMaxKPerAccumulator) return hipErrorInvalidValue;
     const dim3 grid((unsigned)(a.strips * a.splits));
-#define TX_LINE(SS, WW)                                                                                    \
-    if (S == SS && NW == WW) {                                                                             \
-        hipLaunchKernelGGL((line_gemv_kernel<SS, WW>), grid, dim3(64 * (WW + 1)), 0, st, a);              \
+    const int mode = epi ? 1 + aq.mode : 0;  // 0 int32 out, 1 dequantised, 2 / 3 with fused quantisation
+#define TX_LINE(SS, WW, AQQ, EE)                                                                           \
+    if (S == SS && NW == WW && mode == (EE ? 1 + AQQ : 0)) {                                               \
+        hipLaunchKernelGGL((line_gemv_kernel<SS, WW, AQQ, EE>), grid, dim3(64 * (WW + 1)), 0, st, a);     \
         return hipGetLastError();                                                                          \
     }
-    TX_LINE(1, 8)
-    TX_LINE(2, 8)
-    TX_LINE(3, 8)
-    TX_LINE(4, 8)
-    TX_LINE(6, 8)
-    TX_LINE(8, 8)
-    TX_LINE(2, 4)
-    TX_LINE(4, 4)
+#define TX_LINE_S(SS)            \
+    TX_LINE(SS, 8, 0, false)     \
+    TX_LINE(SS, 8, 0, true)      \
+    TX_LINE(SS, 8, 1, true)      \
+    TX_LINE(SS, 8, 2, true)
+    TX_LINE(1, 8, 0, false)
+    TX_LINE_S(2)
+    TX_LINE_S(3)
+    TX_LINE_S(4)
+    TX_LINE_S(6)
+    TX_LINE_S(8)
+    TX_LINE(2, 4, 0, false)
+    TX_LINE(4, 4, 0, false)
+#undef TX_LINE_S
 #undef TX_LINE
     return hipErrorInvalidValue;
 }
+
 
 hipError_t take_line_faults(unsigned* bits) {
     unsigned v = 0;

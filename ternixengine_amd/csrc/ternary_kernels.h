@@ -64,13 +64,6 @@ inline size_t ticket_units(size_t strips) { return strips * (size_t)ticket_strid
 constexpr unsigned kFaultZeroWait = 1u;  // a bounded wait for a strip's zeroed word gave up
 // Synchronises the current device, returns the fault word's bits in *bits and clears them.
 hipError_t take_faults(unsigned* bits);
-// Whole-line decode GEMV (line_gemv.hip): M <= 4, K % 64 == 0, N/4 % 16 == 0, 16-byte aligned A and W;
-// S k-steps per workgroup, NW data waves (4 or 8); K splits added with int32 atomics into C zeroed by
-// each strip's split 0 (tickets: two 64-bit words per 128-byte strip, persistent).
-bool line_gemv_ok(const int8_t* A, const uint8_t* B, int M, int K, int N);
-int line_gemv_splits(int K, int S);
-hipError_t launch_line_gemv(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int S, int NW,
-                            unsigned long long* tk, int tk_stride, hipStream_t st);
 hipError_t take_line_faults(unsigned* bits);
 // Bare streaming read of `bytes` (rounded down to 16) at p (16-byte aligned): the HBM floor reference.
 hipError_t launch_stream_read(const void* p, size_t bytes, int* out, hipStream_t st);
@@ -101,6 +94,17 @@ struct ActQuant {
     float eps = 0.0f;
     float* rs_out = nullptr;
 };
+// Whole-line decode GEMV (line_gemv.hip): M <= 4, K % 64 == 0, N/4 % 16 == 0, 16-byte aligned A and W;
+// S k-steps per workgroup, NW data waves (4 or 8); K splits added with int32 atomics into C zeroed by
+// each strip's split 0 (tickets: two 64-bit words per 128-byte strip, persistent).
+bool line_gemv_ok(const int8_t* A, const uint8_t* B, int M, int K, int N);
+int line_gemv_splits(int K, int S);
+hipError_t launch_line_gemv(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int S, int NW,
+                            unsigned long long* tk, int tk_stride, hipStream_t st, const OutScale& os = OutScale{},
+                            const ActQuant& aq = ActQuant{});
+// (os.Y set: float output through the last-arriving split of each strip, C then being the int32 buffer
+// of the sums, tickets spread one line per strip; aq.mode 1 / 2: fused activation quantisation of
+// fp32 rows aq.X with M * K <= 8192, only with os.Y.)
 bool skinny_short_ok(const uint8_t* B, int M, int K, int N, int steps_per_split, int splits);
 // True when the DMA-staged skinny kernel can run this call: M <= 16, K % 64 == 0, N % 256 == 0,
 // 16-byte aligned A and W, 1..16 k-steps per split.

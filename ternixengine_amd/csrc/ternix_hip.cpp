@@ -475,17 +475,35 @@ bool run_atomic_wave(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, in
 }
 
 // The whole-line GEMV (line_gemv.hip): true when it takes the call (*e then holds the launch status).
-// M <= 4, int32 output into a 16-byte aligned C, the library's tickets (one pair per 128-byte strip,
-// spread as ticket_stride says).  Plan: the fewest k-steps per workgroup
-// (2, 3, 4, 6 or 8) whose grid stays within about one workgroup per CU (<= 250 workgroups) with at most
-// 64 splits per strip; none for wide matrices that would need more (the DMA-staged and wave kernels
-// keep those).  The DBG_LINE switch turns it off (0) or forces the k-steps [0] and data waves [1].
-bool run_line_gemv(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int K, int N, Ctx& c, hipError_t* e) {
+// M <= 4, the library's tickets (one set per 128-byte strip, spread as ticket_stride says), and
+// either an int32 output into a 16-byte aligned C, or a float output (os.Y, optionally SwiGLU) through
+// the kernel's last-arriver epilogue with dC as the int32 buffer of the sums (dC == os.Y only without
+// SwiGLU), with the activations given as int8 or quantised inside the kernel from fp32 rows (aq).
+// Plan: the fewest k-steps per workgroup (2, 3, 4, 6 or 8) whose grid stays within about one
+// workgroup per CU (<= 250 workgroups) with at most 64 splits per strip; none for wide matrices that
+// would need more (the DMA-staged and wave kernels keep those).  The DBG_LINE switch turns it off (0)
+// or forces the k-steps [0] and data waves [1].
+bool run_line_gemv(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int K, int N, Ctx& c, hipError_t* e,
+                   const ternix_hip::OutScale& os = ternix_hip::OutScale{},
+                   const ternix_hip::ActQuant& aq = ternix_hip::ActQuant{}) {
     const int fs = ternix_hip::debug_get(ternix_hip::DBG_LINE, 0), fw = ternix_hip::debug_get(ternix_hip::DBG_LINE, 1);
     if (fs == 0) return false;
     if (!(dC != nullptr && reinterpret_cast<uintptr_t>(dC) % 16 == 0 && ternix_hip::line_gemv_ok(dA, dB, M, K, N)))
         return false;
+    const bool epi = os.Y != nullptr;
+    if (aq.mode != 0 && !(epi && (long)M * K <= 8192 && reinterpret_cast<uintptr_t>(aq.X) % 16 == 0 &&
+                          (aq.mode != 2 || reinterpret_cast<uintptr_t>(aq.G) % 16 == 0)))
+        return false;
+    if (epi) {
+        // the sums' buffer and the float output: the same buffer (same positions, no SwiGLU) or disjoint
+        const uintptr_t c0 = reinterpret_cast<uintptr_t>(dC), c1 = c0 + (size_t)M * (size_t)N * 4;
+        const uintptr_t y0 = reinterpret_cast<uintptr_t>(os.Y),
+                        y1 = y0 + (size_t)M * (size_t)(os.swiglu ? N / 2 : N) * 4;
+        const bool same = y0 == c0 && !os.swiglu, disjoint = y1 <= c0 || c1 <= y0;
+        if (!(same || disjoint) || (os.swiglu && N % 8 != 0) || (aq.mode == 0 && os.rs == nullptr)) return false;
+    }
     const int strips = (N / 4 + 127) / 128;
+    if (epi && ternix_hip::ticket_stride((size_t)strips) < 4) return false;  // the arrival word needs the spread line
     int S = 0;
     if (fs > 0) {
         S = fs;
@@ -500,15 +518,16 @@ bool run_line_gemv(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int 
         }
         if (S == 0) return false;
     }
-    const int NW = fw == 4 ? 4 : 8;
+    const int NW = fw == 4 && !epi ? 4 : 8;
     const int splits = ternix_hip::line_gemv_splits(K, S);
     if (splits > 64) return false;
     const int stride = ternix_hip::ticket_stride((size_t)strips);
     unsigned long long* tk = c.tickets(ternix_hip::ticket_units((size_t)strips));
     if (!tk) return false;
-    c.note("line_gemv_kernel S=%d waves=%d+1 splits=%d (splits added with int32 atomics into C zeroed by each "
-           "strip's split 0)", S, NW, splits);
-    *e = TX_LAUNCH(c, ternix_hip::launch_line_gemv(dA, dB, dC, M, K, N, S, NW, tk, stride, c.st));
+    c.note("line_gemv_kernel S=%d waves=%d+1 splits=%d%s%s (splits added with int32 atomics into C zeroed by each "
+           "strip's split 0)", S, NW, splits, aq.mode == 2 ? " rmsnorm+quantise" : (aq.mode == 1 ? " quantise" : ""),
+           epi ? (os.swiglu ? " dequant+swiglu" : " dequant") : "");
+    *e = TX_LAUNCH(c, ternix_hip::launch_line_gemv(dA, dB, dC, M, K, N, S, NW, tk, stride, c.st, os, aq));
     return true;
 }
 
@@ -554,7 +573,7 @@ hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
     // [1] lowers the row limit (tests and measurements).
     {
         hipError_t e = hipSuccess;
-        if (!generic && aq.mode == 0 && os.Y == nullptr && run_line_gemv(dA, dB, dC, M, K, N, c, &e)) return e;
+        if (!generic && run_line_gemv(dA, dB, dC, M, K, N, c, &e, os, aq)) return e;
         if (!generic && aq.mode == 0 && os.Y == nullptr && run_atomic_wave(dA, dB, dC, M, K, N, c, &e)) return e;
     }
     // Wave-pipelined kernel (32-byte strips, 16-byte with fused quantisation; 2 ring slots per wave),
@@ -1165,8 +1184,11 @@ int ternix_hip_ffn_forward(float* dY, const float* dX, const float* dNormWeight,
     hipStream_t st = static_cast<hipStream_t>(stream);
     const int m = (int)M, hd = (int)H, f = (int)F;
     // Decode shapes: the RMSNorm + quantisation of x and the requantisation of h run inside the two
-    // skinny GEMVs (fused activation prologue, bit-identical to the standalone kernels), leaving
-    // GEMV + reduce twice.  Otherwise: the four separate launches.
+    // skinny GEMVs (fused activation prologue, bit-identical to the standalone kernels).  Up to 4 rows
+    // with M x H and M x F <= 8192 that is two launches of the whole-line GEMV, each dequantising (and,
+    // for gate/up, applying SwiGLU) in its last-arriving split (measured on MI355X, cold weights,
+    // 1 x 2560 x 6912: 20.2 -> 15.9 us per block); otherwise the other skinny kernels with their reduce
+    // or dequantisation launches.  Larger M: the four separate launches.
     if (m <= kSkinnyMaxM && F > 0) {
         ternix_hip::OutScale os1;
         os1.Y = h;

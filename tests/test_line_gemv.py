@@ -128,3 +128,64 @@ def test_line_gemv_interleaved_with_wave_kernel_and_graph(oracle):
                 _check(p, f"eager after replay {rep}")
     finally:
         lib.ternix_hip_debug_reset()
+
+
+def _line_off_and_on(lib, fn):
+    """fn() with the whole-line GEMV switched off, then on (the automatic plan): both results."""
+    try:
+        assert lib.ternix_hip_debug_set(b"line", 0, -1, -1, -1) == 0
+        off = fn()
+    finally:
+        lib.ternix_hip_debug_reset()
+    return off, fn()
+
+
+FUSED_SHAPES = [(1, 2560, 6912), (1, 6912, 2560), (2, 4096, 4096), (4, 2048, 3072), (3, 1024, 1536)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape", FUSED_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_line_gemv_dequant_and_swiglu_bit_equal(shape):
+    """The float-output forms (dequantised, and dequantised + SwiGLU of interleaved column pairs)
+    through the kernel's last-arriving split equal the other kernels' outputs bit for bit."""
+    m, k, n = shape
+    lib = tx._load()
+    rng = np.random.default_rng(sum(shape))
+    a = rng.integers(-128, 128, size=(m, k), dtype=np.int8)
+    wp = (rng.integers(0, 256, size=(k, n // 4), dtype=np.uint16).astype(np.uint8) & 0x77)
+    rs = rng.uniform(0.001, 0.05, size=m).astype(np.float32)
+    log(f"[line dequant] M={m} K={k} N={n}")
+    off, on = _line_off_and_on(lib, lambda: tx.ternary_matmul_dequant(a, wp, rs, 0.03))
+    assert np.array_equal(off.view(np.int32), on.view(np.int32))
+    da, db, drs = hr.DeviceBuffer.from_array(a), hr.DeviceBuffer.from_array(wp), hr.DeviceBuffer.from_array(rs)
+    dscr = hr.DeviceBuffer(4 * m * n)
+
+    def swiglu():
+        dh = hr.DeviceBuffer(4 * m * n // 2)
+        dh.upload(np.full(m * n // 2, np.nan, np.float32))
+        assert lib.ternix_hip_mul_mat_ternary_swiglu(da.value, db.value, dh.value, m, k, n, drs.value, 0.03,
+                                                     dscr.value, None) == 0
+        hr.synchronize()
+        return dh.download(np.float32, (m, n // 2))
+
+    log(f"[line swiglu] M={m} K={k} N={n}")
+    off, on = _line_off_and_on(lib, swiglu)
+    assert np.isfinite(on).all() and np.array_equal(off.view(np.int32), on.view(np.int32))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape", [(1, 2560, 6912), (2, 2048, 2048), (4, 1024, 2816)], ids=lambda s: "x".join(map(str, s)))
+def test_line_gemv_ffn_forward_bit_equal(shape):
+    """The decode feed-forward block with its two GEMVs on the whole-line kernel (RMSNorm + quantise
+    fused into the gate/up GEMV, quantise into the down GEMV, dequantisation and SwiGLU in their last
+    arrivers) equals the block on the other kernels bit for bit."""
+    m, h, f = shape
+    lib = tx._load()
+    rng = np.random.default_rng(m * 7 + h)
+    x = rng.standard_normal((m, h)).astype(np.float32)
+    g = rng.uniform(0.5, 1.5, size=h).astype(np.float32)
+    wgu = (rng.integers(0, 256, size=(h, 2 * f // 4), dtype=np.uint16).astype(np.uint8) & 0x77)
+    wd = (rng.integers(0, 256, size=(f, h // 4), dtype=np.uint16).astype(np.uint8) & 0x77)
+    log(f"[line ffn] M={m} H={h} F={f}")
+    off, on = _line_off_and_on(lib, lambda: tx.ffn_forward(x, g, 1e-5, wgu, 0.02, wd, 0.03))
+    assert np.isfinite(on).all() and np.array_equal(off.view(np.int32), on.view(np.int32))
