@@ -17,8 +17,9 @@
 //   * K splits add into C with int32 atomics (exact, order-free).  C is zeroed inside the launch by
 //     each strip's split 0, with no wait in any data wave: the workgroup's extra protocol wave takes
 //     the call's ticket and, in split 0, zeroes the strip's outputs with agent-scope (write-through)
-//     stores, waits for them and publishes the call's number in the strip's "zeroed" word; in the
-//     other splits it waits for that word.  The data waves only meet it at the barrier before their
+//     stores, waits for them and publishes the call's number in the strip's "zeroed" word at once
+//     (the other splits read it when their own weights have landed, by which time it is there); in
+//     the other splits it waits for that word.  The data waves only meet it at the barrier before their
 //     atomics.
 //
 // Ticket protocol (per strip: a 64-bit ticket counter T and a 64-bit zeroed word Z that persist
@@ -274,9 +275,10 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
     }
 
     if (wave == NW) {
-        __builtin_amdgcn_s_barrier();  // (1) the data waves' weights have landed
         if (zeroer) {
-            // wait until the zeroing stores have completed, then Z += 1 (lane 0 alone enabled)
+            // As soon as the zeroing stores have completed (not at barrier (1), which waits for this
+            // workgroup's weights): Z += 1 (lane 0 alone enabled), so the other splits find it there
+            // when their own weights have landed.
             const unsigned long long one = 1;
             __asm__ volatile(
                 "s_waitcnt vmcnt(0)\n\t"
@@ -287,7 +289,9 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
                 : "=&s"(saved_exec)
                 : "v"(tk + 1), "v"(one)
                 : "memory");
+            __builtin_amdgcn_s_barrier();  // (1)
         } else {
+            __builtin_amdgcn_s_barrier();  // (1) the data waves' weights have landed
             // the coherent (sc1) load of Z, lane 0 alone enabled, then the wait for it and the ticket
             unsigned long long zw;
             __asm__ volatile(
