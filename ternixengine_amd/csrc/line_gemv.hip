@@ -80,6 +80,7 @@ struct LineArgs {
     float* rs_out;                 // AQ: row scales (M), written by workgroup 0
     OutScale os;                   // EPI: float output
     int vec_y;                     // EPI: Y 16-byte aligned
+    int xcd_chunks;                // unit order: 0 split-major by workgroup id, 1 in 8 contiguous chunks
 };
 
 __device__ __forceinline__ int line_swz(int r) { return ((r >> 1) & 3) ^ (((r >> 4) & 1) << 2); }
@@ -114,7 +115,6 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
     static_assert(AQ == 0 || EPI, "fused quantisation comes with the float output");
     constexpr int GW = 8 / NW;  // 16-byte column groups per data wave
     constexpr int STEP = 8192;  // bytes per k-step of the strip (64 rows x 128 bytes)
-    constexpr int QR = AQ ? kLineQK / 256 : 1;
     __shared__ __attribute__((aligned(16))) uint8_t lds[S * STEP];
     __shared__ __attribute__((aligned(16))) float xl[AQ ? kLineQK + 256 : 4];      // rows of X (+ DMA tail)
     __shared__ __attribute__((aligned(16))) float gl[AQ == 2 ? kLineQK + 256 : 4];  // G
@@ -126,8 +126,17 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int strips = args.strips;
-    const int split = (int)blockIdx.x / strips;
-    const int s = (int)blockIdx.x - split * strips;
+    // Workgroup g runs on XCD g mod 8.  With xcd_chunks the split-major unit sequence is cut into 8
+    // contiguous chunks, chunk x taken by the workgroups of XCD x in order, so that neighbouring strips
+    // of one split share an L2 (rows whose length is not a multiple of 128 bytes put one cache line
+    // in two strips).
+    int unit = (int)blockIdx.x;
+    if (args.xcd_chunks) {
+        const int G = strips * args.splits, q = G >> 3, r = G & 7, x = unit & 7;
+        unit = x * q + min(x, r) + (unit >> 3);
+    }
+    const int split = unit / strips;
+    const int s = unit - split * strips;
     const int M = args.M, K = args.K, N = args.N, NB = N >> 2;
     const int s0 = split * S;                 // first k-step
     const int nst = min(S, (K >> 6) - s0);    // k-steps of this unit (>= 1)
@@ -490,7 +499,7 @@ int line_gemv_splits(int K, int S) { return ((K / 64) + S - 1) / S; }
 
 hipError_t launch_line_gemv(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int S, int NW,
                             unsigned long long* tk, int tk_stride, hipStream_t st, const OutScale& os,
-                            const ActQuant& aq) {
+                            const ActQuant& aq, int xcd_chunks) {
     if (!line_gemv_ok(A, B, M, K, N) || tk == nullptr || C == nullptr) return hipErrorInvalidValue;
     const bool epi = os.Y != nullptr;
     if (aq.mode != 0 && (!epi || (size_t)M * (size_t)K > (size_t)kLineQK || aq.X == nullptr || aq.rs_out == nullptr ||
@@ -516,6 +525,7 @@ hipError_t launch_line_gemv(const int8_t* A, const uint8_t* B, int32_t* C, int M
     a.rs_out = aq.rs_out;
     a.os = os;
     a.vec_y = epi && (uintptr_t)os.Y % 16 == 0;
+    a.xcd_chunks = xcd_chunks;
 
     if (a.splits > 64 || (size_t)S * 64 > (size_t)kMaxKPerAccumulator) return hipErrorInvalidValue;
     const dim3 grid((unsigned)(a.strips * a.splits));

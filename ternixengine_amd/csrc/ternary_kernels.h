@@ -101,7 +101,7 @@ bool line_gemv_ok(const int8_t* A, const uint8_t* B, int M, int K, int N);
 int line_gemv_splits(int K, int S);
 hipError_t launch_line_gemv(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int S, int NW,
                             unsigned long long* tk, int tk_stride, hipStream_t st, const OutScale& os = OutScale{},
-                            const ActQuant& aq = ActQuant{});
+                            const ActQuant& aq = ActQuant{}, int xcd_chunks = 0);
 // (os.Y set: float output through the last-arriving split of each strip, C then being the int32 buffer
 // of the sums, tickets spread one line per strip; aq.mode 1 / 2: fused activation quantisation of
 // fp32 rows aq.X with M * K <= 8192, only with os.Y.)

@@ -527,7 +527,13 @@ bool run_line_gemv(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int 
     c.note("line_gemv_kernel S=%d waves=%d+1 splits=%d%s%s (splits added with int32 atomics into C zeroed by each "
            "strip's split 0)", S, NW, splits, aq.mode == 2 ? " rmsnorm+quantise" : (aq.mode == 1 ? " quantise" : ""),
            epi ? (os.swiglu ? " dequant+swiglu" : " dequant") : "");
-    *e = TX_LAUNCH(c, ternix_hip::launch_line_gemv(dA, dB, dC, M, K, N, S, NW, tk, stride, c.st, os, aq));
+    // Rows whose length is not a multiple of 128 bytes share a cache line between neighbouring strips:
+    // those launches take the XCD-chunked unit order (on MI355X, cold: 1x4096x11008 6.40 -> 5.70 us,
+    // 4x4096x11008 7.15 -> 6.46, 1x2560x6912 4.35 -> 4.20; neutral to 3 % slower on aligned rows).
+    // The DBG_LINE switch [2] forces it off (0) or on (1).
+    const int fx = ternix_hip::debug_get(ternix_hip::DBG_LINE, 2);
+    const int xcd = fx >= 0 ? fx : (N / 4) % 128 != 0;
+    *e = TX_LAUNCH(c, ternix_hip::launch_line_gemv(dA, dB, dC, M, K, N, S, NW, tk, stride, c.st, os, aq, xcd));
     return true;
 }
 

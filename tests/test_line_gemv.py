@@ -2,7 +2,7 @@
 workgroup, all staged at once, K splits added with int32 atomics into C that each strip's split 0
 zeroes inside the launch.  Bit-exact against the CPU oracle (the reference's scalar decode, code 10
 included) for every k-step count and wave form, 1 to 4 rows, a partial last strip, a partial last
-split, calls that share the strips' tickets with the other self-zeroing GEMV issued back to back,
+split, both unit orders (split-major and the 8 XCD chunks), calls that share the strips' tickets with the other self-zeroing GEMV issued back to back,
 and graph replays with eager calls between."""
 import ctypes
 
@@ -67,17 +67,18 @@ def _reset(p):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("order", [0, 1], ids=["split_major", "xcd_chunks"])
 @pytest.mark.parametrize("form", FORMS, ids=[f"S{s}_W{w}" for s, w in FORMS])
-def test_line_gemv_matches_oracle(oracle, form):
+def test_line_gemv_matches_oracle(oracle, form, order):
     lib = tx._load()
     rng = np.random.default_rng(7 + form[0] * 10 + form[1])
     probs = [_problem(oracle, rng, *sh) for sh in SHAPES]
     try:
-        assert lib.ternix_hip_debug_set(b"line", form[0], form[1], -1, -1) == 0
+        assert lib.ternix_hip_debug_set(b"line", form[0], form[1], order, -1) == 0
         for p in probs:
             if (p[1] // 64 + form[0] - 1) // form[0] > 64:
                 continue  # more than 64 splits: another plan
-            log(f"[line] S={form[0]} W={form[1]} M={p[0]} K={p[1]} N={p[2]}")
+            log(f"[line] S={form[0]} W={form[1]} order={order} M={p[0]} K={p[1]} N={p[2]}")
             _reset(p)
             _run(p)
             hr.synchronize()
