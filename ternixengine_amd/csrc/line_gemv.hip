@@ -1,4 +1,4 @@
-// line_gemv.hip -- gfx950 whole-line decode GEMV (M <= 4) for the ternary matmul, and its launcher.
+// line_gemv.hip -- gfx950 whole-line decode GEMV (M <= 16) for the ternary matmul, and its launcher.
 // Shared helpers, the weight layout and the decode forms are described in kernel_common.h.
 //
 // Work unit: one 128-byte strip of the packed weight rows (one whole cache line per row, 512 output
@@ -45,6 +45,10 @@
 //     call adds exactly 64 -- split 0 adds 64 - splits at its start, every split 1 once its atomics have
 //     completed), and the split that brings it to 63 mod 64 reads the strip's complete sums back with
 //     coherent loads and writes Y.  One launch, no dequantisation launch.
+//   * RG: ragged operands (K not a multiple of 64, N/4 not a multiple of 16, A or W at any address),
+//     int32 output: the weights are staged through registers from aligned dwords instead of the
+//     DMA, the last k-step is partial (zero rows past K), and the outputs past N are not written --
+//     no padded copy of the operands, one launch.
 
 #include <hip/hip_runtime.h>
 #include <math.h>
@@ -109,10 +113,11 @@ __device__ __forceinline__ float line_block_max(float v, float* red) {
     return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 }
 
-template <int S, int NW, int AQ, bool EPI>
+template <int S, int NW, int AQ, bool EPI, bool RG>
 __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args) {
     static_assert(NW == 4 || NW == 8, "4 or 8 data waves");
     static_assert(AQ == 0 || EPI, "fused quantisation comes with the float output");
+    static_assert(!RG || (AQ == 0 && !EPI), "ragged operands: int32 output from int8 activations");
     constexpr int GW = 8 / NW;  // 16-byte column groups per data wave
     constexpr int STEP = 8192;  // bytes per k-step of the strip (64 rows x 128 bytes)
     __shared__ __attribute__((aligned(16))) uint8_t lds[S * STEP];
@@ -139,7 +144,7 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
     const int s = unit - split * strips;
     const int M = args.M, K = args.K, N = args.N, NB = N >> 2;
     const int s0 = split * S;                 // first k-step
-    const int nst = min(S, (K >> 6) - s0);    // k-steps of this unit (>= 1)
+    const int nst = min(S, ((K + 63) >> 6) - s0);  // k-steps of this unit (>= 1; RG: the last may be partial)
     const int bc0 = s * 128;                  // first byte-column of the strip
     const bool zeroer = split == 0;
     unsigned long long* tk = args.tk + (size_t)args.tk_stride * (size_t)s;
@@ -166,6 +171,50 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
 
     auto issue_weights = [&]() {
         const int r_in = lane >> 3, pos = lane & 7;
+        if constexpr (RG) {
+            // Ragged operands (K % 64, N/4 % 16 or the weights' address arbitrary): register loads of
+            // the same 16-byte pieces as the DMA below, from 4-byte aligned dwords -- only those holding
+            // at least one byte of the piece, so no load leaves the rows' 4-byte aligned extent --
+            // funnel-shifted into place; rows past K are zeros, bytes past the row end are the next
+            // row's (their outputs are not written).  Then written to LDS in the DMA's layout.
+            constexpr int NP = (S * 8 + NW - 1) / NW;
+            uint32_t d[NP][5];
+            int sh[NP];
+#pragma unroll
+            for (int i = 0; i < NP; ++i) {
+                const int p = wave + NW * i;
+                sh[i] = 0;
+#pragma unroll
+                for (int u = 0; u < 5; ++u) d[i][u] = 0;
+                if (p < S * 8) {
+                    const int step = p >> 3, r = (p & 7) * 8 + r_in;
+                    const int c = pos ^ line_swz(r), col = bc0 + 16 * c;
+                    const int kr = (s0 + step) * 64 + r;
+                    const int v = (step < nst && kr < K) ? min(16, NB - col) : 0;  // bytes of the piece
+                    if (v > 0) {
+                        const uintptr_t src = reinterpret_cast<uintptr_t>(args.B) + (size_t)kr * (size_t)NB + (size_t)col;
+                        const uint32_t* w = reinterpret_cast<const uint32_t*>(src & ~uintptr_t(3));
+                        sh[i] = (int)(src & 3);
+#pragma unroll
+                        for (int u = 0; u < 5; ++u)
+                            if (4 * u < sh[i] + v) d[i][u] = w[u];
+                    }
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < NP; ++i) {
+                const int p = wave + NW * i;
+                if (p < S * 8) {
+                    const uint32_t b = (uint32_t)sh[i] * 8u;
+                    v4i o;
+#pragma unroll
+                    for (int u = 0; u < 4; ++u)
+                        o[u] = (int)(uint32_t)((((uint64_t)d[i][u + 1] << 32) | d[i][u]) >> b);
+                    *reinterpret_cast<v4i*>(lds + (p >> 3) * STEP + (p & 7) * 1024 + lane * 16) = o;
+                }
+            }
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < (S * 8 + NW - 1) / NW; ++i) {
             const int p = wave + NW * i;
@@ -338,7 +387,24 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
     v4i a[S];
 #pragma unroll
     for (int st = 0; st < S; ++st) a[st] = v4i{0, 0, 0, 0};
-    if constexpr (AQ == 0) {
+    if constexpr (RG) {
+        // 16 activations at an arbitrary address, from the 4-byte aligned dwords holding them; those
+        // past K multiply the zero rows above.
+#pragma unroll
+        for (int st = 0; st < S; ++st) {
+            const int k0 = (s0 + st) * 64 + kb * 16, v = st < nst && q < M ? min(16, K - k0) : 0;
+            if (v > 0) {
+                const uintptr_t src = reinterpret_cast<uintptr_t>(args.A) + (size_t)q * (size_t)K + (size_t)k0;
+                const uint32_t* w = reinterpret_cast<const uint32_t*>(src & ~uintptr_t(3));
+                const uint32_t b = (uint32_t)(src & 3) * 8u;
+                uint32_t d[5];
+#pragma unroll
+                for (int u = 0; u < 5; ++u) d[u] = 4 * u < (int)(b / 8) + v ? w[u] : 0u;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) a[st][u] = (int)(uint32_t)((((uint64_t)d[u + 1] << 32) | d[u]) >> b);
+            }
+        }
+    } else if constexpr (AQ == 0) {
         const int8_t* arow = args.A + (size_t)min(q, M - 1) * (size_t)K + (size_t)s0 * 64 + kb * 16;
 #pragma unroll
         for (int st = 0; st < S; ++st)
@@ -375,9 +441,11 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
             }
         }
     }
-    TX_LGKMCNT0();  // AQ: the int8 rows are in LDS
+    TX_LGKMCNT0();  // AQ: the int8 rows are in LDS; RG: the weights' LDS writes
     TX_VMCNT(0);
+    if constexpr (RG) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     __builtin_amdgcn_s_barrier();  // (1) every data wave's weights are in LDS
+    if constexpr (RG) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (AQ != 0) {
 #pragma unroll
@@ -437,25 +505,34 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
     __builtin_amdgcn_s_barrier();  // (2) every wave is done with the stage buffers; C is zeroed
     __builtin_amdgcn_sched_barrier(0);
 
-    // Epilogue: lane (q, kb = 0) holds rows i < 4 of columns 4 (bc0 + 16 g + q) + j.  Each wave lays a
-    // row's 64 outputs of a group out in column order in its own 256 bytes of the idle stage buffer,
-    // then adds one column per lane: 64 consecutive int32 per atomic instruction.
+    // Epilogue: lane (q, kb) holds rows 4 kb + i (i < 4) of columns 4 (bc0 + 16 g + q) + j.  Each wave
+    // lays a row's 64 outputs of a group out in column order in its own 256 bytes of the idle stage
+    // buffer, then adds one column per lane: 64 consecutive int32 per atomic instruction.
     int32_t* rb = reinterpret_cast<int32_t*>(lds) + wave * 64;
 #pragma unroll
     for (int gi = 0; gi < GW; ++gi) {
         const int g = wave * GW + gi;
         if (bc0 + 16 * g >= NB) continue;  // wave-uniform
         int32_t* out = args.C + 4 * (bc0 + 16 * g) + lane;
-        for (int i = 0; i < M; ++i) {
-            if (kb == 0) {
-                const v4i v = {acc[gi][0][i] >> 6, acc[gi][1][i] >> 6, acc[gi][2][i] >> 6, acc[gi][3][i] >> 6};
-                *reinterpret_cast<v4i*>(rb + 4 * q) = v;
+        const bool in_row = !RG || 4 * (bc0 + 16 * g) + lane < N;  // RG: a partial last group
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4)
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii) {
+                const int i = 4 * i4 + ii;
+                if (i < M) {  // workgroup-uniform
+                    if (kb == i4) {
+                        const v4i v = {acc[gi][0][ii] >> 6, acc[gi][1][ii] >> 6, acc[gi][2][ii] >> 6,
+                                       acc[gi][3][ii] >> 6};
+                        *reinterpret_cast<v4i*>(rb + 4 * q) = v;
+                    }
+                    __builtin_amdgcn_wave_barrier();
+                    const int32_t v = rb[lane];
+                    __builtin_amdgcn_wave_barrier();
+                    if (in_row)
+                        __hip_atomic_fetch_add(out + (size_t)i * (size_t)N, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
             }
-            __builtin_amdgcn_wave_barrier();
-            const int32_t v = rb[lane];
-            __builtin_amdgcn_wave_barrier();
-            __hip_atomic_fetch_add(out + (size_t)i * (size_t)N, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
     }
     if constexpr (EPI) {
         // Count this split once its atomics have completed; the split that brings the strip's
@@ -490,18 +567,25 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
 
 bool line_gemv_ok(const int8_t* A, const uint8_t* B, int M, int K, int N) {
     const int NB = N / 4;
-    return M >= 1 && M <= 4 && K >= 64 && K % 64 == 0 && NB % 16 == 0 && (uintptr_t)A % 16 == 0 &&
+    return M >= 1 && M <= 16 && K >= 64 && K % 64 == 0 && N % 4 == 0 && NB % 16 == 0 && (uintptr_t)A % 16 == 0 &&
            (uintptr_t)B % 16 == 0 && (size_t)K * (size_t)NB < ((size_t)1 << 40);
 }
 
-int line_gemv_splits(int K, int S) { return ((K / 64) + S - 1) / S; }
+bool line_gemv_ragged_ok(int M, int K, int N) {
+    return M >= 1 && M <= 16 && K >= 1 && N >= 4 && N % 4 == 0 && (size_t)K * (size_t)(N / 4) < ((size_t)1 << 40);
+}
+
+int line_gemv_splits(int K, int S) { return ((K + 63) / 64 + S - 1) / S; }
 
 
 hipError_t launch_line_gemv(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int S, int NW,
                             unsigned long long* tk, int tk_stride, hipStream_t st, const OutScale& os,
                             const ActQuant& aq, int xcd_chunks) {
-    if (!line_gemv_ok(A, B, M, K, N) || tk == nullptr || C == nullptr) return hipErrorInvalidValue;
+    const bool ragged = !line_gemv_ok(A, B, M, K, N);
     const bool epi = os.Y != nullptr;
+    if ((ragged && (!line_gemv_ragged_ok(M, K, N) || epi || aq.mode != 0)) || tk == nullptr || C == nullptr ||
+        (uintptr_t)C % 8 != 0 || (M > 4 && aq.mode != 0))
+        return hipErrorInvalidValue;
     if (aq.mode != 0 && (!epi || (size_t)M * (size_t)K > (size_t)kLineQK || aq.X == nullptr || aq.rs_out == nullptr ||
                          (aq.mode == 2 && aq.G == nullptr) || (uintptr_t)aq.X % 16 != 0 ||
                          (aq.mode == 2 && (uintptr_t)aq.G % 16 != 0)))
@@ -529,25 +613,27 @@ hipError_t launch_line_gemv(const int8_t* A, const uint8_t* B, int32_t* C, int M
 
     if (a.splits > 64 || (size_t)S * 64 > (size_t)kMaxKPerAccumulator) return hipErrorInvalidValue;
     const dim3 grid((unsigned)(a.strips * a.splits));
-    const int mode = epi ? 1 + aq.mode : 0;  // 0 int32 out, 1 dequantised, 2 / 3 with fused quantisation
-#define TX_LINE(SS, WW, AQQ, EE)                                                                           \
-    if (S == SS && NW == WW && mode == (EE ? 1 + AQQ : 0)) {                                               \
-        hipLaunchKernelGGL((line_gemv_kernel<SS, WW, AQQ, EE>), grid, dim3(64 * (WW + 1)), 0, st, a);     \
-        return hipGetLastError();                                                                          \
+    // 0 int32 out, 1 dequantised, 2 / 3 with fused quantisation, 4 int32 out from ragged operands
+    const int mode = ragged ? 4 : (epi ? 1 + aq.mode : 0);
+#define TX_LINE(SS, WW, AQQ, EE, RR)                                                                         \
+    if (S == SS && NW == WW && mode == (RR ? 4 : (EE ? 1 + AQQ : 0))) {                                      \
+        hipLaunchKernelGGL((line_gemv_kernel<SS, WW, AQQ, EE, RR>), grid, dim3(64 * (WW + 1)), 0, st, a);   \
+        return hipGetLastError();                                                                            \
     }
-#define TX_LINE_S(SS)            \
-    TX_LINE(SS, 8, 0, false)     \
-    TX_LINE(SS, 8, 0, true)      \
-    TX_LINE(SS, 8, 1, true)      \
-    TX_LINE(SS, 8, 2, true)
-    TX_LINE(1, 8, 0, false)
+#define TX_LINE_S(SS)                   \
+    TX_LINE(SS, 8, 0, false, false)     \
+    TX_LINE(SS, 8, 0, true, false)      \
+    TX_LINE(SS, 8, 1, true, false)      \
+    TX_LINE(SS, 8, 2, true, false)      \
+    TX_LINE(SS, 8, 0, false, true)
+    TX_LINE(1, 8, 0, false, false)
     TX_LINE_S(2)
     TX_LINE_S(3)
     TX_LINE_S(4)
     TX_LINE_S(6)
     TX_LINE_S(8)
-    TX_LINE(2, 4, 0, false)
-    TX_LINE(4, 4, 0, false)
+    TX_LINE(2, 4, 0, false, false)
+    TX_LINE(4, 4, 0, false, false)
 #undef TX_LINE_S
 #undef TX_LINE
     return hipErrorInvalidValue;

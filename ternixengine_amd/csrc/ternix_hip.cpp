@@ -482,16 +482,27 @@ bool run_atomic_wave(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, in
 // Plan: the fewest k-steps per workgroup (2, 3, 4, 6 or 8) whose grid stays within about one
 // workgroup per CU (<= 250 workgroups) with at most 64 splits per strip; none for wide matrices that
 // would need more (the DMA-staged and wave kernels keep those).  The DBG_LINE switch turns it off (0)
-// or forces the k-steps [0] and data waves [1].
+// or forces the k-steps [0] and data waves [1]; [2] forces the unit order, [3] raises the row limit
+// (up to 16).  Ragged operands (any K, N % 4 == 0, any A / W address) take the kernel's ragged form
+// with an int32 output.
 bool run_line_gemv(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int K, int N, Ctx& c, hipError_t* e,
                    const ternix_hip::OutScale& os = ternix_hip::OutScale{},
                    const ternix_hip::ActQuant& aq = ternix_hip::ActQuant{}) {
     const int fs = ternix_hip::debug_get(ternix_hip::DBG_LINE, 0), fw = ternix_hip::debug_get(ternix_hip::DBG_LINE, 1);
     if (fs == 0) return false;
-    if (!(dC != nullptr && reinterpret_cast<uintptr_t>(dC) % 16 == 0 && ternix_hip::line_gemv_ok(dA, dB, M, K, N)))
-        return false;
     const bool epi = os.Y != nullptr;
-    if (aq.mode != 0 && !(epi && (long)M * K <= 8192 && reinterpret_cast<uintptr_t>(aq.X) % 16 == 0 &&
+    const bool ragged = !ternix_hip::line_gemv_ok(dA, dB, M, K, N);
+    // Rows: up to 4 on aligned operands (5-16 rows measured slower than the wave-pipelined kernel:
+    // 16x2560x6912 9.20 against 7.02 us, more splits of 16-row atomics), up to 16 on ragged ones (no
+    // padded copy); the DBG_LINE switch [3] sets the limit.
+    // Ragged rows past 4 need K >= 1024: on short K the few workgroups serialise their 16-row atomics
+    // (16x130x2044 6.90 against 5.44 us with the padded copy; 16x4093x1028 7.93 against 8.64).
+    const int fm = ternix_hip::debug_get(ternix_hip::DBG_LINE, 3);
+    if (M > (fm > 0 ? std::min(fm, 16) : (ragged && K >= 1024 ? 16 : 4))) return false;
+    if (!(dC != nullptr && reinterpret_cast<uintptr_t>(dC) % 16 == 0 &&
+          (!ragged || (!epi && aq.mode == 0 && ternix_hip::line_gemv_ragged_ok(M, K, N)))))
+        return false;
+    if (aq.mode != 0 && !(epi && M <= 4 && (long)M * K <= 8192 && reinterpret_cast<uintptr_t>(aq.X) % 16 == 0 &&
                           (aq.mode != 2 || reinterpret_cast<uintptr_t>(aq.G) % 16 == 0)))
         return false;
     if (epi) {
@@ -518,14 +529,14 @@ bool run_line_gemv(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int 
         }
         if (S == 0) return false;
     }
-    const int NW = fw == 4 && !epi ? 4 : 8;
+    const int NW = fw == 4 && !epi && !ragged ? 4 : 8;
     const int splits = ternix_hip::line_gemv_splits(K, S);
     if (splits > 64) return false;
     const int stride = ternix_hip::ticket_stride((size_t)strips);
     unsigned long long* tk = c.tickets(ternix_hip::ticket_units((size_t)strips));
     if (!tk) return false;
-    c.note("line_gemv_kernel S=%d waves=%d+1 splits=%d%s%s (splits added with int32 atomics into C zeroed by each "
-           "strip's split 0)", S, NW, splits, aq.mode == 2 ? " rmsnorm+quantise" : (aq.mode == 1 ? " quantise" : ""),
+    c.note("line_gemv_kernel%s S=%d waves=%d+1 splits=%d%s%s (splits added with int32 atomics into C zeroed by each "
+           "strip's split 0)", ragged ? " ragged" : "", S, NW, splits, aq.mode == 2 ? " rmsnorm+quantise" : (aq.mode == 1 ? " quantise" : ""),
            epi ? (os.swiglu ? " dequant+swiglu" : " dequant") : "");
     // Rows whose length is not a multiple of 128 bytes share a cache line between neighbouring strips:
     // those launches take the XCD-chunked unit order (on MI355X, cold: 1x4096x11008 6.40 -> 5.70 us,
@@ -831,7 +842,10 @@ hipError_t run_auto(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int
     (void)st;
     const bool pad_off = ternix_hip::debug_get(ternix_hip::DBG_RAGGED_PAD) == 0;  // tests: generic kernels
     if (!pad_off && needs_padding(dA, dB, K, N, M <= skinny_max)) {
-        const hipError_t e = run_padded(dA, dB, dC, M, K, N, c, os, M <= skinny_max);
+        // up to 16 rows, int32 output: the whole-line GEMV reads the ragged operands as they are, one launch
+        hipError_t e = hipSuccess;
+        if (M <= skinny_max && os.Y == nullptr && run_line_gemv(dA, dB, dC, M, K, N, c, &e)) return e;
+        e = run_padded(dA, dB, dC, M, K, N, c, os, M <= skinny_max);
         if (e != hipErrorNotSupported) return e;
     }
     if (M > skinny_max && M <= 64 && os.Y == nullptr && K % 64 == 0) {  // 33..64 rows: the atomic wave plan if it applies

@@ -34,8 +34,10 @@ def test_plan_names_line_kernel_when_forced():
     try:
         assert lib.ternix_hip_debug_set(b"line", 2, 8, -1, -1) == 0
         assert _plan(lib, 1, 2560, 6912).startswith("line_gemv_kernel S=2 waves=8+1 splits=20")
-        assert not _plan(lib, 5, 2560, 6912).startswith("line_gemv_kernel")  # M <= 4 only
-        assert not _plan(lib, 1, 2560, 6900).startswith("line_gemv_kernel")  # N/4 % 16 != 0
+        assert not _plan(lib, 5, 2560, 6912).startswith("line_gemv_kernel")  # aligned: M <= 4 only
+        assert _plan(lib, 1, 2560, 6900).startswith("line_gemv_kernel ragged S=2")  # N/4 % 16 != 0
+        assert _plan(lib, 16, 2560, 6900).startswith("line_gemv_kernel ragged")  # ragged: up to 16 rows
+        assert not _plan(lib, 16, 1000, 6900).startswith("line_gemv_kernel")  # ... with K >= 1024
         assert lib.ternix_hip_debug_set(b"line", 1, 8, -1, -1) == 0
         assert not _plan(lib, 1, 8192, 4096).startswith("line_gemv_kernel")  # 128 splits > 64
     finally:
@@ -190,3 +192,88 @@ def test_line_gemv_ffn_forward_bit_equal(shape):
     log(f"[line ffn] M={m} H={h} F={f}")
     off, on = _line_off_and_on(lib, lambda: tx.ffn_forward(x, g, 1e-5, wgu, 0.02, wd, 0.03))
     assert np.isfinite(on).all() and np.array_equal(off.view(np.int32), on.view(np.int32))
+
+
+def _ragged_problem(oracle, rng, m, k, n, a_off, b_off):
+    """Operands placed at byte offsets a_off / b_off of their buffers, the weights ending exactly at
+    the end of theirs (so the kernel's last aligned dword is the buffer's last)."""
+    a = rng.integers(-128, 128, size=(m, k), dtype=np.int8)
+    wp = rng.integers(0, 256, size=(k, n // 4), dtype=np.uint8)
+    da = hr.DeviceBuffer(a.nbytes + a_off)
+    db = hr.DeviceBuffer(wp.nbytes + b_off)
+    for buf, arr, off in ((da, a, a_off), (db, wp, b_off)):
+        hr.check(hr._load().hipMemcpy(ctypes.c_void_p(buf.value + off), arr.ctypes.data_as(ctypes.c_void_p),
+                                      arr.nbytes, hr.H2D), "upload")
+    return (m, k, n, da, db, hr.DeviceBuffer(4 * (m * n + GUARD)), oracle.mm("scalar_mt", a, wp, n), a_off, b_off)
+
+
+GUARD = 1024  # int32 after C that no call may write
+
+
+def _check_guarded(dc, m, n, expect, tag):
+    got = dc.download(np.int32, (m * n + GUARD,))
+    assert (got[m * n:] == GARBAGE).all(), (tag, "guard region written")
+    got = got[:m * n].reshape(m, n)
+    assert (got == expect).all(), (tag, int((got != expect).sum()))
+
+
+# (M, K, N, A offset, W offset): the ragged configurations, K < 64, one byte per row, odd row lengths,
+# misaligned operands on aligned shapes, a partial last 16-byte group
+RAGGED = [(1, 1000, 3076, 0, 0), (4, 1000, 3076, 0, 0), (2, 4093, 1028, 0, 0), (3, 37, 20, 0, 0),
+          (1, 5, 4, 0, 0), (2, 777, 516, 3, 1), (4, 4096, 1024, 3, 0), (1, 2560, 6912, 0, 2),
+          (3, 130, 2044, 1, 3), (1, 8191, 2052, 0, 0), (12, 1500, 3076, 0, 0), (16, 4093, 1028, 2, 1)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape", RAGGED, ids=lambda s: "x".join(map(str, s)))
+def test_line_gemv_ragged_matches_oracle(oracle, shape):
+    """Ragged and misaligned operands go to the whole-line GEMV's register-staged form (no padded
+    copy): bit-exact against the oracle, twice in a row on the same tickets, and in graph replays."""
+    lib = tx._load()
+    m, k, n, ao, bo = shape
+    p = _ragged_problem(oracle, np.random.default_rng(sum(shape)), *shape)
+    _, _, _, da, db, dc, expect, _, _ = p
+    buf = ctypes.create_string_buffer(192)
+    assert lib.ternix_hip_plan_describe((1 << 20) + ao, (1 << 24) + bo, m, k, n, buf, len(buf)) == 0
+    assert buf.value.decode().startswith("line_gemv_kernel ragged"), buf.value
+    s = hr.Stream()
+    call = lambda: tx.mul_mat_ternary(da.value + ao, db.value + bo, dc.value, m, k, n, stream=s.handle)
+    log(f"[line ragged] M={m} K={k} N={n} A+{ao} W+{bo}")
+    for rep in range(2):
+        dc.upload(np.full(m * n + GUARD, GARBAGE, np.int32))
+        assert call() == 0
+        s.synchronize()
+        _check_guarded(dc, m, n, expect, rep)
+    g = hr.Graph(s, call)
+    for rep in range(3):
+        dc.upload(np.full(m * n + GUARD, GARBAGE, np.int32))
+        g.launch()
+        s.synchronize()
+        _check_guarded(dc, m, n, expect, ("replay", rep))
+        assert call() == 0
+        s.synchronize()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape", [(5, 2560, 6912), (8, 4096, 4096), (16, 2560, 2560), (16, 6912, 2560),
+                                   (12, 1000, 3076), (7, 64, 512)], ids=lambda s: "x".join(map(str, s)))
+def test_line_gemv_up_to_16_rows(oracle, shape):
+    """With the row limit raised to 16, 5-16 rows run through the whole-line GEMV (every lane group's
+    rows in the epilogue), aligned and ragged, bit-exact against the oracle."""
+    lib = tx._load()
+    m, k, n = shape
+    p = _ragged_problem(oracle, np.random.default_rng(sum(shape)), m, k, n, 0, 0)
+    _, _, _, da, db, dc, expect, _, _ = p
+    try:
+        assert lib.ternix_hip_debug_set(b"line", -1, -1, -1, 16) == 0
+        buf = ctypes.create_string_buffer(192)
+        assert lib.ternix_hip_plan_describe(1 << 20, 1 << 24, m, k, n, buf, len(buf)) == 0
+        assert buf.value.decode().startswith("line_gemv_kernel"), buf.value
+        log(f"[line 16 rows] M={m} K={k} N={n}")
+        for rep in range(2):
+            dc.upload(np.full(m * n + GUARD, GARBAGE, np.int32))
+            assert tx.mul_mat_ternary(da.value, db.value, dc.value, m, k, n) == 0
+            hr.synchronize()
+            _check_guarded(dc, m, n, expect, rep)
+    finally:
+        lib.ternix_hip_debug_reset()
