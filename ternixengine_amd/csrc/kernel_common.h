@@ -89,12 +89,13 @@ __device__ __forceinline__ int xcd_linear(int id, int total) {
 // With os.swiglu the four values are two interleaved (gate, up) pairs and the stored row is N/2 wide:
 // h[col/2 + p] = silu(y[2p]) * y[2p+1], silu(g) = g / (1 + exp(-g)) (reference src/simd_math.cpp:40-46).
 typedef float v2f __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ void store_scaled_f(const OutScale& os, float f, int row, int N, int col, v4i c, int vec);
+__device__ __forceinline__ float store_scaled_f(const OutScale& os, float f, int row, int N, int col, v4i c, int vec);
 __device__ __forceinline__ void store_scaled(const OutScale& os, int row, int N, int col, v4i c, int vec) {
     store_scaled_f(os, os.rs[row] * os.ws, row, N, col, c, vec);
 }
-// As store_scaled with the combined scale f = row_scale * w_scale given.
-__device__ __forceinline__ void store_scaled_f(const OutScale& os, float f, int row, int N, int col, v4i c, int vec) {
+// As store_scaled with the combined scale f = row_scale * w_scale given.  Returns the largest |value|
+// stored (fmaxf from 0, as the absmax of the row statistics takes it).
+__device__ __forceinline__ float store_scaled_f(const OutScale& os, float f, int row, int N, int col, v4i c, int vec) {
     const v4f y = {(float)c[0] * f, (float)c[1] * f, (float)c[2] * f, (float)c[3] * f};
     if (os.swiglu) {
         const v2f h = {(y[0] / (1.0f + expf(-y[0]))) * y[1], (y[2] / (1.0f + expf(-y[2]))) * y[3]};
@@ -105,7 +106,7 @@ __device__ __forceinline__ void store_scaled_f(const OutScale& os, float f, int 
             out[0] = h[0];
             out[1] = h[1];
         }
-        return;
+        return fmaxf(fmaxf(0.0f, fabsf(h[0])), fabsf(h[1]));
     }
     float* out = os.Y + (size_t)row * (size_t)N + col;
     if (vec) {
@@ -114,6 +115,7 @@ __device__ __forceinline__ void store_scaled_f(const OutScale& os, float f, int 
 #pragma unroll
         for (int j = 0; j < 4; ++j) out[j] = y[j];
     }
+    return fmaxf(fmaxf(fmaxf(fmaxf(0.0f, fabsf(y[0])), fabsf(y[1])), fabsf(y[2])), fabsf(y[3]));
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -216,6 +218,9 @@ __device__ __forceinline__ uint32_t lds_read_b32_asm(uint32_t addr) {
 // with lgkmcnt before anything reads it.
 __device__ __forceinline__ void lds_write_b8_asm(uint32_t addr, uint32_t v) {
     __asm__ volatile("ds_write_b8 %0, %1" : : "v"(addr), "v"(v) : "memory");
+}
+__device__ __forceinline__ void lds_write_b32_asm(uint32_t addr, uint32_t v) {
+    __asm__ volatile("ds_write_b32 %0, %1" : : "v"(addr), "v"(v) : "memory");
 }
 __device__ __forceinline__ uint32_t lds_u32(const void* p) {
     return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;

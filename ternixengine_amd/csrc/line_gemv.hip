@@ -36,9 +36,11 @@
 // Fused forms (the decode feed-forward block's GEMVs, and dequantising calls):
 //   * AQ = 1 / 2: the int8 activations are made inside the kernel from fp32 rows X (absmax
 //     quantisation; AQ = 2 RMS-normalises with weight G first), with the loops and rounding of
-//     row_stats.h, so they are bit-identical to quantize_rows_kernel / rmsnorm_kernel.  Every
-//     workgroup DMAs the rows (and G) into LDS ahead of its weights, computes the row statistics
-//     itself and quantises just the 16 activations each lane feeds the MFMA.
+//     row_stats.h, so they are bit-identical to quantize_rows_kernel / rmsnorm_kernel.  In every
+//     workgroup, data wave r < M DMAs row r (and G) into LDS ahead of its weights, computes the
+//     row's statistics alone (no barrier) and quantises the unit's activations of the row.
+//     AQ = 3: the absmax comes from a producer's per-strip maxima of the rows (amax_in, written by
+//     an EPI launch with amax_out), so only the unit's slice of each row is read.
 //   * EPI: a float output Y = C * (row scale * weight scale), optionally with the SwiGLU of
 //     interleaved (gate, up) column pairs.  The splits add into the int32 buffer C as above; each
 //     split then counts itself on the strip's arrival word (the third word of its ticket line: every
@@ -85,33 +87,13 @@ struct LineArgs {
     OutScale os;                   // EPI: float output
     int vec_y;                     // EPI: Y 16-byte aligned
     int xcd_chunks;                // unit order: 0 split-major by workgroup id, 1 in 8 contiguous chunks
+    float* amax_out;               // EPI: per row and strip, the largest |value| the strip stored (or null)
+    int amax_stride;               // floats between rows of amax_out / amax_in (a multiple of 4)
+    const float* amax_in;          // AQ == 3: the producer's per-strip maxima of the rows of X
+    int amax_n;                    // AQ == 3: entries per row of amax_in
 };
 
 __device__ __forceinline__ int line_swz(int r) { return ((r >> 1) & 3) ^ (((r >> 4) & 1) << 2); }
-
-// row_block_sum / row_block_max of row_stats.h for a workgroup of more than four waves: the same
-// butterfly and the same combine of waves 0-3 (threads 0-255 hold the row; the other waves pass 0 and
-// only keep the barrier count), with plain barriers: no memory fence, so no wave waits here for its
-// weight loads in flight.
-__device__ __forceinline__ float line_block_sum(float v, float* red) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
-    __builtin_amdgcn_s_barrier();  // red may still be read from a previous call
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    TX_LGKMCNT0();
-    __builtin_amdgcn_s_barrier();
-    return (red[0] + red[1]) + (red[2] + red[3]);
-}
-
-__device__ __forceinline__ float line_block_max(float v, float* red) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
-    __builtin_amdgcn_s_barrier();
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    TX_LGKMCNT0();
-    __builtin_amdgcn_s_barrier();
-    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-}
 
 template <int S, int NW, int AQ, bool EPI, bool RG>
 __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args) {
@@ -121,10 +103,11 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
     constexpr int GW = 8 / NW;  // 16-byte column groups per data wave
     constexpr int STEP = 8192;  // bytes per k-step of the strip (64 rows x 128 bytes)
     __shared__ __attribute__((aligned(16))) uint8_t lds[S * STEP];
-    __shared__ __attribute__((aligned(16))) float xl[AQ ? kLineQK + 256 : 4];      // rows of X (+ DMA tail)
-    __shared__ __attribute__((aligned(16))) float gl[AQ == 2 ? kLineQK + 256 : 4];  // G
+    // rows of X at a 1 KB-aligned pitch (AQ 3: the unit's slices), G's copies (AQ 3: the row maxima)
+    __shared__ __attribute__((aligned(16))) float xl[AQ ? kLineQK + 1024 : 4];
+    __shared__ __attribute__((aligned(16))) float gl[AQ == 2 ? kLineQK + 1024 : (AQ == 3 ? 2048 : 4)];
+    __shared__ float emax[16 * 4];  // EPI with amax_out: per wave and row, the largest |stored value|
     __shared__ __attribute__((aligned(16))) int8_t qbuf[AQ ? 4 * S * 64 : 16];  // AQ: the unit's int8 rows
-    __shared__ float red[16];
     __shared__ float rscale[4];
     __shared__ int last_flag;
 
@@ -149,21 +132,33 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
     const bool zeroer = split == 0;
     unsigned long long* tk = args.tk + (size_t)args.tk_stride * (size_t)s;
 
-    // AQ: the M rows of X (and G) go global -> LDS ahead of the weights, 1 KB per wave instruction,
-    // chunk c by data wave c % NW (the last chunk's lanes past the end re-read valid bytes into the
-    // padding), so that waiting for them leaves the weight DMAs in flight.
+    // AQ: wave r < M stages what row r needs, global -> LDS ahead of its weights, 1 KB per instruction
+    // (the last chunk's lanes past the end re-read valid bytes into the row's padding), so that
+    // waiting for it leaves the weight DMAs in flight and involves no other wave:
+    //   AQ 1 / 2: the whole row of X (and, AQ 2, a copy of G) at a 1 KB-aligned row pitch;
+    //   AQ 3: the unit's slice of the row (64 nst activations) and the producer's maxima of the row.
+    const int xpitch = AQ == 3 ? ((S * 256 + 1023) & ~1023) : ((K * 4 + 1023) & ~1023);  // bytes per row
+    const int apitch = (args.amax_stride * 4 + 1023) & ~1023;
     if constexpr (AQ != 0) {
-        if (wave < NW) {
-            const int nx = (M * K * 4 + 1023) >> 10, ng = AQ == 2 ? (K * 4 + 1023) >> 10 : 0;
+        if (wave < M) {
             const uint8_t* xb = reinterpret_cast<const uint8_t*>(args.X);
-            const uint8_t* gb = reinterpret_cast<const uint8_t*>(args.G);
-            for (int c = wave; c < nx + ng; c += NW) {
-                if (c < nx) {
-                    const int off = min(c * 1024 + lane * 16, M * K * 4 - 16);
-                    lds_dma16(xb + off, reinterpret_cast<uint8_t*>(xl) + c * 1024);
-                } else {
-                    const int off = min((c - nx) * 1024 + lane * 16, K * 4 - 16);
-                    lds_dma16(gb + off, reinterpret_cast<uint8_t*>(gl) + (c - nx) * 1024);
+            uint8_t* xd = reinterpret_cast<uint8_t*>(xl) + wave * xpitch;
+            if constexpr (AQ == 3) {
+                const int n = nst * 256;
+                const uint8_t* src = xb + ((size_t)wave * (size_t)K + (size_t)s0 * 64) * 4;
+                for (int c = 0; c * 1024 < n; ++c) lds_dma16(src + min(c * 1024 + lane * 16, n - 16), xd + c * 1024);
+                const int na = args.amax_stride * 4;
+                const uint8_t* asrc = reinterpret_cast<const uint8_t*>(args.amax_in + (size_t)wave * args.amax_stride);
+                uint8_t* ad = reinterpret_cast<uint8_t*>(gl) + wave * apitch;
+                for (int c = 0; c * 1024 < na; ++c) lds_dma16(asrc + min(c * 1024 + lane * 16, na - 16), ad + c * 1024);
+            } else {
+                const int n = K * 4;
+                const uint8_t* src = xb + (size_t)wave * (size_t)n;
+                for (int c = 0; c * 1024 < n; ++c) lds_dma16(src + min(c * 1024 + lane * 16, n - 16), xd + c * 1024);
+                if constexpr (AQ == 2) {
+                    const uint8_t* gb = reinterpret_cast<const uint8_t*>(args.G);
+                    uint8_t* gd = reinterpret_cast<uint8_t*>(gl) + wave * xpitch;
+                    for (int c = 0; c * 1024 < n; ++c) lds_dma16(gb + min(c * 1024 + lane * 16, n - 16), gd + c * 1024);
                 }
             }
         }
@@ -281,54 +276,111 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
         issue_weights();
     }
 
-    // AQ: the row statistics of every row.  Waves 0-3 hold the row (thread t: k = t + 256 j, in
-    // increasing j, the order of row_stats.h) and do the arithmetic; every wave takes part in the
-    // reductions' barriers.  LDS is read with inline-assembly reads, eight per thread and wait: a
-    // compiler-placed LDS read would first wait for every LDS DMA in flight, the weights included.
-    float r_inv[4] = {1.0f, 1.0f, 1.0f, 1.0f}, r_sc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    // AQ: wave r < M makes row r's int8 activations for this unit, with no barrier and no other wave.
+    // The row statistics follow row_stats.h exactly (a 256-thread workgroup, thread t summing
+    // k = t + 256 j in increasing j, the xor butterfly 32 .. 1 over each wave's 64 threads, then
+    // (w0 + w1) + (w2 + w3)): lane l plays threads 4 l .. 4 l + 3 (one 16-byte LDS read each j), the
+    // butterfly's offsets 32 .. 4 are lane offsets 8 .. 1 and 2, 1 are within the lane, and the four
+    // waves' sums sit in lanes 0, 16, 32, 48.  The absmax is a maximum (exact in any order); AQ 3
+    // takes it over the producer's per-strip maxima.  The unit's M x 64 nst values are quantised into
+    // qbuf; rscale[r] (and, in workgroup 0, rs_out[r]) gets the row scale.  LDS is read and written
+    // with inline assembly: a compiler-placed LDS access would first wait for every LDS DMA in flight.
     if constexpr (AQ != 0) {
-        if (wave < NW) TX_VMCNT((S * 8 + NW - 1) / NW);  // this wave's row chunks have landed (its weights may not)
-        __builtin_amdgcn_s_barrier();                      // ... every wave's
-        __builtin_amdgcn_sched_barrier(0);
-        // visit(f): f(x, g) for this thread's elements of row r, in increasing k (waves 0-3 only)
-        auto visit = [&](int r, auto&& f) {
-            if (wave >= 4) return;
-            const uint32_t xa = lds_u32(xl + r * K), ga = lds_u32(gl);
-            for (int k0 = 0; k0 < K; k0 += 2048) {
-                uint32_t xb[8], gb[8];
-#pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    const int k = min(k0 + tid + 256 * u, K - 1);  // clamped: only used when in the row
-                    xb[u] = lds_read_b32_asm(xa + 4 * k);
-                    gb[u] = AQ == 2 ? lds_read_b32_asm(ga + 4 * k) : 0u;
+        if (wave < M) {
+            TX_VMCNT((S * 8 + NW - 1) / NW);  // this wave's row data have landed (its weights may not)
+            const int r = wave;
+            const uint32_t xa = lds_u32(xl) + (uint32_t)(r * xpitch);
+            const uint32_t ga = lds_u32(gl) + (uint32_t)(r * (AQ == 3 ? apitch : xpitch));
+            float inv = 1.0f, m = 0.0f;
+            if constexpr (AQ == 3) {
+                for (int i0 = 0; i0 < args.amax_n; i0 += 64) {
+                    uint32_t v = lds_read_b32_asm(ga + 4 * min(i0 + lane, args.amax_n - 1));
+                    TX_LGKMCNT0();
+                    __asm__ volatile("" : "+v"(v));
+                    if (i0 + lane < args.amax_n) m = fmaxf(m, __uint_as_float(v));
                 }
-                TX_LGKMCNT0();
+            } else {
+                if constexpr (AQ == 2) {
+                    float ss[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                    for (int j0 = 0; j0 < K; j0 += 256 * 8) {
+                        v4i xb[8];
 #pragma unroll
-                for (int u = 0; u < 8; ++u) __asm__ volatile("" : "+v"(xb[u]), "+v"(gb[u]));
+                        for (int u = 0; u < 8; ++u) xb[u] = lds_read_b128_asm(xa + 4 * min(j0 + 256 * u + 4 * lane, K - 4));
+                        TX_LGKMCNT0();
 #pragma unroll
-                for (int u = 0; u < 8; ++u)
-                    if (k0 + tid + 256 * u < K) f(__uint_as_float(xb[u]), __uint_as_float(gb[u]));
+                        for (int u = 0; u < 8; ++u) {
+                            __asm__ volatile("" : "+v"(xb[u]));
+                            if (j0 + 256 * u + 4 * lane < K) {
+#pragma unroll
+                                for (int c = 0; c < 4; ++c) {
+                                    const float x = __int_as_float(xb[u][c]);
+                                    ss[c] = fmaf(x, x, ss[c]);
+                                }
+                            }
+                        }
+                    }
+#pragma unroll
+                    for (int off = 8; off >= 1; off >>= 1)
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) ss[c] += __shfl_xor(ss[c], off);
+                    // offsets 2 and 1: thread 4 l + c holds (ss[c] + ss[c ^ 2]) + (ss[c ^ 1] + ss[c ^ 3]) in
+                    // the same order for c = 0 (the value lanes 16 w pass on as wave w's sum)
+                    const float w = (ss[0] + ss[2]) + (ss[1] + ss[3]);
+                    const float w0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), 0));
+                    const float w1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), 16));
+                    const float w2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), 32));
+                    const float w3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), 48));
+                    inv = 1.0f / sqrtf(((w0 + w1) + (w2 + w3)) / (float)K + args.eps);
+                }
+                for (int j0 = 0; j0 < K; j0 += 256 * 4) {
+                    v4i xb[4], gb[4];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const uint32_t o = 4 * min(j0 + 256 * u + 4 * lane, K - 4);
+                        xb[u] = lds_read_b128_asm(xa + o);
+                        gb[u] = AQ == 2 ? lds_read_b128_asm(ga + o) : v4i{0, 0, 0, 0};
+                    }
+                    TX_LGKMCNT0();
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        __asm__ volatile("" : "+v"(xb[u]), "+v"(gb[u]));
+                        if (j0 + 256 * u + 4 * lane < K) {
+#pragma unroll
+                            for (int c = 0; c < 4; ++c) {
+                                const float x = __int_as_float(xb[u][c]);
+                                m = fmaxf(m, fabsf(AQ == 2 ? x * inv * __int_as_float(gb[u][c]) : x));
+                            }
+                        }
+                    }
+                }
             }
-        };
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            if (r >= M) break;  // workgroup-uniform
-            float inv = 1.0f;
-            if constexpr (AQ == 2) {
-                float ss = 0.0f;
-                visit(r, [&](float x, float) { ss = fmaf(x, x, ss); });
-                ss = line_block_sum(ss, red);
-                inv = 1.0f / sqrtf(ss / (float)K + args.eps);
-            }
-            float amax = 0.0f;
-            visit(r, [&](float x, float g) { amax = fmaxf(amax, fabsf(AQ == 2 ? x * inv * g : x)); });
-            const float am = fmaxf(line_block_max(amax, red), 1e-5f);
-            if (tid == 0) {
-                rscale[r] = am / 127.0f;
+            for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+            const float am = fmaxf(m, 1e-5f), sc = 127.0f / am;
+            if (lane == 0) {
+                lds_write_b32_asm(lds_u32(rscale) + 4 * r, __float_as_uint(am / 127.0f));
                 if (blockIdx.x == 0) args.rs_out[r] = am / 127.0f;
             }
-            r_inv[r] = inv;
-            r_sc[r] = 127.0f / am;
+            // this unit's values of the row: k = 64 s0 + i, i < 64 nst, lane i % 64
+            const uint32_t qa = lds_u32(qbuf) + (uint32_t)(r * (S * 64));
+            uint32_t xv[S], gv[S];
+#pragma unroll
+            for (int u = 0; u < S; ++u) {
+                const int i = min(u, nst - 1) * 64 + lane;
+                const int k = AQ == 3 ? i : s0 * 64 + i;
+                xv[u] = lds_read_b32_asm(xa + 4 * k);
+                gv[u] = AQ == 2 ? lds_read_b32_asm(ga + 4 * k) : 0u;
+            }
+            TX_LGKMCNT0();
+#pragma unroll
+            for (int u = 0; u < S; ++u) {
+                __asm__ volatile("" : "+v"(xv[u]), "+v"(gv[u]));
+                if (u < nst) {
+                    const float x = __uint_as_float(xv[u]);
+                    const float v = AQ == 2 ? x * inv * __uint_as_float(gv[u]) : x;
+                    lds_write_b8_asm(qa + (uint32_t)(u * 64 + lane), (uint32_t)quantize_value(v, sc) & 0xFFu);
+                }
+            }
         }
     }
 
@@ -409,37 +461,6 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
 #pragma unroll
         for (int st = 0; st < S; ++st)
             if (st < nst && q < M) a[st] = *reinterpret_cast<const v4i*>(arow + st * 64);
-    } else {
-        // Quantised once per workgroup: the M x 64 nst activations of the unit, one per data-wave
-        // thread and pass, q = clamp(rint(v * s)), v = x (* inv * g), into LDS as int8 rows; each lane
-        // then reads its 16-byte fragment after the barrier below.
-        const uint32_t xa = lds_u32(xl), ga = lds_u32(gl), qa = lds_u32(qbuf);
-        const int per_row = nst * 64, total = M * per_row;
-        for (int e0 = 0; e0 < total; e0 += NW * 64 * 4) {
-            uint32_t xb[4], gb[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int e = min(e0 + tid + NW * 64 * u, total - 1);
-                const int r = e / per_row, k = s0 * 64 + e % per_row;
-                xb[u] = lds_read_b32_asm(xa + 4 * (r * K + k));
-                gb[u] = AQ == 2 ? lds_read_b32_asm(ga + 4 * k) : 0u;
-            }
-            TX_LGKMCNT0();
-#pragma unroll
-            for (int u = 0; u < 4; ++u) __asm__ volatile("" : "+v"(xb[u]), "+v"(gb[u]));
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int e = e0 + tid + NW * 64 * u;
-                if (e < total) {
-                    const int r = e / per_row, kk = e % per_row;
-                    const float inv = r == 0 ? r_inv[0] : (r == 1 ? r_inv[1] : (r == 2 ? r_inv[2] : r_inv[3]));
-                    const float sc = r == 0 ? r_sc[0] : (r == 1 ? r_sc[1] : (r == 2 ? r_sc[2] : r_sc[3]));
-                    const float xv = __uint_as_float(xb[u]);
-                    const float v = AQ == 2 ? xv * inv * __uint_as_float(gb[u]) : xv;
-                    lds_write_b8_asm(qa + (uint32_t)(r * (S * 64) + kk), (uint32_t)quantize_value(v, sc) & 0xFFu);
-                }
-            }
-        }
     }
     TX_LGKMCNT0();  // AQ: the int8 rows are in LDS; RG: the weights' LDS writes
     TX_VMCNT(0);
@@ -549,6 +570,7 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
         // The strip's sums, read with coherent loads (they bypass this XCD's L2, which may hold none of
         // the other splits' additions), four consecutive columns per lane, every row.
         const int ncol = min(512, N - 4 * bc0);
+        float lm[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // amax_out: per row, the largest |value| this thread stored
         for (int idx = tid; idx < M * 128; idx += NW * 64) {
             const int r = idx >> 7, c4 = (idx & 127) * 4;
             if (c4 >= ncol) continue;
@@ -558,7 +580,26 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
             const unsigned long long u1 = __hip_atomic_load(src + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             const v4i v = {(int)(uint32_t)u0, (int)(uint32_t)(u0 >> 32), (int)(uint32_t)u1, (int)(uint32_t)(u1 >> 32)};
             const float f = (AQ != 0 ? rscale[r] : args.os.rs[r]) * args.os.ws;
-            store_scaled_f(args.os, f, r, N, 4 * bc0 + c4, v, args.vec_y);
+            const float mx = store_scaled_f(args.os, f, r, N, 4 * bc0 + c4, v, args.vec_y);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (i == r) lm[i] = fmaxf(lm[i], mx);
+        }
+        if (args.amax_out != nullptr) {
+            // The strip's largest |value| per row (M <= 4), for the consumer's quantisation.
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float m = lm[i];
+#pragma unroll
+                for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+                if (lane == 0) emax[wave * 4 + i] = m;
+            }
+            __syncthreads();
+            if (tid < M) {
+                float m = 0.0f;
+                for (int w = 0; w < NW; ++w) m = fmaxf(m, emax[w * 4 + tid]);
+                args.amax_out[(size_t)tid * (size_t)args.amax_stride + s] = m;
+            }
         }
     }
 }
@@ -586,9 +627,14 @@ hipError_t launch_line_gemv(const int8_t* A, const uint8_t* B, int32_t* C, int M
     if ((ragged && (!line_gemv_ragged_ok(M, K, N) || epi || aq.mode != 0)) || tk == nullptr || C == nullptr ||
         (uintptr_t)C % 8 != 0 || (M > 4 && aq.mode != 0))
         return hipErrorInvalidValue;
-    if (aq.mode != 0 && (!epi || (size_t)M * (size_t)K > (size_t)kLineQK || aq.X == nullptr || aq.rs_out == nullptr ||
-                         (aq.mode == 2 && aq.G == nullptr) || (uintptr_t)aq.X % 16 != 0 ||
-                         (aq.mode == 2 && (uintptr_t)aq.G % 16 != 0)))
+    if (aq.mode != 0 && (!epi || M > 4 || (aq.mode != 3 && (size_t)M * (size_t)K > (size_t)kLineQK) ||
+                         aq.X == nullptr || aq.rs_out == nullptr || (aq.mode == 2 && aq.G == nullptr) ||
+                         (uintptr_t)aq.X % 16 != 0 || (aq.mode == 2 && (uintptr_t)aq.G % 16 != 0)))
+        return hipErrorInvalidValue;
+    if (aq.mode == 3 && (aq.amax_in == nullptr || (uintptr_t)aq.amax_in % 16 != 0 || aq.amax_n < 1 ||
+                         aq.amax_stride < aq.amax_n || aq.amax_stride % 4 != 0 || M * aq.amax_stride * 4 > 8192))
+        return hipErrorInvalidValue;
+    if (aq.amax_out != nullptr && (!epi || M > 4 || aq.amax_stride < (N / 4 + 127) / 128))
         return hipErrorInvalidValue;
     if (epi && (tk_stride < 4 || (aq.mode == 0 && os.rs == nullptr) || (os.swiglu && N % 8 != 0)))
         return hipErrorInvalidValue;
@@ -610,13 +656,17 @@ hipError_t launch_line_gemv(const int8_t* A, const uint8_t* B, int32_t* C, int M
     a.os = os;
     a.vec_y = epi && (uintptr_t)os.Y % 16 == 0;
     a.xcd_chunks = xcd_chunks;
+    a.amax_out = aq.amax_out;
+    a.amax_stride = aq.amax_stride;
+    a.amax_in = aq.amax_in;
+    a.amax_n = aq.amax_n;
 
     if (a.splits > 64 || (size_t)S * 64 > (size_t)kMaxKPerAccumulator) return hipErrorInvalidValue;
     const dim3 grid((unsigned)(a.strips * a.splits));
-    // 0 int32 out, 1 dequantised, 2 / 3 with fused quantisation, 4 int32 out from ragged operands
-    const int mode = ragged ? 4 : (epi ? 1 + aq.mode : 0);
+    // 0 int32 out, 1 dequantised, 2 / 3 / 4 with fused quantisation, 5 int32 out from ragged operands
+    const int mode = ragged ? 5 : (epi ? 1 + aq.mode : 0);
 #define TX_LINE(SS, WW, AQQ, EE, RR)                                                                         \
-    if (S == SS && NW == WW && mode == (RR ? 4 : (EE ? 1 + AQQ : 0))) {                                      \
+    if (S == SS && NW == WW && mode == (RR ? 5 : (EE ? 1 + AQQ : 0))) {                                      \
         hipLaunchKernelGGL((line_gemv_kernel<SS, WW, AQQ, EE, RR>), grid, dim3(64 * (WW + 1)), 0, st, a);   \
         return hipGetLastError();                                                                            \
     }
@@ -625,6 +675,7 @@ hipError_t launch_line_gemv(const int8_t* A, const uint8_t* B, int32_t* C, int M
     TX_LINE(SS, 8, 0, true, false)      \
     TX_LINE(SS, 8, 1, true, false)      \
     TX_LINE(SS, 8, 2, true, false)      \
+    TX_LINE(SS, 8, 3, true, false)      \
     TX_LINE(SS, 8, 0, false, true)
     TX_LINE(1, 8, 0, false, false)
     TX_LINE_S(2)

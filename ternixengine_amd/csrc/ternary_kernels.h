@@ -48,6 +48,7 @@ enum DebugKey : int {
     DBG_NT,              // [0] DMA-staged GEMV, [1] wave-pipelined GEMV: 1 non-temporal weight loads, 0 plain
     DBG_WAVE_TICKET,     // [0] 1 / 0: wave-pipelined GEMV waits for its split ticket in the first step / before it
     DBG_LINE,            // [0] 0: no whole-line GEMV; > 0: its k-steps per workgroup forced; [1] its data waves (4 / 8)
+    DBG_FFN_AMAX,        // [0] == 0: the decode FFN block's down GEMV takes whole rows of h, not the maxima
     DBG_COUNT
 };
 int debug_get(DebugKey key, int idx = 0);
@@ -93,6 +94,13 @@ struct ActQuant {
     const float* G = nullptr;
     float eps = 0.0f;
     float* rs_out = nullptr;
+    // Whole-line GEMV only.  Producer (float output): per row and strip the largest |value| stored,
+    // at amax_out[row * amax_stride + strip].  Consumer (mode 3): X's rows quantised with the absmax
+    // taken from amax_in[row * amax_stride + i], i < amax_n (a producer's per-strip maxima of X).
+    float* amax_out = nullptr;
+    const float* amax_in = nullptr;
+    int amax_stride = 0;
+    int amax_n = 0;
 };
 // Whole-line decode GEMV (line_gemv.hip): M <= 16, K % 64 == 0, N/4 % 16 == 0, 16-byte aligned A and W
 // (or, int32 output only, any K, N % 4 == 0 and any A / W address: the ragged form); 8-byte aligned C;
@@ -106,7 +114,8 @@ hipError_t launch_line_gemv(const int8_t* A, const uint8_t* B, int32_t* C, int M
                             const ActQuant& aq = ActQuant{}, int xcd_chunks = 0);
 // (os.Y set: float output through the last-arriving split of each strip, C then being the int32 buffer
 // of the sums, tickets spread one line per strip; aq.mode 1 / 2: fused activation quantisation of
-// fp32 rows aq.X with M <= 4 and M * K <= 8192, only with os.Y.)
+// fp32 rows aq.X with M <= 4 and M * K <= 8192, only with os.Y; mode 3: any K, from a producer's
+// per-strip maxima.)
 bool skinny_short_ok(const uint8_t* B, int M, int K, int N, int steps_per_split, int splits);
 // True when the DMA-staged skinny kernel can run this call: M <= 16, K % 64 == 0, N % 256 == 0,
 // 16-byte aligned A and W, 1..16 k-steps per split.

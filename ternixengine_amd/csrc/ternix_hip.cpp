@@ -502,7 +502,7 @@ bool run_line_gemv(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int 
     if (!(dC != nullptr && reinterpret_cast<uintptr_t>(dC) % 16 == 0 &&
           (!ragged || (!epi && aq.mode == 0 && ternix_hip::line_gemv_ragged_ok(M, K, N)))))
         return false;
-    if (aq.mode != 0 && !(epi && M <= 4 && (long)M * K <= 8192 && reinterpret_cast<uintptr_t>(aq.X) % 16 == 0 &&
+    if (aq.mode != 0 && !(epi && M <= 4 && (aq.mode == 3 || (long)M * K <= 8192) && reinterpret_cast<uintptr_t>(aq.X) % 16 == 0 &&
                           (aq.mode != 2 || reinterpret_cast<uintptr_t>(aq.G) % 16 == 0)))
         return false;
     if (epi) {
@@ -1160,8 +1160,10 @@ namespace {
 // Feed-forward workspace: q1 [M][H] int8 | rs1 [M] | h [M][F] f32 | q2 [M][F] int8 | rs2 [M] |
 // scratch [M][2F] int32 (used only when a matmul cannot fuse its epilogue); 256-byte aligned regions.
 struct FfnLayout {
-    size_t q1, rs1, h, q2, rs2, scratch, total;
+    size_t q1, rs1, h, q2, rs2, scratch, amax, total;
 };
+// Per row, one float per 128-byte strip of the gate/up weights (2F/4 bytes a row), rounded up to 4.
+int ffn_amax_stride(int64_t F) { return (int)(((2 * F / 4 + 127) / 128 + 3) / 4 * 4); }
 FfnLayout ffn_layout(int64_t M, int64_t H, int64_t F) {
     auto up = [](size_t x) { return (x + 255) & ~size_t(255); };
     FfnLayout l{};
@@ -1172,6 +1174,7 @@ FfnLayout ffn_layout(int64_t M, int64_t H, int64_t F) {
     l.q2 = o; o = up(o + (size_t)M * (size_t)F);
     l.rs2 = o; o = up(o + 4 * (size_t)M);
     l.scratch = o; o = up(o + 8 * (size_t)M * (size_t)F);
+    l.amax = o; o = up(o + 4 * (size_t)M * (size_t)ffn_amax_stride(F));
     l.total = o;
     return l;
 }
@@ -1201,6 +1204,7 @@ int ternix_hip_ffn_forward(float* dY, const float* dX, const float* dNormWeight,
     int8_t* q2 = reinterpret_cast<int8_t*>(ws + l.q2);
     float* rs2 = reinterpret_cast<float*>(ws + l.rs2);
     int32_t* scratch = reinterpret_cast<int32_t*>(ws + l.scratch);
+    float* amax = reinterpret_cast<float*>(ws + l.amax);
     hipStream_t st = static_cast<hipStream_t>(stream);
     const int m = (int)M, hd = (int)H, f = (int)F;
     // Decode shapes: the RMSNorm + quantisation of x and the requantisation of h run inside the two
@@ -1229,6 +1233,26 @@ int ternix_hip_ffn_forward(float* dY, const float* dX, const float* dNormWeight,
         aq2.mode = 1;
         aq2.X = h;
         aq2.rs_out = rs2;
+        // Both on the whole-line GEMV: the gate/up launch also leaves each strip's largest |h| per row,
+        // so the down launch quantises h from its own slice and those maxima (the absmax is exact in
+        // any order) instead of every workgroup reading whole rows of h.
+        if (ternix_hip::debug_get(ternix_hip::DBG_FFN_AMAX) != 0) {
+            Ctx c = ctx_of(st);
+            hipError_t e = hipSuccess;
+            ternix_hip::ActQuant g1 = aq1;
+            g1.amax_out = amax;
+            g1.amax_stride = ffn_amax_stride(F);
+            if (run_line_gemv(nullptr, dWgu, scratch, m, hd, 2 * f, c, &e, os1, g1)) {
+                if (e != hipSuccess) return (int)e;
+                ternix_hip::ActQuant g2 = aq2;
+                g2.mode = 3;
+                g2.amax_in = amax;
+                g2.amax_stride = g1.amax_stride;
+                g2.amax_n = (2 * f / 4 + 127) / 128;
+                if (run_line_gemv(nullptr, dWd, reinterpret_cast<int32_t*>(dY), m, f, hd, c, &e, os2, g2)) return (int)e;
+                return (int)run_skinny(nullptr, dWd, reinterpret_cast<int32_t*>(dY), m, f, hd, c, os2, aq2);
+            }
+        }
         const SkinnyPlan p1 = plan_skinny(m, hd, 2 * f), p2 = plan_skinny(m, f, hd);
         if (ternix_hip::skinny_short_ok(dWgu, m, hd, 2 * f, p1.sps, p1.splits) &&
             ternix_hip::skinny_short_ok(dWd, m, f, hd, p2.sps, p2.splits)) {
@@ -1381,7 +1405,7 @@ int ternix_hip_debug_set(const char* key, int v0, int v1, int v2, int v3) {
         {"deep", ternix_hip::DBG_DEEP},             {"sk_order", ternix_hip::DBG_SK_ORDER},
         {"m1_atomic", ternix_hip::DBG_M1_ATOMIC},     {"self_zero", ternix_hip::DBG_SELF_ZERO},
         {"gemm_gm", ternix_hip::DBG_GEMM_GM},         {"nt", ternix_hip::DBG_NT}, {"wave_ticket", ternix_hip::DBG_WAVE_TICKET},
-        {"line", ternix_hip::DBG_LINE},
+        {"line", ternix_hip::DBG_LINE}, {"ffn_amax", ternix_hip::DBG_FFN_AMAX},
     };
     if (key == nullptr) return (int)hipErrorInvalidValue;
     for (const auto& n : names) {

@@ -277,3 +277,32 @@ def test_line_gemv_up_to_16_rows(oracle, shape):
             _check_guarded(dc, m, n, expect, rep)
     finally:
         lib.ternix_hip_debug_reset()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape", [(1, 2560, 6912), (2, 2048, 2048), (4, 1024, 2816), (1, 1024, 16384), (3, 512, 640)],
+                         ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("zero_x", [False, True], ids=["x", "x0"])
+def test_line_gemv_ffn_strip_maxima_bit_equal(shape, zero_x):
+    """The decode block's down GEMV quantising h from the gate/up launch's per-strip maxima equals the
+    same block with the down GEMV reading whole rows of h (and the block on the other kernels) bit for
+    bit; an all-zero x gives all-zero h, whose absmax is the 1e-5 floor."""
+    m, h, f = shape
+    lib = tx._load()
+    rng = np.random.default_rng(m * 11 + f)
+    x = np.zeros((m, h), np.float32) if zero_x else rng.standard_normal((m, h)).astype(np.float32)
+    g = rng.uniform(0.5, 1.5, size=h).astype(np.float32)
+    wgu = (rng.integers(0, 256, size=(h, 2 * f // 4), dtype=np.uint16).astype(np.uint8) & 0x77)
+    wd = (rng.integers(0, 256, size=(f, h // 4), dtype=np.uint16).astype(np.uint8) & 0x77)
+    run = lambda: tx.ffn_forward(x, g, 1e-5, wgu, 0.02, wd, 0.03)
+    log(f"[line ffn maxima] M={m} H={h} F={f} zero_x={zero_x}")
+    try:
+        assert lib.ternix_hip_debug_set(b"ffn_amax", 0, -1, -1, -1) == 0
+        rows = run()
+    finally:
+        lib.ternix_hip_debug_reset()
+    maxima = run()
+    off, _ = _line_off_and_on(lib, run)
+    assert np.isfinite(maxima).all()
+    assert np.array_equal(rows.view(np.int32), maxima.view(np.int32))
+    assert np.array_equal(off.view(np.int32), maxima.view(np.int32))
