@@ -8,6 +8,8 @@
 // plus impl strings "hip", "hip_gemv", "hip_gemm", "hip_tiled", "hip_naive" (libternix_hip.so through
 // its C-ABI, GIL released during the device call, RuntimeError("HIP error: ...") on any device-side
 // failure, including a shape the tiled kernel rejects, as the reference's cuda_tiled does) and has_hip.
+// "cuda_naive" / "cuda_tiled" are not aliased: as in a reference build without CUDA they raise
+// ValueError("unknown impl ...") and has_cuda is False; hip_naive / hip_tiled are their counterparts.
 //
 // The CPU impl strings ("naive", "scalar", "avx2", "avx2_blocked") run the reference's own CPU
 // kernels, which the drop-in keeps unchanged in its ternix_core library (mul_mat_ternary.h:18-60).
