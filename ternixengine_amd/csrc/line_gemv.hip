@@ -95,6 +95,19 @@ struct LineArgs {
 
 __device__ __forceinline__ int line_swz(int r) { return ((r >> 1) & 3) ^ (((r >> 4) & 1) << 2); }
 
+// v from lane l ^ m of the same 16-lane row (m = 1, 2, 4, 8), through DPP (no LDS): quad
+// permutations for 1 and 2; for 4 and 8 the row shifts up and down, each lane taking the one that
+// reaches its partner.
+template <int m>
+__device__ __forceinline__ float row_xor(float v, int lane) {
+    const int x = __float_as_int(v);
+    if constexpr (m == 1) return __int_as_float(__builtin_amdgcn_update_dpp(x, x, 0xB1, 0xF, 0xF, false));
+    if constexpr (m == 2) return __int_as_float(__builtin_amdgcn_update_dpp(x, x, 0x4E, 0xF, 0xF, false));
+    const int up = __builtin_amdgcn_update_dpp(x, x, 0x100 + m, 0xF, 0xF, false);    // row_shl: lane l + m
+    const int down = __builtin_amdgcn_update_dpp(x, x, 0x110 + m, 0xF, 0xF, false);  // row_shr: lane l - m
+    return __int_as_float((lane & m) ? down : up);
+}
+
 template <int S, int NW, int AQ, bool EPI, bool RG>
 __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args) {
     static_assert(NW == 4 || NW == 8, "4 or 8 data waves");
@@ -139,8 +152,32 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
     //   AQ 3: the unit's slice of the row (64 nst activations) and the producer's maxima of the row.
     const int xpitch = AQ == 3 ? ((S * 256 + 1023) & ~1023) : ((K * 4 + 1023) & ~1023);  // bytes per row
     const int apitch = (args.amax_stride * 4 + 1023) & ~1023;
+    // AQ 1 / 2 with K <= 256 KJ: row r and G go straight into wave r's registers instead (lane l: k =
+    // 256 j + 4 l .. + 3), with this unit's 64 nst values of each (lane l: k = 64 (s0 + u) + l).
+    constexpr int KJ = (AQ == 1 || AQ == 2) ? 12 : 1;
+    const bool regs = (AQ == 1 || AQ == 2) && K <= 256 * KJ;
+    v4i xr[KJ], gr[KJ];
+    uint32_t xs[S], gs[S];
+    if constexpr (AQ == 1 || AQ == 2) {
+        if (wave < M && regs) {
+            const float* xrow = args.X + (size_t)wave * (size_t)K;
+#pragma unroll
+            for (int j = 0; j < KJ; ++j) {
+                const int k = 256 * j + 4 * lane;
+                xr[j] = k < K ? *reinterpret_cast<const v4i*>(xrow + k) : v4i{0, 0, 0, 0};
+                gr[j] = AQ == 2 && k < K ? *reinterpret_cast<const v4i*>(args.G + k) : v4i{0, 0, 0, 0};
+            }
+#pragma unroll
+            for (int u = 0; u < S; ++u) {
+                const int k = 64 * (s0 + min(u, nst - 1)) + lane;
+                xs[u] = __float_as_uint(xrow[k]);
+                gs[u] = AQ == 2 ? __float_as_uint(args.G[k]) : 0u;
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);  // these loads ahead of the weights' DMAs (in-order counter)
+    }
     if constexpr (AQ != 0) {
-        if (wave < M) {
+        if (wave < M && !regs) {
             const uint8_t* xb = reinterpret_cast<const uint8_t*>(args.X);
             uint8_t* xd = reinterpret_cast<uint8_t*>(xl) + wave * xpitch;
             if constexpr (AQ == 3) {
@@ -299,6 +336,42 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
                     __asm__ volatile("" : "+v"(v));
                     if (i0 + lane < args.amax_n) m = fmaxf(m, __uint_as_float(v));
                 }
+            } else if (regs) {
+                if constexpr (AQ == 2) {
+                    float ss[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int j = 0; j < KJ; ++j)
+                        if (256 * j + 4 * lane < K) {
+#pragma unroll
+                            for (int c = 0; c < 4; ++c) {
+                                const float x = __int_as_float(xr[j][c]);
+                                ss[c] = fmaf(x, x, ss[c]);
+                            }
+                        }
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) ss[c] += row_xor<8>(ss[c], lane);
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) ss[c] += row_xor<4>(ss[c], lane);
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) ss[c] += row_xor<2>(ss[c], lane);
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) ss[c] += row_xor<1>(ss[c], lane);
+                    const float w = (ss[0] + ss[2]) + (ss[1] + ss[3]);
+                    const float w0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), 0));
+                    const float w1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), 16));
+                    const float w2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), 32));
+                    const float w3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), 48));
+                    inv = 1.0f / sqrtf(((w0 + w1) + (w2 + w3)) / (float)K + args.eps);
+                }
+#pragma unroll
+                for (int j = 0; j < KJ; ++j)
+                    if (256 * j + 4 * lane < K) {
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) {
+                            const float x = __int_as_float(xr[j][c]);
+                            m = fmaxf(m, fabsf(AQ == 2 ? x * inv * __int_as_float(gr[j][c]) : x));
+                        }
+                    }
             } else {
                 if constexpr (AQ == 2) {
                     float ss[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -354,8 +427,14 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
                     }
                 }
             }
-#pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+            m = fmaxf(m, row_xor<8>(m, lane));
+            m = fmaxf(m, row_xor<4>(m, lane));
+            m = fmaxf(m, row_xor<2>(m, lane));
+            m = fmaxf(m, row_xor<1>(m, lane));
+            m = fmaxf(fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 0)),
+                            __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 16))),
+                      fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 32)),
+                            __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 48))));
             const float am = fmaxf(m, 1e-5f), sc = 127.0f / am;
             if (lane == 0) {
                 lds_write_b32_asm(lds_u32(rscale) + 4 * r, __float_as_uint(am / 127.0f));
@@ -364,14 +443,22 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
             // this unit's values of the row: k = 64 s0 + i, i < 64 nst, lane i % 64
             const uint32_t qa = lds_u32(qbuf) + (uint32_t)(r * (S * 64));
             uint32_t xv[S], gv[S];
+            if (regs) {
 #pragma unroll
-            for (int u = 0; u < S; ++u) {
-                const int i = min(u, nst - 1) * 64 + lane;
-                const int k = AQ == 3 ? i : s0 * 64 + i;
-                xv[u] = lds_read_b32_asm(xa + 4 * k);
-                gv[u] = AQ == 2 ? lds_read_b32_asm(ga + 4 * k) : 0u;
+                for (int u = 0; u < S; ++u) {
+                    xv[u] = xs[u];
+                    gv[u] = gs[u];
+                }
+            } else {
+#pragma unroll
+                for (int u = 0; u < S; ++u) {
+                    const int i = min(u, nst - 1) * 64 + lane;
+                    const int k = AQ == 3 ? i : s0 * 64 + i;
+                    xv[u] = lds_read_b32_asm(xa + 4 * k);
+                    gv[u] = AQ == 2 ? lds_read_b32_asm(ga + 4 * k) : 0u;
+                }
+                TX_LGKMCNT0();
             }
-            TX_LGKMCNT0();
 #pragma unroll
             for (int u = 0; u < S; ++u) {
                 __asm__ volatile("" : "+v"(xv[u]), "+v"(gv[u]));
@@ -589,9 +676,16 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
             // The strip's largest |value| per row (M <= 4), for the consumer's quantisation.
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
+                if (i >= M) break;  // workgroup-uniform
                 float m = lm[i];
-#pragma unroll
-                for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+                m = fmaxf(m, row_xor<8>(m, lane));
+                m = fmaxf(m, row_xor<4>(m, lane));
+                m = fmaxf(m, row_xor<2>(m, lane));
+                m = fmaxf(m, row_xor<1>(m, lane));
+                m = fmaxf(fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 0)),
+                                __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 16))),
+                          fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 32)),
+                                __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 48))));
                 if (lane == 0) emax[wave * 4 + i] = m;
             }
             __syncthreads();
