@@ -3,7 +3,9 @@
 //
 // Work unit: one 128-byte strip of the packed weight rows (one whole cache line per row, 512 output
 // columns) over S consecutive 64-row k-steps.  Unit (strip s, split t) is workgroup t * strips + s,
-// so every strip's split 0 is dispatched before any other split of it.
+// so every strip's split 0 is dispatched before any other split of it; or, when the rows share cache
+// lines between strips and the whole grid is resident at once, the units are taken in 8 contiguous
+// chunks, one per XCD (xcd_chunks).
 //
 //   * Weights: the unit's S x 8 KB go global -> LDS with global_load_lds_dwordx4, all issued at
 //     once (S instructions per wave for 8 data waves); one wave instruction moves 8 whole 128-byte

@@ -542,8 +542,11 @@ bool run_line_gemv(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int 
     // those launches take the XCD-chunked unit order (on MI355X, cold: 1x4096x11008 6.40 -> 5.70 us,
     // 4x4096x11008 7.15 -> 6.46, 1x2560x6912 4.35 -> 4.20; neutral to 3 % slower on aligned rows).
     // The DBG_LINE switch [2] forces it off (0) or on (1).
+    // The chunked order does not dispatch every strip's split 0 ahead of the strip's other splits, so
+    // it is only taken when the whole grid is resident at once (one workgroup per CU at most).
     const int fx = ternix_hip::debug_get(ternix_hip::DBG_LINE, 2);
-    const int xcd = fx >= 0 ? fx : (N / 4) % 128 != 0;
+    const bool resident = (long)strips * splits <= (long)cu_count();
+    const int xcd = fx >= 0 ? fx : ((N / 4) % 128 != 0 && resident);
     *e = TX_LAUNCH(c, ternix_hip::launch_line_gemv(dA, dB, dC, M, K, N, S, NW, tk, stride, c.st, os, aq, xcd));
     return true;
 }
