@@ -280,7 +280,8 @@ def test_line_gemv_up_to_16_rows(oracle, shape):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("shape", [(1, 2560, 6912), (2, 2048, 2048), (4, 1024, 2816), (1, 1024, 16384), (3, 512, 640)],
+@pytest.mark.parametrize("shape", [(1, 2560, 6912), (2, 2048, 2048), (4, 1024, 2816), (1, 1024, 16384), (3, 512, 640),
+                                   (1, 512, 20480), (2, 4096, 2048)],
                          ids=lambda s: "x".join(map(str, s)))
 @pytest.mark.parametrize("zero_x", [False, True], ids=["x", "x0"])
 def test_line_gemv_ffn_strip_maxima_bit_equal(shape, zero_x):
