@@ -110,11 +110,12 @@ __device__ __forceinline__ float row_xor(float v, int lane) {
     return __int_as_float((lane & m) ? down : up);
 }
 
-template <int S, int NW, int AQ, bool EPI, bool RG>
+template <int S, int NW, int AQ, bool EPI, bool RG, int MG = 1>
 __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args) {
     static_assert(NW == 4 || NW == 8, "4 or 8 data waves");
     static_assert(AQ == 0 || EPI, "fused quantisation comes with the float output");
     static_assert(!RG || (AQ == 0 && !EPI), "ragged operands: int32 output from int8 activations");
+    static_assert(MG == 1 || (MG == 2 && RG), "two 16-row groups (17-32 rows) on ragged operands only");
     constexpr int GW = 8 / NW;  // 16-byte column groups per data wave
     constexpr int STEP = 8192;  // bytes per k-step of the strip (64 rows x 128 bytes)
     __shared__ __attribute__((aligned(16))) uint8_t lds[S * STEP];
@@ -523,33 +524,40 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
         return;
     }
 
-    // Activation fragments: lane (q, kb) feeds row q, activations 16 kb .. 16 kb + 15 of each k-step.
+    // Activation fragments: lane (q, kb) feeds row 16 mg + q of m-group mg, activations 16 kb .. 16 kb
+    // + 15 of each k-step.
     const int q = lane & 15, kb = lane >> 4;
-    v4i a[S];
+    v4i a[MG][S];
 #pragma unroll
-    for (int st = 0; st < S; ++st) a[st] = v4i{0, 0, 0, 0};
+    for (int mg = 0; mg < MG; ++mg)
+#pragma unroll
+        for (int st = 0; st < S; ++st) a[mg][st] = v4i{0, 0, 0, 0};
     if constexpr (RG) {
         // 16 activations at an arbitrary address, from the 4-byte aligned dwords holding them; those
         // past K multiply the zero rows above.
 #pragma unroll
-        for (int st = 0; st < S; ++st) {
-            const int k0 = (s0 + st) * 64 + kb * 16, v = st < nst && q < M ? min(16, K - k0) : 0;
-            if (v > 0) {
-                const uintptr_t src = reinterpret_cast<uintptr_t>(args.A) + (size_t)q * (size_t)K + (size_t)k0;
-                const uint32_t* w = reinterpret_cast<const uint32_t*>(src & ~uintptr_t(3));
-                const uint32_t b = (uint32_t)(src & 3) * 8u;
-                uint32_t d[5];
+        for (int mg = 0; mg < MG; ++mg)
 #pragma unroll
-                for (int u = 0; u < 5; ++u) d[u] = 4 * u < (int)(b / 8) + v ? w[u] : 0u;
+            for (int st = 0; st < S; ++st) {
+                const int row = 16 * mg + q;
+                const int k0 = (s0 + st) * 64 + kb * 16, v = st < nst && row < M ? min(16, K - k0) : 0;
+                if (v > 0) {
+                    const uintptr_t src = reinterpret_cast<uintptr_t>(args.A) + (size_t)row * (size_t)K + (size_t)k0;
+                    const uint32_t* w = reinterpret_cast<const uint32_t*>(src & ~uintptr_t(3));
+                    const uint32_t b = (uint32_t)(src & 3) * 8u;
+                    uint32_t d[5];
 #pragma unroll
-                for (int u = 0; u < 4; ++u) a[st][u] = (int)(uint32_t)((((uint64_t)d[u + 1] << 32) | d[u]) >> b);
+                    for (int u = 0; u < 5; ++u) d[u] = 4 * u < (int)(b / 8) + v ? w[u] : 0u;
+#pragma unroll
+                    for (int u = 0; u < 4; ++u)
+                        a[mg][st][u] = (int)(uint32_t)((((uint64_t)d[u + 1] << 32) | d[u]) >> b);
+                }
             }
-        }
     } else if constexpr (AQ == 0) {
         const int8_t* arow = args.A + (size_t)min(q, M - 1) * (size_t)K + (size_t)s0 * 64 + kb * 16;
 #pragma unroll
         for (int st = 0; st < S; ++st)
-            if (st < nst && q < M) a[st] = *reinterpret_cast<const v4i*>(arow + st * 64);
+            if (st < nst && q < M) a[0][st] = *reinterpret_cast<const v4i*>(arow + st * 64);
     }
     TX_LGKMCNT0();  // AQ: the int8 rows are in LDS; RG: the weights' LDS writes
     TX_VMCNT(0);
@@ -560,14 +568,16 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
     if constexpr (AQ != 0) {
 #pragma unroll
         for (int st = 0; st < S; ++st)
-            if (st < nst && q < M) a[st] = *reinterpret_cast<const v4i*>(qbuf + q * (S * 64) + st * 64 + kb * 16);
+            if (st < nst && q < M) a[0][st] = *reinterpret_cast<const v4i*>(qbuf + q * (S * 64) + st * 64 + kb * 16);
     }
 
-    v4i acc[GW][4];
+    v4i acc[MG][GW][4];
 #pragma unroll
-    for (int gi = 0; gi < GW; ++gi)
+    for (int mg = 0; mg < MG; ++mg)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[gi][j] = v4i{0, 0, 0, 0};
+        for (int gi = 0; gi < GW; ++gi)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[mg][gi][j] = v4i{0, 0, 0, 0};
     // Every fragment read of the unit first (two transposing reads per k-step and group), one wait,
     // then the decode and the MFMAs: the LDS latency is paid once, not once per k-step.
     const int r0 = kb * 16 + (q >> 1), r1 = r0 + 8;
@@ -608,7 +618,9 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
                     bfr[3][r4] = (int)(x & 0xC0C0C0C0u);
                 }
 #pragma unroll
-                for (int j = 0; j < 4; ++j) acc[gi][j] = mfma_i8(a[st], bfr[j], acc[gi][j]);
+                for (int mg = 0; mg < MG; ++mg)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) acc[mg][gi][j] = mfma_i8(a[mg][st], bfr[j], acc[mg][gi][j]);
             }
         }
     }
@@ -626,14 +638,16 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
         int32_t* out = args.C + 4 * (bc0 + 16 * g) + lane;
         const bool in_row = !RG || 4 * (bc0 + 16 * g) + lane < N;  // RG: a partial last group
 #pragma unroll
+        for (int mg = 0; mg < MG; ++mg)
+#pragma unroll
         for (int i4 = 0; i4 < 4; ++i4)
 #pragma unroll
             for (int ii = 0; ii < 4; ++ii) {
-                const int i = 4 * i4 + ii;
+                const int i = 16 * mg + 4 * i4 + ii;
                 if (i < M) {  // workgroup-uniform
                     if (kb == i4) {
-                        const v4i v = {acc[gi][0][ii] >> 6, acc[gi][1][ii] >> 6, acc[gi][2][ii] >> 6,
-                                       acc[gi][3][ii] >> 6};
+                        const v4i v = {acc[mg][gi][0][ii] >> 6, acc[mg][gi][1][ii] >> 6, acc[mg][gi][2][ii] >> 6,
+                                       acc[mg][gi][3][ii] >> 6};
                         *reinterpret_cast<v4i*>(rb + 4 * q) = v;
                     }
                     __builtin_amdgcn_wave_barrier();
@@ -709,7 +723,7 @@ bool line_gemv_ok(const int8_t* A, const uint8_t* B, int M, int K, int N) {
 }
 
 bool line_gemv_ragged_ok(int M, int K, int N) {
-    return M >= 1 && M <= 16 && K >= 1 && N >= 4 && N % 4 == 0 && (size_t)K * (size_t)(N / 4) < ((size_t)1 << 40);
+    return M >= 1 && M <= 32 && K >= 1 && N >= 4 && N % 4 == 0 && (size_t)K * (size_t)(N / 4) < ((size_t)1 << 40);
 }
 
 int line_gemv_splits(int K, int S) { return ((K + 63) / 64 + S - 1) / S; }
@@ -759,11 +773,17 @@ hipError_t launch_line_gemv(const int8_t* A, const uint8_t* B, int32_t* C, int M
 
     if (a.splits > 64 || (size_t)S * 64 > (size_t)kMaxKPerAccumulator) return hipErrorInvalidValue;
     const dim3 grid((unsigned)(a.strips * a.splits));
-    // 0 int32 out, 1 dequantised, 2 / 3 / 4 with fused quantisation, 5 int32 out from ragged operands
-    const int mode = ragged ? 5 : (epi ? 1 + aq.mode : 0);
+    // 0 int32 out, 1 dequantised, 2 / 3 / 4 with fused quantisation, 5 / 6 int32 out from ragged
+    // operands in one / two 16-row groups
+    const int mode = ragged ? (M > 16 ? 6 : 5) : (epi ? 1 + aq.mode : 0);
 #define TX_LINE(SS, WW, AQQ, EE, RR)                                                                         \
     if (S == SS && NW == WW && mode == (RR ? 5 : (EE ? 1 + AQQ : 0))) {                                      \
         hipLaunchKernelGGL((line_gemv_kernel<SS, WW, AQQ, EE, RR>), grid, dim3(64 * (WW + 1)), 0, st, a);   \
+        return hipGetLastError();                                                                            \
+    }
+#define TX_LINE_RG2(SS)                                                                                      \
+    if (S == SS && NW == 8 && mode == 6) {                                                                   \
+        hipLaunchKernelGGL((line_gemv_kernel<SS, 8, 0, false, true, 2>), grid, dim3(64 * 9), 0, st, a);     \
         return hipGetLastError();                                                                            \
     }
 #define TX_LINE_S(SS)                   \
@@ -779,9 +799,14 @@ hipError_t launch_line_gemv(const int8_t* A, const uint8_t* B, int32_t* C, int M
     TX_LINE_S(4)
     TX_LINE_S(6)
     TX_LINE_S(8)
+    TX_LINE_RG2(2)  // two 16-row groups: up to 6 k-steps (8 would spill)
+    TX_LINE_RG2(3)
+    TX_LINE_RG2(4)
+    TX_LINE_RG2(6)
     TX_LINE(2, 4, 0, false, false)
     TX_LINE(4, 4, 0, false, false)
 #undef TX_LINE_S
+#undef TX_LINE_RG2
 #undef TX_LINE
     return hipErrorInvalidValue;
 }

@@ -498,7 +498,7 @@ bool run_line_gemv(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int 
     // Ragged rows past 4 need K >= 1024: on short K the few workgroups serialise their 16-row atomics
     // (16x130x2044 6.90 against 5.44 us with the padded copy; 16x4093x1028 7.93 against 8.64).
     const int fm = ternix_hip::debug_get(ternix_hip::DBG_LINE, 3);
-    if (M > (fm > 0 ? std::min(fm, 16) : (ragged && K >= 1024 ? 16 : 4))) return false;
+    if (M > (fm > 0 ? std::min(fm, ragged ? 32 : 16) : (ragged && K >= 1024 ? 32 : 4))) return false;
     if (!(dC != nullptr && reinterpret_cast<uintptr_t>(dC) % 16 == 0 &&
           (!ragged || (!epi && aq.mode == 0 && ternix_hip::line_gemv_ragged_ok(M, K, N)))))
         return false;
@@ -529,6 +529,7 @@ bool run_line_gemv(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int 
         }
         if (S == 0) return false;
     }
+    if (ragged && M > 16 && S > 6) return false;  // two 16-row groups: at most 6 k-steps per workgroup
     const int NW = fw == 4 && !epi && !ragged ? 4 : 8;
     const int splits = ternix_hip::line_gemv_splits(K, S);
     if (splits > 64) return false;

@@ -38,6 +38,8 @@ def test_plan_names_line_kernel_when_forced():
         assert _plan(lib, 1, 2560, 6900).startswith("line_gemv_kernel ragged S=2")  # N/4 % 16 != 0
         assert _plan(lib, 16, 2560, 6900).startswith("line_gemv_kernel ragged")  # ragged: up to 16 rows
         assert not _plan(lib, 16, 1000, 6900).startswith("line_gemv_kernel")  # ... with K >= 1024
+        assert _plan(lib, 32, 2560, 6900).startswith("line_gemv_kernel ragged")  # two 16-row groups
+        assert not _plan(lib, 33, 2560, 6900).startswith("line_gemv_kernel")
         assert lib.ternix_hip_debug_set(b"line", 1, 8, -1, -1) == 0
         assert not _plan(lib, 1, 8192, 4096).startswith("line_gemv_kernel")  # 128 splits > 64
     finally:
@@ -221,14 +223,16 @@ def _check_guarded(dc, m, n, expect, tag):
 # misaligned operands on aligned shapes, a partial last 16-byte group
 RAGGED = [(1, 1000, 3076, 0, 0), (4, 1000, 3076, 0, 0), (2, 4093, 1028, 0, 0), (3, 37, 20, 0, 0),
           (1, 5, 4, 0, 0), (2, 777, 516, 3, 1), (4, 4096, 1024, 3, 0), (1, 2560, 6912, 0, 2),
-          (3, 130, 2044, 1, 3), (1, 8191, 2052, 0, 0), (12, 1500, 3076, 0, 0), (16, 4093, 1028, 2, 1)]
+          (3, 130, 2044, 1, 3), (1, 8191, 2052, 0, 0), (12, 1500, 3076, 0, 0), (16, 4093, 1028, 2, 1),
+          (17, 4093, 1028, 0, 0), (24, 2000, 1036, 1, 2), (32, 1500, 516, 0, 0)]
 
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("shape", RAGGED, ids=lambda s: "x".join(map(str, s)))
 def test_line_gemv_ragged_matches_oracle(oracle, shape):
     """Ragged and misaligned operands go to the whole-line GEMV's register-staged form (no padded
-    copy): bit-exact against the oracle, twice in a row on the same tickets, and in graph replays."""
+    copy; 17-32 rows in two 16-row groups): bit-exact against the oracle, twice in a row on the same
+    tickets, and in graph replays."""
     lib = tx._load()
     m, k, n, ao, bo = shape
     p = _ragged_problem(oracle, np.random.default_rng(sum(shape)), *shape)

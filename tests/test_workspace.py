@@ -49,7 +49,7 @@ def test_workspace_size_and_plan_host():
         assert st == 0 and d and d not in ("none", "rejected"), (s, d)
     assert describe(lib, 1, 2560, 6912)[1].startswith("line_gemv_kernel")
     assert describe(lib, 1, 2560, 6912, (1 << 20) + 1)[1].startswith("line_gemv_kernel ragged")  # misaligned A
-    assert "pad_rows_kernel" in describe(lib, 17, 2560, 6912, (1 << 20) + 1)[1]  # 17 rows misaligned: padded
+    assert "pad_rows_kernel" in describe(lib, 33, 2560, 6912, (1 << 20) + 1)[1]  # 33 rows misaligned: padded
     assert describe(lib, 1, 64, 6)[0] == 1
     buf = ctypes.create_string_buffer(8)
     assert lib.ternix_hip_plan_describe(1 << 20, 1 << 24, 1, 64, 64, buf, 0) == 1
