@@ -1,4 +1,5 @@
-// line_gemv.hip -- gfx950 whole-line decode GEMV (M <= 16) for the ternary matmul, and its launcher.
+// line_gemv.hip -- gfx950 whole-line decode GEMV (M <= 16; ragged operands M <= 32) for the ternary
+// matmul, and its launcher.
 // Shared helpers, the weight layout and the decode forms are described in kernel_common.h.
 //
 // Work unit: one 128-byte strip of the packed weight rows (one whole cache line per row, 512 output
@@ -15,7 +16,8 @@
 //   * Data wave w owns the strip's w-th 16-byte column group (GW = 8 / NW groups per wave): per k-step
 //     two ds_read_b64_tr_b8 give lane q byte-column q of 16 k-rows, the shift-form decode makes four
 //     B operands, and v_mfma_i32_16x16x64_i8 against the activation fragment (row q < M, 16 bytes of
-//     k-block kb, loaded straight from global memory) accumulates 64 output columns.
+//     k-block kb, loaded straight from global memory; MG = 2: a second fragment for rows 16 .. 31)
+//     accumulates 64 output columns.
 //   * K splits add into C with int32 atomics (exact, order-free).  C is zeroed inside the launch by
 //     each strip's split 0, with no wait in any data wave: the workgroup's extra protocol wave takes
 //     the call's ticket and, in split 0, zeroes the strip's outputs with agent-scope (write-through)
@@ -39,8 +41,9 @@
 //   * AQ = 1 / 2: the int8 activations are made inside the kernel from fp32 rows X (absmax
 //     quantisation; AQ = 2 RMS-normalises with weight G first), with the loops and rounding of
 //     row_stats.h, so they are bit-identical to quantize_rows_kernel / rmsnorm_kernel.  In every
-//     workgroup, data wave r < M DMAs row r (and G) into LDS ahead of its weights, computes the
-//     row's statistics alone (no barrier) and quantises the unit's activations of the row.
+//     workgroup, data wave r < M loads row r (and G) ahead of its weights -- into its registers for
+//     rows up to 3072 wide, else by DMA into LDS --, computes the row's statistics alone (no barrier,
+//     DPP row exchanges instead of LDS shuffles) and quantises the unit's activations of the row.
 //     AQ = 3: the absmax comes from a producer's per-strip maxima of the rows (amax_in, written by
 //     an EPI launch with amax_out), so only the unit's slice of each row is read.
 //   * EPI: a float output Y = C * (row scale * weight scale), optionally with the SwiGLU of
