@@ -737,7 +737,11 @@ GemmChoice gemm_choice(const int8_t* A, const uint8_t* B, int M, int K, int N, i
     // 2048x14336x4096 90.6 -> 90.4 (one round: equal).  With a K split the 128-row tiles stay
     // (256x16384x4096: 31.8 against 35.5 us).  Small M (64 rows or fewer): the same four-wave
     // workgroups, so no MFMA row or A byte is spent on padding rows; the caller splits K to fill the chip.
-    if (M <= small_m_max || bm == 64 || (splits == 1 && bm == 128 && bm_env <= 0)) return GemmChoice::Pipe64;
+    // With a K split, 64-row tiles also where the last 128-row tile would be mostly padding (M mod 128
+    // in 1 .. 64): 129x8192x2304 in 8 splits 22.1 -> 20.3 us (the padded copy of 129x8191x2052).
+    const bool pad_rows64 = splits > 1 && bm_env <= 0 && ((M + 63) / 64) * 64 < ((M + 127) / 128) * 128;
+    if (M <= small_m_max || bm == 64 || pad_rows64 || (splits == 1 && bm == 128 && bm_env <= 0))
+        return GemmChoice::Pipe64;
     return bm == 128 ? GemmChoice::Pipe128 : GemmChoice::Fast256;
 }
 

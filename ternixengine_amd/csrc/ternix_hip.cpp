@@ -704,7 +704,9 @@ hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
 // the partial tiles go through the same workspace and reduce launch as the skinny path.
 int gemm_splits(int M, int K, int N) {
     const int env = ternix_hip::debug_get(ternix_hip::DBG_GEMM_SPLITS);  // tests
-    const int bm = M <= 64 ? 64 : 128;  // the tile height launch_gemm picks for a split launch
+    // the tile height launch_gemm picks for a split launch (64 also where a last 128-row tile would
+    // be mostly padding)
+    const int bm = M <= 64 || ((M + 63) / 64) * 64 < ((M + 127) / 128) * 128 ? 64 : 128;
     const bool narrow = ternix_hip::gemm_narrow_wanted(M, K, N);  // 64-column tiles instead of 256
     const long tiles = (long)((M + bm - 1) / bm) * (long)((N / 4 + 63) / 64) * (narrow ? 4 : 1);
     const long cus = cu_count();
