@@ -848,7 +848,7 @@ hipError_t run_auto(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int
     (void)st;
     const bool pad_off = ternix_hip::debug_get(ternix_hip::DBG_RAGGED_PAD) == 0;  // tests: generic kernels
     if (!pad_off && needs_padding(dA, dB, K, N, M <= skinny_max)) {
-        // up to 16 rows, int32 output: the whole-line GEMV reads the ragged operands as they are, one launch
+        // up to 32 rows, int32 output: the whole-line GEMV reads the ragged operands as they are, one launch
         hipError_t e = hipSuccess;
         if (M <= skinny_max && os.Y == nullptr && run_line_gemv(dA, dB, dC, M, K, N, c, &e)) return e;
         e = run_padded(dA, dB, dC, M, K, N, c, os, M <= skinny_max);
@@ -1215,10 +1215,11 @@ int ternix_hip_ffn_forward(float* dY, const float* dX, const float* dNormWeight,
     const int m = (int)M, hd = (int)H, f = (int)F;
     // Decode shapes: the RMSNorm + quantisation of x and the requantisation of h run inside the two
     // skinny GEMVs (fused activation prologue, bit-identical to the standalone kernels).  Up to 4 rows
-    // with M x H and M x F <= 8192 that is two launches of the whole-line GEMV, each dequantising (and,
-    // for gate/up, applying SwiGLU) in its last-arriving split (measured on MI355X, cold weights,
-    // 1 x 2560 x 6912: 20.2 -> 15.9 us per block); otherwise the other skinny kernels with their reduce
-    // or dequantisation launches.  Larger M: the four separate launches.
+    // with M x H <= 8192 that is two launches of the whole-line GEMV, each dequantising (and, for
+    // gate/up, applying SwiGLU) in its last-arriving split, the down launch quantising h with the
+    // gate/up launch's per-strip maxima (measured on MI355X, cold weights, 1 x 2560 x 6912: 20.2 ->
+    // 13.2 us per block); otherwise the other skinny kernels with their reduce or dequantisation
+    // launches.  Larger M: the four separate launches.
     if (m <= kSkinnyMaxM && F > 0) {
         ternix_hip::OutScale os1;
         os1.Y = h;

@@ -36,7 +36,7 @@ def test_plan_names_line_kernel_when_forced():
         assert _plan(lib, 1, 2560, 6912).startswith("line_gemv_kernel S=2 waves=8+1 splits=20")
         assert not _plan(lib, 5, 2560, 6912).startswith("line_gemv_kernel")  # aligned: M <= 4 only
         assert _plan(lib, 1, 2560, 6900).startswith("line_gemv_kernel ragged S=2")  # N/4 % 16 != 0
-        assert _plan(lib, 16, 2560, 6900).startswith("line_gemv_kernel ragged")  # ragged: up to 16 rows
+        assert _plan(lib, 16, 2560, 6900).startswith("line_gemv_kernel ragged")  # ragged: more rows
         assert not _plan(lib, 16, 1000, 6900).startswith("line_gemv_kernel")  # ... with K >= 1024
         assert _plan(lib, 32, 2560, 6900).startswith("line_gemv_kernel ragged")  # two 16-row groups
         assert not _plan(lib, 33, 2560, 6900).startswith("line_gemv_kernel")
