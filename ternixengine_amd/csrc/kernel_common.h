@@ -118,6 +118,22 @@ __device__ __forceinline__ float store_scaled_f(const OutScale& os, float f, int
     return fmaxf(fmaxf(fmaxf(fmaxf(0.0f, fabsf(y[0])), fabsf(y[1])), fabsf(y[2])), fabsf(y[3]));
 }
 
+// The same for two consecutive outputs c0, c1 of one row (an even column `col`), with the same two
+// roundings per output; with os.swiglu they are one (gate, up) pair and the one value h[col / 2] is
+// stored.  Returns the largest |value| stored (fmaxf from 0).
+__device__ __forceinline__ float store_scaled_pair(const OutScale& os, float f, int row, int N, int col, int c0, int c1) {
+    const float y0 = (float)c0 * f, y1 = (float)c1 * f;
+    if (os.swiglu) {
+        const float h = (y0 / (1.0f + expf(-y0))) * y1;
+        os.Y[(size_t)row * (size_t)(N / 2) + col / 2] = h;
+        return fmaxf(0.0f, fabsf(h));
+    }
+    float* out = os.Y + (size_t)row * (size_t)N + col;
+    out[0] = y0;
+    out[1] = y1;
+    return fmaxf(fmaxf(0.0f, fabsf(y0)), fabsf(y1));
+}
+
 // ------------------------------------------------------------------------------------------------
 // Loads with optional bounds / alignment handling.
 // ------------------------------------------------------------------------------------------------

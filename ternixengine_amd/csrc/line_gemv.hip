@@ -125,10 +125,9 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
     // rows of X at a 1 KB-aligned pitch (AQ 3: the unit's slices), G's copies (AQ 3: the row maxima)
     __shared__ __attribute__((aligned(16))) float xl[AQ ? kLineQK + 1024 : 4];
     __shared__ __attribute__((aligned(16))) float gl[AQ == 2 ? kLineQK + 1024 : (AQ == 3 ? 2048 : 4)];
-    __shared__ float emax[16 * 4];  // EPI with amax_out: per wave and row, the largest |stored value|
     __shared__ __attribute__((aligned(16))) int8_t qbuf[AQ ? 4 * S * 64 : 16];  // AQ: the unit's int8 rows
     __shared__ float rscale[4];
-    __shared__ int last_flag;
+    __shared__ float wmax[16 * 4];  // EPI with amax_out: per wave and row, the largest |value| written
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -275,30 +274,21 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
                 unsigned long long* z = reinterpret_cast<unsigned long long*>(args.C + (size_t)r * (size_t)N + 4 * bc0);
                 for (int u = lane; u < n8; u += 64) __hip_atomic_store(z + u, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
-            // T += 64 - (splits - 1) (no return needed); with EPI also arrivals += 64 - splits.  Lane 0
-            // alone enabled; nothing waited for here.
-            const unsigned long long inc = (unsigned long long)(64 - (args.splits - 1));
-            if constexpr (EPI) {
-                const unsigned long long inc_a = (unsigned long long)(64 - args.splits);
-                __asm__ volatile(
-                    "s_mov_b64 %0, exec\n\t"
-                    "s_mov_b64 exec, 1\n\t"
-                    "global_atomic_add_x2 %1, %2, off\n\t"
-                    "global_atomic_add_x2 %3, %4, off\n\t"
-                    "s_mov_b64 exec, %0"
-                    : "=&s"(saved_exec)
-                    : "v"(tk), "v"(inc), "v"(tk + 2), "v"(inc_a)
-                    : "memory");
-            } else {
-                __asm__ volatile(
-                    "s_mov_b64 %0, exec\n\t"
-                    "s_mov_b64 exec, 1\n\t"
-                    "global_atomic_add_x2 %1, %2, off\n\t"
-                    "s_mov_b64 exec, %0"
-                    : "=&s"(saved_exec)
-                    : "v"(tk), "v"(inc)
-                    : "memory");
+            if constexpr (EPI) {  // the strip's maxima start at 0 too (published with the zeroed word)
+                if (args.amax_out != nullptr && lane < M)
+                    __hip_atomic_store(reinterpret_cast<unsigned int*>(args.amax_out) + (size_t)lane * args.amax_stride + s,
+                                       0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
+            // T += 64 - (splits - 1) (no return needed).  Lane 0 alone enabled; nothing waited for here.
+            const unsigned long long inc = (unsigned long long)(64 - (args.splits - 1));
+            __asm__ volatile(
+                "s_mov_b64 %0, exec\n\t"
+                "s_mov_b64 exec, 1\n\t"
+                "global_atomic_add_x2 %1, %2, off\n\t"
+                "s_mov_b64 exec, %0"
+                : "=&s"(saved_exec)
+                : "v"(tk), "v"(inc)
+                : "memory");
         } else {
             // The returning T += 1 (its value / 64 + 1 names this call), lane 0 alone enabled, not
             // waited for here: `old` is only read after the wait below, which names it.
@@ -632,14 +622,24 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
 
     // Epilogue: lane (q, kb) holds rows 4 kb + i (i < 4) of columns 4 (bc0 + 16 g + q) + j.  Each wave
     // lays a row's 64 outputs of a group out in column order in its own 256 bytes of the idle stage
-    // buffer, then adds one column per lane: 64 consecutive int32 per atomic instruction.
+    // buffer, then adds them to C:
+    //   * int32 output: one column per lane, 64 consecutive int32 per atomic instruction;
+    //   * EPI: the sums still scaled by 64 (the decode's factor), so their low 6 bits are free; lane l
+    //     adds column pair l as one 64-bit integer (2^32 (odd column) + even column + 1) with a
+    //     returning atomic.  The even column's low 6 bits count the splits added so far, and the
+    //     64-bit sum is exact, so the split that sees splits - 1 there is the pair's last adder: it
+    //     recovers both sums (even = (low half - splits) / 64, odd = (sum - low half) / 2^32 / 64) and
+    //     writes the float output (dequantised, optionally the SwiGLU of the pair) -- no arrival
+    //     counter and no second pass over the sums.
     int32_t* rb = reinterpret_cast<int32_t*>(lds) + wave * 64;
+    float lm[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // EPI with amax_out: per row, the largest |value| this lane wrote
 #pragma unroll
     for (int gi = 0; gi < GW; ++gi) {
         const int g = wave * GW + gi;
         if (bc0 + 16 * g >= NB) continue;  // wave-uniform
-        int32_t* out = args.C + 4 * (bc0 + 16 * g) + lane;
-        const bool in_row = !RG || 4 * (bc0 + 16 * g) + lane < N;  // RG: a partial last group
+        const int col0 = 4 * (bc0 + 16 * g);  // the group's first column
+        int32_t* out = args.C + col0 + lane;
+        const bool in_row = !RG || col0 + lane < N;  // RG: a partial last group
 #pragma unroll
         for (int mg = 0; mg < MG; ++mg)
 #pragma unroll
@@ -649,54 +649,51 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
                 const int i = 16 * mg + 4 * i4 + ii;
                 if (i < M) {  // workgroup-uniform
                     if (kb == i4) {
-                        const v4i v = {acc[mg][gi][0][ii] >> 6, acc[mg][gi][1][ii] >> 6, acc[mg][gi][2][ii] >> 6,
-                                       acc[mg][gi][3][ii] >> 6};
+                        const int sh = EPI ? 0 : 6;
+                        const v4i v = {acc[mg][gi][0][ii] >> sh, acc[mg][gi][1][ii] >> sh, acc[mg][gi][2][ii] >> sh,
+                                       acc[mg][gi][3][ii] >> sh};
                         *reinterpret_cast<v4i*>(rb + 4 * q) = v;
                     }
                     __builtin_amdgcn_wave_barrier();
-                    const int32_t v = rb[lane];
-                    __builtin_amdgcn_wave_barrier();
-                    if (in_row)
-                        __hip_atomic_fetch_add(out + (size_t)i * (size_t)N, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if constexpr (EPI) {
+                        const int32_t e = rb[2 * (lane & 31)], o = rb[2 * (lane & 31) + 1];
+                        __builtin_amdgcn_wave_barrier();
+                        const int c = col0 + 2 * lane;
+                        if (lane < 32 && c < N) {
+                            const unsigned long long add =
+                                ((unsigned long long)(uint32_t)o << 32) + (unsigned long long)(long long)(e + 1);
+                            unsigned long long* word = reinterpret_cast<unsigned long long*>(args.C + (size_t)i * (size_t)N + c);
+                            const unsigned long long prev = __hip_atomic_fetch_add(word, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                            if ((int)((uint32_t)prev & 63u) == args.splits - 1) {
+                                const long long tot = (long long)(prev + add);
+                                const int lo = (int)(uint32_t)tot;
+                                const int ce = (lo - args.splits) >> 6;
+                                const int co = (int)((tot - (long long)lo) >> 38);
+                                const float f = (AQ != 0 ? rscale[i] : args.os.rs[i]) * args.os.ws;
+                                const float mx = store_scaled_pair(args.os, f, i, N, c, ce, co);
+#pragma unroll
+                                for (int r = 0; r < 4; ++r)
+                                    if (r == i) lm[r] = fmaxf(lm[r], mx);
+                            }
+                        }
+                    } else {
+                        const int32_t v = rb[lane];
+                        __builtin_amdgcn_wave_barrier();
+                        if (in_row)
+                            __hip_atomic_fetch_add(out + (size_t)i * (size_t)N, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    }
                 }
             }
     }
     if constexpr (EPI) {
-        // Count this split once its atomics have completed; the split that brings the strip's
-        // arrival word to 63 mod 64 has every split's sums and writes the float output.
-        TX_VMCNT(0);
-        __builtin_amdgcn_s_barrier();  // (3) every data wave's atomics have completed (the protocol wave has left)
-        if (tid == 0) {
-            const unsigned long long a_old =
-                __hip_atomic_fetch_add(tk + 2, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            last_flag = (a_old & 63) == 63;
-        }
-        __syncthreads();  // (4)
-        if (!last_flag) return;
-        // The strip's sums, read with coherent loads (they bypass this XCD's L2, which may hold none of
-        // the other splits' additions), four consecutive columns per lane, every row.
-        const int ncol = min(512, N - 4 * bc0);
-        float lm[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // amax_out: per row, the largest |value| this thread stored
-        for (int idx = tid; idx < M * 128; idx += NW * 64) {
-            const int r = idx >> 7, c4 = (idx & 127) * 4;
-            if (c4 >= ncol) continue;
-            const unsigned long long* src =
-                reinterpret_cast<const unsigned long long*>(args.C + (size_t)r * (size_t)N + 4 * bc0 + c4);
-            const unsigned long long u0 = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const unsigned long long u1 = __hip_atomic_load(src + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const v4i v = {(int)(uint32_t)u0, (int)(uint32_t)(u0 >> 32), (int)(uint32_t)u1, (int)(uint32_t)(u1 >> 32)};
-            const float f = (AQ != 0 ? rscale[r] : args.os.rs[r]) * args.os.ws;
-            const float mx = store_scaled_f(args.os, f, r, N, 4 * bc0 + c4, v, args.vec_y);
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                if (i == r) lm[i] = fmaxf(lm[i], mx);
-        }
         if (args.amax_out != nullptr) {
-            // The strip's largest |value| per row (M <= 4), for the consumer's quantisation.
+            // The strip's largest |value| per row (M <= 4), for the consumer's quantisation: a maximum
+            // over the pairs this wave finished, folded into the strip's entry (non-negative floats
+            // order as their bit patterns).
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                if (i >= M) break;  // workgroup-uniform
-                float m = lm[i];
+            for (int r = 0; r < 4; ++r) {
+                if (r >= M) break;  // workgroup-uniform
+                float m = lm[r];
                 m = fmaxf(m, row_xor<8>(m, lane));
                 m = fmaxf(m, row_xor<4>(m, lane));
                 m = fmaxf(m, row_xor<2>(m, lane));
@@ -705,13 +702,15 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
                                 __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 16))),
                           fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 32)),
                                 __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 48))));
-                if (lane == 0) emax[wave * 4 + i] = m;
+                if (lane == 0) wmax[wave * 4 + r] = m;
             }
-            __syncthreads();
+            __syncthreads();  // the data waves only (the protocol wave has left)
             if (tid < M) {
                 float m = 0.0f;
-                for (int w = 0; w < NW; ++w) m = fmaxf(m, emax[w * 4 + tid]);
-                args.amax_out[(size_t)tid * (size_t)args.amax_stride + s] = m;
+                for (int w = 0; w < NW; ++w) m = fmaxf(m, wmax[w * 4 + tid]);
+                if (m > 0.0f)  // one atomic per workgroup and row: the strip's entry is shared by its splits
+                    __hip_atomic_fetch_max(reinterpret_cast<unsigned int*>(args.amax_out) + (size_t)tid * args.amax_stride + s,
+                                           __float_as_uint(m), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         }
     }
@@ -749,7 +748,7 @@ hipError_t launch_line_gemv(const int8_t* A, const uint8_t* B, int32_t* C, int M
         return hipErrorInvalidValue;
     if (aq.amax_out != nullptr && (!epi || M > 4 || aq.amax_stride < (N / 4 + 127) / 128))
         return hipErrorInvalidValue;
-    if (epi && (tk_stride < 4 || (aq.mode == 0 && os.rs == nullptr) || (os.swiglu && N % 8 != 0)))
+    if (epi && ((aq.mode == 0 && os.rs == nullptr) || (os.swiglu && N % 8 != 0) || K > 65536))
         return hipErrorInvalidValue;
     LineArgs a;
     a.A = A;
