@@ -47,11 +47,11 @@
 //     AQ = 3: the absmax comes from a producer's per-strip maxima of the rows (amax_in, written by
 //     an EPI launch with amax_out), so only the unit's slice of each row is read.
 //   * EPI: a float output Y = C * (row scale * weight scale), optionally with the SwiGLU of
-//     interleaved (gate, up) column pairs.  The splits add into the int32 buffer C as above; each
-//     split then counts itself on the strip's arrival word (the third word of its ticket line: every
-//     call adds exactly 64 -- split 0 adds 64 - splits at its start, every split 1 once its atomics have
-//     completed), and the split that brings it to 63 mod 64 reads the strip's complete sums back with
-//     coherent loads and writes Y.  One launch, no dequantisation launch.
+//     interleaved (gate, up) column pairs.  The splits add their sums, still scaled by 64, a column
+//     pair at a time as one 64-bit integer with a returning atomic into the int32 buffer C (zeroed as
+//     above); the low 6 bits of the even column count the splits added, so each pair's last adder
+//     knows it, recovers both sums and writes Y.  One launch, no dequantisation launch, no arrival
+//     counter.  With amax_out the per-strip maxima of |Y| are folded into zeroed entries.
 //   * RG: ragged operands (K not a multiple of 64, N/4 not a multiple of 16, A or W at any address),
 //     int32 output: the weights are staged through registers from aligned dwords instead of the
 //     DMA, the last k-step is partial (zero rows past K), and the outputs past N are not written --
