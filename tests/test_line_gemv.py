@@ -259,6 +259,28 @@ def test_line_gemv_ragged_matches_oracle(oracle, shape):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("m", [1, 4])
+def test_line_gemv_one_workgroup_per_cu(oracle, m):
+    """8192 x 8192 on the automatic plan: 16 strips x 16 splits of 8 k-steps fill the CUs exactly (a
+    grid of one workgroup per CU is the plan's limit), bit-exact against the oracle on two calls."""
+    lib = tx._load()
+    k = n = 8192
+    p = _ragged_problem(oracle, np.random.default_rng(8192 + m), m, k, n, 0, 0)
+    _, _, _, da, db, dc, expect, _, _ = p
+    buf = ctypes.create_string_buffer(192)
+    assert lib.ternix_hip_plan_describe(1 << 20, 1 << 24, m, k, n, buf, len(buf)) == 0
+    plan = buf.value.decode()
+    if hr.device_attribute(hr.ATTR_MULTIPROCESSOR_COUNT) == 256:
+        assert plan.startswith("line_gemv_kernel S=8 waves=8+1 splits=16"), plan
+    log(f"[line one per CU] M={m} K={k} N={n} plan={plan[:40]}")
+    for rep in range(2):
+        dc.upload(np.full(m * n + GUARD, GARBAGE, np.int32))
+        assert tx.mul_mat_ternary(da.value, db.value, dc.value, m, k, n) == 0
+        hr.synchronize()
+        _check_guarded(dc, m, n, expect, rep)
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("shape", [(5, 2560, 6912), (8, 4096, 4096), (16, 2560, 2560), (16, 6912, 2560),
                                    (12, 1000, 3076), (7, 64, 512)], ids=lambda s: "x".join(map(str, s)))
 def test_line_gemv_up_to_16_rows(oracle, shape):
