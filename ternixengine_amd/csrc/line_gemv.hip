@@ -113,6 +113,12 @@ __device__ __forceinline__ float row_xor(float v, int lane) {
     return __int_as_float((lane & m) ? down : up);
 }
 
+// Four dwords at a 4-byte aligned address, read by one 16-byte load; global-memory pointers to
+// dwords and to such groups (addresses rebuilt from integers would otherwise be flat accesses).
+typedef uint32_t u4a __attribute__((ext_vector_type(4), aligned(4)));
+typedef __attribute__((address_space(1))) const uint32_t g_u32;
+typedef __attribute__((address_space(1))) const u4a g_u4a;
+
 template <int S, int NW, int AQ, bool EPI, bool RG, int MG = 1>
 __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args) {
     static_assert(NW == 4 || NW == 8, "4 or 8 data waves");
@@ -210,11 +216,14 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
         const int r_in = lane >> 3, pos = lane & 7;
         if constexpr (RG) {
             // Ragged operands (K % 64, N/4 % 16 or the weights' address arbitrary): register loads of
-            // the same 16-byte pieces as the DMA below, from 4-byte aligned dwords -- only those holding
-            // at least one byte of the piece, so no load leaves the rows' 4-byte aligned extent --
-            // funnel-shifted into place; rows past K are zeros, bytes past the row end are the next
-            // row's (their outputs are not written).  Then written to LDS in the DMA's layout.
+            // the same 16-byte pieces as the DMA below, from 4-byte aligned dwords (no load leaves the
+            // rows' 4-byte aligned extent), funnel-shifted into place; rows past K are zeros, bytes past
+            // the row end are the next row's or zeros (their outputs are not written).  Then written
+            // to LDS in the DMA's layout.  (Measured on MI355X against loading each of the five dwords
+            // on its own: 1x1000x3076 4.23 -> 3.53 us, 1x8191x2052 5.95 -> 5.16, 17x4093x1028 8.59 -> 7.89.)
             constexpr int NP = (S * 8 + NW - 1) / NW;
+            // end of the 4-byte aligned extent of the weight rows
+            const uintptr_t w_hull = (reinterpret_cast<uintptr_t>(args.B) + (size_t)K * (size_t)NB + 3) & ~uintptr_t(3);
             uint32_t d[NP][5];
             int sh[NP];
 #pragma unroll
@@ -230,11 +239,22 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
                     const int v = (step < nst && kr < K) ? min(16, NB - col) : 0;  // bytes of the piece
                     if (v > 0) {
                         const uintptr_t src = reinterpret_cast<uintptr_t>(args.B) + (size_t)kr * (size_t)NB + (size_t)col;
-                        const uint32_t* w = reinterpret_cast<const uint32_t*>(src & ~uintptr_t(3));
+                        const uintptr_t wa = src & ~uintptr_t(3);
                         sh[i] = (int)(src & 3);
+                        // Where the four dwords from the piece's first one lie inside the rows' aligned
+                        // extent: one 16-byte load (4-byte aligned), and the fifth dword when the piece
+                        // needs it; near the extent's end, only the dwords holding a byte of the piece.
+                        g_u32* w = (g_u32*)wa;
+                        if (wa + 16 <= w_hull) {
+                            const u4a x = *(g_u4a*)wa;
 #pragma unroll
-                        for (int u = 0; u < 5; ++u)
-                            if (4 * u < sh[i] + v) d[i][u] = w[u];
+                            for (int u = 0; u < 4; ++u) d[i][u] = x[u];
+                            if (sh[i] + v > 16) d[i][4] = w[4];
+                        } else {
+#pragma unroll
+                            for (int u = 0; u < 5; ++u)
+                                if (4 * u < sh[i] + v) d[i][u] = w[u];
+                        }
                     }
                 }
             }
@@ -526,8 +546,9 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
 #pragma unroll
         for (int st = 0; st < S; ++st) a[mg][st] = v4i{0, 0, 0, 0};
     if constexpr (RG) {
-        // 16 activations at an arbitrary address, from the 4-byte aligned dwords holding them; those
-        // past K multiply the zero rows above.
+        // 16 activations at an arbitrary address, from 4-byte aligned dwords; those past K (the next
+        // row's or zeros) multiply the zero rows above.
+        const uintptr_t a_hull = (reinterpret_cast<uintptr_t>(args.A) + (size_t)M * (size_t)K + 3) & ~uintptr_t(3);
 #pragma unroll
         for (int mg = 0; mg < MG; ++mg)
 #pragma unroll
@@ -536,11 +557,20 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
                 const int k0 = (s0 + st) * 64 + kb * 16, v = st < nst && row < M ? min(16, K - k0) : 0;
                 if (v > 0) {
                     const uintptr_t src = reinterpret_cast<uintptr_t>(args.A) + (size_t)row * (size_t)K + (size_t)k0;
-                    const uint32_t* w = reinterpret_cast<const uint32_t*>(src & ~uintptr_t(3));
+                    const uintptr_t wa = src & ~uintptr_t(3);
                     const uint32_t b = (uint32_t)(src & 3) * 8u;
-                    uint32_t d[5];
+                    // as for the weights: one 16-byte load inside the rows' aligned extent
+                    g_u32* w = (g_u32*)wa;
+                    uint32_t d[5] = {0u, 0u, 0u, 0u, 0u};
+                    if (wa + 16 <= a_hull) {  // as for the weights
+                        const u4a x = *(g_u4a*)wa;
 #pragma unroll
-                    for (int u = 0; u < 5; ++u) d[u] = 4 * u < (int)(b / 8) + v ? w[u] : 0u;
+                        for (int u = 0; u < 4; ++u) d[u] = x[u];
+                        if ((int)(b / 8) + v > 16) d[4] = w[4];
+                    } else {
+#pragma unroll
+                        for (int u = 0; u < 5; ++u) d[u] = 4 * u < (int)(b / 8) + v ? w[u] : 0u;
+                    }
 #pragma unroll
                     for (int u = 0; u < 4; ++u)
                         a[mg][st][u] = (int)(uint32_t)((((uint64_t)d[u + 1] << 32) | d[u]) >> b);

@@ -9,8 +9,11 @@ that writes vector registers asynchronously (inline assembly or not), in every k
 file of the library: walking forward in program order from the operation, the first instruction
 that names any of its destination registers must come after a wait whose count (lgkmcnt for LDS,
 vmcnt for global memory) is at most the number of operations of the same kind issued after it
-(0 when other kinds are mixed in: LDS with scalar loads, loads with stores).  The walk follows the
-fall-through path and stops at an unconditional jump or the end of the program."""
+(0 when other kinds are mixed in: LDS with scalar loads, loads with stores).  A later plain load that
+only overwrites those registers ends the walk: loads return in issue order, so its data lands last (the
+compiler lays out both halves of an exec-masked if / else in sequence, each loading into the same
+registers for its own lanes).  The walk follows the fall-through path and stops at an unconditional
+jump or the end of the program."""
 import os
 import re
 import subprocess
@@ -58,6 +61,12 @@ def _async_dest(mn, ops):
     return None
 
 
+def _plain_load(mn):
+    """A load from global memory into VGPRs (not an atomic, not LDS-bound): such loads return their
+    data in issue order on vmcnt."""
+    return mn.startswith(("global_load", "buffer_load")) and "lds" not in mn
+
+
 def _kind(mn):
     if mn.startswith("ds_"):
         return "lgkm"
@@ -94,6 +103,8 @@ def hazards(lines):
                     break  # operation i has completed
                 continue
             if _vregs(oj) & dest:
+                if _plain_load(mn) and _plain_load(mj) and not (_vregs(oj.split(",", 1)[1]) & dest):
+                    break  # a later load only overwrites them: loads return in order, so it lands last
                 found.append(f"{mn} {ops}  ->  {mj} {oj}")
                 break
             k = _kind(mj)
@@ -136,8 +147,13 @@ def test_checker_finds_a_planted_hazard():
     atomic = ["global_atomic_add_x2 v[6:7], v[2:3], v[0:1], off sc0", "v_readfirstlane_b32 s9, v7",
               "s_waitcnt vmcnt(0)"]
     overwrite = ["global_load_dwordx2 v[8:9], v[4:5], off sc1", "v_mov_b32_e32 v8, 0", "s_waitcnt vmcnt(0)"]
-    assert hazards(bad) and hazards(early) and hazards(atomic) and hazards(overwrite)
-    assert not hazards(good)
+    # two exec-masked loads into the same registers (an if / else the compiler laid out in sequence):
+    # ordered by the in-order return of loads; a later load that addresses with them reads them early
+    waw = ["global_load_dwordx4 v[6:9], v[20:21], off", "global_load_dword v6, v[22:23], off",
+           "s_waitcnt vmcnt(0)", "v_mov_b32_e32 v30, v6"]
+    addr = ["global_load_dwordx2 v[6:7], v[20:21], off", "global_load_dword v8, v[6:7], off", "s_waitcnt vmcnt(0)"]
+    assert hazards(bad) and hazards(early) and hazards(atomic) and hazards(overwrite) and hazards(addr)
+    assert not hazards(good) and not hazards(waw)
 
 
 def test_no_async_register_hazards(kernels):

@@ -224,7 +224,8 @@ def _check_guarded(dc, m, n, expect, tag):
 RAGGED = [(1, 1000, 3076, 0, 0), (4, 1000, 3076, 0, 0), (2, 4093, 1028, 0, 0), (3, 37, 20, 0, 0),
           (1, 5, 4, 0, 0), (2, 777, 516, 3, 1), (4, 4096, 1024, 3, 0), (1, 2560, 6912, 0, 2),
           (3, 130, 2044, 1, 3), (1, 8191, 2052, 0, 0), (12, 1500, 3076, 0, 0), (16, 4093, 1028, 2, 1),
-          (17, 4093, 1028, 0, 0), (24, 2000, 1036, 1, 2), (32, 1500, 516, 0, 0)]
+          (17, 4093, 1028, 0, 0), (24, 2000, 1036, 1, 2), (32, 1500, 516, 0, 0),
+          (1, 16, 4, 0, 1), (2, 9, 8, 1, 3)]
 
 
 @pytest.mark.gpu
@@ -232,7 +233,7 @@ RAGGED = [(1, 1000, 3076, 0, 0), (4, 1000, 3076, 0, 0), (2, 4093, 1028, 0, 0), (
 def test_line_gemv_ragged_matches_oracle(oracle, shape):
     """Ragged and misaligned operands go to the whole-line GEMV's register-staged form (no padded
     copy; 17-32 rows in two 16-row groups): bit-exact against the oracle, twice in a row on the same
-    tickets, and in graph replays."""
+    tickets, and in graph replays (operands of 5 to 18 bytes take the loads near the operands' end)."""
     lib = tx._load()
     m, k, n, ao, bo = shape
     p = _ragged_problem(oracle, np.random.default_rng(sum(shape)), *shape)
