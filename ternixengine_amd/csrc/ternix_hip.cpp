@@ -519,18 +519,22 @@ bool run_line_gemv(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int 
     if (fs > 0) {
         S = fs;
     } else {
-        // At most one workgroup per CU (on MI355X, cold: 1x8192x8192 7.86 -> 6.91 us with 256 workgroups of
-        // 8 k-steps, against the wave-pipelined kernel a cap of 250 left it to).  The FFN's down launch,
-        // which quantises its slice of h from the strip maxima first, starts at 4 k-steps (1x6912x2560:
-        // 27 splits instead of 36; the block 12.31 -> 12.11 us).
-        const long cap = std::max(1L, (long)cu_count());
-        for (int cand : {2, 3, 4, 6, 8}) {
-            if (aq.mode == 3 && cand < 4) continue;
-            const long sp = ternix_hip::line_gemv_splits(K, cand);
-            if (sp <= 64 && (long)strips * sp <= cap) {
-                S = cand;
-                break;
+        // About one workgroup per CU: first within 250 workgroups, else within the CU count (on MI355X,
+        // cold: a full 256-workgroup grid of 2 k-steps is slower than 176 of 3 for 1x4096x4096, 4.29
+        // against 4.19 us, but 1x8192x8192 runs 7.86 -> 6.91 us with 256 workgroups of 8 k-steps
+        // against the wave-pipelined kernel).  The FFN's down launch, which quantises its slice of h
+        // from the strip maxima first, starts at 4 k-steps (1x6912x2560: 27 splits instead of 36; the
+        // block 12.31 -> 12.11 us).
+        for (const long cap : {std::max(1L, (long)cu_count() * 250 / 256), std::max(1L, (long)cu_count())}) {
+            for (int cand : {2, 3, 4, 6, 8}) {
+                if (aq.mode == 3 && cand < 4) continue;
+                const long sp = ternix_hip::line_gemv_splits(K, cand);
+                if (sp <= 64 && (long)strips * sp <= cap) {
+                    S = cand;
+                    break;
+                }
             }
+            if (S != 0) break;
         }
         if (S == 0) return false;
     }
