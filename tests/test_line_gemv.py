@@ -260,6 +260,27 @@ def test_line_gemv_ragged_matches_oracle(oracle, shape):
 
 
 @pytest.mark.gpu
+def test_line_gemv_random_ragged_offsets(oracle):
+    """Seeded random ragged shapes up to 32 rows with A and W at random byte offsets, each operand
+    ending exactly at the end of its buffer, on the automatic path: bit-exact against the oracle,
+    nothing written past C."""
+    rng = np.random.default_rng(909)
+    s = hr.Stream()
+    for t in range(30):
+        m = int(rng.integers(1, 33))
+        k = int(rng.integers(1, 3000))
+        n = 4 * int(rng.integers(1, 800))
+        ao, bo = int(rng.integers(0, 16)), int(rng.integers(0, 16))
+        p = _ragged_problem(oracle, np.random.default_rng(t), m, k, n, ao, bo)
+        _, _, _, da, db, dc, expect, _, _ = p
+        log(f"[line random offsets] trial {t} M={m} K={k} N={n} A+{ao} W+{bo}")
+        dc.upload(np.full(m * n + GUARD, GARBAGE, np.int32))
+        assert tx.mul_mat_ternary(da.value + ao, db.value + bo, dc.value, m, k, n, stream=s.handle) == 0
+        s.synchronize()
+        _check_guarded(dc, m, n, expect, t)
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("m", [1, 4])
 def test_line_gemv_one_workgroup_per_cu(oracle, m):
     """8192 x 8192 on the automatic plan: 16 strips x 16 splits of 8 k-steps fill the CUs exactly (a
