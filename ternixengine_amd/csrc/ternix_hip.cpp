@@ -495,10 +495,13 @@ bool run_line_gemv(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int 
     // Rows: up to 4 on aligned operands (5-16 rows measured slower than the wave-pipelined kernel:
     // 16x2560x6912 9.20 against 7.02 us, more splits of 16-row atomics), up to 16 on ragged ones (no
     // padded copy); the DBG_LINE switch [3] sets the limit.
-    // Ragged rows past 4 need K >= 1024: on short K the few workgroups serialise their 16-row atomics
-    // (16x130x2044 6.90 against 5.44 us with the padded copy; 16x4093x1028 7.93 against 8.64).
+    // Ragged rows: up to 8 at any K, up to 16 from K = 256 and up to 32 from K = 1024; on shorter K the
+    // few workgroups serialise their 16-row atomics (on MI355X, cold, against the padded copy:
+    // 8x130x2044 4.82 / 5.38 us, 16x130x2044 6.61 / 5.44, 16x500x2044 7.01 / 7.76, 12x600x4100 6.09 /
+    // 8.08, 32x700x516 10.30 / 7.41, 24x1000x3076 8.90 / 8.40, 17x4093x1028 7.89 / 9.2).
     const int fm = ternix_hip::debug_get(ternix_hip::DBG_LINE, 3);
-    if (M > (fm > 0 ? std::min(fm, ragged ? 32 : 16) : (ragged && K >= 1024 ? 32 : 4))) return false;
+    const int ragged_rows = K >= 1024 ? 32 : (K >= 256 ? 16 : 8);
+    if (M > (fm > 0 ? std::min(fm, ragged ? 32 : 16) : (ragged ? ragged_rows : 4))) return false;
     if (!(dC != nullptr && reinterpret_cast<uintptr_t>(dC) % 16 == 0 &&
           (!ragged || (!epi && aq.mode == 0 && ternix_hip::line_gemv_ragged_ok(M, K, N)))))
         return false;

@@ -37,7 +37,10 @@ def test_plan_names_line_kernel_when_forced():
         assert not _plan(lib, 5, 2560, 6912).startswith("line_gemv_kernel")  # aligned: M <= 4 only
         assert _plan(lib, 1, 2560, 6900).startswith("line_gemv_kernel ragged S=2")  # N/4 % 16 != 0
         assert _plan(lib, 16, 2560, 6900).startswith("line_gemv_kernel ragged")  # ragged: more rows
-        assert not _plan(lib, 16, 1000, 6900).startswith("line_gemv_kernel")  # ... with K >= 1024
+        assert _plan(lib, 16, 1000, 6900).startswith("line_gemv_kernel ragged")  # 16 rows from K = 256
+        assert not _plan(lib, 16, 200, 6900).startswith("line_gemv_kernel")
+        assert _plan(lib, 8, 200, 6900).startswith("line_gemv_kernel ragged")  # 8 rows at any K
+        assert not _plan(lib, 17, 1000, 6900).startswith("line_gemv_kernel")  # 17-32 rows from K = 1024
         assert _plan(lib, 32, 2560, 6900).startswith("line_gemv_kernel ragged")  # two 16-row groups
         assert not _plan(lib, 33, 2560, 6900).startswith("line_gemv_kernel")
         assert lib.ternix_hip_debug_set(b"line", 1, 8, -1, -1) == 0
