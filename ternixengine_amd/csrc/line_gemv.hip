@@ -119,12 +119,13 @@ typedef uint32_t u4a __attribute__((ext_vector_type(4), aligned(4)));
 typedef __attribute__((address_space(1))) const uint32_t g_u32;
 typedef __attribute__((address_space(1))) const u4a g_u4a;
 
-template <int S, int NW, int AQ, bool EPI, bool RG, int MG = 1>
+template <int S, int NW, int AQ, bool EPI, bool RG, int MG = 1, bool T64 = false>
 __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args) {
     static_assert(NW == 4 || NW == 8, "4 or 8 data waves");
     static_assert(AQ == 0 || EPI, "fused quantisation comes with the float output");
     static_assert(!RG || (AQ == 0 && !EPI), "ragged operands: int32 output from int8 activations");
     static_assert(MG == 1 || (MG == 2 && RG), "two 16-row groups (17-32 rows) on ragged operands only");
+    static_assert(!(T64 && RG), "tile-64 weights are aligned by contract");
     constexpr int GW = 8 / NW;  // 16-byte column groups per data wave
     constexpr int STEP = 8192;  // bytes per k-step of the strip (64 rows x 128 bytes)
     __shared__ __attribute__((aligned(16))) uint8_t lds[S * STEP];
@@ -279,7 +280,11 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
                 const int step = min(p >> 3, nst - 1), r = (p & 7) * 8 + r_in;
                 int c = pos ^ line_swz(r);
                 if (bc0 + 16 * c >= NB) c = 0;  // past the last column (a partial last strip): a valid chunk, unused
-                const uint8_t* src = args.B + ((size_t)(s0 + step) * 64 + (size_t)r) * (size_t)NB + (size_t)(bc0 + 16 * c);
+                // T64: the same piece in the tile-64 layout (the 8 rows of one chunk that an instruction
+                // reads are one contiguous 128-byte line of their block)
+                const uint8_t* src =
+                    T64 ? args.B + tile64_offset((bc0 >> 4) + c, (s0 + step) * 64 + r, K >> 6)
+                        : args.B + ((size_t)(s0 + step) * 64 + (size_t)r) * (size_t)NB + (size_t)(bc0 + 16 * c);
                 lds_dma16(src, lds + (p >> 3) * STEP + (p & 7) * 1024);
             }
         }
@@ -763,8 +768,11 @@ int line_gemv_splits(int K, int S) { return ((K + 63) / 64 + S - 1) / S; }
 
 hipError_t launch_line_gemv(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int S, int NW,
                             unsigned long long* tk, int tk_stride, hipStream_t st, const OutScale& os,
-                            const ActQuant& aq, int xcd_chunks) {
+                            const ActQuant& aq, int xcd_chunks, int tiled) {
     const bool ragged = !line_gemv_ok(A, B, M, K, N);
+    // tile-64 weights: aligned operands (K % 128, N % 256 by the layout's contract), 4 GiB at most
+    if (tiled && (ragged || K % 128 != 0 || N % 256 != 0 || (size_t)K * (size_t)(N / 4) >= ((size_t)1 << 32)))
+        return hipErrorInvalidValue;
     const bool epi = os.Y != nullptr;
     if ((ragged && (!line_gemv_ragged_ok(M, K, N) || epi || aq.mode != 0)) || tk == nullptr || C == nullptr ||
         (uintptr_t)C % 8 != 0 || (M > 4 && aq.mode != 0))
@@ -810,7 +818,11 @@ hipError_t launch_line_gemv(const int8_t* A, const uint8_t* B, int32_t* C, int M
     const int mode = ragged ? (M > 16 ? 6 : 5) : (epi ? 1 + aq.mode : 0);
 #define TX_LINE(SS, WW, AQQ, EE, RR)                                                                         \
     if (S == SS && NW == WW && mode == (RR ? 5 : (EE ? 1 + AQQ : 0))) {                                      \
-        hipLaunchKernelGGL((line_gemv_kernel<SS, WW, AQQ, EE, RR>), grid, dim3(64 * (WW + 1)), 0, st, a);   \
+        if (tiled)                                                                                           \
+            hipLaunchKernelGGL((line_gemv_kernel<SS, WW, AQQ, EE, false, 1, true>), grid, dim3(64 * (WW + 1)), \
+                               0, st, a);                                                                    \
+        else                                                                                                 \
+            hipLaunchKernelGGL((line_gemv_kernel<SS, WW, AQQ, EE, RR>), grid, dim3(64 * (WW + 1)), 0, st, a); \
         return hipGetLastError();                                                                            \
     }
 #define TX_LINE_RG2(SS)                                                                                      \

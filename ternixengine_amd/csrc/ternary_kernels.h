@@ -105,13 +105,14 @@ struct ActQuant {
 // Whole-line decode GEMV (line_gemv.hip): M <= 16, K % 64 == 0, N/4 % 16 == 0, 16-byte aligned A and W
 // (or, int32 output only, any K, N % 4 == 0 and any A / W address: the ragged form); 8-byte aligned C;
 // S k-steps per workgroup, NW data waves (4 or 8); K splits added with int32 atomics into C zeroed by
-// each strip's split 0 (tickets: two 64-bit words per 128-byte strip, persistent).
+// each strip's split 0 (tickets: two 64-bit words per 128-byte strip, persistent).  tiled: W in the
+// tile-64 layout (K % 128 == 0, N % 256 == 0), read in the same pieces.
 bool line_gemv_ok(const int8_t* A, const uint8_t* B, int M, int K, int N);
 bool line_gemv_ragged_ok(int M, int K, int N);  // the ragged-operand form (int32 output)
 int line_gemv_splits(int K, int S);
 hipError_t launch_line_gemv(const int8_t* A, const uint8_t* B, int32_t* C, int M, int K, int N, int S, int NW,
                             unsigned long long* tk, int tk_stride, hipStream_t st, const OutScale& os = OutScale{},
-                            const ActQuant& aq = ActQuant{}, int xcd_chunks = 0);
+                            const ActQuant& aq = ActQuant{}, int xcd_chunks = 0, int tiled = 0);
 // (os.Y set: float output through the last-arriving split of each strip, C then being the int32 buffer
 // of the sums, tickets spread one line per strip; aq.mode 1 / 2: fused activation quantisation of
 // fp32 rows aq.X with M <= 4 and M * K <= 8192, only with os.Y; mode 3: any K, from a producer's

@@ -487,11 +487,12 @@ bool run_atomic_wave(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, in
 // with an int32 output.
 bool run_line_gemv(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int K, int N, Ctx& c, hipError_t* e,
                    const ternix_hip::OutScale& os = ternix_hip::OutScale{},
-                   const ternix_hip::ActQuant& aq = ternix_hip::ActQuant{}) {
+                   const ternix_hip::ActQuant& aq = ternix_hip::ActQuant{}, int tiled = 0) {
     const int fs = ternix_hip::debug_get(ternix_hip::DBG_LINE, 0), fw = ternix_hip::debug_get(ternix_hip::DBG_LINE, 1);
     if (fs == 0) return false;
     const bool epi = os.Y != nullptr;
     const bool ragged = !ternix_hip::line_gemv_ok(dA, dB, M, K, N);
+    if (tiled && ragged) return false;  // (the tile-64 contract keeps its operands aligned)
     // Rows: up to 4 on aligned operands (5-16 rows measured slower than the wave-pipelined kernel:
     // 16x2560x6912 9.20 against 7.02 us, more splits of 16-row atomics), up to 16 on ragged ones (no
     // padded copy); the DBG_LINE switch [3] sets the limit.
@@ -549,7 +550,7 @@ bool run_line_gemv(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int 
     unsigned long long* tk = c.tickets(ternix_hip::ticket_units((size_t)strips));
     if (!tk) return false;
     c.note("line_gemv_kernel%s S=%d waves=%d+1 splits=%d%s%s (splits added with int32 atomics into C zeroed by each "
-           "strip's split 0)", ragged ? " ragged" : "", S, NW, splits, aq.mode == 2 ? " rmsnorm+quantise" : (aq.mode == 1 ? " quantise" : ""),
+           "strip's split 0)", ragged ? " ragged" : (tiled ? " (tile-64)" : ""), S, NW, splits, aq.mode == 2 ? " rmsnorm+quantise" : (aq.mode == 1 ? " quantise" : ""),
            epi ? (os.swiglu ? " dequant+swiglu" : " dequant") : "");
     // Rows whose length is not a multiple of 128 bytes share a cache line between neighbouring strips:
     // those launches take the XCD-chunked unit order (on MI355X, cold: 1x4096x11008 6.40 -> 5.70 us,
@@ -560,7 +561,7 @@ bool run_line_gemv(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int 
     const int fx = ternix_hip::debug_get(ternix_hip::DBG_LINE, 2);
     const bool resident = (long)strips * splits <= (long)cu_count();
     const int xcd = fx >= 0 ? fx : ((N / 4) % 128 != 0 && resident);
-    *e = TX_LAUNCH(c, ternix_hip::launch_line_gemv(dA, dB, dC, M, K, N, S, NW, tk, stride, c.st, os, aq, xcd));
+    *e = TX_LAUNCH(c, ternix_hip::launch_line_gemv(dA, dB, dC, M, K, N, S, NW, tk, stride, c.st, os, aq, xcd, tiled));
     return true;
 }
 
@@ -881,6 +882,14 @@ hipError_t run_tile64(const int8_t* dA, const uint8_t* dWt, int32_t* dC, int M, 
                       const ternix_hip::OutScale& os = ternix_hip::OutScale{}) {
     const hipStream_t st = c.st;
     (void)st;
+    // One row: the whole-line GEMV, which reads the tile-64 blocks in the same 128-byte lines as
+    // row-major rows (on MI355X, cold: 1x2560x6912 4.61 -> 4.23 us, 1x6912x2560 4.74 -> 4.50,
+    // 1x4096x4096 4.94 -> 4.30; at 4 rows the wave-pipelined plans below are as fast or faster,
+    // 4x11008x4096 6.62 against 6.81).
+    if (M == 1) {
+        hipError_t e = hipSuccess;
+        if (run_line_gemv(dA, dWt, dC, M, K, N, c, &e, os, ternix_hip::ActQuant{}, 1)) return e;
+    }
     // The self-zeroing atomic plan below applies to int32 output up to 16 rows; where it does, it is
     // faster than the whole-K kernel (cold, one box, us: cfg1 4.80 -> 3.64, cfg2 up 5.10 -> 4.49, 4x4096x11008
     // 6.46 -> 6.32, 16x4096x11008 7.69 -> 7.31), which keeps the dequantising calls.
@@ -1197,6 +1206,34 @@ FfnLayout ffn_layout(int64_t M, int64_t H, int64_t F) {
     return l;
 }
 
+// Both GEMVs of the decode FFN block on the whole-line GEMV, two launches: the gate/up launch applies
+// RMSNorm + quantisation to x (aq1), dequantises with SwiGLU (os1) and leaves each strip's largest |h|
+// per row in amax; the down launch quantises its slice of h from those maxima (the absmax is exact in
+// any order), writing its row scales to rs2 (those os2 reads), and dequantises (os2) -- no workgroup
+// reads whole rows of h.  Returns false, with nothing
+// queued, when the gate/up plan does not apply; *down_done is false when only the gate/up launch ran
+// (the caller then runs the down GEMV another way).  tiled: both weight matrices in the tile-64 layout.
+bool ffn_line(const uint8_t* dWgu, const uint8_t* dWd, float* dY, int32_t* scratch, float* amax, int m, int hd, int f,
+              const ternix_hip::OutScale& os1, const ternix_hip::ActQuant& aq1, const ternix_hip::OutScale& os2,
+              float* rs2, Ctx c, int tiled, hipError_t* e, bool* down_done) {
+    *down_done = false;
+    if (ternix_hip::debug_get(ternix_hip::DBG_FFN_AMAX) == 0) return false;
+    ternix_hip::ActQuant g1 = aq1;
+    g1.amax_out = amax;
+    g1.amax_stride = ffn_amax_stride(f);
+    if (!run_line_gemv(nullptr, dWgu, scratch, m, hd, 2 * f, c, e, os1, g1, tiled)) return false;
+    if (*e != hipSuccess) return true;
+    ternix_hip::ActQuant g2;
+    g2.mode = 3;
+    g2.X = os1.Y;
+    g2.rs_out = rs2;
+    g2.amax_in = amax;
+    g2.amax_stride = g1.amax_stride;
+    g2.amax_n = (2 * f / 4 + 127) / 128;
+    *down_done = run_line_gemv(nullptr, dWd, reinterpret_cast<int32_t*>(dY), m, f, hd, c, e, os2, g2, tiled);
+    return true;
+}
+
 }  // namespace
 
 size_t ternix_hip_ffn_workspace_size(int64_t M, int64_t H, int64_t F) {
@@ -1255,22 +1292,11 @@ int ternix_hip_ffn_forward(float* dY, const float* dX, const float* dNormWeight,
         // Both on the whole-line GEMV: the gate/up launch also leaves each strip's largest |h| per row,
         // so the down launch quantises h from its own slice and those maxima (the absmax is exact in
         // any order) instead of every workgroup reading whole rows of h.
-        if (ternix_hip::debug_get(ternix_hip::DBG_FFN_AMAX) != 0) {
-            Ctx c = ctx_of(st);
-            hipError_t e = hipSuccess;
-            ternix_hip::ActQuant g1 = aq1;
-            g1.amax_out = amax;
-            g1.amax_stride = ffn_amax_stride(F);
-            if (run_line_gemv(nullptr, dWgu, scratch, m, hd, 2 * f, c, &e, os1, g1)) {
-                if (e != hipSuccess) return (int)e;
-                ternix_hip::ActQuant g2 = aq2;
-                g2.mode = 3;
-                g2.amax_in = amax;
-                g2.amax_stride = g1.amax_stride;
-                g2.amax_n = (2 * f / 4 + 127) / 128;
-                if (run_line_gemv(nullptr, dWd, reinterpret_cast<int32_t*>(dY), m, f, hd, c, &e, os2, g2)) return (int)e;
-                return (int)run_skinny(nullptr, dWd, reinterpret_cast<int32_t*>(dY), m, f, hd, c, os2, aq2);
-            }
+        bool down_done = false;
+        hipError_t e = hipSuccess;
+        if (ffn_line(dWgu, dWd, dY, scratch, amax, m, hd, f, os1, aq1, os2, rs2, ctx_of(st), 0, &e, &down_done)) {
+            if (e != hipSuccess || down_done) return (int)e;
+            return (int)run_skinny(nullptr, dWd, reinterpret_cast<int32_t*>(dY), m, f, hd, ctx_of(st), os2, aq2);
         }
         const SkinnyPlan p1 = plan_skinny(m, hd, 2 * f), p2 = plan_skinny(m, f, hd);
         if (ternix_hip::skinny_short_ok(dWgu, m, hd, 2 * f, p1.sps, p1.splits) &&
@@ -1318,7 +1344,29 @@ int ternix_hip_ffn_forward_tile64(float* dY, const float* dX, const float* dNorm
     os1.rs = rs1;
     os1.ws = ws_gu;
     os1.swiglu = 1;
-    hipError_t e;
+    hipError_t e = hipSuccess;
+    {
+        // Up to 4 rows: two launches of the whole-line GEMV on the tile-64 blocks, as on row-major
+        // weights (on MI355X, cold, H 2560, F 6912, M = 1: 21.9 -> 12.8 us per block).
+        ternix_hip::ActQuant aq1;
+        aq1.mode = 2;
+        aq1.X = dX;
+        aq1.G = dNormWeight;
+        aq1.eps = eps;
+        aq1.rs_out = rs1;
+        ternix_hip::OutScale os2;
+        os2.Y = dY;
+        os2.rs = rs2;
+        os2.ws = ws_d;
+        bool down_done = false;
+        float* amax = reinterpret_cast<float*>(ws + l.amax);
+        if (ffn_line(dWguT, dWdT, dY, scratch, amax, m, hd, f, os1, aq1, os2, rs2, ctx_of(st), 1, &e, &down_done)) {
+            if (e != hipSuccess || down_done) return (int)e;
+            e = ternix_hip::launch_quantize_rows(h, q2, rs2, m, f, st);
+            if (e != hipSuccess) return (int)e;
+            return (int)run_tile64(q2, dWdT, reinterpret_cast<int32_t*>(dY), m, f, hd, ctx_of(st), os2);
+        }
+    }
     if (m <= 16 && hd <= 4096) {
         // RMSNorm + quantisation of x inside the gate/up GEMV (one launch, whole rows per workgroup).
         ternix_hip::ActQuant aq1;

@@ -214,10 +214,12 @@ def test_gpu_ffn_forward(oracle, shape):
 
 
 @gpu
-@pytest.mark.parametrize("shape", [(1, 2560, 6912), (4, 2560, 6912), (16, 1024, 2816), (24, 512, 1024)])
+@pytest.mark.parametrize("shape", [(1, 2560, 6912), (4, 2560, 6912), (3, 1024, 2304), (16, 1024, 2816),
+                                   (24, 512, 1024)])
 def test_gpu_ffn_forward_tile64(shape):
-    """The block on tile-64 weights equals the block on the contract layout, bit for bit (fused
-    RMSNorm + quantisation in the gate/up GEMV for M <= 16, the separate launches above)."""
+    """The block on tile-64 weights equals the block on the contract layout, bit for bit (up to 4 rows
+    the two whole-line GEMV launches on the tile-64 blocks, fused RMSNorm + quantisation in the gate/up
+    GEMV up to 16 rows, the separate launches above)."""
     m, hd, f = shape
     log(f"[ffn tile-64] M={m} H={hd} F={f}")
     rng = np.random.default_rng(7 * m + hd + f)
