@@ -120,7 +120,11 @@ typedef __attribute__((address_space(1))) const uint32_t g_u32;
 typedef __attribute__((address_space(1))) const u4a g_u4a;
 
 template <int S, int NW, int AQ, bool EPI, bool RG, int MG = 1, bool T64 = false>
-__global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args) {
+__global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(const uint8_t* Bp, const void* Ap, const void* Gp, int32_t* Cp, int Mp,
+                                                         int Kp, int Np, int strips_p, int splits_p, int xcd_p,
+                                                         LineArgs args) {
+    // Leading scalars (preloaded into SGPRs by the command processor): Ap is A, or X with fused
+    // quantisation; Gp is G (AQ 2) or the producer's maxima (AQ 3).
     static_assert(NW == 4 || NW == 8, "4 or 8 data waves");
     static_assert(AQ == 0 || EPI, "fused quantisation comes with the float output");
     static_assert(!RG || (AQ == 0 && !EPI), "ragged operands: int32 output from int8 activations");
@@ -138,19 +142,19 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int strips = args.strips;
+    const int strips = strips_p;
     // Workgroup g runs on XCD g mod 8.  With xcd_chunks the split-major unit sequence is cut into 8
     // contiguous chunks, chunk x taken by the workgroups of XCD x in order, so that neighbouring strips
     // of one split share an L2 (rows whose length is not a multiple of 128 bytes put one cache line
     // in two strips).
     int unit = (int)blockIdx.x;
-    if (args.xcd_chunks) {
-        const int G = strips * args.splits, q = G >> 3, r = G & 7, x = unit & 7;
+    if (xcd_p) {
+        const int G = strips * splits_p, q = G >> 3, r = G & 7, x = unit & 7;
         unit = x * q + min(x, r) + (unit >> 3);
     }
     const int split = unit / strips;
     const int s = unit - split * strips;
-    const int M = args.M, K = args.K, N = args.N, NB = N >> 2;
+    const int M = Mp, K = Kp, N = Np, NB = N >> 2;
     const int s0 = split * S;                 // first k-step
     const int nst = min(S, ((K + 63) >> 6) - s0);  // k-steps of this unit (>= 1; RG: the last may be partial)
     const int bc0 = s * 128;                  // first byte-column of the strip
@@ -172,32 +176,32 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
     uint32_t xs[S], gs[S];
     if constexpr (AQ == 1 || AQ == 2) {
         if (wave < M && regs) {
-            const float* xrow = args.X + (size_t)wave * (size_t)K;
+            const float* xrow = reinterpret_cast<const float*>(Ap) + (size_t)wave * (size_t)K;
 #pragma unroll
             for (int j = 0; j < KJ; ++j) {
                 const int k = 256 * j + 4 * lane;
                 xr[j] = k < K ? *reinterpret_cast<const v4i*>(xrow + k) : v4i{0, 0, 0, 0};
-                gr[j] = AQ == 2 && k < K ? *reinterpret_cast<const v4i*>(args.G + k) : v4i{0, 0, 0, 0};
+                gr[j] = AQ == 2 && k < K ? *reinterpret_cast<const v4i*>(reinterpret_cast<const float*>(Gp) + k) : v4i{0, 0, 0, 0};
             }
 #pragma unroll
             for (int u = 0; u < S; ++u) {
                 const int k = 64 * (s0 + min(u, nst - 1)) + lane;
                 xs[u] = __float_as_uint(xrow[k]);
-                gs[u] = AQ == 2 ? __float_as_uint(args.G[k]) : 0u;
+                gs[u] = AQ == 2 ? __float_as_uint(reinterpret_cast<const float*>(Gp)[k]) : 0u;
             }
         }
         __builtin_amdgcn_sched_barrier(0);  // these loads ahead of the weights' DMAs (in-order counter)
     }
     if constexpr (AQ != 0) {
         if (wave < M && !regs) {
-            const uint8_t* xb = reinterpret_cast<const uint8_t*>(args.X);
+            const uint8_t* xb = reinterpret_cast<const uint8_t*>(Ap);
             uint8_t* xd = reinterpret_cast<uint8_t*>(xl) + wave * xpitch;
             if constexpr (AQ == 3) {
                 const int n = nst * 256;
                 const uint8_t* src = xb + ((size_t)wave * (size_t)K + (size_t)s0 * 64) * 4;
                 for (int c = 0; c * 1024 < n; ++c) lds_dma16(src + min(c * 1024 + lane * 16, n - 16), xd + c * 1024);
                 const int na = args.amax_stride * 4;
-                const uint8_t* asrc = reinterpret_cast<const uint8_t*>(args.amax_in + (size_t)wave * args.amax_stride);
+                const uint8_t* asrc = reinterpret_cast<const uint8_t*>(reinterpret_cast<const float*>(Gp) + (size_t)wave * args.amax_stride);
                 uint8_t* ad = reinterpret_cast<uint8_t*>(gl) + wave * apitch;
                 for (int c = 0; c * 1024 < na; ++c) lds_dma16(asrc + min(c * 1024 + lane * 16, na - 16), ad + c * 1024);
             } else {
@@ -205,7 +209,7 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
                 const uint8_t* src = xb + (size_t)wave * (size_t)n;
                 for (int c = 0; c * 1024 < n; ++c) lds_dma16(src + min(c * 1024 + lane * 16, n - 16), xd + c * 1024);
                 if constexpr (AQ == 2) {
-                    const uint8_t* gb = reinterpret_cast<const uint8_t*>(args.G);
+                    const uint8_t* gb = reinterpret_cast<const uint8_t*>(reinterpret_cast<const float*>(Gp));
                     uint8_t* gd = reinterpret_cast<uint8_t*>(gl) + wave * xpitch;
                     for (int c = 0; c * 1024 < n; ++c) lds_dma16(gb + min(c * 1024 + lane * 16, n - 16), gd + c * 1024);
                 }
@@ -224,7 +228,7 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
             // on its own: 1x1000x3076 4.23 -> 3.53 us, 1x8191x2052 5.95 -> 5.16, 17x4093x1028 8.59 -> 7.89.)
             constexpr int NP = (S * 8 + NW - 1) / NW;
             // end of the 4-byte aligned extent of the weight rows
-            const uintptr_t w_hull = (reinterpret_cast<uintptr_t>(args.B) + (size_t)K * (size_t)NB + 3) & ~uintptr_t(3);
+            const uintptr_t w_hull = (reinterpret_cast<uintptr_t>(Bp) + (size_t)K * (size_t)NB + 3) & ~uintptr_t(3);
             uint32_t d[NP][5];
             int sh[NP];
 #pragma unroll
@@ -239,7 +243,7 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
                     const int kr = (s0 + step) * 64 + r;
                     const int v = (step < nst && kr < K) ? min(16, NB - col) : 0;  // bytes of the piece
                     if (v > 0) {
-                        const uintptr_t src = reinterpret_cast<uintptr_t>(args.B) + (size_t)kr * (size_t)NB + (size_t)col;
+                        const uintptr_t src = reinterpret_cast<uintptr_t>(Bp) + (size_t)kr * (size_t)NB + (size_t)col;
                         const uintptr_t wa = src & ~uintptr_t(3);
                         sh[i] = (int)(src & 3);
                         // Where the four dwords from the piece's first one lie inside the rows' aligned
@@ -283,8 +287,8 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
                 // T64: the same piece in the tile-64 layout (the 8 rows of one chunk that an instruction
                 // reads are one contiguous 128-byte line of their block)
                 const uint8_t* src =
-                    T64 ? args.B + tile64_offset((bc0 >> 4) + c, (s0 + step) * 64 + r, K >> 6)
-                        : args.B + ((size_t)(s0 + step) * 64 + (size_t)r) * (size_t)NB + (size_t)(bc0 + 16 * c);
+                    T64 ? Bp + tile64_offset((bc0 >> 4) + c, (s0 + step) * 64 + r, K >> 6)
+                        : Bp + ((size_t)(s0 + step) * 64 + (size_t)r) * (size_t)NB + (size_t)(bc0 + 16 * c);
                 lds_dma16(src, lds + (p >> 3) * STEP + (p & 7) * 1024);
             }
         }
@@ -296,7 +300,7 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
         if (zeroer) {
             const int n8 = 2 * min(128, NB - bc0);  // 8-byte units of the strip's outputs in one row
             for (int r = 0; r < M; ++r) {
-                unsigned long long* z = reinterpret_cast<unsigned long long*>(args.C + (size_t)r * (size_t)N + 4 * bc0);
+                unsigned long long* z = reinterpret_cast<unsigned long long*>(Cp + (size_t)r * (size_t)N + 4 * bc0);
                 for (int u = lane; u < n8; u += 64) __hip_atomic_store(z + u, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
             if constexpr (EPI) {  // the strip's maxima start at 0 too (published with the zeroed word)
@@ -305,7 +309,7 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
                                        0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
             // T += 64 - (splits - 1) (no return needed).  Lane 0 alone enabled; nothing waited for here.
-            const unsigned long long inc = (unsigned long long)(64 - (args.splits - 1));
+            const unsigned long long inc = (unsigned long long)(64 - (splits_p - 1));
             __asm__ volatile(
                 "s_mov_b64 %0, exec\n\t"
                 "s_mov_b64 exec, 1\n\t"
@@ -553,7 +557,7 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
     if constexpr (RG) {
         // 16 activations at an arbitrary address, from 4-byte aligned dwords; those past K (the next
         // row's or zeros) multiply the zero rows above.
-        const uintptr_t a_hull = (reinterpret_cast<uintptr_t>(args.A) + (size_t)M * (size_t)K + 3) & ~uintptr_t(3);
+        const uintptr_t a_hull = (reinterpret_cast<uintptr_t>(Ap) + (size_t)M * (size_t)K + 3) & ~uintptr_t(3);
 #pragma unroll
         for (int mg = 0; mg < MG; ++mg)
 #pragma unroll
@@ -561,7 +565,7 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
                 const int row = 16 * mg + q;
                 const int k0 = (s0 + st) * 64 + kb * 16, v = st < nst && row < M ? min(16, K - k0) : 0;
                 if (v > 0) {
-                    const uintptr_t src = reinterpret_cast<uintptr_t>(args.A) + (size_t)row * (size_t)K + (size_t)k0;
+                    const uintptr_t src = reinterpret_cast<uintptr_t>(Ap) + (size_t)row * (size_t)K + (size_t)k0;
                     const uintptr_t wa = src & ~uintptr_t(3);
                     const uint32_t b = (uint32_t)(src & 3) * 8u;
                     // as for the weights: one 16-byte load inside the rows' aligned extent
@@ -582,7 +586,7 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
                 }
             }
     } else if constexpr (AQ == 0) {
-        const int8_t* arow = args.A + (size_t)min(q, M - 1) * (size_t)K + (size_t)s0 * 64 + kb * 16;
+        const int8_t* arow = reinterpret_cast<const int8_t*>(Ap) + (size_t)min(q, M - 1) * (size_t)K + (size_t)s0 * 64 + kb * 16;
 #pragma unroll
         for (int st = 0; st < S; ++st)
             if (st < nst && q < M) a[0][st] = *reinterpret_cast<const v4i*>(arow + st * 64);
@@ -673,7 +677,7 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
         const int g = wave * GW + gi;
         if (bc0 + 16 * g >= NB) continue;  // wave-uniform
         const int col0 = 4 * (bc0 + 16 * g);  // the group's first column
-        int32_t* out = args.C + col0 + lane;
+        int32_t* out = Cp + col0 + lane;
         const bool in_row = !RG || col0 + lane < N;  // RG: a partial last group
 #pragma unroll
         for (int mg = 0; mg < MG; ++mg)
@@ -697,12 +701,12 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(LineArgs args)
                         if (lane < 32 && c < N) {
                             const unsigned long long add =
                                 ((unsigned long long)(uint32_t)o << 32) + (unsigned long long)(long long)(e + 1);
-                            unsigned long long* word = reinterpret_cast<unsigned long long*>(args.C + (size_t)i * (size_t)N + c);
+                            unsigned long long* word = reinterpret_cast<unsigned long long*>(Cp + (size_t)i * (size_t)N + c);
                             const unsigned long long prev = __hip_atomic_fetch_add(word, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                            if ((int)((uint32_t)prev & 63u) == args.splits - 1) {
+                            if ((int)((uint32_t)prev & 63u) == splits_p - 1) {
                                 const long long tot = (long long)(prev + add);
                                 const int lo = (int)(uint32_t)tot;
-                                const int ce = (lo - args.splits) >> 6;
+                                const int ce = (lo - splits_p) >> 6;
                                 const int co = (int)((tot - (long long)lo) >> 38);
                                 const float f = (AQ != 0 ? rscale[i] : args.os.rs[i]) * args.os.ws;
                                 const float mx = store_scaled_pair(args.os, f, i, N, c, ce, co);
@@ -816,18 +820,21 @@ hipError_t launch_line_gemv(const int8_t* A, const uint8_t* B, int32_t* C, int M
     // 0 int32 out, 1 dequantised, 2 / 3 / 4 with fused quantisation, 5 / 6 int32 out from ragged
     // operands in one / two 16-row groups
     const int mode = ragged ? (M > 16 ? 6 : 5) : (epi ? 1 + aq.mode : 0);
+#define TX_LINE_ARGS a.B, aq.mode ? (const void*)a.X : (const void*)a.A, aq.mode == 3 ? (const void*)a.amax_in : (const void*)a.G, \
+    a.C, a.M, a.K, a.N, a.strips, a.splits, a.xcd_chunks, a
 #define TX_LINE(SS, WW, AQQ, EE, RR)                                                                         \
     if (S == SS && NW == WW && mode == (RR ? 5 : (EE ? 1 + AQQ : 0))) {                                      \
         if (tiled)                                                                                           \
             hipLaunchKernelGGL((line_gemv_kernel<SS, WW, AQQ, EE, false, 1, true>), grid, dim3(64 * (WW + 1)), \
-                               0, st, a);                                                                    \
+                               0, st, TX_LINE_ARGS);                                                         \
         else                                                                                                 \
-            hipLaunchKernelGGL((line_gemv_kernel<SS, WW, AQQ, EE, RR>), grid, dim3(64 * (WW + 1)), 0, st, a); \
+            hipLaunchKernelGGL((line_gemv_kernel<SS, WW, AQQ, EE, RR>), grid, dim3(64 * (WW + 1)), 0, st,     \
+                               TX_LINE_ARGS);                                                                \
         return hipGetLastError();                                                                            \
     }
 #define TX_LINE_RG2(SS)                                                                                      \
     if (S == SS && NW == 8 && mode == 6) {                                                                   \
-        hipLaunchKernelGGL((line_gemv_kernel<SS, 8, 0, false, true, 2>), grid, dim3(64 * 9), 0, st, a);     \
+        hipLaunchKernelGGL((line_gemv_kernel<SS, 8, 0, false, true, 2>), grid, dim3(64 * 9), 0, st, TX_LINE_ARGS); \
         return hipGetLastError();                                                                            \
     }
 #define TX_LINE_S(SS)                   \
@@ -852,6 +859,7 @@ hipError_t launch_line_gemv(const int8_t* A, const uint8_t* B, int32_t* C, int M
 #undef TX_LINE_S
 #undef TX_LINE_RG2
 #undef TX_LINE
+#undef TX_LINE_ARGS
     return hipErrorInvalidValue;
 }
 

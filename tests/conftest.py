@@ -16,6 +16,17 @@ if ROOT not in sys.path:
 GOLDEN = os.path.join(ROOT, "tests", "golden")
 
 
+def hip_file_flags(src):
+    """Extra hipcc flags the library's Makefile gives one source (the whole-line GEMV's kernel-argument
+    preload count), so that tests reading the emitted code see what the library runs."""
+    if src != "line_gemv.hip":
+        return []
+    import re
+    with open(os.path.join(ROOT, "ternixengine_amd", "csrc", "Makefile")) as f:
+        n = re.search(r"^LINE_PRELOAD \?= (\d+)", f.read(), re.M).group(1)
+    return ["-mllvm", f"-amdgpu-kernarg-preload-count={n}"]
+
+
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU")
 

@@ -20,6 +20,8 @@ import subprocess
 
 import pytest
 
+from conftest import hip_file_flags
+
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 CSRC = os.path.join(ROOT, "ternixengine_amd", "csrc")
 HIPCC = "/opt/rocm/bin/hipcc"
@@ -129,7 +131,8 @@ def kernels(tmp_path_factory):
         out = d / (src + ".s")
         subprocess.run([HIPCC, "--offload-arch=gfx950", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
                         "-O3", "-std=c++17", f"-I{ROOT}/include", f"-I{CSRC}", "--cuda-device-only", "-S", "-o",
-                        str(out), os.path.join(CSRC, src)], check=True, capture_output=True, timeout=900)
+                        str(out), os.path.join(CSRC, src)] + hip_file_flags(src), check=True, capture_output=True,
+                       timeout=900)
         text = out.read_text()
         for m in re.finditer(r"^(_Z\w*):\s*(?:;.*)?$", text, re.M):
             end = text.find(".Lfunc_end", m.end())

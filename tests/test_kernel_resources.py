@@ -15,6 +15,8 @@ import subprocess
 
 import pytest
 
+from conftest import hip_file_flags
+
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 CSRC = os.path.join(ROOT, "ternixengine_amd", "csrc")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -24,7 +26,7 @@ SOURCES = sorted(f for f in os.listdir(CSRC) if f.endswith(".hip"))
 def _resources(src):
     cmd = [HIPCC, "--offload-arch=gfx950", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-O3",
            "-std=c++17", "-fPIC", "-I" + os.path.join(ROOT, "include"), "-I" + CSRC, "--cuda-device-only", "-c",
-           "-o", os.devnull, os.path.join(CSRC, src), "-Rpass-analysis=kernel-resource-usage"]
+           "-o", os.devnull, os.path.join(CSRC, src), "-Rpass-analysis=kernel-resource-usage"] + hip_file_flags(src)
     out = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
     assert out.returncode == 0, out.stderr[-2000:]
     kernels, name = {}, None
