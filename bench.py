@@ -107,6 +107,20 @@ def calibrate_copy():
     hr.synchronize()
 
 
+def device_pool(arr, copies):
+    """`copies` device buffers holding `arr`: one upload from the host, the others device-to-device
+    copies (no per-copy pass through the runtime's pageable host staging)."""
+    from ternixengine_amd import hip_runtime as hr
+    first = hr.DeviceBuffer.from_array(arr)
+    out = [first]
+    for _ in range(copies - 1):
+        d = hr.DeviceBuffer(arr.nbytes)
+        hr.check(hr._load().hipMemcpy(d.ptr, first.ptr, arr.nbytes, hr.D2D), "hipMemcpy D2D")
+        out.append(d)
+    hr.synchronize()
+    return out
+
+
 class Problem:
     """Device-resident inputs of one case, with `copies` distinct weight buffers."""
 
@@ -117,7 +131,7 @@ class Problem:
         self.a = configs.gen_a(case)
         self.wp = configs.gen_w_packed(case)
         self.dA = hr.DeviceBuffer.from_array(self.a)
-        self.dW = [hr.DeviceBuffer.from_array(self.wp) for _ in range(copies)]
+        self.dW = device_pool(self.wp, copies)
         self.dC = hr.DeviceBuffer(4 * case.M * case.N)
 
 
@@ -362,8 +376,8 @@ def bench_ffn(args, stream, lib):
     wd = rng.integers(0, 256, size=(f, h // 4), dtype=np.uint16).astype(np.uint8) & 0x77
     per = wgu.nbytes + wd.nbytes
     copies = max(2, -(-POOL_MIN_BYTES // per))
-    dgu = [hr.DeviceBuffer.from_array(wgu) for _ in range(copies)]
-    dd = [hr.DeviceBuffer.from_array(wd) for _ in range(copies)]
+    dgu = device_pool(wgu, copies)
+    dd = device_pool(wd, copies)
     dx, dg, dy = hr.DeviceBuffer.from_array(x), hr.DeviceBuffer.from_array(g), hr.DeviceBuffer(4 * m * h)
     nws = lib.ternix_hip_ffn_workspace_size(m, h, f)
     dws = hr.DeviceBuffer(nws)
@@ -380,8 +394,8 @@ def bench_ffn(args, stream, lib):
     moved = per + 4 * m * h * 2 + 4 * h
     # the same block on tile-64 weights (converted once, untimed), same pools; output compared
     import ternixengine_amd as tx
-    tgu = [hr.DeviceBuffer.from_array(tx.interleave_tile64(wgu)) for _ in range(copies)]
-    td = [hr.DeviceBuffer.from_array(tx.interleave_tile64(wd)) for _ in range(copies)]
+    tgu = device_pool(tx.interleave_tile64(wgu), copies)
+    td = device_pool(tx.interleave_tile64(wd), copies)
     dyt = hr.DeviceBuffer(4 * m * h)
 
     def one_t(i):
