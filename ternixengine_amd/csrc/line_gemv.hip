@@ -120,11 +120,13 @@ typedef __attribute__((address_space(1))) const uint32_t g_u32;
 typedef __attribute__((address_space(1))) const u4a g_u4a;
 
 template <int S, int NW, int AQ, bool EPI, bool RG, int MG = 1, bool T64 = false>
-__global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(const uint8_t* Bp, const void* Ap, const void* Gp, int32_t* Cp, int Mp,
-                                                         int Kp, int Np, int strips_p, int splits_p, int xcd_p,
-                                                         LineArgs args) {
+__global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(const uint8_t* Bp, const void* Ap, const void* Gp, int32_t* Cp,
+                                                         unsigned long long* tkp, int Kp, int Np, unsigned shape_p,
+                                                         int tk_stride_p, LineArgs args) {
     // Leading scalars (preloaded into SGPRs by the command processor): Ap is A, or X with fused
-    // quantisation; Gp is G (AQ 2) or the producer's maxima (AQ 3).
+    // quantisation; Gp is G (AQ 2) or the producer's maxima (AQ 3); tkp the strips' tickets; shape_p
+    // packs the strip count (bits 0-15), the split count (16-22), the XCD-chunked order (23) and M
+    // (24-31).
     static_assert(NW == 4 || NW == 8, "4 or 8 data waves");
     static_assert(AQ == 0 || EPI, "fused quantisation comes with the float output");
     static_assert(!RG || (AQ == 0 && !EPI), "ragged operands: int32 output from int8 activations");
@@ -142,7 +144,8 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(const uint8_t*
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int strips = strips_p;
+    const int strips = (int)(shape_p & 0xFFFFu), splits_p = (int)((shape_p >> 16) & 0x7Fu);
+    const int xcd_p = (int)((shape_p >> 23) & 1u), Mp = (int)(shape_p >> 24);
     // Workgroup g runs on XCD g mod 8.  With xcd_chunks the split-major unit sequence is cut into 8
     // contiguous chunks, chunk x taken by the workgroups of XCD x in order, so that neighbouring strips
     // of one split share an L2 (rows whose length is not a multiple of 128 bytes put one cache line
@@ -159,7 +162,7 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(const uint8_t*
     const int nst = min(S, ((K + 63) >> 6) - s0);  // k-steps of this unit (>= 1; RG: the last may be partial)
     const int bc0 = s * 128;                  // first byte-column of the strip
     const bool zeroer = split == 0;
-    unsigned long long* tk = args.tk + (size_t)args.tk_stride * (size_t)s;
+    unsigned long long* tk = tkp + (size_t)tk_stride_p * (size_t)s;
 
     // AQ: wave r < M stages what row r needs, global -> LDS ahead of its weights, 1 KB per instruction
     // (the last chunk's lanes past the end re-read valid bytes into the row's padding), so that
@@ -815,13 +818,16 @@ hipError_t launch_line_gemv(const int8_t* A, const uint8_t* B, int32_t* C, int M
     a.amax_in = aq.amax_in;
     a.amax_n = aq.amax_n;
 
-    if (a.splits > 64 || (size_t)S * 64 > (size_t)kMaxKPerAccumulator) return hipErrorInvalidValue;
+    if (a.splits > 64 || a.strips > 0xFFFF || M > 255 || (size_t)S * 64 > (size_t)kMaxKPerAccumulator)
+        return hipErrorInvalidValue;
     const dim3 grid((unsigned)(a.strips * a.splits));
     // 0 int32 out, 1 dequantised, 2 / 3 / 4 with fused quantisation, 5 / 6 int32 out from ragged
     // operands in one / two 16-row groups
     const int mode = ragged ? (M > 16 ? 6 : 5) : (epi ? 1 + aq.mode : 0);
+    const unsigned shape = (unsigned)a.strips | ((unsigned)a.splits << 16) | ((a.xcd_chunks ? 1u : 0u) << 23) |
+                           ((unsigned)a.M << 24);
 #define TX_LINE_ARGS a.B, aq.mode ? (const void*)a.X : (const void*)a.A, aq.mode == 3 ? (const void*)a.amax_in : (const void*)a.G, \
-    a.C, a.M, a.K, a.N, a.strips, a.splits, a.xcd_chunks, a
+    a.C, a.tk, a.K, a.N, shape, a.tk_stride, a
 #define TX_LINE(SS, WW, AQQ, EE, RR)                                                                         \
     if (S == SS && NW == WW && mode == (RR ? 5 : (EE ? 1 + AQQ : 0))) {                                      \
         if (tiled)                                                                                           \
