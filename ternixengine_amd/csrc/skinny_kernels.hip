@@ -657,7 +657,16 @@ __device__ __forceinline__ int sd_swz(int r) { return (r & 7) | (((r >> 4) & 1) 
 
 template <int NS, int NAD, bool LOW_M, int AQ = 0>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
-void skinny_dma_kernel(SkinnyArgs args) {
+void skinny_dma_kernel(const uint8_t* Bp, const void* Ap, int32_t* Cp, unsigned long long* tkp, int Kp, int Np,
+                                         int spsp, int tk_stride_p, unsigned flags_p, SkinnyArgs args) {
+    // Leading scalars, preloaded into SGPRs by the command processor (SkinnyArgs holds the same
+    // values): flags_p packs M (bits 0-7), splits (8-17), mode (18-20), nt (21), line_units (22),
+    // defer_ticket (23), tiled (24) and order (25).
+    const int f_M = (int)(flags_p & 0xFFu), f_splits = (int)((flags_p >> 8) & 0x3FFu);
+    const int f_mode = (int)((flags_p >> 18) & 7u), f_nt = (int)((flags_p >> 21) & 1u);
+    const int f_line = (int)((flags_p >> 22) & 1u), f_defer = (int)((flags_p >> 23) & 1u);
+    const int f_tiled = (int)((flags_p >> 24) & 1u), f_order = (int)((flags_p >> 25) & 1u);
+    (void)f_line; (void)f_defer; (void)f_tiled; (void)f_order; (void)f_nt;
     static_assert(NS >= 2 && NS <= 4, "2 to 4 stages");
     __shared__ __attribute__((aligned(16))) uint8_t sW0[SD_STAGE];
     __shared__ __attribute__((aligned(16))) uint8_t sW1[SD_STAGE];
@@ -666,9 +675,9 @@ void skinny_dma_kernel(SkinnyArgs args) {
     __shared__ __attribute__((aligned(16))) int8_t sA[NAD * 256 * 16];
     auto stage_w = [&](int i) -> uint8_t* { return i == 0 ? sW0 : (i == 1 ? sW1 : (i == 2 ? sW2 : sW3)); };
 
-    const int8_t* __restrict__ A = args.A;
-    const uint8_t* __restrict__ B = args.B;
-    const int M = args.M, K = args.K, NB = args.N >> 2;
+    const int8_t* __restrict__ A = reinterpret_cast<const int8_t*>(Ap);
+    const uint8_t* __restrict__ B = Bp;
+    const int M = f_M, K = Kp, NB = Np >> 2;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -681,8 +690,8 @@ void skinny_dma_kernel(SkinnyArgs args) {
     }
     const int bc0 = cx * SD_BNB;
     const int m0 = blockIdx.z * 16;
-    const int s_begin = sy * args.steps_per_split;
-    const int nst = min(K >> 6, s_begin + args.steps_per_split) - s_begin;  // >= 1 (planner)
+    const int s_begin = sy * spsp;
+    const int nst = min(K >> 6, s_begin + spsp) - s_begin;  // >= 1 (planner)
 
     // Activation slice: position j = 16 c + r holds 16-byte chunk c of row r (rows clamped to the
     // m-group, chunks to the k-range).  AQ > 0: built below from the fp32 rows instead.
@@ -699,8 +708,8 @@ void skinny_dma_kernel(SkinnyArgs args) {
     };
     // SK_ATOMZ (as in skinny_wave_kernel): wave 0 takes the strip's ticket before any DMA; the
     // first loop wait of wave 0 (for a step issued after it) covers its return.
-    const bool ticket = args.mode == SK_ATOMZ && wave == 0;
-    unsigned long long* tk = args.tick + (size_t)args.tk_stride * (size_t)cx;
+    const bool ticket = f_mode == SK_ATOMZ && wave == 0;
+    unsigned long long* tk = tkp + (size_t)tk_stride_p * (size_t)cx;
     unsigned long long old = 0, call1 = 0, zw = 0;
     bool zeroer = false;
     if (ticket && lane == 0)
@@ -714,12 +723,12 @@ void skinny_dma_kernel(SkinnyArgs args) {
         const int rank = (int)(old & 63);
         call1 = (old >> 6) + 1;
         zeroer = rank == 0;
-        if (rank == args.splits - 1 && args.splits < 64 && lane == 0)
-            __hip_atomic_fetch_add(tk, (unsigned long long)(64 - args.splits), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (rank == f_splits - 1 && f_splits < 64 && lane == 0)
+            __hip_atomic_fetch_add(tk, (unsigned long long)(64 - f_splits), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (zeroer)
             for (int r = 0; r < a_rows; ++r) {
                 unsigned long long* z =
-                    reinterpret_cast<unsigned long long*>(args.C + (size_t)(m0 + r) * (size_t)args.N + 4 * bc0);
+                    reinterpret_cast<unsigned long long*>(Cp + (size_t)(m0 + r) * (size_t)Np + 4 * bc0);
                 const int n8 = min(SD_BNB, NB - bc0) * 2;  // 8-byte units of this strip's outputs
                 for (int u = lane; u < n8; u += 64)
                     __hip_atomic_store(z + u, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -756,7 +765,7 @@ void skinny_dma_kernel(SkinnyArgs args) {
     auto issue = [&](int st, int buf) {
         const uint8_t* wbase = B + (size_t)(s_begin + st) * 64 * (size_t)NB;
         uint8_t* wdst = stage_w(buf);
-        if (args.nt) {
+        if (f_nt) {
 #pragma unroll
             for (int p = 0; p < SD_NL; ++p) lds_dma16_nt(wbase + w_off[p], wdst + (p * 4 + wave) * 1024);
         } else {
@@ -873,7 +882,7 @@ void skinny_dma_kernel(SkinnyArgs args) {
         step(it, it % NS);
         __builtin_amdgcn_sched_barrier(0);
     }
-    if (args.mode == SK_ATOMZ) {
+    if (f_mode == SK_ATOMZ) {
         // every wave's atomics wait until the strip is zeroed (wave 0 checks, the barrier spreads it)
         if (wave == 0 && !zeroer && lane == 0)
             wait_zeroed(tk, zw, call1);
@@ -881,7 +890,7 @@ void skinny_dma_kernel(SkinnyArgs args) {
     }
 
     // Epilogue: lane (q, kb) holds rows 4kb+i of byte-columns bc0 + 16(4 wave + g) + q.
-    if (LOW_M && args.mode == SK_ATOMZ) {
+    if (LOW_M && f_mode == SK_ATOMZ) {
         // Few rows into C with atomics: each wave lays its row's 256 outputs out in column order in
         // its own 1 KB of the (now idle) stage buffer, then adds one column per lane per instruction
         // (64 consecutive int32 per atomic instruction, no per-element branch).  The barrier above
@@ -900,7 +909,7 @@ void skinny_dma_kernel(SkinnyArgs args) {
             int32_t vals[4];
 #pragma unroll
             for (int u = 0; u < 4; ++u) vals[u] = row_lds[64 * u + lane];
-            int32_t* out = args.C + (size_t)(m0 + i) * (size_t)args.N + 4 * col0;
+            int32_t* out = Cp + (size_t)(m0 + i) * (size_t)Np + 4 * col0;
 #pragma unroll
             for (int u = 0; u < 4; ++u)
                 if (col0 + 16 * u + lane / 4 < NB) atomicAdd(out + 64 * u + lane, vals[u]);
@@ -910,8 +919,8 @@ void skinny_dma_kernel(SkinnyArgs args) {
         return;
     }
     if (LOW_M && kb != 0) return;
-    int32_t* out_base = args.mode == SK_PARTIAL ? args.P + (size_t)sy * (size_t)M * (size_t)args.N : args.C;
-    const bool vec = args.mode == SK_PARTIAL || args.vec_store;
+    int32_t* out_base = f_mode == SK_PARTIAL ? args.P + (size_t)sy * (size_t)M * (size_t)Np : Cp;
+    const bool vec = f_mode == SK_PARTIAL || args.vec_store;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int row = m0 + 4 * kb + i;
@@ -921,12 +930,12 @@ void skinny_dma_kernel(SkinnyArgs args) {
             const int bcol = bc0 + (wave * 4 + g) * 16 + q;
             if (bcol >= NB) continue;
             const v4i v = {acc[g][0][i] >> 6, acc[g][1][i] >> 6, acc[g][2][i] >> 6, acc[g][3][i] >> 6};
-            if (args.mode == SK_STORE && args.os.Y) {
-                store_scaled(args.os, row, args.N, 4 * bcol, v, args.vec_store);
+            if (f_mode == SK_STORE && args.os.Y) {
+                store_scaled(args.os, row, Np, 4 * bcol, v, args.vec_store);
                 continue;
             }
-            int32_t* out = out_base + (size_t)row * (size_t)args.N + 4 * bcol;
-            if (args.mode == SK_ATOMIC || args.mode == SK_ATOMZ) {
+            int32_t* out = out_base + (size_t)row * (size_t)Np + 4 * bcol;
+            if (f_mode == SK_ATOMIC || f_mode == SK_ATOMZ) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
                     if (v[j] != 0) atomicAdd(out + j, v[j]);
@@ -959,7 +968,16 @@ void skinny_dma_kernel(SkinnyArgs args) {
 // ------------------------------------------------------------------------------------------------
 template <int SW, int NSW, bool LOW_M, int AQ = 0, bool CW = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
-void skinny_wave_kernel(SkinnyArgs args) {
+void skinny_wave_kernel(const uint8_t* Bp, const void* Ap, int32_t* Cp, unsigned long long* tkp, int Kp, int Np,
+                                         int spsp, int tk_stride_p, unsigned flags_p, SkinnyArgs args) {
+    // Leading scalars, preloaded into SGPRs by the command processor (SkinnyArgs holds the same
+    // values): flags_p packs M (bits 0-7), splits (8-17), mode (18-20), nt (21), line_units (22),
+    // defer_ticket (23), tiled (24) and order (25).
+    const int f_M = (int)(flags_p & 0xFFu), f_splits = (int)((flags_p >> 8) & 0x3FFu);
+    const int f_mode = (int)((flags_p >> 18) & 7u), f_nt = (int)((flags_p >> 21) & 1u);
+    const int f_line = (int)((flags_p >> 22) & 1u), f_defer = (int)((flags_p >> 23) & 1u);
+    const int f_tiled = (int)((flags_p >> 24) & 1u), f_order = (int)((flags_p >> 25) & 1u);
+    (void)f_line; (void)f_defer; (void)f_tiled; (void)f_order; (void)f_nt;
     static_assert(SW == 16 || SW == 32, "16- or 32-byte strips");
     // CW (column waves, self-zeroing atomics at M <= 4 only): the workgroup owns a 4 * SW-byte strip
     // and wave w its w-th SW-byte part over every k-step of the range, so the four parts of each
@@ -975,9 +993,9 @@ void skinny_wave_kernel(SkinnyArgs args) {
     __shared__ __attribute__((aligned(16))) int8_t qbuf[AQ ? 16 : 1][AQ ? QK : 16];
     __shared__ float rscale[16];
 
-    const int8_t* __restrict__ A = args.A;
-    const uint8_t* __restrict__ B = args.B;
-    const int M = args.M, K = args.K, NB = args.N >> 2;
+    const int8_t* __restrict__ A = reinterpret_cast<const int8_t*>(Ap);
+    const uint8_t* __restrict__ B = Bp;
+    const int M = f_M, K = Kp, NB = Np >> 2;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int q = lane & 15, kb = lane >> 4;
@@ -992,22 +1010,22 @@ void skinny_wave_kernel(SkinnyArgs args) {
     int c4 = 0;
     bool part_ok = true;  // CW: this wave's part lies inside the matrix
     if (CW) {
-        const int total = n_cw * args.splits;
+        const int total = n_cw * f_splits;
         if ((int)blockIdx.x >= total) return;
         const int lin = xcd_linear(blockIdx.x, total);
         c4 = lin % n_cw;
         sy = lin / n_cw;
         part_ok = c4 * 4 + wave < n_strips;
         cx = min(c4 * 4 + wave, n_strips - 1);  // a part past the last column re-reads the last one
-    } else if (args.line_units) {
+    } else if (f_line) {
         const int b = blockIdx.x, t = b >> 3;
         const int u = (b & 7) + 8 * (t / SPL);  // unit: (split, line group)
         sy = u / lines;
         cx = (u % lines) * SPL + t % SPL;
-        if (sy >= args.splits || cx >= n_strips) return;  // whole workgroup: no barrier reached yet
+        if (sy >= f_splits || cx >= n_strips) return;  // whole workgroup: no barrier reached yet
     } else {
         // contiguous strip ranges per XCD (balanced; lines at range ends are fetched by two L2s)
-        const int total = n_strips * args.splits;
+        const int total = n_strips * f_splits;
         if ((int)blockIdx.x >= total) return;
         const int lin = xcd_linear(blockIdx.x, total);
         cx = lin % n_strips;
@@ -1015,8 +1033,8 @@ void skinny_wave_kernel(SkinnyArgs args) {
     }
     const int bc0 = cx * SW;
     const int m0 = blockIdx.z * 16;
-    const int s_begin = sy * args.steps_per_split;
-    const int nst = min(K >> 6, s_begin + args.steps_per_split) - s_begin;  // >= 1
+    const int s_begin = sy * spsp;
+    const int nst = min(K >> 6, s_begin + spsp) - s_begin;  // >= 1
     const int nreal = CW ? nst : (nst > wave ? (nst - wave + 3) / 4 : 0);    // this wave's k-steps
     uint8_t* ring = lds + wave * NSW * SLOT;
 
@@ -1042,11 +1060,11 @@ void skinny_wave_kernel(SkinnyArgs args) {
     auto issue = [&](int it, int slot_c, v4i& a_dst) {
         const int s = CW ? min(s_begin + it, s_last) : min(s_begin + wave + 4 * it, s_last);
         uint8_t* dst = ring + slot_c * SLOT;
-        if (SW == 16 && args.tiled) {  // one contiguous 1 KB block, already in LDS order
+        if (SW == 16 && f_tiled) {  // one contiguous 1 KB block, already in LDS order
             lds_dma16(B + ((size_t)cx * (size_t)(K >> 6) + (size_t)s) * 1024 + lane * 16, dst);
         } else {
             const uint8_t* wbase = B + (size_t)s * 64 * (size_t)NB;
-            if (args.nt) {
+            if (f_nt) {
 #pragma unroll
                 for (int p = 0; p < NL; ++p) lds_dma16_nt(wbase + w_off[p], dst + p * 1024);
             } else {
@@ -1099,12 +1117,12 @@ void skinny_wave_kernel(SkinnyArgs args) {
     unsigned long long call1 = 0;  // this call's number + 1, as the zeroer writes it
     bool zeroer = false;
     // Atomic modes: C has CN columns at pitch CN (a padded problem's real columns when n_out > 0)
-    const int CN = args.n_out > 0 ? args.n_out : args.N;
+    const int CN = args.n_out > 0 ? args.n_out : Np;
     // one ticket pair per (m-group, strip)
-    unsigned long long* tk = CW ? args.tick + (size_t)args.tk_stride * ((size_t)blockIdx.z * (size_t)n_cw + (size_t)c4)
-                                : args.tick + (size_t)args.tk_stride * ((size_t)blockIdx.z * (size_t)n_strips + (size_t)cx);
+    unsigned long long* tk = CW ? tkp + (size_t)tk_stride_p * ((size_t)blockIdx.z * (size_t)n_cw + (size_t)c4)
+                                : tkp + (size_t)tk_stride_p * ((size_t)blockIdx.z * (size_t)n_strips + (size_t)cx);
     unsigned long long old = 0;
-    const bool ticket = AQ == 0 && args.mode == SK_ATOMZ && wave == 0;
+    const bool ticket = AQ == 0 && f_mode == SK_ATOMZ && wave == 0;
     if (ticket && lane == 0)
         __asm__ volatile("global_atomic_add_x2 %0, %1, %2, off sc0" : "=v"(old) : "v"(tk), "v"(1ull) : "memory");
 #pragma unroll
@@ -1119,8 +1137,8 @@ void skinny_wave_kernel(SkinnyArgs args) {
         const int rank = (int)(old & 63);
         call1 = (old >> 6) + 1;
         zeroer = rank == 0;
-        if (rank == args.splits - 1 && args.splits < 64 && lane == 0)
-            __hip_atomic_fetch_add(tk, (unsigned long long)(64 - args.splits), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (rank == f_splits - 1 && f_splits < 64 && lane == 0)
+            __hip_atomic_fetch_add(tk, (unsigned long long)(64 - f_splits), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (zeroer) {
             // rows m0 .. m0 + a_rows - 1, the strip's columns (4 * SW, or 16 * SW with CW): 8 bytes a lane
             constexpr int ZB = CW ? 4 * SW : SW;  // strip bytes per row
@@ -1129,7 +1147,7 @@ void skinny_wave_kernel(SkinnyArgs args) {
                 for (int u = lane; u < ZB * 2; u += 64) {
                     if (4 * zb0 + 2 * u < CN) {
                         unsigned long long* z =
-                            reinterpret_cast<unsigned long long*>(args.C + (size_t)(m0 + r) * (size_t)CN + 4 * zb0) + u;
+                            reinterpret_cast<unsigned long long*>(Cp + (size_t)(m0 + r) * (size_t)CN + 4 * zb0) + u;
                         __hip_atomic_store(z, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     }
                 }
@@ -1139,7 +1157,7 @@ void skinny_wave_kernel(SkinnyArgs args) {
             if (lane == 0) __hip_atomic_store(tk + 1, call1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     };
-    if (ticket && !args.defer_ticket) {
+    if (ticket && !f_defer) {
         TX_VMCNT((NSW - 1) * (NL + 1));  // the ticket has returned (the weight loads may not have)
         take_ticket();
     }
@@ -1193,7 +1211,7 @@ void skinny_wave_kernel(SkinnyArgs args) {
             else if (later == 2) TX_VMCNT(2 * VPS);
             else if (later == 1) TX_VMCNT(VPS);
             else TX_VMCNT(0);
-            if (ticket && args.defer_ticket && it == 0) take_ticket();  // the older ticket has too
+            if (ticket && f_defer && it == 0) take_ticket();  // the older ticket has too
             if (ticket && !zeroer && it == nreal - 1 && lane == 0)
                 zw = __hip_atomic_load(tk + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             {
@@ -1255,7 +1273,7 @@ void skinny_wave_kernel(SkinnyArgs args) {
             int32_t vals[G];
 #pragma unroll
             for (int u = 0; u < G; ++u) vals[u] = row_lds[64 * u + lane];
-            int32_t* out = args.C + (size_t)(m0 + i) * (size_t)CN + 4 * bc0;
+            int32_t* out = Cp + (size_t)(m0 + i) * (size_t)CN + 4 * bc0;
 #pragma unroll
             for (int u = 0; u < G; ++u)
                 if (4 * bc0 + 64 * u + lane < CN) atomicAdd(out + 64 * u + lane, vals[u]);
@@ -1274,7 +1292,7 @@ void skinny_wave_kernel(SkinnyArgs args) {
             for (int j = 0; j < 4; ++j) r[(g * 4 + j) * 64 + lane] = acc[g][j];
     }
     __syncthreads();
-    if (wave != 0 && args.mode != SK_LAST) return;
+    if (wave != 0 && f_mode != SK_LAST) return;
     if (wave == 0) {
 #pragma unroll
         for (int w = 0; w < 3; ++w) {
@@ -1285,9 +1303,9 @@ void skinny_wave_kernel(SkinnyArgs args) {
                 for (int j = 0; j < 4; ++j) acc[g][j] += r[(g * 4 + j) * 64 + lane];
         }
     }
-    if (args.mode == SK_LAST) {
+    if (f_mode == SK_LAST) {
         __shared__ int s_last;
-        const size_t MN = (size_t)M * (size_t)args.N;
+        const size_t MN = (size_t)M * (size_t)Np;
         int* counter = args.cnt + (size_t)blockIdx.z * (size_t)n_strips + cx;
         if (wave == 0) {
             int32_t* mine = args.P + (size_t)sy * MN;
@@ -1297,8 +1315,8 @@ void skinny_wave_kernel(SkinnyArgs args) {
 #pragma unroll
                 for (int g = 0; g < G; ++g) {
                     if ((LOW_M && kb != 0) || row >= M) continue;
-                    int32_t* out = mine + (size_t)row * (size_t)args.N + 4 * (bc0 + 16 * g + q);
-                    if (args.order) {
+                    int32_t* out = mine + (size_t)row * (size_t)Np + 4 * (bc0 + 16 * g + q);
+                    if (f_order) {
                         *reinterpret_cast<v4i*>(out) =
                             v4i{acc[g][0][i] >> 6, acc[g][1][i] >> 6, acc[g][2][i] >> 6, acc[g][3][i] >> 6};
                         continue;
@@ -1308,22 +1326,22 @@ void skinny_wave_kernel(SkinnyArgs args) {
                         __hip_atomic_store(out + j, acc[g][j][i] >> 6, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 }
             }
-            if (!args.order) {
+            if (!f_order) {
                 __builtin_amdgcn_s_waitcnt(0);  // the partial stores are complete, coherent at agent scope
                 __atomic_signal_fence(__ATOMIC_SEQ_CST);
                 if (lane == 0)
                     s_last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                             args.splits - 1;
+                             f_splits - 1;
             }
         }
-        if (args.order) {
+        if (f_order) {
             // Release/acquire form: the barrier orders every partial store of the workgroup before
             // thread 0's agent-scope release, and its acquire (with the barrier after it) orders the
             // last arriver's loads after every other split's release.
             __syncthreads();
             if (tid == 0)
                 s_last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) ==
-                         args.splits - 1;
+                         f_splits - 1;
         }
         __syncthreads();
         if (!s_last) return;  // workgroup-uniform
@@ -1332,20 +1350,20 @@ void skinny_wave_kernel(SkinnyArgs args) {
         const int rows = min(16, M - m0);
         for (int idx = tid; idx < rows * SW; idx += 256) {
             const int row = m0 + idx / SW, col = 4 * (bc0 + idx % SW);
-            const size_t off = (size_t)row * (size_t)args.N + col;
+            const size_t off = (size_t)row * (size_t)Np + col;
             v4i v = {0, 0, 0, 0};
-            for (int c0 = 0; c0 < args.splits; c0 += 8) {
+            for (int c0 = 0; c0 < f_splits; c0 += 8) {
                 uint64_t lo[8], hi[8];
 #pragma unroll
                 for (int u = 0; u < 8; ++u) {
                     const uint64_t* src =
-                        reinterpret_cast<const uint64_t*>(args.P + (size_t)min(c0 + u, args.splits - 1) * MN + off);
+                        reinterpret_cast<const uint64_t*>(args.P + (size_t)min(c0 + u, f_splits - 1) * MN + off);
                     lo[u] = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     hi[u] = __hip_atomic_load(src + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 }
 #pragma unroll
                 for (int u = 0; u < 8; ++u) {
-                    if (c0 + u >= args.splits) continue;
+                    if (c0 + u >= f_splits) continue;
                     v[0] += (int)(uint32_t)lo[u];
                     v[1] += (int)(uint32_t)(lo[u] >> 32);
                     v[2] += (int)(uint32_t)hi[u];
@@ -1353,23 +1371,23 @@ void skinny_wave_kernel(SkinnyArgs args) {
                 }
             }
             if (args.os.Y) {
-                store_scaled(args.os, row, args.N, col, v, args.vec_store);
+                store_scaled(args.os, row, Np, col, v, args.vec_store);
             } else if (args.vec_store) {
-                *reinterpret_cast<v4i*>(args.C + off) = v;
+                *reinterpret_cast<v4i*>(Cp + off) = v;
             } else {
 #pragma unroll
-                for (int j = 0; j < 4; ++j) args.C[off + j] = v[j];
+                for (int j = 0; j < 4; ++j) Cp[off + j] = v[j];
             }
         }
         if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;
     }
-    if (AQ == 0 && args.mode == SK_ATOMZ && !zeroer) {  // wave 0: wait until the strip is zeroed
+    if (AQ == 0 && f_mode == SK_ATOMZ && !zeroer) {  // wave 0: wait until the strip is zeroed
         if (lane == 0)
             wait_zeroed(tk, zw, call1);
         __builtin_amdgcn_wave_barrier();
     }
-    if (LOW_M && AQ == 0 && (args.mode == SK_ATOMIC || args.mode == SK_ATOMZ)) {
+    if (LOW_M && AQ == 0 && (f_mode == SK_ATOMIC || f_mode == SK_ATOMZ)) {
         // Few rows: wave 0 lays each row's 4 * SW outputs out in LDS in column order (lane q of
         // group g holds columns 4 (16 g + q) + j), then every lane adds one column per instruction:
         // 64 consecutive int32 per atomic instruction, no per-element branch.  The LDS area is the
@@ -1387,7 +1405,7 @@ void skinny_wave_kernel(SkinnyArgs args) {
             int32_t vals[G];
 #pragma unroll
             for (int u = 0; u < G; ++u) vals[u] = row_lds[64 * u + lane];
-            int32_t* out = args.C + (size_t)(m0 + i) * (size_t)CN + 4 * bc0;
+            int32_t* out = Cp + (size_t)(m0 + i) * (size_t)CN + 4 * bc0;
 #pragma unroll
             for (int u = 0; u < G; ++u)
                 if (4 * bc0 + 64 * u + lane < CN) atomicAdd(out + 64 * u + lane, vals[u]);
@@ -1396,7 +1414,7 @@ void skinny_wave_kernel(SkinnyArgs args) {
         }
         return;
     }
-    if (!LOW_M && AQ == 0 && args.mode == SK_ATOMZ) {
+    if (!LOW_M && AQ == 0 && f_mode == SK_ATOMZ) {
         // Up to 16 rows: wave 0 lays every row's 4 * SW outputs out in LDS in column order (row r at
         // r * 4 * SW; lane (q, kb) holds rows 4 kb + i), then adds one column per lane per instruction,
         // row by row: 64 consecutive int32 per atomic instruction.  The LDS area is the reduction
@@ -1415,7 +1433,7 @@ void skinny_wave_kernel(SkinnyArgs args) {
         }
         __builtin_amdgcn_wave_barrier();
         for (int r = 0; r < rows; ++r) {
-            int32_t* out = args.C + (size_t)(m0 + r) * (size_t)CN + 4 * bc0;
+            int32_t* out = Cp + (size_t)(m0 + r) * (size_t)CN + 4 * bc0;
 #pragma unroll
             for (int u = 0; u < G; ++u)
                 if (4 * bc0 + 64 * u + lane < CN) atomicAdd(out + 64 * u + lane, row_lds[r * 4 * SW + 64 * u + lane]);
@@ -1423,10 +1441,10 @@ void skinny_wave_kernel(SkinnyArgs args) {
         return;
     }
     if (LOW_M && kb != 0) return;
-    int32_t* out_base = args.mode == SK_PARTIAL ? args.P + (size_t)sy * (size_t)M * (size_t)args.N : args.C;
-    const bool vec = args.mode == SK_PARTIAL || args.vec_store;
+    int32_t* out_base = f_mode == SK_PARTIAL ? args.P + (size_t)sy * (size_t)M * (size_t)Np : Cp;
+    const bool vec = f_mode == SK_PARTIAL || args.vec_store;
     // Store mode writes n_out columns at pitch n_out (a padded problem's real columns).
-    const int NO = (args.mode == SK_STORE && args.n_out > 0) ? args.n_out : args.N;
+    const int NO = (f_mode == SK_STORE && args.n_out > 0) ? args.n_out : Np;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int row = m0 + 4 * kb + i;
@@ -1436,13 +1454,13 @@ void skinny_wave_kernel(SkinnyArgs args) {
             const int bcol = bc0 + 16 * g + q;
             if (4 * bcol >= NO) continue;
             const v4i v = {acc[g][0][i] >> 6, acc[g][1][i] >> 6, acc[g][2][i] >> 6, acc[g][3][i] >> 6};
-            if (args.mode == SK_STORE && args.os.Y) {
+            if (f_mode == SK_STORE && args.os.Y) {
                 if constexpr (AQ != 0) store_scaled_f(args.os, rscale[row - m0] * args.os.ws, row, NO, 4 * bcol, v, args.vec_store);
                 else store_scaled(args.os, row, NO, 4 * bcol, v, args.vec_store);
                 continue;
             }
             int32_t* out = out_base + (size_t)row * (size_t)NO + 4 * bcol;
-            if (args.mode == SK_ATOMIC || args.mode == SK_ATOMZ) {
+            if (f_mode == SK_ATOMIC || f_mode == SK_ATOMZ) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
                     if (v[j] != 0) atomicAdd(out + j, v[j]);
@@ -1526,16 +1544,26 @@ hipError_t launch_generic(const SkinnyArgs& a, dim3 grid, hipStream_t st) {
     return hipGetLastError();
 }
 
+// The leading scalar arguments of skinny_dma_kernel / skinny_wave_kernel (see their flags_p).
+unsigned sk_flags(const SkinnyArgs& a) {
+    return (unsigned)a.M | ((unsigned)a.splits << 8) | ((unsigned)a.mode << 18) | ((a.nt ? 1u : 0u) << 21) |
+           ((a.line_units ? 1u : 0u) << 22) | ((a.defer_ticket ? 1u : 0u) << 23) | ((a.tiled ? 1u : 0u) << 24) |
+           ((a.order ? 1u : 0u) << 25);
+}
+#define TX_SK_ARGS(a) \
+    (a).B, (const void*)(a).A, (a).C, (a).tick, (a).K, (a).N, (a).steps_per_split, (a).tk_stride, sk_flags(a), (a)
+
 template <int NS, bool LOW_M, int AQ = 0>
 void launch_dma_ns(const SkinnyArgs& a, dim3 grid, hipStream_t st) {
     const int sps = a.steps_per_split;
-    if (sps <= 4) hipLaunchKernelGGL((skinny_dma_kernel<NS, 1, LOW_M, AQ>), grid, dim3(256), 0, st, a);
-    else if (sps <= 8) hipLaunchKernelGGL((skinny_dma_kernel<NS, 2, LOW_M, AQ>), grid, dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((skinny_dma_kernel<NS, 4, LOW_M, AQ>), grid, dim3(256), 0, st, a);
+    if (sps <= 4) hipLaunchKernelGGL((skinny_dma_kernel<NS, 1, LOW_M, AQ>), grid, dim3(256), 0, st, TX_SK_ARGS(a));
+    else if (sps <= 8) hipLaunchKernelGGL((skinny_dma_kernel<NS, 2, LOW_M, AQ>), grid, dim3(256), 0, st, TX_SK_ARGS(a));
+    else hipLaunchKernelGGL((skinny_dma_kernel<NS, 4, LOW_M, AQ>), grid, dim3(256), 0, st, TX_SK_ARGS(a));
 }
 
 // Fused activation quantisation (aq 1 or 2) runs with 3 stages only.
 hipError_t launch_dma(const SkinnyArgs& a, dim3 grid, int ns, int aq, hipStream_t st) {
+    if (a.M > 255 || a.splits > 1023) return hipErrorInvalidValue;  // the packed leading scalars
     const bool low = a.M <= 4;
     if (aq == 1) low ? launch_dma_ns<3, true, 1>(a, grid, st) : launch_dma_ns<3, false, 1>(a, grid, st);
     else if (aq == 2) low ? launch_dma_ns<3, true, 2>(a, grid, st) : launch_dma_ns<3, false, 2>(a, grid, st);
@@ -1749,24 +1777,25 @@ hipError_t launch_skinny_wave(const int8_t* A, const uint8_t* B, int32_t* C, int
     const dim3 grid(gx, 1, (M + 15) / 16), block(256);
     const bool low = M <= 4;
     a.tk_stride = ticket_stride(column_waves ? (size_t)((NB + 127) / 128) : (size_t)(NB / sw) * (size_t)((M + 15) / 16));
+    if (a.M > 255 || a.splits > 1023) return hipErrorInvalidValue;  // the packed leading scalars
     if (column_waves) {  // 128-byte strips, wave w on 32-byte part w (skinny_wave_kernel's CW form)
         if (!(mode == SK_ATOMZ && low && sw == 32 && nsw == 2 && aq.mode == 0 && !tiled)) return hipErrorInvalidValue;
         a.line_units = 0;
         const dim3 gcw((unsigned)(((NB + 127) / 128) * splits), 1, 1);
-        hipLaunchKernelGGL((skinny_wave_kernel<32, 2, true, 0, true>), gcw, block, 0, st, a);
+        hipLaunchKernelGGL((skinny_wave_kernel<32, 2, true, 0, true>), gcw, block, 0, st, TX_SK_ARGS(a));
         return hipGetLastError();
     }
 #define TX_SW_LAUNCH(SW_, NSW_)                                                              \
     do {                                                                                      \
-        if (low) hipLaunchKernelGGL((skinny_wave_kernel<SW_, NSW_, true>), grid, block, 0, st, a);  \
-        else hipLaunchKernelGGL((skinny_wave_kernel<SW_, NSW_, false>), grid, block, 0, st, a);     \
+        if (low) hipLaunchKernelGGL((skinny_wave_kernel<SW_, NSW_, true>), grid, block, 0, st, TX_SK_ARGS(a));  \
+        else hipLaunchKernelGGL((skinny_wave_kernel<SW_, NSW_, false>), grid, block, 0, st, TX_SK_ARGS(a));     \
     } while (0)
     if (aq.mode == 1) {
-        if (low) hipLaunchKernelGGL((skinny_wave_kernel<16, 2, true, 1>), grid, block, 0, st, a);
-        else hipLaunchKernelGGL((skinny_wave_kernel<16, 2, false, 1>), grid, block, 0, st, a);
+        if (low) hipLaunchKernelGGL((skinny_wave_kernel<16, 2, true, 1>), grid, block, 0, st, TX_SK_ARGS(a));
+        else hipLaunchKernelGGL((skinny_wave_kernel<16, 2, false, 1>), grid, block, 0, st, TX_SK_ARGS(a));
     } else if (aq.mode == 2) {
-        if (low) hipLaunchKernelGGL((skinny_wave_kernel<16, 2, true, 2>), grid, block, 0, st, a);
-        else hipLaunchKernelGGL((skinny_wave_kernel<16, 2, false, 2>), grid, block, 0, st, a);
+        if (low) hipLaunchKernelGGL((skinny_wave_kernel<16, 2, true, 2>), grid, block, 0, st, TX_SK_ARGS(a));
+        else hipLaunchKernelGGL((skinny_wave_kernel<16, 2, false, 2>), grid, block, 0, st, TX_SK_ARGS(a));
     } else if (sw == 32 && nsw == 4) TX_SW_LAUNCH(32, 4);
     else if (sw == 32) TX_SW_LAUNCH(32, 2);
     else if (nsw == 4) TX_SW_LAUNCH(16, 4);

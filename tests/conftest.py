@@ -17,9 +17,9 @@ GOLDEN = os.path.join(ROOT, "tests", "golden")
 
 
 def hip_file_flags(src):
-    """Extra hipcc flags the library's Makefile gives one source (the whole-line GEMV's kernel-argument
+    """Extra hipcc flags the library's Makefile gives one source (the GEMV kernels' kernel-argument
     preload count), so that tests reading the emitted code see what the library runs."""
-    if src != "line_gemv.hip":
+    if src not in ("line_gemv.hip", "skinny_kernels.hip"):
         return []
     import re
     with open(os.path.join(ROOT, "ternixengine_amd", "csrc", "Makefile")) as f:

@@ -12,6 +12,8 @@ import subprocess
 
 import pytest
 
+from conftest import hip_file_flags
+
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 CSRC = os.path.join(ROOT, "ternixengine_amd", "csrc")
 HIPCC = "/opt/rocm/bin/hipcc"
@@ -24,7 +26,8 @@ def wave_kernels(tmp_path_factory):
     out = tmp_path_factory.mktemp("isa") / "skinny.s"
     subprocess.run([HIPCC, "--offload-arch=gfx950", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
                     "-O3", "-std=c++17", f"-I{ROOT}/include", f"-I{CSRC}", "--cuda-device-only", "-S", "-o", str(out),
-                    os.path.join(CSRC, "skinny_kernels.hip")], check=True, capture_output=True, timeout=600)
+                    os.path.join(CSRC, "skinny_kernels.hip")] + hip_file_flags("skinny_kernels.hip"), check=True,
+                   capture_output=True, timeout=600)
     text = out.read_text()
     funcs = {}
     for m in re.finditer(r"^(_Z\w*skinny_wave_kernel\w*):", text, re.M):
