@@ -122,11 +122,11 @@ typedef __attribute__((address_space(1))) const u4a g_u4a;
 template <int S, int NW, int AQ, bool EPI, bool RG, int MG = 1, bool T64 = false>
 __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(const uint8_t* Bp, const void* Ap, const void* Gp, int32_t* Cp,
                                                          unsigned long long* tkp, int Kp, int Np, unsigned shape_p,
-                                                         int tk_stride_p, LineArgs args) {
+                                                         unsigned aux_p, LineArgs args) {
     // Leading scalars (preloaded into SGPRs by the command processor): Ap is A, or X with fused
     // quantisation; Gp is G (AQ 2) or the producer's maxima (AQ 3); tkp the strips' tickets; shape_p
     // packs the strip count (bits 0-15), the split count (16-22), the XCD-chunked order (23) and M
-    // (24-31).
+    // (24-31); aux_p the tickets' stride (bits 0-5) and the maxima's row stride (6-31).
     static_assert(NW == 4 || NW == 8, "4 or 8 data waves");
     static_assert(AQ == 0 || EPI, "fused quantisation comes with the float output");
     static_assert(!RG || (AQ == 0 && !EPI), "ragged operands: int32 output from int8 activations");
@@ -146,6 +146,7 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(const uint8_t*
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int strips = (int)(shape_p & 0xFFFFu), splits_p = (int)((shape_p >> 16) & 0x7Fu);
     const int xcd_p = (int)((shape_p >> 23) & 1u), Mp = (int)(shape_p >> 24);
+    const int tk_stride_p = (int)(aux_p & 63u), amax_stride_p = (int)(aux_p >> 6);
     // Workgroup g runs on XCD g mod 8.  With xcd_chunks the split-major unit sequence is cut into 8
     // contiguous chunks, chunk x taken by the workgroups of XCD x in order, so that neighbouring strips
     // of one split share an L2 (rows whose length is not a multiple of 128 bytes put one cache line
@@ -170,7 +171,7 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(const uint8_t*
     //   AQ 1 / 2: the whole row of X (and, AQ 2, a copy of G) at a 1 KB-aligned row pitch;
     //   AQ 3: the unit's slice of the row (64 nst activations) and the producer's maxima of the row.
     const int xpitch = AQ == 3 ? ((S * 256 + 1023) & ~1023) : ((K * 4 + 1023) & ~1023);  // bytes per row
-    const int apitch = (args.amax_stride * 4 + 1023) & ~1023;
+    const int apitch = (amax_stride_p * 4 + 1023) & ~1023;
     // AQ 1 / 2 with K <= 256 KJ: row r and G go straight into wave r's registers instead (lane l: k =
     // 256 j + 4 l .. + 3), with this unit's 64 nst values of each (lane l: k = 64 (s0 + u) + l).
     constexpr int KJ = (AQ == 1 || AQ == 2) ? 12 : 1;
@@ -203,8 +204,8 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(const uint8_t*
                 const int n = nst * 256;
                 const uint8_t* src = xb + ((size_t)wave * (size_t)K + (size_t)s0 * 64) * 4;
                 for (int c = 0; c * 1024 < n; ++c) lds_dma16(src + min(c * 1024 + lane * 16, n - 16), xd + c * 1024);
-                const int na = args.amax_stride * 4;
-                const uint8_t* asrc = reinterpret_cast<const uint8_t*>(reinterpret_cast<const float*>(Gp) + (size_t)wave * args.amax_stride);
+                const int na = amax_stride_p * 4;
+                const uint8_t* asrc = reinterpret_cast<const uint8_t*>(reinterpret_cast<const float*>(Gp) + (size_t)wave * amax_stride_p);
                 uint8_t* ad = reinterpret_cast<uint8_t*>(gl) + wave * apitch;
                 for (int c = 0; c * 1024 < na; ++c) lds_dma16(asrc + min(c * 1024 + lane * 16, na - 16), ad + c * 1024);
             } else {
@@ -308,7 +309,7 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(const uint8_t*
             }
             if constexpr (EPI) {  // the strip's maxima start at 0 too (published with the zeroed word)
                 if (args.amax_out != nullptr && lane < M)
-                    __hip_atomic_store(reinterpret_cast<unsigned int*>(args.amax_out) + (size_t)lane * args.amax_stride + s,
+                    __hip_atomic_store(reinterpret_cast<unsigned int*>(args.amax_out) + (size_t)lane * amax_stride_p + s,
                                        0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
             // T += 64 - (splits - 1) (no return needed).  Lane 0 alone enabled; nothing waited for here.
@@ -751,7 +752,7 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(const uint8_t*
                 float m = 0.0f;
                 for (int w = 0; w < NW; ++w) m = fmaxf(m, wmax[w * 4 + tid]);
                 if (m > 0.0f)  // one atomic per workgroup and row: the strip's entry is shared by its splits
-                    __hip_atomic_fetch_max(reinterpret_cast<unsigned int*>(args.amax_out) + (size_t)tid * args.amax_stride + s,
+                    __hip_atomic_fetch_max(reinterpret_cast<unsigned int*>(args.amax_out) + (size_t)tid * amax_stride_p + s,
                                            __float_as_uint(m), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         }
@@ -818,16 +819,18 @@ hipError_t launch_line_gemv(const int8_t* A, const uint8_t* B, int32_t* C, int M
     a.amax_in = aq.amax_in;
     a.amax_n = aq.amax_n;
 
-    if (a.splits > 64 || a.strips > 0xFFFF || M > 255 || (size_t)S * 64 > (size_t)kMaxKPerAccumulator)
+    if (a.splits > 64 || a.strips > 0xFFFF || M > 255 || a.tk_stride > 63 || a.amax_stride > (1 << 25) ||
+        (size_t)S * 64 > (size_t)kMaxKPerAccumulator)
         return hipErrorInvalidValue;
     const dim3 grid((unsigned)(a.strips * a.splits));
     // 0 int32 out, 1 dequantised, 2 / 3 / 4 with fused quantisation, 5 / 6 int32 out from ragged
     // operands in one / two 16-row groups
     const int mode = ragged ? (M > 16 ? 6 : 5) : (epi ? 1 + aq.mode : 0);
+    const unsigned aux = (unsigned)a.tk_stride | ((unsigned)a.amax_stride << 6);
     const unsigned shape = (unsigned)a.strips | ((unsigned)a.splits << 16) | ((a.xcd_chunks ? 1u : 0u) << 23) |
                            ((unsigned)a.M << 24);
 #define TX_LINE_ARGS a.B, aq.mode ? (const void*)a.X : (const void*)a.A, aq.mode == 3 ? (const void*)a.amax_in : (const void*)a.G, \
-    a.C, a.tk, a.K, a.N, shape, a.tk_stride, a
+    a.C, a.tk, a.K, a.N, shape, aux, a
 #define TX_LINE(SS, WW, AQQ, EE, RR)                                                                         \
     if (S == SS && NW == WW && mode == (RR ? 5 : (EE ? 1 + AQQ : 0))) {                                      \
         if (tiled)                                                                                           \
