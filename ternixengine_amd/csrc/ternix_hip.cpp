@@ -408,8 +408,14 @@ bool run_atomic_wave(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, in
         sw = 32;
         sp = std::min(cus / (NB / 32), std::max(1, nsteps / 4));
     } else if (M > 1 && NB % 32 == 0) {
+        // About one workgroup per CU for one m-group; about two, and at most 6 splits, for several
+        // (measured on MI355X, cold, us, splits in brackets: 24x2560x6912 11.8 [1, another plan] ->
+        // 7.26-7.64 [4-6], 24x4096x11008 13.4 -> 10.6 [3], 33x4096x4096 9.8 [2] -> 7.9-8.0 [4-6],
+        // 64x6912x2560 10.3 [3] -> 9.4 [6]).
         sw = 32;
-        sp = (int)std::min<long>((long)cus * 53 / 50 / ((long)(NB / 32) * mgroups), std::max(1, nsteps / 4));
+        const long per = mgroups > 1 ? 2L * cus * 53 / 50 : (long)cus * 53 / 50;
+        sp = (int)std::min<long>(per / ((long)(NB / 32) * mgroups), std::max(1, nsteps / 4));
+        if (mgroups > 1) sp = std::min(sp, 6);
     }
     const int fsw = ternix_hip::debug_get(ternix_hip::DBG_WAVE_SW, 0), fsp = ternix_hip::debug_get(ternix_hip::DBG_WAVE_SW, 1);
     if ((fsw == 16 || fsw == 32) && fsp > 1 && NB % fsw == 0) {  // forced split plan (tests and tuning)
@@ -421,10 +427,12 @@ bool run_atomic_wave(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, in
     if (!(splits > 1 && sps * 64 <= ternix_hip::kMaxKPerAccumulator)) return false;
     // 33..64 rows (several m-groups) only with short k-ranges per split: against the narrow-tile GEMM,
     // measured on MI355X (cold): 64x4096x4096 14.1 -> 10.6 us (32 steps per split), 64x6912x2560 11.1
-    // -> 10.4 (36), but 64x11008x4096 15.6 -> 21.5 (86) and 64x14336x4096 17.9 -> 26.4 (112).  Up to
+    // -> 10.4 (36), but 64x11008x4096 15.6 -> 21.5 (86) and 64x14336x4096 17.9 -> 26.4 (112); with
+    // the two-per-CU split count, 48x4096x11008 14.0 (32 steps) against 13.0 and 64x2560x6912 9.3
+    // (20) against 9.6 for the GEMM, so at most 24 steps per split.  Up to
     // 32 rows it wins wherever it splits K (24 and 32 rows: 1.11-1.42x against the in-launch sums and
     // the reduce launch on five decode shapes).
-    if (M > 32 && sps > 40 && fsp <= 1) return false;
+    if (M > 32 && sps > 24 && fsp <= 1) return false;
     // Column waves (M <= 4, 32-byte parts): a workgroup owns a 128-byte strip and each wave one
     // 32-byte part over the workgroup's whole k-range, so the four parts of each weight line reach one
     // CU together.  More K splits for the same workgroups (more atomic adds per output), so only where
@@ -491,7 +499,10 @@ bool run_line_gemv(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int 
     const int fs = ternix_hip::debug_get(ternix_hip::DBG_LINE, 0), fw = ternix_hip::debug_get(ternix_hip::DBG_LINE, 1);
     if (fs == 0) return false;
     const bool epi = os.Y != nullptr;
-    const bool ragged = !ternix_hip::line_gemv_ok(dA, dB, M, K, N);
+    // Ragged: the operands' sizes or addresses rule out the DMA form (not the row count: aligned
+    // operands with 17-32 rows take the wave-pipelined kernel, 1.2-1.9x faster than the ragged form's
+    // two row groups, e.g. 32x6912x2560 14.8 against 7.7 us on MI355X).
+    const bool ragged = !ternix_hip::line_gemv_ok(dA, dB, std::min(M, 16), K, N);
     if (tiled && ragged) return false;  // (the tile-64 contract keeps its operands aligned)
     // Rows: up to 4 on aligned operands (5-16 rows measured slower than the wave-pipelined kernel:
     // 16x2560x6912 9.20 against 7.02 us, more splits of 16-row atomics), up to 16 on ragged ones (no

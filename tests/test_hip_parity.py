@@ -496,3 +496,25 @@ def test_wave_kernel_shapes(oracle, m, k, n):
     wp = rng.integers(0, 256, size=(k, n // 4), dtype=np.uint8)
     log(f"[wave] M={m} K={k} N={n}")
     assert (run("auto", a, wp, n) == oracle.mm("scalar_mt", a, wp, n)).all()
+
+
+@pytest.mark.parametrize("m,k,n,splits", [(17, 4096, 4096, 6), (24, 2560, 6912, 5), (32, 6912, 2560, 6),
+                                          (40, 4096, 4096, 5), (48, 2560, 6912, 3), (64, 6912, 2560, 6)])
+def test_several_m_groups_self_zeroing_wave(oracle, m, k, n, splits):
+    """Aligned operands with 17-64 rows take the wave-pipelined kernel's self-zeroing plan, about two
+    workgroups per CU (not the ragged form of the whole-line GEMV, whose two row groups are for ragged
+    operands), bit-exact against the oracle on two calls in a row."""
+    lib = tx._load()
+    buf = ctypes.create_string_buffer(192)
+    assert lib.ternix_hip_plan_describe(1 << 20, 1 << 24, m, k, n, buf, len(buf)) == 0
+    plan = buf.value.decode()
+    assert plan.startswith("skinny_wave_kernel sw=32"), plan
+    if hr.device_attribute(hr.ATTR_MULTIPROCESSOR_COUNT) == 256:
+        assert f"splits={splits} " in plan, plan
+    rng = np.random.default_rng(m * 31 + k + n)
+    a = rng.integers(-128, 128, size=(m, k), dtype=np.int8)
+    wp = rng.integers(0, 256, size=(k, n // 4), dtype=np.uint8)
+    expect = oracle.mm("scalar_mt", a, wp, n)
+    log(f"[wave m-groups] M={m} K={k} N={n} {plan[:44]}")
+    for rep in range(2):
+        assert (run("auto", a, wp, n) == expect).all(), rep
