@@ -554,6 +554,10 @@ bool run_line_gemv(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int 
         if (S == 0) return false;
     }
     if (ragged && M > 16 && S > 6) return false;  // two 16-row groups: at most 6 k-steps per workgroup
+    // Two 16-row groups need at least 64 workgroups (on MI355X, cold, against the padded copy:
+    // 32x1500x516, 24 workgroups, 10.66 / 7.55 us; 17x4093x1028, 96, 7.60 / 9.55; 20x4093x2052, 160,
+    // 10.0 / 11.0).
+    if (ragged && M > 16 && (long)strips * ternix_hip::line_gemv_splits(K, S) < 64) return false;
     const int NW = fw == 4 && !epi && !ragged ? 4 : 8;
     const int splits = ternix_hip::line_gemv_splits(K, S);
     if (splits > 64) return false;

@@ -243,7 +243,11 @@ def test_line_gemv_ragged_matches_oracle(oracle, shape):
     _, _, _, da, db, dc, expect, _, _ = p
     buf = ctypes.create_string_buffer(192)
     assert lib.ternix_hip_plan_describe((1 << 20) + ao, (1 << 24) + bo, m, k, n, buf, len(buf)) == 0
-    assert buf.value.decode().startswith("line_gemv_kernel ragged"), buf.value
+    # two row groups take the ragged form on 64 workgroups or more (2 k-steps each here), else the
+    # padded copy
+    strips, splits = -(-(n // 4) // 128), -(-(-(-k // 64)) // 2)
+    want = "pad_rows_kernel" if m > 16 and strips * splits < 64 else "line_gemv_kernel ragged"
+    assert buf.value.decode().startswith(want), buf.value
     s = hr.Stream()
     call = lambda: tx.mul_mat_ternary(da.value + ao, db.value + bo, dc.value, m, k, n, stream=s.handle)
     log(f"[line ragged] M={m} K={k} N={n} A+{ao} W+{bo}")
