@@ -183,10 +183,10 @@ int device_cu_count() {
 // ------------------------------------------------------------------------------------------------
 // Padded copy for ragged shapes: rows of `len` bytes at pitch src_pitch (any alignment) into rows of
 // dst_pitch bytes (16-byte aligned, dst_pitch % 16 == 0), zero-filled past len and for the rows
-// rows..dst_rows-1.  Each thread writes one 16-byte chunk from five aligned dword loads and
-// v_alignbyte; an aligned dword holding at least one byte of the source buffer never crosses a page
-// the buffer does not touch, so loads stay within the buffer's pages (dwords starting past its last
-// byte are not loaded).
+// rows..dst_rows-1.  Each thread writes one 16-byte chunk from the aligned dwords holding its bytes
+// (one 16-byte load where the four lie inside the source's 4-byte aligned extent, dword by dword at
+// its end) and v_alignbyte; an aligned dword holding at least one byte of the source buffer never
+// crosses a page the buffer does not touch, so loads stay within the buffer's pages.
 // ------------------------------------------------------------------------------------------------
 struct PadJob {
     const uint8_t* src;
@@ -195,19 +195,33 @@ struct PadJob {
     size_t chunks;  // dst_rows * dst_pitch / 16
 };
 
-__device__ __forceinline__ void pad_chunk(const PadJob& j, size_t idx) {
-    const int cpr = j.dst_pitch >> 4;
-    const int r = (int)(idx / (size_t)cpr), c = (int)(idx % (size_t)cpr);
+typedef uint32_t pad_u4 __attribute__((ext_vector_type(4), aligned(4)));
+typedef __attribute__((address_space(1))) const uint32_t pad_g32;
+typedef __attribute__((address_space(1))) const pad_u4 pad_g4;
+
+template <typename I>
+__device__ __forceinline__ void pad_chunk(const PadJob& j, I idx) {
+    const I cpr = (I)(j.dst_pitch >> 4);
+    const int r = (int)(idx / cpr), c = (int)(idx % cpr);
     v4i out = {0, 0, 0, 0};
     const int n = min(max(j.len - 16 * c, 0), 16);  // source bytes in this chunk
     if (r < j.rows && n > 0) {
-        const uint8_t* p = j.src + (size_t)r * (size_t)j.src_pitch + 16 * c;
-        const uint8_t* end = j.src + (size_t)(j.rows - 1) * (size_t)j.src_pitch + j.len;
-        const uint32_t* pa = reinterpret_cast<const uint32_t*>((uintptr_t)p & ~(uintptr_t)3);
-        const uint32_t sh = (uint32_t)((uintptr_t)p & 3);
-        uint32_t d[5];
+        const uintptr_t p = reinterpret_cast<uintptr_t>(j.src) + (size_t)r * (size_t)j.src_pitch + 16 * c;
+        const uintptr_t end = reinterpret_cast<uintptr_t>(j.src) + (size_t)(j.rows - 1) * (size_t)j.src_pitch + j.len;
+        const uintptr_t pa = p & ~(uintptr_t)3;
+        const uint32_t sh = (uint32_t)(p & 3);
+        uint32_t d[5] = {0u, 0u, 0u, 0u, 0u};
+        if (pa + 16 <= ((end + 3) & ~(uintptr_t)3)) {
+            // the four dwords from the chunk's first one lie inside the source's aligned extent: one
+            // 16-byte load, and the fifth dword when the chunk reaches into it
+            const pad_u4 x = *(pad_g4*)pa;
 #pragma unroll
-        for (int k = 0; k < 5; ++k) d[k] = reinterpret_cast<const uint8_t*>(pa + k) < end ? pa[k] : 0u;
+            for (int k = 0; k < 4; ++k) d[k] = x[k];
+            if (pa + 16 < end && sh + n > 16) d[4] = *((pad_g32*)pa + 4);
+        } else {
+#pragma unroll
+            for (int k = 0; k < 5; ++k) d[k] = pa + 4 * k < end ? *((pad_g32*)pa + k) : 0u;
+        }
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
             uint32_t v = __builtin_amdgcn_alignbyte(d[m + 1], d[m], sh);
@@ -219,11 +233,13 @@ __device__ __forceinline__ void pad_chunk(const PadJob& j, size_t idx) {
     *reinterpret_cast<v4i*>(j.dst + (size_t)r * (size_t)j.dst_pitch + 16 * c) = out;
 }
 
+// I: the chunk index type (32-bit when both jobs' chunks fit, which keeps the row division short).
+template <typename I>
 __global__ __launch_bounds__(256) void pad_rows_kernel(PadJob j0, PadJob j1) {
-    const size_t total = j0.chunks + j1.chunks;
-    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (size_t)gridDim.x * 256) {
-        if (i < j0.chunks) pad_chunk(j0, i);
-        else pad_chunk(j1, i - j0.chunks);
+    const I total = (I)(j0.chunks + j1.chunks), c0 = (I)j0.chunks;
+    for (I i = (I)blockIdx.x * 256 + threadIdx.x; i < total; i += (I)gridDim.x * 256) {
+        if (i < c0) pad_chunk<I>(j0, i);
+        else pad_chunk<I>(j1, i - c0);
     }
 }
 
@@ -240,7 +256,10 @@ hipError_t launch_pad_rows(const uint8_t* src0, uint8_t* dst0, int rows0, int ds
     const size_t total = j0.chunks + j1.chunks;
     if (total == 0) return hipSuccess;
     const unsigned blocks = (unsigned)std::min<size_t>((total + 255) / 256, 8192);
-    hipLaunchKernelGGL(pad_rows_kernel, dim3(blocks), dim3(256), 0, st, j0, j1);
+    if (total < ((size_t)1 << 31))
+        hipLaunchKernelGGL(pad_rows_kernel<uint32_t>, dim3(blocks), dim3(256), 0, st, j0, j1);
+    else
+        hipLaunchKernelGGL(pad_rows_kernel<size_t>, dim3(blocks), dim3(256), 0, st, j0, j1);
     return hipGetLastError();
 }
 
