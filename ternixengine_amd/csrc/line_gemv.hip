@@ -151,13 +151,16 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(const uint8_t*
     // contiguous chunks, chunk x taken by the workgroups of XCD x in order, so that neighbouring strips
     // of one split share an L2 (rows whose length is not a multiple of 128 bytes put one cache line
     // in two strips).
-    int unit = (int)blockIdx.x;
+    // Without it the grid is (strips, splits): dispatched in the same split-major order, with no
+    // division to find the unit's strip and split.
+    int split = (int)blockIdx.y, s = (int)blockIdx.x;
     if (xcd_p) {
-        const int G = strips * splits_p, q = G >> 3, r = G & 7, x = unit & 7;
-        unit = x * q + min(x, r) + (unit >> 3);
+        const int unit0 = (int)blockIdx.x;
+        const int G = strips * splits_p, q = G >> 3, r = G & 7, x = unit0 & 7;
+        const int unit = x * q + min(x, r) + (unit0 >> 3);
+        split = unit / strips;
+        s = unit - split * strips;
     }
-    const int split = unit / strips;
-    const int s = unit - split * strips;
     const int M = Mp, K = Kp, N = Np, NB = N >> 2;
     const int s0 = split * S;                 // first k-step
     const int nst = min(S, ((K + 63) >> 6) - s0);  // k-steps of this unit (>= 1; RG: the last may be partial)
@@ -467,7 +470,7 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(const uint8_t*
             const float am = fmaxf(m, 1e-5f), sc = 127.0f / am;
             if (lane == 0) {
                 lds_write_b32_asm(lds_u32(rscale) + 4 * r, __float_as_uint(am / 127.0f));
-                if (blockIdx.x == 0) args.rs_out[r] = am / 127.0f;
+                if (blockIdx.x == 0 && blockIdx.y == 0) args.rs_out[r] = am / 127.0f;
             }
             // this unit's values of the row: k = 64 s0 + i, i < 64 nst, lane i % 64
             const uint32_t qa = lds_u32(qbuf) + (uint32_t)(r * (S * 64));
@@ -822,7 +825,7 @@ hipError_t launch_line_gemv(const int8_t* A, const uint8_t* B, int32_t* C, int M
     if (a.splits > 64 || a.strips > 0xFFFF || M > 255 || a.tk_stride > 63 || a.amax_stride > (1 << 25) ||
         (size_t)S * 64 > (size_t)kMaxKPerAccumulator)
         return hipErrorInvalidValue;
-    const dim3 grid((unsigned)(a.strips * a.splits));
+    const dim3 grid = xcd_chunks ? dim3((unsigned)(a.strips * a.splits)) : dim3((unsigned)a.strips, (unsigned)a.splits);
     // 0 int32 out, 1 dequantised, 2 / 3 / 4 with fused quantisation, 5 / 6 int32 out from ragged
     // operands in one / two 16-row groups
     const int mode = ragged ? (M > 16 ? 6 : 5) : (epi ? 1 + aq.mode : 0);
