@@ -293,9 +293,11 @@ __global__ __launch_bounds__(64 * (NW + 1)) void line_gemv_kernel(const uint8_t*
                 if (bc0 + 16 * c >= NB) c = 0;  // past the last column (a partial last strip): a valid chunk, unused
                 // T64: the same piece in the tile-64 layout (the 8 rows of one chunk that an instruction
                 // reads are one contiguous 128-byte line of their block)
+                // (row-major: a wave-uniform base for the instruction's 8 rows, a 32-bit lane offset)
                 const uint8_t* src =
                     T64 ? Bp + tile64_offset((bc0 >> 4) + c, (s0 + step) * 64 + r, K >> 6)
-                        : Bp + ((size_t)(s0 + step) * 64 + (size_t)r) * (size_t)NB + (size_t)(bc0 + 16 * c);
+                        : Bp + (size_t)((s0 + step) * 64 + (p & 7) * 8) * (size_t)NB +
+                              (uint32_t)(r_in * NB + bc0 + 16 * c);
                 lds_dma16(src, lds + (p >> 3) * STEP + (p & 7) * 1024);
             }
         }
