@@ -504,16 +504,20 @@ bool run_line_gemv(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int 
     // two row groups, e.g. 32x6912x2560 14.8 against 7.7 us on MI355X).
     const bool ragged = !ternix_hip::line_gemv_ok(dA, dB, std::min(M, 16), K, N);
     if (tiled && ragged) return false;  // (the tile-64 contract keeps its operands aligned)
-    // Rows: up to 4 on aligned operands (5-16 rows measured slower than the wave-pipelined kernel:
-    // 16x2560x6912 9.20 against 7.02 us, more splits of 16-row atomics), up to 16 on ragged ones (no
-    // padded copy); the DBG_LINE switch [3] sets the limit.
+    // Rows: up to 8 on aligned operands with int32 output, 4 with float output (9-16 rows measured
+    // slower than the wave-pipelined kernel: 16x2560x6912 9.20 against 7.02 us, more splits of 16-row
+    // atomics), more on ragged ones (no padded copy, below); the DBG_LINE switch [3] sets the limit.
     // Ragged rows: up to 8 at any K, up to 16 from K = 256 and up to 32 from K = 1024; on shorter K the
     // few workgroups serialise their 16-row atomics (on MI355X, cold, against the padded copy:
     // 8x130x2044 4.82 / 5.38 us, 16x130x2044 6.61 / 5.44, 16x500x2044 7.01 / 7.76, 12x600x4100 6.09 /
     // 8.08, 32x700x516 10.30 / 7.41, 24x1000x3076 8.90 / 8.40, 17x4093x1028 7.89 / 9.2).
     const int fm = ternix_hip::debug_get(ternix_hip::DBG_LINE, 3);
     const int ragged_rows = K >= 1024 ? 32 : (K >= 256 ? 16 : 8);
-    if (M > (fm > 0 ? std::min(fm, ragged ? 32 : 16) : (ragged ? ragged_rows : 4))) return false;
+    // Aligned operands, int32 output: up to 8 rows (on MI355X, cold, against the wave-pipelined
+    // kernel: 5x4096x11008 7.75 -> 6.30 us, 8x11008x4096 8.28 -> 7.51, 6x2560x6912 5.80 -> 5.05,
+    // 8x4096x4096 5.5 either way; 12x4096x4096 6.8 against 5.9).
+    const int aligned_rows = epi ? 4 : 8;
+    if (M > (fm > 0 ? std::min(fm, ragged ? 32 : 16) : (ragged ? ragged_rows : aligned_rows))) return false;
     if (!(dC != nullptr && reinterpret_cast<uintptr_t>(dC) % 16 == 0 &&
           (!ragged || (!epi && aq.mode == 0 && ternix_hip::line_gemv_ragged_ok(M, K, N)))))
         return false;

@@ -34,7 +34,8 @@ def test_plan_names_line_kernel_when_forced():
     try:
         assert lib.ternix_hip_debug_set(b"line", 2, 8, -1, -1) == 0
         assert _plan(lib, 1, 2560, 6912).startswith("line_gemv_kernel S=2 waves=8+1 splits=20")
-        assert not _plan(lib, 5, 2560, 6912).startswith("line_gemv_kernel")  # aligned: M <= 4 only
+        assert _plan(lib, 8, 2560, 6912).startswith("line_gemv_kernel S=2")  # aligned, int32: M <= 8
+        assert not _plan(lib, 9, 2560, 6912).startswith("line_gemv_kernel")
         assert _plan(lib, 1, 2560, 6900).startswith("line_gemv_kernel ragged S=2")  # N/4 % 16 != 0
         assert _plan(lib, 16, 2560, 6900).startswith("line_gemv_kernel ragged")  # ragged: more rows
         assert _plan(lib, 16, 1000, 6900).startswith("line_gemv_kernel ragged")  # 16 rows from K = 256
@@ -264,6 +265,25 @@ def test_line_gemv_ragged_matches_oracle(oracle, shape):
         _check_guarded(dc, m, n, expect, ("replay", rep))
         assert call() == 0
         s.synchronize()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape", [(5, 4096, 11008), (6, 2560, 6912), (7, 192, 1024), (8, 11008, 4096)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_line_gemv_five_to_eight_rows(oracle, shape):
+    """Aligned operands with 5-8 rows and an int32 output take the whole-line GEMV on the automatic
+    plan: bit-exact against the oracle on two calls in a row."""
+    lib = tx._load()
+    m, k, n = shape
+    p = _ragged_problem(oracle, np.random.default_rng(sum(shape) + 5), m, k, n, 0, 0)
+    _, _, _, da, db, dc, expect, _, _ = p
+    assert _plan(lib, m, k, n).startswith("line_gemv_kernel S="), _plan(lib, m, k, n)
+    log(f"[line 5-8 rows] M={m} K={k} N={n}")
+    for rep in range(2):
+        dc.upload(np.full(m * n + GUARD, GARBAGE, np.int32))
+        assert tx.mul_mat_ternary(da.value, db.value, dc.value, m, k, n) == 0
+        hr.synchronize()
+        _check_guarded(dc, m, n, expect, rep)
 
 
 @pytest.mark.gpu
