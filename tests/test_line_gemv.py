@@ -309,9 +309,9 @@ def test_line_gemv_random_ragged_offsets(oracle):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("m", [1, 4])
-def test_line_gemv_one_workgroup_per_cu(oracle, m):
-    """8192 x 8192 on the automatic plan: 16 strips x 16 splits of 8 k-steps fill the CUs exactly (a
-    grid of one workgroup per CU is the plan's limit), bit-exact against the oracle on two calls."""
+def test_line_gemv_two_workgroups_per_cu(oracle, m):
+    """8192 x 8192 on the automatic plan: 16 strips x 32 splits of 4 k-steps, two workgroups per CU
+    (preferred to 16 splits of 8 k-steps on one), bit-exact against the oracle on two calls."""
     lib = tx._load()
     k = n = 8192
     p = _ragged_problem(oracle, np.random.default_rng(8192 + m), m, k, n, 0, 0)
@@ -320,8 +320,8 @@ def test_line_gemv_one_workgroup_per_cu(oracle, m):
     assert lib.ternix_hip_plan_describe(1 << 20, 1 << 24, m, k, n, buf, len(buf)) == 0
     plan = buf.value.decode()
     if hr.device_attribute(hr.ATTR_MULTIPROCESSOR_COUNT) == 256:
-        assert plan.startswith("line_gemv_kernel S=8 waves=8+1 splits=16"), plan
-    log(f"[line one per CU] M={m} K={k} N={n} plan={plan[:40]}")
+        assert plan.startswith("line_gemv_kernel S=4 waves=8+1 splits=32"), plan
+    log(f"[line two per CU] M={m} K={k} N={n} plan={plan[:40]}")
     for rep in range(2):
         dc.upload(np.full(m * n + GUARD, GARBAGE, np.int32))
         assert tx.mul_mat_ternary(da.value, db.value, dc.value, m, k, n) == 0
