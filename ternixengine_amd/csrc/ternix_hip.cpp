@@ -555,13 +555,14 @@ bool run_line_gemv(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int 
             }
             if (S != 0) break;
         }
-        // int32 output: within two workgroups per CU when nothing fits one (13x5120 K=13824: 7.94 ->
-        // 7.22 us with 360 workgroups of 6 k-steps against the wave-pipelined kernel; 4x13824 K=5120 8.85
-        // -> 7.71), and 4 k-steps on up to two per CU instead of 8 on one (1x4096x14336 6.33 -> 6.02,
-        // 1x8192x8192 6.47 -> 6.28, 1x14336x4096 6.67 -> 6.47; measured on MI355X, cold).
+        // int32 output: up to 6 k-steps within two workgroups per CU when nothing fits one (13x5120
+        // K=13824: 7.94 -> 7.22 us with 360 workgroups of 6 k-steps against the wave-pipelined kernel;
+        // 4x13824 K=5120 8.85 -> 7.71, 4x6144x16384 11.5 -> 8.96; with 8 k-steps the DMA-staged kernel
+        // is faster, 1x4096x28672 9.1 against 11.8), and 4 k-steps on up to two per CU instead of 8 on
+        // one (1x4096x14336 6.33 -> 6.02, 1x8192x8192 6.47 -> 6.28; measured on MI355X, cold).
         const long cap2 = 2L * (long)cu_count();
         if (S == 0 && !epi && aq.mode == 0) {
-            for (int cand : {2, 3, 4, 6, 8}) {
+            for (int cand : {2, 3, 4, 6}) {
                 const long sp = ternix_hip::line_gemv_splits(K, cand);
                 if (sp <= 64 && (long)strips * sp <= cap2) {
                     S = cand;
