@@ -461,6 +461,11 @@ bool run_atomic_wave(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, in
         sps = cw_sps;
         splits = (nsteps + sps - 1) / sps;
     }
+    // Up to 4 rows, more than 12 k-steps per workgroup (shapes the whole-line GEMV declines): the
+    // DMA-staged kernel streams them faster (on MI355X, cold: 1x28672x8192 19.2 -> 12.5 us,
+    // 4x28672x8192 22.5 -> 14.2, 1x14336x8192 11.0 -> 8.9, 1x32768x4096 12.4 -> 9.7, 4x11008x16384
+    // 18.4 -> 12.1, 3x24576x6144 14.8 -> 11.0).
+    if (M <= 4 && sps > 12 && fsp <= 1 && ternix_hip::skinny_dma_ok(dA, dB, M, K, N, 1)) return false;
     unsigned long long* tk = ternix_hip::debug_get(ternix_hip::DBG_SELF_ZERO) != 0 && splits <= 64
                                  ? c.tickets(ternix_hip::ticket_units(cw ? (size_t)((NB + 127) / 128) : (size_t)(NB / sw) * (size_t)mgroups))
                                  : nullptr;
