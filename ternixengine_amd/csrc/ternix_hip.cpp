@@ -500,7 +500,7 @@ bool run_atomic_wave(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, in
 // with an int32 output.
 bool run_line_gemv(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int K, int N, Ctx& c, hipError_t* e,
                    const ternix_hip::OutScale& os = ternix_hip::OutScale{},
-                   const ternix_hip::ActQuant& aq = ternix_hip::ActQuant{}, int tiled = 0) {
+                   const ternix_hip::ActQuant& aq = ternix_hip::ActQuant{}, int tiled = 0, bool pad_alt = false) {
     const int fs = ternix_hip::debug_get(ternix_hip::DBG_LINE, 0), fw = ternix_hip::debug_get(ternix_hip::DBG_LINE, 1);
     if (fs == 0) return false;
     const bool epi = os.Y != nullptr;
@@ -522,9 +522,16 @@ bool run_line_gemv(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int 
     // kernel: 5x4096x11008 7.75 -> 6.30 us, 8x11008x4096 8.28 -> 7.51, 6x2560x6912 5.80 -> 5.05,
     // 8x4096x4096 5.5 either way; 12x4096x4096 6.8 against 5.9).
     const int aligned_rows = epi ? 4 : 8;
-    if (M > (fm > 0 ? std::min(fm, ragged ? 32 : 16) : (ragged ? ragged_rows : aligned_rows))) return false;
+    // pad_alt: the caller's alternative is the padded copy (operands aligned for this kernel but not
+    // for the wave-pipelined one, e.g. N/4 % 64 != 0): the ragged limits hold up to 16 rows (on MI355X,
+    // cold, against the padded copy: 16x4864x896 6.71 / 8.15 us, 12x2432x896 5.51 / 7.35; above 16
+    // rows the kernel's two-row-group form is slower, 32x4864x896 10.7 / 9.2).
+    const bool rows_ragged = ragged || pad_alt;
+    const int pad_rows = ragged ? ragged_rows : std::min(ragged_rows, 16);
+    if (M > (fm > 0 ? std::min(fm, rows_ragged ? 32 : 16) : (rows_ragged ? pad_rows : aligned_rows))) return false;
+    const bool rag_form = ragged || M > 16;
     if (!(dC != nullptr && reinterpret_cast<uintptr_t>(dC) % 16 == 0 &&
-          (!ragged || (!epi && aq.mode == 0 && ternix_hip::line_gemv_ragged_ok(M, K, N)))))
+          (!rag_form || (!epi && aq.mode == 0 && ternix_hip::line_gemv_ragged_ok(M, K, N)))))
         return false;
     if (aq.mode != 0 && !(epi && M <= 4 && (aq.mode == 3 || (long)M * K <= 8192) && reinterpret_cast<uintptr_t>(aq.X) % 16 == 0 &&
                           (aq.mode != 2 || reinterpret_cast<uintptr_t>(aq.G) % 16 == 0)))
@@ -549,9 +556,16 @@ bool run_line_gemv(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int 
         // against the wave-pipelined kernel).  The FFN's down launch, which quantises its slice of h
         // from the strip maxima first, starts at 4 k-steps (1x6912x2560: 27 splits instead of 36; the
         // block 12.31 -> 12.11 us).
+        // Fewest k-steps per workgroup on aligned operands: more k-steps cut the splits' atomics and
+        // each workgroup's fixed cost where the grid is narrow (on MI355X, cold, k-steps 2 / 3 / 4:
+        // 1x8192x1024 4.52 / 3.81 / 3.57 us, 1x6144x1024 3.80 / 3.45 / 3.40, 1x4608x1024 3.46 / 3.29 /
+        // 3.30, 1x5504x2048 3.78 / 3.63 / 3.88; with 5-8 rows 8x2560x6912 6.73 / 5.64 / 5.34 and 8x4096x4096
+        // 6.21 / 5.56 / 5.29).  3 from 64 k-steps, 4 from 96, and 4 from 40 k-steps with 5-8 rows.
+        const int ks = (K + 63) / 64;
+        const int min_s = rag_form ? 2 : ((M >= 5 && ks >= 40) || ks >= 96 ? 4 : (ks >= 64 ? 3 : 2));
         for (const long cap : {std::max(1L, (long)cu_count() * 250 / 256), std::max(1L, (long)cu_count())}) {
             for (int cand : {2, 3, 4, 6, 8}) {
-                if (aq.mode == 3 && cand < 4) continue;
+                if ((aq.mode == 3 && cand < 4) || cand < min_s) continue;
                 const long sp = ternix_hip::line_gemv_splits(K, cand);
                 if (sp <= 64 && (long)strips * sp <= cap) {
                     S = cand;
@@ -568,6 +582,7 @@ bool run_line_gemv(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int 
         const long cap2 = 2L * (long)cu_count();
         if (S == 0 && !epi && aq.mode == 0) {
             for (int cand : {2, 3, 4, 6}) {
+                if (cand < min_s) continue;
                 const long sp = ternix_hip::line_gemv_splits(K, cand);
                 if (sp <= 64 && (long)strips * sp <= cap2) {
                     S = cand;
@@ -581,19 +596,19 @@ bool run_line_gemv(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int 
         }
         if (S == 0) return false;
     }
-    if (ragged && M > 16 && S > 6) return false;  // two 16-row groups: at most 6 k-steps per workgroup
+    if (M > 16 && S > 6) return false;  // two 16-row groups: at most 6 k-steps per workgroup
     // Two 16-row groups need at least 64 workgroups (on MI355X, cold, against the padded copy:
     // 32x1500x516, 24 workgroups, 10.66 / 7.55 us; 17x4093x1028, 96, 7.60 / 9.55; 20x4093x2052, 160,
     // 10.0 / 11.0).
-    if (ragged && M > 16 && (long)strips * ternix_hip::line_gemv_splits(K, S) < 64) return false;
-    const int NW = fw == 4 && !epi && !ragged ? 4 : 8;
+    if (M > 16 && (long)strips * ternix_hip::line_gemv_splits(K, S) < 64) return false;
+    const int NW = fw == 4 && !epi && !rag_form ? 4 : 8;
     const int splits = ternix_hip::line_gemv_splits(K, S);
     if (splits > 64) return false;
     const int stride = ternix_hip::ticket_stride((size_t)strips);
     unsigned long long* tk = c.tickets(ternix_hip::ticket_units((size_t)strips));
     if (!tk) return false;
     c.note("line_gemv_kernel%s S=%d waves=%d+1 splits=%d%s%s (splits added with int32 atomics into C zeroed by each "
-           "strip's split 0)", ragged ? " ragged" : (tiled ? " (tile-64)" : ""), S, NW, splits, aq.mode == 2 ? " rmsnorm+quantise" : (aq.mode == 1 ? " quantise" : ""),
+           "strip's split 0)", rag_form ? " ragged" : (tiled ? " (tile-64)" : ""), S, NW, splits, aq.mode == 2 ? " rmsnorm+quantise" : (aq.mode == 1 ? " quantise" : ""),
            epi ? (os.swiglu ? " dequant+swiglu" : " dequant") : "");
     // Rows whose length is not a multiple of 128 bytes share a cache line between neighbouring strips:
     // those launches take the XCD-chunked unit order (on MI355X, cold: 1x4096x11008 6.40 -> 5.70 us,
@@ -906,7 +921,9 @@ hipError_t run_auto(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int
     if (!pad_off && needs_padding(dA, dB, K, N, M <= skinny_max)) {
         // up to 32 rows, int32 output: the whole-line GEMV reads the ragged operands as they are, one launch
         hipError_t e = hipSuccess;
-        if (M <= skinny_max && os.Y == nullptr && run_line_gemv(dA, dB, dC, M, K, N, c, &e)) return e;
+        if (M <= skinny_max && os.Y == nullptr &&
+            run_line_gemv(dA, dB, dC, M, K, N, c, &e, ternix_hip::OutScale{}, ternix_hip::ActQuant{}, 0, true))
+            return e;
         e = run_padded(dA, dB, dC, M, K, N, c, os, M <= skinny_max);
         if (e != hipErrorNotSupported) return e;
     }

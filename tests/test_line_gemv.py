@@ -44,6 +44,11 @@ def test_plan_names_line_kernel_when_forced():
         assert not _plan(lib, 17, 1000, 6900).startswith("line_gemv_kernel")  # 17-32 rows from K = 1024
         assert _plan(lib, 32, 2560, 6900).startswith("line_gemv_kernel ragged")  # two 16-row groups
         assert not _plan(lib, 33, 2560, 6900).startswith("line_gemv_kernel")
+        # N/4 = 224: aligned for this kernel, not for the wave kernels (N/4 % 64 != 0), whose route
+        # is the padded copy: up to 16 rows here, the padded copy above
+        assert _plan(lib, 16, 4864, 896).startswith("line_gemv_kernel S=2")
+        assert not _plan(lib, 17, 4864, 896).startswith("line_gemv_kernel")
+        assert not _plan(lib, 9, 4864, 1024).startswith("line_gemv_kernel")  # N/4 % 64 == 0: wave kernels
         assert lib.ternix_hip_debug_set(b"line", 1, 8, -1, -1) == 0
         assert not _plan(lib, 1, 8192, 4096).startswith("line_gemv_kernel")  # 128 splits > 64
     finally:
@@ -382,3 +387,45 @@ def test_line_gemv_ffn_strip_maxima_bit_equal(shape, zero_x):
     assert np.isfinite(maxima).all()
     assert np.array_equal(rows.view(np.int32), maxima.view(np.int32))
     assert np.array_equal(off.view(np.int32), maxima.view(np.int32))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape", [(9, 4864, 896), (16, 2432, 896), (16, 8192, 896), (12, 130, 448)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_line_gemv_rows_instead_of_padded_copy(oracle, shape):
+    """Operands aligned for the whole-line GEMV but not for the wave kernels (N/4 % 64 != 0) take the
+    whole-line GEMV up to 16 rows (8 below K = 256) instead of the padded copy: bit-exact against
+    the oracle on two calls in a row."""
+    lib = tx._load()
+    m, k, n = shape
+    p = _ragged_problem(oracle, np.random.default_rng(sum(shape) + 11), m, k, n, 0, 0)
+    _, _, _, da, db, dc, expect, _, _ = p
+    plan = _plan(lib, m, k, n)
+    assert plan.startswith("line_gemv_kernel S=") == (k >= 256), plan
+    log(f"[line instead of padded copy] M={m} K={k} N={n} plan={plan[:40]}")
+    for rep in range(2):
+        dc.upload(np.full(m * n + GUARD, GARBAGE, np.int32))
+        assert tx.mul_mat_ternary(da.value, db.value, dc.value, m, k, n) == 0
+        hr.synchronize()
+        _check_guarded(dc, m, n, expect, rep)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape,s", [((1, 8192, 1024), 4), ((1, 4096, 4096), 3), ((8, 2560, 6912), 4),
+                                     ((1, 2560, 6912), 3), ((4, 6912, 2560), 4), ((1, 4096, 1024), 3)],
+                         ids=lambda v: "x".join(map(str, v)) if isinstance(v, tuple) else f"S{v}")
+def test_line_gemv_minimum_k_steps(oracle, shape, s):
+    """The automatic plan's k-steps per workgroup: at least 3 from 64 k-steps, 4 from 96 and 4 with
+    5-8 rows from 40 (a 256-CU device), bit-exact against the oracle."""
+    lib = tx._load()
+    m, k, n = shape
+    p = _ragged_problem(oracle, np.random.default_rng(sum(shape) + 13), m, k, n, 0, 0)
+    _, _, _, da, db, dc, expect, _, _ = p
+    plan = _plan(lib, m, k, n)
+    if hr.device_attribute(hr.ATTR_MULTIPROCESSOR_COUNT) == 256:
+        assert plan.startswith(f"line_gemv_kernel S={s} "), plan
+    log(f"[line minimum k-steps] M={m} K={k} N={n} plan={plan[:40]}")
+    dc.upload(np.full(m * n + GUARD, GARBAGE, np.int32))
+    assert tx.mul_mat_ternary(da.value, db.value, dc.value, m, k, n) == 0
+    hr.synchronize()
+    _check_guarded(dc, m, n, expect, 0)
