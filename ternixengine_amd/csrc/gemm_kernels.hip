@@ -695,13 +695,43 @@ hipError_t launch_gemm_t(const int8_t* A, const uint8_t* B, int32_t* C, int M, i
 bool gemm_narrow_wanted(int M, int K, int N) {
     const int env = debug_get(DBG_GEMM_NARROW);
     const int NB = N >> 2;
-    if (env == 0 || M > 64 || NB % 16 != 0 || K % 256 != 0) return false;
+    if (env == 0 || NB % 16 != 0 || K % 256 != 0) return false;
     if (env > 0) return true;
+    if (M > 64) return false;
     return (long)((M + 63) / 64) * (NB / 16) <= device_cu_count();
 }
 
 bool gemm_narrow_ok(int M, int K, int N, int k_len, int splits, int k_split) {
     return gemm_narrow_wanted(M, K, N) && k_len % 256 == 0 && (splits == 1 || k_split % 256 == 0);
+}
+
+// Tile height of a split-K launch: 64-row tiles of four waves or 128-row tiles of eight, each with
+// the split count sized to one workgroup per CU (at most 16 splits of >= 256 k-rows).  The plan that
+// keeps more CUs busy wins; on a tie the 64-row tiles win where they need no split at all on a full
+// grid, the 128-row ones where each workgroup carries >= 80 M multiply-adds (their second wave per
+// SIMD pays for the larger partials), else the 64-row ones.  On MI355X, cold weights, 64 / 128 rows:
+// 128x11008x4096 15.4 / 19.3 us, 256x16384x4096 27.1 / 28.3, 256x8192x2048 14.4 / 19.3, 512x8192x2048
+// 18.8 / 22.9 (ties, fewer multiply-adds); 512x11008x4096 33.2 / 32.1, 512x16384x4096 42.8 / 39.7,
+// 768x16384x4096 64.1 / 55.1 (ties, more); 384x11008x4096 32.0 / 28.4 (192 against 240 workgroups);
+// 1024x11008x4096 45.3 / 49.0 and 1024x16384x4096 65.1 / 62.4 (the 64-row tiles without a split).
+int gemm_split_rows(int M, int K, int N) {
+    const int bm_env = debug_get(DBG_GEMM_BM);
+    if (bm_env == 64 || bm_env == 128) return bm_env;  // tests and measurements
+    if (M % 128 != 0) return 64;  // no padding rows
+    const long cus = device_cu_count();
+    const long smax = std::min<long>(std::max(1, K / 256), 16);
+    auto plan = [&](int rows, long* splits) {  // busy CUs of the plan's last round, as a fraction x cus
+        const long t = (long)((M + rows - 1) / rows) * (long)((N / 4 + 63) / 64);
+        *splits = std::min<long>(t * 2 <= cus ? cus / t : 1, smax);
+        const long wgs = t * *splits;
+        return wgs % cus == 0 ? cus : wgs % cus;
+    };
+    long s64 = 1, s128 = 1;
+    const long f64 = plan(64, &s64), f128 = plan(128, &s128);
+    if (f128 != f64) return f128 > f64 ? 128 : 64;
+    if (s64 == 1 && f64 == cus) return 64;
+    const double macs = (double)M * (double)N * (double)K / (double)cus;
+    return macs >= 80e6 ? 128 : 64;
 }
 
 // Which GEMM kernel a launch_gemm call runs (the single place the choice is made).
@@ -729,18 +759,16 @@ GemmChoice gemm_choice(const int8_t* A, const uint8_t* B, int M, int K, int N, i
     constexpr int small_m_max = 64;
     // 64 x 64 output tiles (16 bytes of every weight row): enough workgroups without a K split where
     // the 256-column tiles would need one; one m-tile per wave, 256-deep stages.
-    if (M <= small_m_max && gemm_narrow_ok(M, K, N, k_end - k_begin, splits, k_split)) return GemmChoice::Narrow64;
+    if ((M <= small_m_max || debug_get(DBG_GEMM_NARROW) > 0) && gemm_narrow_ok(M, K, N, k_end - k_begin, splits, k_split)) return GemmChoice::Narrow64;
     // Without a K split, 64-row tiles in workgroups of four waves (two co-resident per CU, whose
     // barriers and final stores overlap each other's work) instead of 128-row tiles of eight waves:
     // measured on MI355X, cold weights, 2048x4096x4096 29.1 -> 27.6 us, 1024x4096x4096 25.4 -> 20.3,
     // 512x4096x4096 25.1 -> 19.5, 768x4096x11008 52.2 -> 46.1, 1536x4096x11008 81.2 -> 71.7,
-    // 2048x14336x4096 90.6 -> 90.4 (one round: equal).  With a K split the 128-row tiles stay
-    // (256x16384x4096: 31.8 against 35.5 us).  Small M (64 rows or fewer): the same four-wave
-    // workgroups, so no MFMA row or A byte is spent on padding rows; the caller splits K to fill the chip.
-    // With a K split, 64-row tiles also where the last 128-row tile would be mostly padding (M mod 128
-    // in 1 .. 64): 129x8192x2304 in 8 splits 22.1 -> 20.3 us (the padded copy of 129x8191x2052).
-    const bool pad_rows64 = splits > 1 && bm_env <= 0 && ((M + 63) / 64) * 64 < ((M + 127) / 128) * 128;
-    if (M <= small_m_max || bm == 64 || pad_rows64 || (splits == 1 && bm == 128 && bm_env <= 0))
+    // 2048x14336x4096 90.6 -> 90.4 (one round: equal).  With a K split: gemm_split_rows.  Small M (64
+    // rows or fewer): the same four-wave workgroups, so no MFMA row or A byte is spent on padding
+    // rows; the caller splits K to fill the chip.
+    const bool split64 = splits > 1 && bm_env <= 0 && gemm_split_rows(M, K, N) == 64;
+    if (M <= small_m_max || bm == 64 || split64 || (splits == 1 && bm == 128 && bm_env <= 0))
         return GemmChoice::Pipe64;
     return bm == 128 ? GemmChoice::Pipe128 : GemmChoice::Fast256;
 }

@@ -775,10 +775,10 @@ hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
 // the partial tiles go through the same workspace and reduce launch as the skinny path.
 int gemm_splits(int M, int K, int N) {
     const int env = ternix_hip::debug_get(ternix_hip::DBG_GEMM_SPLITS);  // tests
-    // the tile height launch_gemm picks for a split launch (64 also where a last 128-row tile would
-    // be mostly padding)
-    const int bm = M <= 64 || ((M + 63) / 64) * 64 < ((M + 127) / 128) * 128 ? 64 : 128;
+    // the tile height launch_gemm picks for a split launch; one workgroup per CU over the tiles and
+    // splits
     const bool narrow = ternix_hip::gemm_narrow_wanted(M, K, N);  // 64-column tiles instead of 256
+    const int bm = narrow ? 64 : ternix_hip::gemm_split_rows(M, K, N);
     const long tiles = (long)((M + bm - 1) / bm) * (long)((N / 4 + 63) / 64) * (narrow ? 4 : 1);
     const long cus = cu_count();
     // K <= 4096: the reduce launch and the partial sums cost more than the idle CUs (measured on

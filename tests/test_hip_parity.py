@@ -518,3 +518,26 @@ def test_several_m_groups_self_zeroing_wave(oracle, m, k, n, splits):
     log(f"[wave m-groups] M={m} K={k} N={n} {plan[:44]}")
     for rep in range(2):
         assert (run("auto", a, wp, n) == expect).all(), rep
+
+
+@pytest.mark.parametrize("m,k,n,rows,splits", [(96, 8192, 2048, 64, 16), (128, 6144, 8192, 64, 4),
+                                               (256, 8192, 2048, 64, 8), (512, 11008, 4096, 128, 4),
+                                               (384, 11008, 4096, 128, 5)])
+def test_split_gemm_tile_height(oracle, m, k, n, rows, splits):
+    """Split-K GEMMs: 64-row or 128-row tiles with the split count sized to one workgroup per CU, the
+    128-row ones where they keep more CUs busy or carry >= 80 M multiply-adds per workgroup (plans on
+    a 256-CU device), bit-exact against the oracle on two calls in a row."""
+    lib = tx._load()
+    buf = ctypes.create_string_buffer(192)
+    assert lib.ternix_hip_plan_describe(1 << 20, 1 << 24, m, k, n, buf, len(buf)) == 0
+    plan = buf.value.decode()
+    if hr.device_attribute(hr.ATTR_MULTIPROCESSOR_COUNT) == 256:
+        assert plan.startswith(f"gemm_pipe_kernel<{rows} rows x 256 cols"), plan
+        assert f"splits={splits} " in plan, plan
+    rng = np.random.default_rng(m + k + n)
+    a = rng.integers(-128, 128, size=(m, k), dtype=np.int8)
+    wp = rng.integers(0, 256, size=(k, n // 4), dtype=np.uint8)
+    expect = oracle.mm("scalar_mt", a, wp, n)
+    log(f"[split GEMM tiles] M={m} K={k} N={n} {plan[:60]}")
+    for rep in range(2):
+        assert (run("auto", a, wp, n) == expect).all(), rep
