@@ -697,7 +697,10 @@ bool gemm_narrow_wanted(int M, int K, int N) {
     const int NB = N >> 2;
     if (env == 0 || NB % 16 != 0 || K % 256 != 0) return false;
     if (env > 0) return true;
-    if (M > 64) return false;
+    // Not where K is split (K > 4096): there the 256-column tiles with more splits win (on MI355X,
+    // cold, 64 / 256 columns: 64x11008x4096 14.4 / 13.1 us, 48x11008x4096 13.8 / 11.9, 40x16384x4096
+    // 16.4 / 12.8, 64x16384x8192 30.1 / 21.4, 33x8192x4096 11.5 / 10.5).
+    if (M > 64 || K > 4096) return false;
     return (long)((M + 63) / 64) * (NB / 16) <= device_cu_count();
 }
 
