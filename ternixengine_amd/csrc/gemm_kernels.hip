@@ -692,20 +692,21 @@ hipError_t launch_gemm_t(const int8_t* A, const uint8_t* B, int32_t* C, int M, i
 // MI355X: cfg3 M=64 up 18.0 -> 13.4 us with no K split, 4096^2 at M=64 16.2 -> 9.9 us; with more
 // tiles than CUs, e.g. N = 28672, the 256-column tiles are faster).  The gemm_narrow debug switch (0 / 1) turns
 // the choice off / on regardless (experiments).
-bool gemm_narrow_wanted(int M, int K, int N) {
+bool gemm_narrow_wanted(int M, int K, int N, int tiled) {
     const int env = debug_get(DBG_GEMM_NARROW);
     const int NB = N >> 2;
     if (env == 0 || NB % 16 != 0 || K % 256 != 0) return false;
     if (env > 0) return true;
-    // Not where K is split (K > 4096): there the 256-column tiles with more splits win (on MI355X,
-    // cold, 64 / 256 columns: 64x11008x4096 14.4 / 13.1 us, 48x11008x4096 13.8 / 11.9, 40x16384x4096
-    // 16.4 / 12.8, 64x16384x8192 30.1 / 21.4, 33x8192x4096 11.5 / 10.5).
-    if (M > 64 || K > 4096) return false;
+    // Row-major weights: not where K is split (K > 4096), where the 256-column tiles with more splits
+    // win (on MI355X, cold, 64 / 256 columns: 64x11008x4096 14.4 / 13.1 us, 48x11008x4096 13.8 /
+    // 11.9, 40x16384x4096 16.4 / 12.8, 64x16384x8192 30.1 / 21.4, 33x8192x4096 11.5 / 10.5).  The
+    // tile-64 layout keeps them (its 1 KB blocks: 64x11008x4096 11.1 against 13.0 us).
+    if (M > 64 || (K > 4096 && !tiled)) return false;
     return (long)((M + 63) / 64) * (NB / 16) <= device_cu_count();
 }
 
-bool gemm_narrow_ok(int M, int K, int N, int k_len, int splits, int k_split) {
-    return gemm_narrow_wanted(M, K, N) && k_len % 256 == 0 && (splits == 1 || k_split % 256 == 0);
+bool gemm_narrow_ok(int M, int K, int N, int k_len, int splits, int k_split, int tiled) {
+    return gemm_narrow_wanted(M, K, N, tiled) && k_len % 256 == 0 && (splits == 1 || k_split % 256 == 0);
 }
 
 // Tile height of a split-K launch: 64-row tiles of four waves or 128-row tiles of eight, each with
@@ -762,7 +763,7 @@ GemmChoice gemm_choice(const int8_t* A, const uint8_t* B, int M, int K, int N, i
     constexpr int small_m_max = 64;
     // 64 x 64 output tiles (16 bytes of every weight row): enough workgroups without a K split where
     // the 256-column tiles would need one; one m-tile per wave, 256-deep stages.
-    if ((M <= small_m_max || debug_get(DBG_GEMM_NARROW) > 0) && gemm_narrow_ok(M, K, N, k_end - k_begin, splits, k_split)) return GemmChoice::Narrow64;
+    if ((M <= small_m_max || debug_get(DBG_GEMM_NARROW) > 0) && gemm_narrow_ok(M, K, N, k_end - k_begin, splits, k_split, tiled)) return GemmChoice::Narrow64;
     // Without a K split, 64-row tiles in workgroups of four waves (two co-resident per CU, whose
     // barriers and final stores overlap each other's work) instead of 128-row tiles of eight waves:
     // measured on MI355X, cold weights, 2048x4096x4096 29.1 -> 27.6 us, 1024x4096x4096 25.4 -> 20.3,

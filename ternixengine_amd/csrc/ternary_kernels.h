@@ -151,7 +151,7 @@ hipError_t launch_skinny_wave(const int8_t* A, const uint8_t* B, int32_t* C, int
 // nsw 2); the dequantising epilogue then uses the kernel's own row scales.)
 // True when launch_gemm runs this M <= 64 shape on 64 x 64 tiles (K % 256 == 0, N/4 % 16 == 0, at
 // most one tile per CU); split-K k-ranges must then be multiples of 256.
-bool gemm_narrow_wanted(int M, int K, int N);
+bool gemm_narrow_wanted(int M, int K, int N, int tiled = 0);
 // Tile height (64 or 128 rows) launch_gemm uses for this shape when K is split.
 int gemm_split_rows(int M, int K, int N);
 // The GEMM kernel launch_gemm runs for these arguments (Invalid: it would return hipErrorInvalidValue).

@@ -773,11 +773,11 @@ hipError_t run_skinny(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, i
 // Split-K for GEMMs with too few output tiles to fill the chip (mid-size M against a long K, e.g.
 // cfg3 M=64, the worst case M=256): each split covers a contiguous k-range of whole 128-row stages,
 // the partial tiles go through the same workspace and reduce launch as the skinny path.
-int gemm_splits(int M, int K, int N) {
+int gemm_splits(int M, int K, int N, int tiled = 0) {
     const int env = ternix_hip::debug_get(ternix_hip::DBG_GEMM_SPLITS);  // tests
     // the tile height launch_gemm picks for a split launch; one workgroup per CU over the tiles and
     // splits
-    const bool narrow = ternix_hip::gemm_narrow_wanted(M, K, N);  // 64-column tiles instead of 256
+    const bool narrow = ternix_hip::gemm_narrow_wanted(M, K, N, tiled);  // 64-column tiles instead of 256
     const int bm = narrow ? 64 : ternix_hip::gemm_split_rows(M, K, N);
     const long tiles = (long)((M + bm - 1) / bm) * (long)((N / 4 + 63) / 64) * (narrow ? 4 : 1);
     const long cus = cu_count();
@@ -796,10 +796,10 @@ hipError_t run_gemm(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int
     const hipStream_t st = c.st;
     (void)st;
     if (K <= ternix_hip::kMaxKPerAccumulator) {
-        int splits = gemm_splits(M, K, N);
+        int splits = gemm_splits(M, K, N, tiled);
         if (splits > 1) {
             // whole stages per split: 256 rows for the narrow tiles, 128 for the others
-            const int unit = ternix_hip::gemm_narrow_wanted(M, K, N) ? 256 : (K % 128 == 0 ? 128 : 64);
+            const int unit = ternix_hip::gemm_narrow_wanted(M, K, N, tiled) ? 256 : (K % 128 == 0 ? 128 : 64);
             const int k_split = ((K + splits - 1) / splits + unit - 1) / unit * unit;
             splits = (K + k_split - 1) / k_split;
             const size_t need = (size_t)splits * (size_t)M * (size_t)N * sizeof(int32_t);
