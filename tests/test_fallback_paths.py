@@ -11,7 +11,7 @@ from ternixengine_amd import hip_runtime as hr
 
 SHAPES = [(1, 2560, 2560), (1, 6912, 2560), (4, 4096, 1024), (16, 2048, 4096), (16, 8192, 1024), (24, 4096, 512),
           (32, 2560, 1024), (48, 1024, 2048), (64, 4096, 1024), (129, 1001, 516), (1, 1000, 3076), (17, 4093, 1028),
-          (256, 2048, 1024), (320, 1024, 2048)]
+          (256, 2048, 1024), (320, 1024, 2048), (96, 8192, 1024), (256, 6144, 1024)]
 
 SWITCHES = [
     {"skinny_wave": 0},                                    # DMA-staged GEMVs
@@ -28,6 +28,9 @@ SWITCHES = [
     {"self_zero": 0},                                      # M = 1 atomic plan with the fill launch
     {"gemm_bm": 128},                                      # 128-row GEMM tiles of eight waves
     {"gemm_bm": 256},                                      # 256-row GEMM tiles
+    {"gemm_bm": 64},                                       # 64-row GEMM tiles, split or not
+    {"gemm_narrow": 1},                                    # 64 x 64 GEMM tiles at any M and split
+    {"gemm_splits": 3},                                    # an odd GEMM split count
     {"nt": (1, 1)},                                        # non-temporal weight loads in both GEMV kernels
     {"skinny_wave": 0, "nt": (1, 1)},                      # ... in the DMA-staged GEMVs on every shape
     {"skinny_wave": 0, "skinny_dma": (3, 12)},             # DMA-staged GEMVs with a forced split count
