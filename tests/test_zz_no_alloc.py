@@ -15,6 +15,7 @@ PAIRS = [
     ((64, 11008, 4096), (40, 6144, 2048)),    # GEMM split-K, then a smaller split
     ((129, 8191, 2052), (17, 4093, 1028)),    # ragged: padded copies of W and A, then smaller ones
     ((256, 4096, 4096), (1, 1000, 3076)),     # GEMM without scratch, then ragged GEMV
+    ((256, 16384, 4096), (128, 11008, 4096)),  # split-K 64-row tiles (16 MiB of partials), then 8 splits
 ]
 
 
