@@ -726,7 +726,7 @@ int gemm_split_rows(int M, int K, int N) {
     if (M % 128 != 0) return 64;  // no padding rows
     const long cus = device_cu_count();
     const long smax = std::min<long>(std::max(1, K / 256), 16);
-    auto plan = [&](int rows, long* splits) {  // busy CUs of the plan's last round, as a fraction x cus
+    auto plan = [&](int rows, long* splits) {  // CUs busy in the plan's last wave of workgroups
         const long t = (long)((M + rows - 1) / rows) * (long)((N / 4 + 63) / 64);
         *splits = std::min<long>(t * 2 <= cus ? cus / t : 1, smax);
         const long wgs = t * *splits;
