@@ -433,6 +433,11 @@ bool run_atomic_wave(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, in
     // 32 rows it wins wherever it splits K (24 and 32 rows: 1.11-1.42x against the in-launch sums and
     // the reduce launch on five decode shapes).
     if (M > 32 && sps > 24 && fsp <= 1) return false;
+    // ... and not where the narrow GEMM runs K whole on at least 96 of its 64-column tiles (on MI355X,
+    // cold, wave / GEMM: 64x2560x6912 8.99 / 7.79 us, 48x2560x6912 8.08 / 7.61, 48x2048x8192 8.63 /
+    // 6.91, 36x2048x8192 7.64 / 6.88; with fewer tiles the wave kernel stays faster, 48x4096x4096 7.67 /
+    // 9.86, 64x6912x2560 8.70 / 10.41).
+    if (M > 32 && fsp <= 1 && ternix_hip::gemm_narrow_wanted(M, K, N) && (N / 4) / 16 >= 96) return false;
     // Column waves (M <= 4, 32-byte parts): a workgroup owns a 128-byte strip and each wave one
     // 32-byte part over the workgroup's whole k-range, so the four parts of each weight line reach one
     // CU together.  More K splits for the same workgroups (more atomic adds per output), so only where

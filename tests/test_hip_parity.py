@@ -499,7 +499,7 @@ def test_wave_kernel_shapes(oracle, m, k, n):
 
 
 @pytest.mark.parametrize("m,k,n,splits", [(17, 4096, 4096, 6), (24, 2560, 6912, 5), (32, 6912, 2560, 6),
-                                          (40, 4096, 4096, 5), (48, 2560, 6912, 3), (64, 6912, 2560, 6)])
+                                          (40, 4096, 4096, 5), (48, 4096, 4096, 5), (64, 6912, 2560, 6)])
 def test_several_m_groups_self_zeroing_wave(oracle, m, k, n, splits):
     """Aligned operands with 17-64 rows take the wave-pipelined kernel's self-zeroing plan, about two
     workgroups per CU (not the ragged form of the whole-line GEMV, whose two row groups are for ragged
@@ -541,3 +541,24 @@ def test_split_gemm_tile_height(oracle, m, k, n, rows, splits):
     log(f"[split GEMM tiles] M={m} K={k} N={n} {plan[:60]}")
     for rep in range(2):
         assert (run("auto", a, wp, n) == expect).all(), rep
+
+
+@pytest.mark.parametrize("m,k,n,kernel", [(48, 2560, 6912, "gemm_pipe_kernel<64 rows x 64 cols"),
+                                          (64, 2048, 8192, "gemm_pipe_kernel<64 rows x 64 cols"),
+                                          (48, 4096, 4096, "skinny_wave_kernel"),
+                                          (64, 6912, 2560, "skinny_wave_kernel")])
+def test_many_rows_wave_or_narrow_gemm(oracle, m, k, n, kernel):
+    """33-64 rows: the unsplit narrow GEMM where it has at least 96 column tiles, else the
+    wave-pipelined kernel's split plan (plans on a 256-CU device), bit-exact against the oracle."""
+    lib = tx._load()
+    buf = ctypes.create_string_buffer(192)
+    assert lib.ternix_hip_plan_describe(1 << 20, 1 << 24, m, k, n, buf, len(buf)) == 0
+    plan = buf.value.decode()
+    if hr.device_attribute(hr.ATTR_MULTIPROCESSOR_COUNT) == 256:
+        assert plan.startswith(kernel), plan
+    rng = np.random.default_rng(m * 7 + k + n)
+    a = rng.integers(-128, 128, size=(m, k), dtype=np.int8)
+    wp = rng.integers(0, 256, size=(k, n // 4), dtype=np.uint8)
+    expect = oracle.mm("scalar_mt", a, wp, n)
+    log(f"[rows 33-64] M={m} K={k} N={n} {plan[:50]}")
+    assert (run("auto", a, wp, n) == expect).all()
