@@ -585,6 +585,7 @@ bool run_line_gemv(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int 
         // is faster, 1x4096x28672 9.1 against 11.8), and 4 k-steps on up to two per CU instead of 8 on
         // one (1x4096x14336 6.33 -> 6.02, 1x8192x8192 6.47 -> 6.28; measured on MI355X, cold).
         const long cap2 = 2L * (long)cu_count();
+        const int S1 = S;  // the one-per-CU plan (0: none)
         if (S == 0 && !epi && aq.mode == 0) {
             for (int cand : {2, 3, 4, 6}) {
                 if (cand < min_s) continue;
@@ -600,6 +601,10 @@ bool run_line_gemv(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int 
             if (sp4 <= 64 && (long)strips * sp4 <= cap2) S = 4;
         }
         if (S == 0) return false;
+        // 7-8 rows on operands the wave-pipelined kernel takes: no plan of two workgroups per CU
+        // (on MI355X, cold, against that kernel: 8x8192x8192 10.48 / 9.79 us, 8x14336x4096 10.17 /
+        // 8.99, 7x14336x4096 9.81 / 8.88; the one-per-CU plans stay, 8x11008x4096 7.47 / 8.33).
+        if (M >= 7 && !rows_ragged && S != S1) return false;
     }
     if (M > 16 && S > 6) return false;  // two 16-row groups: at most 6 k-steps per workgroup
     // Two 16-row groups need at least 64 workgroups (on MI355X, cold, against the padded copy:

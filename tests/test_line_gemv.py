@@ -429,3 +429,23 @@ def test_line_gemv_minimum_k_steps(oracle, shape, s):
     assert tx.mul_mat_ternary(da.value, db.value, dc.value, m, k, n) == 0
     hr.synchronize()
     _check_guarded(dc, m, n, expect, 0)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape,line", [((8, 8192, 8192), False), ((7, 14336, 4096), False), ((8, 11008, 4096), True),
+                                        ((6, 8192, 8192), True)], ids=lambda v: "x".join(map(str, v)) if isinstance(v, tuple) else str(v))
+def test_line_gemv_seven_eight_rows_one_per_cu(oracle, shape, line):
+    """7-8 rows on aligned operands: the whole-line GEMV only with one workgroup per CU, else the
+    wave-pipelined kernel (plans on a 256-CU device); bit-exact against the oracle."""
+    lib = tx._load()
+    m, k, n = shape
+    p = _ragged_problem(oracle, np.random.default_rng(sum(shape) + 17), m, k, n, 0, 0)
+    _, _, _, da, db, dc, expect, _, _ = p
+    plan = _plan(lib, m, k, n)
+    if hr.device_attribute(hr.ATTR_MULTIPROCESSOR_COUNT) == 256:
+        assert plan.startswith("line_gemv_kernel S=") == line, plan
+    log(f"[line 7-8 rows] M={m} K={k} N={n} plan={plan[:40]}")
+    dc.upload(np.full(m * n + GUARD, GARBAGE, np.int32))
+    assert tx.mul_mat_ternary(da.value, db.value, dc.value, m, k, n) == 0
+    hr.synchronize()
+    _check_guarded(dc, m, n, expect, 0)
