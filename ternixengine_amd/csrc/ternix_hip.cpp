@@ -605,6 +605,10 @@ bool run_line_gemv(const int8_t* dA, const uint8_t* dB, int32_t* dC, int M, int 
         // (on MI355X, cold, against that kernel: 8x8192x8192 10.48 / 9.79 us, 8x14336x4096 10.17 /
         // 8.99, 7x14336x4096 9.81 / 8.88; the one-per-CU plans stay, 8x11008x4096 7.47 / 8.33).
         if (M >= 7 && !rows_ragged && S != S1) return false;
+        // One row: no 6-k-step plan of two workgroups per CU either; the DMA-staged kernel is level
+        // or faster (1x5120x13824 7.41 / 7.14 us, 1x3584x18944 7.12 / 7.01, 1x2560x27648 7.36 / 7.39;
+        // at 4 rows the whole-line GEMV stays well ahead, 4x5120x13824 7.84 / 8.67).
+        if (M == 1 && !rows_ragged && S != S1 && S == 6) return false;
     }
     if (M > 16 && S > 6) return false;  // two 16-row groups: at most 6 k-steps per workgroup
     // Two 16-row groups need at least 64 workgroups (on MI355X, cold, against the padded copy:
